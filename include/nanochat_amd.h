@@ -1,0 +1,116 @@
+/*
+ * nanochat_amd: the C ABI of the MI355X (gfx950) fp8 KV-cache decode path.
+ *
+ * Every pointer argument is a device address unless stated otherwise; sizes are element counts. Every
+ * entry point is stream-ordered on `stream` (a hipStream_t; NULL = the null stream) and never
+ * synchronizes. Entry points that return int return NC_OK (0), a negative NC_ERR_* code for an argument
+ * the host can check, or a positive hipError_t from the launch.
+ *
+ * Data formats (the build's; the reference caches bf16, model/kernels/decode.cu:726):
+ *   bf16             raw 16-bit patterns (torch.bfloat16 storage)
+ *   k_pages, v_pages uint8 [num_pages][Hkv][2048]: one 16-token page of one KV head, OCP e4m3fn codes in
+ *                    the MFMA tiling documented in nanochat_amd/csrc/nc_device.h (k/v_page_offset)
+ *   k_scale, v_scale fp32 [num_pages][Hkv][16]: one absmax/448 scale per (token, KV head)
+ *   block_table      int32 [B][max_pages]: position p of sequence b is slot p % 16 of page
+ *                    block_table[b][p / 16]
+ * Query head h reads KV head h / (Hq / Hkv); Hq must be a multiple of Hkv with Hq / Hkv <= 16.
+ */
+#ifndef NANOCHAT_AMD_H
+#define NANOCHAT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    NC_OK = 0,
+    NC_ERR_NULL = -1,       /* a required pointer is NULL */
+    NC_ERR_SHAPE = -2,      /* a size or head count out of the supported range */
+    NC_ERR_WORKSPACE = -3,  /* the workspace is smaller than nc_decode_workspace_bytes */
+};
+
+/* Text of a status code (static storage). */
+const char *nc_status_string(int status);
+
+/* Version of this ABI (bumped on any signature or format change). */
+int nc_abi_version(void);
+
+/*
+ * Training-form fused q/k prologue; same symbol, arguments and meaning as the reference's
+ * model/kernels/qk_prologue.cu:111-118 (called by model/ops/qk_prologue.py:13-21 qk_forward):
+ * q, k: bf16 (B, T, H, 128) views with token stride 3*H*128 (the fused projection); gq, gk: fp32 [128];
+ * qo, ko: bf16 contiguous (B, T, H, 128); cos, sin: fp32 [T][64] indexed by the token's position t;
+ * rows = B*T*H. Per row: RMS norm (eps FLT_EPSILON), gain, -theta rotation, one bf16 rounding.
+ * Like the reference it returns nothing; nc_last_error() reports its launch status.
+ */
+void qkp_forward(const void *q, const void *k, const void *gq, const void *gk, void *qo, void *ko, const void *cos,
+                 const void *sin, long long rows, int H, int T, void *stream);
+
+/* Status of the last void entry point's launch on this host thread (NC_OK or a hipError_t). */
+int nc_last_error(void);
+
+/*
+ * Quantize and append T new tokens per sequence to the paged fp8 cache. Replaces the cache store of the
+ * reference's k_prologue (model/kernels/decode.cu:551-565, `kc/vc[cs][p] = bf16(k/v)`).
+ * k, v: bf16 [B][T][Hkv][128] at token stride `token_stride` elements (batch stride T*token_stride);
+ * token t of sequence b is written at position start_pos[b] + t; num_new (nullable) limits sequence b to
+ * its first num_new[b] tokens. Per (token, KV head): scale = max|x| / 448 (1 if all zero),
+ * code = e4m3fn_rne(clamp(x / scale, +-448)). Tokens whose page lies outside the block table or the
+ * page pool are skipped.
+ */
+int nc_kv_append_fp8(const void *k, const void *v, long long token_stride, int B, int T, int Hkv,
+                     const int32_t *start_pos, const int32_t *num_new, const int32_t *block_table, int max_pages,
+                     void *k_pages, void *v_pages, float *k_scale, float *v_scale, int num_pages, void *stream);
+
+/*
+ * The fused append of a decode or prefill step: the reference's attn_prologue q/k math
+ * (model/kernels/decode.cu:478-507 via qk_row.cuh:26-51) followed by nc_kv_append_fp8's quantized store.
+ * qkv: bf16 [B][T][(Hq + 2*Hkv)*128] at token stride `token_stride` elements: q heads, then k heads, then
+ * v heads. q and k rows are RMS-normed (eps FLT_EPSILON), multiplied by q_gain / k_gain (fp32 [128]) and
+ * rotated by -theta with cos, sin (fp32 [rope_len][64]) at the token's position, then rounded to bf16;
+ * q goes to q_out (bf16 [B][T][Hq][128], contiguous), k and v (unchanged) are quantized into the cache.
+ * Tokens at positions >= rope_len are skipped.
+ */
+int nc_qk_norm_rope_append_fp8(const void *qkv, long long token_stride, int B, int T, int Hq, int Hkv,
+                               const int32_t *start_pos, const int32_t *num_new, const float *q_gain,
+                               const float *k_gain, const float *cos, const float *sin, int rope_len, void *q_out,
+                               const int32_t *block_table, int max_pages, void *k_pages, void *v_pages,
+                               float *k_scale, float *v_scale, int num_pages, void *stream);
+
+/* Workspace bytes nc_decode_attn_fp8 needs for these sizes (0 when one split covers every sequence). */
+size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window, int pages_per_split);
+
+/*
+ * Single-token decode attention over the paged fp8 cache (split-K flash-decode). Replaces the reference's
+ * k_attn (model/kernels/decode.cu:567-675): sequence b's query at position p = seq_lens[b] - 1 attends
+ * keys [max(p - window, 0), p] (window < 0: all), scores (q . k) * sm_scale, fp32 softmax, out bf16.
+ * The current token must already be appended (nc_kv_append_fp8 / nc_qk_norm_rope_append_fp8).
+ * q: bf16 [B][Hq][128]; out: bf16 [B][Hq][128]; seq_lens: int32 [B] (<= 0: inactive, output zeros);
+ * max_seq_len: a host bound on seq_lens (sizes the grid; a longer sequence's output is NaN);
+ * pages_per_split: pages per work-group (0: automatic). A block-table entry outside [0, num_pages)
+ * makes that sequence's output NaN instead of reading outside the pool.
+ */
+int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *k_scale,
+                       const float *v_scale, const int32_t *block_table, int max_pages, int num_pages,
+                       const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window, float sm_scale,
+                       int pages_per_split, void *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Chunked-prefill attention over the paged fp8 cache (MFMA). Replaces the reference's prefill rows
+ * (model/kernels/decode.cu:1041-1051 with enqueue_body's append-then-attend order, 859-863): row t of
+ * sequence b sits at position start_pos[b] + t and attends keys [max(p - window, 0), p]; the chunk must
+ * already be appended. q, out: bf16 [B][T][Hq][128].
+ */
+int nc_prefill_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *k_scale,
+                        const float *v_scale, const int32_t *block_table, int max_pages, int num_pages,
+                        const int32_t *start_pos, int B, int T, int Hq, int Hkv, int window, float sm_scale,
+                        void *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOCHAT_AMD_H */

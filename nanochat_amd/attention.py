@@ -1,0 +1,102 @@
+"""Host wrappers of the fp8 KV path's HIP entry points (include/nanochat_amd.h).
+
+- qk_norm_rope_append: the fused append of a decode or prefill step — the reference's attn_prologue
+  q/k math (model/kernels/decode.cu:478-507, qk_row.cuh:26-51) plus the fp8 store that replaces
+  k_prologue's bf16 store (decode.cu:551-565).
+- decode_attention: split-K flash-decode over the paged cache, replacing k_attn (decode.cu:567-675).
+- prefill_attention: MFMA chunked prefill, replacing the prefill rows of dec_prefill
+  (decode.cu:1041-1051, append-then-attend order 859-863).
+
+Every function launches on the current torch stream and requires device tensors: there is no CPU path.
+"""
+import torch
+
+from .config import HEAD_DIM
+from .kv_cache import PagedKVCache, _require
+from .native import check, hip_library, pointer, stream
+
+
+def qk_norm_rope_append(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache, block_table: torch.Tensor,
+                        start_pos: torch.Tensor, q_gain: torch.Tensor, k_gain: torch.Tensor, cos: torch.Tensor,
+                        sin: torch.Tensor, num_new: torch.Tensor | None = None) -> torch.Tensor:
+    """qkv bf16 [B, T, (Hq + 2 Hkv) * 128] (rows contiguous; token stride = qkv.stride(1)) -> q bf16
+    [B, T, Hq, 128] normed and rotated; k (normed, rotated) and v are quantized into `cache` at positions
+    start_pos[b] + t."""
+    B, T, W = qkv.shape
+    Hkv = cache.num_kv_heads
+    if W != (num_q_heads + 2 * Hkv) * HEAD_DIM:
+        raise ValueError(f"qkv width {W} != (Hq + 2 Hkv) * {HEAD_DIM} = {(num_q_heads + 2 * Hkv) * HEAD_DIM}")
+    if qkv.dtype != torch.bfloat16 or not qkv.is_cuda or qkv.stride(2) != 1 or qkv.stride(0) != T * qkv.stride(1):
+        raise ValueError("qkv must be a bf16 device tensor with contiguous rows and a uniform token stride")
+    for name, t in (("q_gain", q_gain), ("k_gain", k_gain), ("cos", cos), ("sin", sin)):
+        _require(t, name, torch.float32)
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.size(1) != HEAD_DIM // 2:
+        raise ValueError("cos, sin must be [positions, 64]")
+    _require(start_pos, "start_pos", torch.int32)
+    if num_new is not None:
+        _require(num_new, "num_new", torch.int32)
+    cache.check_table(block_table)
+    q_out = torch.empty(B, T, num_q_heads, HEAD_DIM, dtype=torch.bfloat16, device=qkv.device)
+    check(hip_library().nc_qk_norm_rope_append_fp8(
+        pointer(qkv), qkv.stride(1), B, T, num_q_heads, Hkv, pointer(start_pos),
+        pointer(num_new) if num_new is not None else None, pointer(q_gain), pointer(k_gain), pointer(cos),
+        pointer(sin), cos.size(0), pointer(q_out), pointer(block_table), block_table.size(1),
+        pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.k_scale), pointer(cache.v_scale),
+        cache.num_pages, stream()))
+    return q_out
+
+
+def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int, window: int = -1,
+                           pages_per_split: int = 0) -> int:
+    return hip_library().nc_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_seq_len, window,
+                                                   pages_per_split)
+
+
+def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                     max_seq_len: int, window: int = -1, sm_scale: float | None = None, pages_per_split: int = 0,
+                     out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """q bf16 [B, Hq, 128] (the current token's, already appended) -> out bf16 [B, Hq, 128].
+
+    Sequence b attends its keys [max(p - window, 0), p], p = seq_lens[b] - 1; max_seq_len bounds seq_lens."""
+    _require(q, "q", torch.bfloat16)
+    B, Hq, D = q.shape
+    if D != HEAD_DIM:
+        raise ValueError(f"q must be [B, Hq, {HEAD_DIM}]")
+    _require(seq_lens, "seq_lens", torch.int32)
+    cache.check_table(block_table)
+    if sm_scale is None:
+        sm_scale = HEAD_DIM ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    _require(out, "out", torch.bfloat16)
+    lib = hip_library()
+    need = lib.nc_decode_workspace_bytes(B, Hq, cache.num_kv_heads, max_seq_len, window, pages_per_split)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    check(lib.nc_decode_attn_fp8(
+        pointer(q), pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.k_scale), pointer(cache.v_scale),
+        pointer(block_table), block_table.size(1), cache.num_pages, pointer(seq_lens), max_seq_len, B, Hq,
+        cache.num_kv_heads, window, sm_scale, pages_per_split, pointer(out),
+        pointer(workspace) if need else None, need, stream()))
+    return out
+
+
+def prefill_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Tensor, start_pos: torch.Tensor,
+                      window: int = -1, sm_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """q bf16 [B, T, Hq, 128] of a chunk already appended at positions start_pos[b] + t -> out bf16 like q."""
+    _require(q, "q", torch.bfloat16)
+    B, T, Hq, D = q.shape
+    if D != HEAD_DIM:
+        raise ValueError(f"q must be [B, T, Hq, {HEAD_DIM}]")
+    _require(start_pos, "start_pos", torch.int32)
+    cache.check_table(block_table)
+    if sm_scale is None:
+        sm_scale = HEAD_DIM ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    _require(out, "out", torch.bfloat16)
+    check(hip_library().nc_prefill_attn_fp8(
+        pointer(q), pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.k_scale), pointer(cache.v_scale),
+        pointer(block_table), block_table.size(1), cache.num_pages, pointer(start_pos), B, T, Hq, cache.num_kv_heads,
+        window, sm_scale, pointer(out), stream()))
+    return out

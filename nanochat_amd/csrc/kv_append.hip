@@ -1,0 +1,225 @@
+/*
+ * Cache append for the fp8 KV path on gfx950: the fused q/k RMS norm + gain + -theta rotation, the
+ * per-(token, KV head) absmax e4m3fn quantizer and the paged store; plus the training-form q/k prologue
+ * (the reference's qkp_forward) on the same row math.
+ *
+ * One wave per (token, head) row: lane l holds the rotation pair (dims l, l + 64), so the rotation is
+ * lane-local and the row's sum of squares is one xor butterfly over the wave. Reference row math:
+ * model/kernels/qk_row.cuh:19-51 (qk_row_sum, qk_rstd, qk_rotate); the build fixes the summation order
+ * (lane partial x[l]^2 + x[l+64]^2, then offsets 32..1) and uses a correctly rounded 1/sqrt where the
+ * reference has rsqrtf.
+ */
+#include "nc_device.h"
+#include "nanochat_amd.h"
+
+namespace nc {
+
+/* RMS norm (eps FLT_EPSILON), gain and -theta rotation of one row held as lane pairs (x1 = dim l,
+ * x2 = dim l + 64); results before the bf16 rounding. Every operation is a single rounded fp32 op in the
+ * order of the oracle's qk_norm_rope. All 64 lanes of the wave must call it together. */
+__device__ __forceinline__ void norm_rope_pair(float x1, float x2, float g1, float g2, float c, float s, float &y1,
+                                               float &y2) {
+    const float part = x1 * x1 + x2 * x2;
+    const float ss = wave_sum_butterfly(part);
+    const float v = ss / 128.0f + FLT_EPS;
+    const float r = 1.0f / __builtin_sqrtf(v);  /* correctly rounded (HIP's __fsqrt_rn is not, here) */
+    const float n1 = (x1 * r) * g1;
+    const float n2 = (x2 * r) * g2;
+    y1 = n1 * c + n2 * s;
+    y2 = n2 * c - n1 * s;
+}
+
+/* Quantize one row (lane pair x1 = dim l, x2 = dim l + 64, bf16 values) and store its codes into a page
+ * at the byte offsets OFF(slot, dim); lane 0 stores the scale. */
+template <int (*OFF)(int, int)>
+__device__ __forceinline__ void quantize_store(float x1, float x2, uint8_t *page, float *scale_at, int slot, int lane) {
+    const float amax = wave_max(fmaxf(fabsf(x1), fabsf(x2)));
+    const float scale = amax > 0.0f ? amax / FP8_MAX : 1.0f;
+    const float q1 = fminf(fmaxf(x1 / scale, -FP8_MAX), FP8_MAX);
+    const float q2 = fminf(fmaxf(x2 / scale, -FP8_MAX), FP8_MAX);
+    page[OFF(slot, lane)] = (uint8_t)e4m3_encode(q1);
+    page[OFF(slot, lane + HALF)] = (uint8_t)e4m3_encode(q2);
+    if (lane == 0) *scale_at = scale;
+}
+
+struct AppendArgs {
+    const uint16_t *k, *v;     /* plain append: [B][T][Hkv][128] at token_stride */
+    const uint16_t *qkv;       /* fused append: [B][T][(Hq + 2 Hkv) 128] at token_stride */
+    long long token_stride;
+    int B, T, Hq, Hkv;
+    const int32_t *start_pos, *num_new;
+    const float *q_gain, *k_gain, *cos, *sin;
+    int rope_len;
+    uint16_t *q_out;           /* [B][T][Hq][128] */
+    const int32_t *block_table;
+    int max_pages;
+    uint8_t *k_pages, *v_pages;
+    float *k_scale, *v_scale;
+    int num_pages;
+};
+
+/* Grid: x = token (b T + t), y = groups of 4 head rows; block = 4 waves, one head row each.
+ * FUSED: rows [0, Hq) are q heads (normed, rotated, stored to q_out), rows [Hq, Hq + Hkv) KV heads (k
+ * normed and rotated, then k and v quantized into the cache). Plain: rows [0, Hkv) KV heads, no rotation. */
+template <bool FUSED>
+__global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (row >= (FUSED ? a.Hq + a.Hkv : a.Hkv)) return;
+    const long long tok = blockIdx.x;
+    const int b = (int)(tok / a.T), t = (int)(tok % a.T);
+    if (a.num_new && t >= a.num_new[b]) return;
+    const int p = a.start_pos[b] + t;
+    if (p < 0) return;
+    if (FUSED && p >= a.rope_len) return;
+    const uint16_t *in = (FUSED ? a.qkv : a.k) + tok * a.token_stride;
+    float c = 0.0f, s = 0.0f;
+    if (FUSED) {
+        c = a.cos[(long long)p * HALF + lane];
+        s = a.sin[(long long)p * HALF + lane];
+    }
+    if (FUSED && row < a.Hq) {
+        const uint16_t *x = in + row * HEAD_DIM;
+        float y1, y2;
+        norm_rope_pair(bf16_to_f32(x[lane]), bf16_to_f32(x[lane + HALF]), a.q_gain[lane], a.q_gain[lane + HALF], c, s,
+                       y1, y2);
+        uint16_t *q = a.q_out + (tok * a.Hq + row) * HEAD_DIM;
+        q[lane] = f32_to_bf16(y1);
+        q[lane + HALF] = f32_to_bf16(y2);
+        return;
+    }
+    const int kvh = FUSED ? row - a.Hq : row;
+    const int lp = p / PAGE;
+    if (lp >= a.max_pages) return;
+    const int page = a.block_table[(long long)b * a.max_pages + lp];
+    if (page < 0 || page >= a.num_pages) return;
+    const int slot = p % PAGE;
+    const long long at = (long long)page * a.Hkv + kvh;
+    const uint16_t *kx = FUSED ? in + (a.Hq + kvh) * HEAD_DIM : in + kvh * HEAD_DIM;
+    const uint16_t *vx = FUSED ? in + (a.Hq + a.Hkv + kvh) * HEAD_DIM : a.v + tok * a.token_stride + kvh * HEAD_DIM;
+    float k1 = bf16_to_f32(kx[lane]), k2 = bf16_to_f32(kx[lane + HALF]);
+    if (FUSED) {
+        float y1, y2;
+        norm_rope_pair(k1, k2, a.k_gain[lane], a.k_gain[lane + HALF], c, s, y1, y2);
+        k1 = bf16_to_f32(f32_to_bf16(y1));
+        k2 = bf16_to_f32(f32_to_bf16(y2));
+    }
+    quantize_store<k_page_offset>(k1, k2, a.k_pages + at * PAGE_BYTES, a.k_scale + at * PAGE + slot, slot, lane);
+    quantize_store<v_page_offset>(bf16_to_f32(vx[lane]), bf16_to_f32(vx[lane + HALF]), a.v_pages + at * PAGE_BYTES,
+                                  a.v_scale + at * PAGE + slot, slot, lane);
+}
+
+/* The training-form prologue (reference model/kernels/qk_prologue.cu:8-32): token p = blockIdx.x of rows/H,
+ * rows [0, H) q heads, [H, 2H) k heads; input token stride 3 H 128, output contiguous, position p % T. */
+__global__ void __launch_bounds__(256) qkp_forward_kernel(const uint16_t *q, const uint16_t *k, const float *gq,
+                                                          const float *gk, uint16_t *qo, uint16_t *ko,
+                                                          const float *cos, const float *sin, int H, int T) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (row >= 2 * H) return;
+    const long long p = blockIdx.x;
+    const bool isq = row < H;
+    const int h = isq ? row : row - H;
+    const uint16_t *x = (isq ? q : k) + p * 3 * H * HEAD_DIM + h * HEAD_DIM;
+    const float *g = isq ? gq : gk;
+    const long long tab = (p % T) * HALF + lane;
+    float y1, y2;
+    norm_rope_pair(bf16_to_f32(x[lane]), bf16_to_f32(x[lane + HALF]), g[lane], g[lane + HALF], cos[tab], sin[tab], y1,
+                   y2);
+    uint16_t *y = (isq ? qo : ko) + (p * H + h) * HEAD_DIM;
+    y[lane] = f32_to_bf16(y1);
+    y[lane + HALF] = f32_to_bf16(y2);
+}
+
+static thread_local int last_error = NC_OK;
+
+static int launch_append(const AppendArgs &a, bool fused, hipStream_t stream) {
+    const int rows = fused ? a.Hq + a.Hkv : a.Hkv;
+    const dim3 grid((unsigned)((long long)a.B * a.T), (unsigned)((rows + 3) / 4));
+    if (fused)
+        hipLaunchKernelGGL(append_kernel<true>, grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(append_kernel<false>, grid, dim3(256), 0, stream, a);
+    return (int)hipGetLastError();
+}
+
+}  // namespace nc
+
+using namespace nc;
+
+extern "C" int nc_kv_append_fp8(const void *k, const void *v, long long token_stride, int B, int T, int Hkv,
+                                const int32_t *start_pos, const int32_t *num_new, const int32_t *block_table,
+                                int max_pages, void *k_pages, void *v_pages, float *k_scale, float *v_scale,
+                                int num_pages, void *stream) {
+    if (!k || !v || !start_pos || !block_table || !k_pages || !v_pages || !k_scale || !v_scale) return NC_ERR_NULL;
+    if (B <= 0 || T <= 0 || Hkv <= 0 || max_pages <= 0 || num_pages <= 0 || token_stride < (long long)Hkv * HEAD_DIM)
+        return NC_ERR_SHAPE;
+    if ((long long)B * T > 0x7FFFFFFFLL) return NC_ERR_SHAPE;
+    AppendArgs a = {};
+    a.k = (const uint16_t *)k;
+    a.v = (const uint16_t *)v;
+    a.token_stride = token_stride;
+    a.B = B; a.T = T; a.Hq = 0; a.Hkv = Hkv;
+    a.start_pos = start_pos; a.num_new = num_new;
+    a.block_table = block_table; a.max_pages = max_pages;
+    a.k_pages = (uint8_t *)k_pages; a.v_pages = (uint8_t *)v_pages;
+    a.k_scale = k_scale; a.v_scale = v_scale; a.num_pages = num_pages;
+    return launch_append(a, false, (hipStream_t)stream);
+}
+
+extern "C" int nc_qk_norm_rope_append_fp8(const void *qkv, long long token_stride, int B, int T, int Hq, int Hkv,
+                                          const int32_t *start_pos, const int32_t *num_new, const float *q_gain,
+                                          const float *k_gain, const float *cos, const float *sin, int rope_len,
+                                          void *q_out, const int32_t *block_table, int max_pages, void *k_pages,
+                                          void *v_pages, float *k_scale, float *v_scale, int num_pages,
+                                          void *stream) {
+    if (!qkv || !start_pos || !q_gain || !k_gain || !cos || !sin || !q_out || !block_table || !k_pages || !v_pages ||
+        !k_scale || !v_scale)
+        return NC_ERR_NULL;
+    if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || max_pages <= 0 || num_pages <= 0 || rope_len <= 0 ||
+        token_stride < (long long)(Hq + 2 * Hkv) * HEAD_DIM)
+        return NC_ERR_SHAPE;
+    if ((long long)B * T > 0x7FFFFFFFLL) return NC_ERR_SHAPE;
+    AppendArgs a = {};
+    a.qkv = (const uint16_t *)qkv;
+    a.token_stride = token_stride;
+    a.B = B; a.T = T; a.Hq = Hq; a.Hkv = Hkv;
+    a.start_pos = start_pos; a.num_new = num_new;
+    a.q_gain = q_gain; a.k_gain = k_gain; a.cos = cos; a.sin = sin; a.rope_len = rope_len;
+    a.q_out = (uint16_t *)q_out;
+    a.block_table = block_table; a.max_pages = max_pages;
+    a.k_pages = (uint8_t *)k_pages; a.v_pages = (uint8_t *)v_pages;
+    a.k_scale = k_scale; a.v_scale = v_scale; a.num_pages = num_pages;
+    return launch_append(a, true, (hipStream_t)stream);
+}
+
+extern "C" void qkp_forward(const void *q, const void *k, const void *gq, const void *gk, void *qo, void *ko,
+                            const void *cos, const void *sin, long long rows, int H, int T, void *stream) {
+    if (!q || !k || !gq || !gk || !qo || !ko || !cos || !sin) {
+        last_error = NC_ERR_NULL;
+        return;
+    }
+    if (H <= 0 || T <= 0 || rows <= 0 || rows % H || rows / H > 0x7FFFFFFFLL) {
+        last_error = NC_ERR_SHAPE;
+        return;
+    }
+    const dim3 grid((unsigned)(rows / H), (unsigned)((2 * H + 3) / 4));
+    hipLaunchKernelGGL(qkp_forward_kernel, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t *)q,
+                       (const uint16_t *)k, (const float *)gq, (const float *)gk, (uint16_t *)qo, (uint16_t *)ko,
+                       (const float *)cos, (const float *)sin, H, T);
+    last_error = (int)hipGetLastError();
+}
+
+extern "C" int nc_last_error(void) { return last_error; }
+
+extern "C" const char *nc_status_string(int status) {
+    switch (status) {
+        case NC_OK: return "ok";
+        case NC_ERR_NULL: return "a required pointer is NULL";
+        case NC_ERR_SHAPE: return "a size or head count is out of the supported range";
+        case NC_ERR_WORKSPACE: return "the workspace is smaller than nc_decode_workspace_bytes";
+        default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
+    }
+}
+
+extern "C" int nc_abi_version(void) { return 1; }

@@ -1,0 +1,96 @@
+/*
+ * Device helpers shared by the gfx950 kernels of the fp8 KV-cache path: raw bf16 / e4m3fn formats in
+ * integer arithmetic, wave-64 reductions, the paged-cache tile layout and the MFMA operand types.
+ *
+ * Every kernel file is built with -ffp-contract=off: an a*b+c written in these sources is two rounded
+ * operations unless it is spelled __builtin_fmaf.
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#ifndef HEAD_DIM
+#define HEAD_DIM 128
+#endif
+static_assert(HEAD_DIM == 128, "the page tiling and MFMA mapping assume 128-wide heads");
+
+namespace nc {
+
+constexpr int WAVE = 64;
+constexpr int HALF = HEAD_DIM / 2;   /* rotation pairs: dims i and i + HALF, one pair per lane */
+constexpr int PAGE = 16;             /* tokens per cache page */
+constexpr int PAGE_BYTES = PAGE * HEAD_DIM;   /* one page of one KV head: 2 KiB of e4m3fn codes */
+constexpr float FP8_MAX = 448.0f;
+constexpr float FLT_EPS = 1.1920928955078125e-07f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+/* bf16 bits -> fp32 (exact). */
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+/* fp32 -> bf16 bits, round to nearest even (finite inputs). */
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+/* fp32 with |x| <= 448 -> OCP e4m3fn code, round to nearest even; the sign bit is copied (so -0 -> 0x80).
+ * Normal range: round the fp32 pattern to 3 mantissa bits (a carry moves into the exponent), rebias 127 -> 7.
+ * Below 2^-6: |x| * 2^9 is exact and rounds to the subnormal count 0..8 (8 = the smallest normal, 0x08). */
+__device__ __forceinline__ uint32_t e4m3_encode(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t au = u & 0x7FFFFFFFu;
+    const float a = __uint_as_float(au);
+    uint32_t code;
+    if (a >= 0x1p-6f)
+        code = ((au + 0x7FFFFu + ((au >> 20) & 1u)) >> 20) - ((127u - 7u) << 3);
+    else
+        code = (uint32_t)__builtin_rintf(a * 512.0f);
+    return code | sign;
+}
+
+/* Sum over the wave by an xor butterfly (offsets 32, 16, ..., 1): every lane ends with the same value. */
+__device__ __forceinline__ float wave_sum_butterfly(float v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v = v + __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+/* Byte offset of (slot, dim) inside a K page: the 16x16x32 MFMA A-operand tiling (lane = group*16 + slot
+ * holds dims group*32 + h*16 .. +15 at h*1024 + lane*16). */
+__device__ __forceinline__ int k_page_offset(int slot, int dim) {
+    return ((dim & 31) >> 4) * 1024 + (((dim >> 5) << 4) + slot) * 16 + (dim & 15);
+}
+
+/* Byte offset of (slot, dim) inside a V page: the transposed A-operand tiling of the PV MFMA (lane =
+ * (slot/4)*16 + dim%16 holds, for tiles t = 4h..4h+3, the 4 slots of its group at dim 16t + dim%16). */
+__device__ __forceinline__ int v_page_offset(int slot, int dim) {
+    const int t = dim >> 4;
+    return (t >> 2) * 1024 + (((slot >> 2) << 4) + (dim & 15)) * 16 + (t & 3) * 4 + (slot & 3);
+}
+
+/* Four e4m3fn codes (one dword) -> four bf16 (exact) as the low or high half of an MFMA operand. */
+__device__ __forceinline__ void fp8x4_to_bf16(uint32_t w, bf16x8 &dst, int at) {
+    const bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false);
+    const bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, true);
+    dst[at + 0] = lo[0];
+    dst[at + 1] = lo[1];
+    dst[at + 2] = hi[0];
+    dst[at + 3] = hi[1];
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace nc

@@ -1,0 +1,129 @@
+"""GPU parity of the append entry points against the oracle: fp8 cache bytes and scales bit-exact, q/k after
+the fused norm + rotation bit-exact (bf16)."""
+import dataclasses
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from nanochat_amd.attention import qk_norm_rope_append
+from nanochat_amd.kv_cache import PagedKVCache, contiguous_block_table, permuted_block_table
+from nanochat_amd.qk_prologue import qk_forward
+from nanochat_amd.rotary import rotary_tables
+from nanochat_amd.workloads import DECODE, decode_inputs
+from oracle.numerics import bf16_bits, bf16_to_f32
+from oracle.rope import qk_norm_rope
+from tests.paged_util import device_cache, expected_codes, f32, read_sequence
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).parent / "golden"
+
+
+def append_rows(rows: np.ndarray, device) -> tuple:
+    """Append fp32-held bf16 rows (n, 128) as n tokens of one KV head of one sequence; read them back."""
+    n = rows.shape[0]
+    x = torch.from_numpy(rows).to(torch.bfloat16).view(1, n, 1, 128).to(device)
+    mp = (n + 15) // 16
+    table = contiguous_block_table(1, mp, device)
+    cache = PagedKVCache(mp, 1, device)
+    cache.append(x, x, torch.zeros(1, dtype=torch.int32, device=device), table)
+    torch.cuda.synchronize()
+    return read_sequence(cache, table, 0, n)
+
+
+def test_every_bf16_value(device):
+    """All finite bf16 bit patterns, grouped by magnitude (each row spans a narrow range, so every code of
+    every binade appears) and shuffled (each row mixes magnitudes)."""
+    x = bf16_to_f32(np.arange(1 << 16, dtype=np.uint32).astype(np.uint16))
+    x = x[np.isfinite(x)]
+    pad = (-x.size) % 128
+    x = np.concatenate([x, np.zeros(pad, np.float32)])
+    by_mag = x[np.argsort(np.abs(x), kind="stable")].reshape(-1, 128)
+    shuffled = x[np.random.default_rng(0).permutation(x.size)].reshape(-1, 128)
+    for rows in (by_mag, shuffled):
+        kc, ks, vc, vs = append_rows(rows, device)
+        wc, ws, _, _ = expected_codes(rows[:, None], rows[:, None])
+        assert np.array_equal(kc, wc) and np.array_equal(vc, wc)
+        assert np.array_equal(ks, ws) and np.array_equal(vs, ws)
+
+
+@pytest.mark.parametrize("name", ["c1", "c3"])
+def test_cache_bytes_match_oracle(device, name):
+    w = DECODE[name]
+    if name == "c3":   # the ragged outlier workload at 6 sequences
+        w = dataclasses.replace(w, batch=6, name="c3-small")
+    inp = decode_inputs(w, seed=0)
+    cache, table, lens = device_cache(inp, w.kv_heads, device)
+    for b in range(w.batch):
+        n = int(inp["ctx_lens"][b])
+        got = read_sequence(cache, table, b, n + 1)
+        k = np.concatenate([f32(inp["k_cache"][b, :n]), f32(inp["k_new"][b])])
+        v = np.concatenate([f32(inp["v_cache"][b, :n]), f32(inp["v_new"][b])])
+        for g, e in zip(got, expected_codes(k, v)):
+            assert np.array_equal(g, e)
+
+
+def test_config1_golden_bytes(device):
+    want = np.load(GOLDEN / "config1.npz")
+    inp = decode_inputs(DECODE["c1"], seed=0)
+    cache, table, _ = device_cache(inp, 6, device)
+    kc, ks, vc, vs = read_sequence(cache, table, 0, 1025)
+    assert np.array_equal(kc, want["k_codes"]) and np.array_equal(ks, want["k_scale"])
+    assert np.array_equal(vc, want["v_codes"]) and np.array_equal(vs, want["v_scale"])
+
+
+@pytest.mark.parametrize("Hq,Hkv,theta", [(8, 2, 1e4), (6, 6, 1e6), (16, 4, 1e4)])
+def test_fused_norm_rope_append(device, Hq, Hkv, theta):
+    B, T = 3, 37
+    gen = torch.Generator().manual_seed(Hq * 100 + Hkv)
+    qkv = (torch.randn(B, T, (Hq + 2 * Hkv) * 128, generator=gen) * 2).to(torch.bfloat16)
+    qg = 1 + 0.1 * torch.randn(128, generator=gen)
+    kg = 1 + 0.1 * torch.randn(128, generator=gen)
+    start = torch.tensor([0, 5, 100], dtype=torch.int32)
+    cos, sin = rotary_tables(256, theta)
+    mp = (100 + T + 15) // 16
+    table = permuted_block_table(B, mp, gen, device)
+    cache = PagedKVCache(B * mp, Hkv, device)
+    q = qk_norm_rope_append(qkv.to(device), Hq, cache, table, start.to(device), qg.to(device), kg.to(device),
+                            cos.to(device), sin.to(device))
+    torch.cuda.synchronize()
+    x = f32(qkv).reshape(B, T, Hq + 2 * Hkv, 128)
+    for b in range(B):
+        pos = int(start[b]) + np.arange(T)
+        c, s = cos.numpy()[pos][:, None], sin.numpy()[pos][:, None]
+        wq = qk_norm_rope(x[b, :, :Hq], qg.numpy(), c, s)
+        assert np.array_equal(bf16_bits(wq), q[b].view(torch.int16).cpu().numpy().view(np.uint16))
+        wk = qk_norm_rope(x[b, :, Hq:Hq + Hkv], kg.numpy(), c, s)
+        got = read_sequence(cache, table, b, int(pos[-1]) + 1)
+        got = [a[pos] for a in got]
+        for g, e in zip(got, expected_codes(wk, x[b, :, Hq + Hkv:])):
+            assert np.array_equal(g, e)
+
+
+def test_qk_forward_matches_oracle(device):
+    B, T, H = 2, 33, 6
+    gen = torch.Generator().manual_seed(3)
+    qkv = torch.randn(B, T, 3, H, 128, generator=gen).to(torch.bfloat16).to(device)
+    qg = (1 + 0.1 * torch.randn(128, generator=gen)).to(device)
+    kg = (1 + 0.1 * torch.randn(128, generator=gen)).to(device)
+    cos, sin = rotary_tables(T, 1e6, device)
+    q, k = qkv[:, :, 0], qkv[:, :, 1]
+    qo, ko = qk_forward(q, k, qg, kg, cos, sin)
+    torch.cuda.synchronize()
+    c, s = cos.cpu().numpy()[None, :, None], sin.cpu().numpy()[None, :, None]
+    for got, x, g in ((qo, q, qg), (ko, k, kg)):
+        want = qk_norm_rope(f32(x), g.cpu().numpy(), c, s)
+        assert np.array_equal(bf16_bits(want), got.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+def test_append_skips_out_of_range_pages(device):
+    """A position past the block table, or a table entry outside the pool, writes nothing."""
+    cache = PagedKVCache(2, 1, device)
+    table = torch.tensor([[1, 7]], dtype=torch.int32, device=device)     # page 7 is outside the pool
+    x = torch.ones(1, 3, 1, 128, dtype=torch.bfloat16, device=device)
+    cache.append(x, x, torch.tensor([15], dtype=torch.int32, device=device), table)   # positions 15, 16, 17
+    torch.cuda.synchronize()
+    assert cache.k_scale[1, 0, 15].item() == pytest.approx(1 / 448)
+    assert int(cache.k_pages[0].count_nonzero()) == 0 and cache.k_scale[0].abs().sum().item() == 0
+    assert int(cache.k_pages[1].count_nonzero()) == 128

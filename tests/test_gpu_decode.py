@@ -1,0 +1,113 @@
+"""GPU parity of split-K decode attention against the float64 oracle (max abs <= 2e-2, mean <= 2e-3), plus the
+properties that hold at full size: page-permutation invariance (bitwise), determinism, split-count
+independence, inactive sequences and out-of-pool pages."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from nanochat_amd.attention import decode_attention
+from nanochat_amd.workloads import DECODE, DecodeWorkload, decode_inputs
+from oracle.attention import decode_attention as oracle_decode
+from tests.conftest import ATTN_MAX_ABS, ATTN_MEAN_ABS
+from tests.paged_util import attn_errors, device_cache, f32, oracle_cache
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).parent / "golden"
+
+
+def run(w: DecodeWorkload, device, seed=0, window=-1, pps=0, seqs=None, inp=None):
+    inp = inp or decode_inputs(w, seed)
+    cache, table, lens = device_cache(inp, w.kv_heads, device)
+    q = inp["q"].to(device)
+    out = decode_attention(q, cache, table, lens, inp["max_seq_len"], window=window, pages_per_split=pps)
+    torch.cuda.synchronize()
+    seqs = range(w.batch) if seqs is None else seqs
+    ocache, otable, olens = oracle_cache(inp, w.kv_heads, seqs)
+    want = oracle_decode(f32(inp["q"][list(seqs)]), ocache, otable, olens, window=window)
+    return out, want, inp, (cache, table, lens, q)
+
+
+SMALL = [
+    DecodeWorkload("mha-tiny", 3, 4, 4, 100, ctx_min=1),
+    DecodeWorkload("gqa4", 2, 16, 4, 1000, ctx_min=513, paged=True, outliers=0.01),
+    DecodeWorkload("gqa8-window", 4, 8, 1, 200, ctx_min=30, paged=True),
+    DecodeWorkload("c2-like", 2, 10, 10, 4096, ctx_min=300),
+    DecodeWorkload("gqa16", 1, 16, 1, 77, paged=True),
+    DecodeWorkload("gqa2-odd", 5, 4, 2, 33, ctx_min=1, paged=True),
+]
+
+
+@pytest.mark.parametrize("w", SMALL, ids=lambda w: w.name)
+@pytest.mark.parametrize("pps", [0, 2, 6])
+def test_decode_matches_oracle(device, w, pps):
+    window = 50 if "window" in w.name else -1
+    out, want, _, _ = run(w, device, window=window, pps=pps)
+    mx, mean = attn_errors(out, want)
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("window", [0, 1, 15, 16, 17, 100])
+def test_decode_windows(device, window):
+    w = DecodeWorkload("win", 3, 8, 2, 300, ctx_min=1, paged=True)
+    out, want, _, _ = run(w, device, seed=window, window=window, pps=4)
+    mx, mean = attn_errors(out, want)
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+
+
+def test_config1_golden_output(device):
+    want = np.load(GOLDEN / "config1.npz")
+    out, _, _, _ = run(DECODE["c1"], device)
+    mx, mean = attn_errors(out, want["out_f64"])
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+
+
+def test_permutation_invariance_and_determinism(device):
+    w = DecodeWorkload("perm", 4, 16, 4, 700, ctx_min=100, paged=True, outliers=0.01)
+    inp = decode_inputs(w, 1)
+    outs = []
+    for table in (inp["block_table"], torch.arange(inp["num_pages"], dtype=torch.int32).view_as(inp["block_table"])):
+        cache, tab, lens = device_cache({**inp, "block_table": table}, w.kv_heads, device)
+        for _ in range(2):
+            outs.append(decode_attention(inp["q"].to(device), cache, tab, lens, inp["max_seq_len"]).cpu())
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+
+
+def test_split_count_independence(device):
+    w = DecodeWorkload("splits", 2, 8, 2, 2000, paged=True)
+    inp = decode_inputs(w, 2)
+    cache, table, lens = device_cache(inp, w.kv_heads, device)
+    q = inp["q"].to(device)
+    ref = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_split=1000).float()
+    for pps in (2, 8, 32, 0):
+        o = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_split=pps).float()
+        assert (o - ref).abs().max().item() <= 1e-2
+
+
+def test_inactive_and_bad_pages(device):
+    w = DecodeWorkload("inactive", 3, 4, 2, 64, paged=True)
+    inp = decode_inputs(w, 3)
+    cache, table, lens = device_cache(inp, w.kv_heads, device)
+    lens[1] = 0
+    q = inp["q"].to(device)
+    for pps in (2, 0):
+        out = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_split=pps)
+        assert out[1].abs().sum().item() == 0 and torch.isfinite(out.float()).all()
+    bad = table.clone()
+    bad[2, 1] = cache.num_pages + 5
+    for pps in (2, 0):
+        out = decode_attention(q, cache, bad, lens, inp["max_seq_len"], pages_per_split=pps).float()
+        assert torch.isnan(out[2]).all() and torch.isfinite(out[0]).all()
+
+
+@pytest.mark.parametrize("name", ["c3u", "c3", "c2"])
+def test_full_size_subset(device, name):
+    """BASELINE shapes at full size; the float64 oracle checks four sequences (first, last, two inside)."""
+    w = DECODE[name]
+    seqs = [0, w.batch // 3, 2 * w.batch // 3, w.batch - 1]
+    out, want, _, _ = run(w, device, seqs=seqs)
+    mx, mean = attn_errors(out[seqs], want)
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+    assert torch.isfinite(out.float()).all()
