@@ -1,0 +1,199 @@
+"""Decode-step benchmark of the fp8 KV path on one MI355X.
+
+A step is one pass of the hot path over one batch: the fused QK-norm + RoPE + fp8 append of the step's token
+for every sequence (nc_qk_norm_rope_append_fp8), then split-K decode attention over the paged fp8 cache
+(nc_decode_attn_fp8). Default workload: the headline "bs64 ctx8K" (B = 64, 16 query / 4 KV heads, 8192
+cached tokens + the step's, 16-token pages under a random-permutation block table, 1% outliers at 8 sigma),
+synthetic seeded data resident in HBM before the timed region.
+
+value = algorithmic HBM bytes of the step / step time (GB/s). Attention bytes per (sequence, KV head):
+(n + 1) * 264 (fp8 K + V and two fp32 scales per key) + G * 128 * 2 * 2 (q in, out) + ceil((n + 1) / 16) * 4
+(block table); the append adds (Hq + 2 Hkv) * 256 read and Hq * 256 + Hkv * 264 written per token.
+
+    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2] [--pages-per-split P] [--cpu-seqs S]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode-attn HBM GB/s (% of peak) + decode tokens/sec, bs64 ctx8K"
+HBM_PEAK_GBS = 8000.0
+PROFILES = ROOT / "profiles"
+
+
+def attention_bytes(ctx_lens, q_heads, kv_heads):
+    """Algorithmic bytes of one decode-attention launch: sum over (sequence, KV head)."""
+    G = q_heads // kv_heads
+    total = 0
+    for n in ctx_lens:
+        keys = int(n) + 1
+        total += kv_heads * (keys * 264 + G * 128 * 2 * 2 + ((keys + 15) // 16) * 4)
+    return total
+
+
+def append_bytes(batch, q_heads, kv_heads):
+    return batch * ((q_heads + 2 * kv_heads) * 256 + q_heads * 256 + kv_heads * 264)
+
+
+def traffic_from_profiles(kernel, workload):
+    """HBM bytes per launch from the committed rocprofv3 counter summary, if one exists for this workload."""
+    f = PROFILES / f"{kernel}_{workload}_traffic.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text())
+    return d.get("bytes_per_launch")
+
+
+def cpu_baseline(w, inp, seqs):
+    """The CPU oracle (float64 numpy restatement) on a bounded sample of the same workload: the first `seqs`
+    sequences' gather + dequantize + attention, timed after building their cache (not timed)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle.attention import decode_attention as oracle_decode
+    from oracle.layout import PAGE, PagedCache
+
+    cores = min(16, os.cpu_count() or 1)
+    sample = list(range(min(seqs, w.batch)))
+    lens = [int(inp["ctx_lens"][b]) + 1 for b in sample]
+    mp = (max(lens) + PAGE - 1) // PAGE
+    table = np.arange(len(sample) * mp, dtype=np.int32).reshape(len(sample), mp)
+    cache = PagedCache(table.size, w.kv_heads)
+    for i, b in enumerate(sample):
+        n = lens[i] - 1
+        cache.append(table, i, np.arange(n), inp["k_cache"][b, :n].float().numpy(), inp["v_cache"][b, :n].float().numpy())
+        cache.append(table, i, np.array([n]), inp["k_new"][b].float().numpy(), inp["v_new"][b].float().numpy())
+    q = inp["q"][sample].float().numpy()
+    with threadpool_limits(limits=cores):
+        t0 = time.perf_counter()
+        oracle_decode(q, cache, table, np.array(lens))
+        dt = time.perf_counter() - t0
+    nbytes = attention_bytes([n - 1 for n in lens], w.q_heads, w.kv_heads)
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"oracle decode attention (numpy, float64) of {len(sample)} of {w.batch} sequences "
+                      f"({sum(lens)} keys), {dt:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c3u")
+    ap.add_argument("--pages-per-split", type=int, default=0)
+    ap.add_argument("--cpu-seqs", type=int, default=6, help="sequences in the CPU baseline sample (0: skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: the fp8 KV decode path is single-GPU by design (asked for {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from nanochat_amd.attention import decode_attention, decode_workspace_bytes, qk_norm_rope_append
+    from nanochat_amd.kv_cache import PagedKVCache
+    from nanochat_amd.rotary import rotary_tables
+    from nanochat_amd.workloads import DECODE, decode_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    w = DECODE[args.workload]
+    inp = decode_inputs(w, seed=0)
+    B, Hq, Hkv = w.batch, w.q_heads, w.kv_heads
+
+    # resident state: the cache (built through the append entry point), the step's inputs and outputs
+    cache = PagedKVCache(inp["num_pages"], Hkv, dev)
+    table = inp["block_table"].to(dev)
+    ctx = inp["ctx_lens"].to(dev)
+    cache.append(inp["k_cache"].to(dev), inp["v_cache"].to(dev), torch.zeros_like(ctx), table, num_new=ctx)
+    qkv = torch.cat([inp["q"].reshape(B, 1, -1), inp["k_new"].reshape(B, 1, -1), inp["v_new"].reshape(B, 1, -1)],
+                    dim=2).contiguous().to(dev)
+    gain = torch.ones(128, dtype=torch.float32, device=dev)
+    cos, sin = rotary_tables(w.ctx + 2, 1e6, dev)
+    seq_lens = ctx + 1
+    q_out = torch.empty(B, 1, Hq, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(1, decode_workspace_bytes(B, Hq, Hkv, inp["max_seq_len"], -1, args.pages_per_split)),
+                     dtype=torch.uint8, device=dev)
+
+    def append():
+        qk_norm_rope_append(qkv, Hq, cache, table, ctx, gain, gain, cos, sin, q_out=q_out)
+
+    def attend():
+        decode_attention(q_out.view(B, Hq, 128), cache, table, seq_lens, inp["max_seq_len"],
+                         pages_per_split=args.pages_per_split, out=out, workspace=ws)
+
+    for _ in range(args.warmup):
+        append()
+        attend()
+    torch.cuda.synchronize()
+
+    # timed region: K whole steps between two events on the launch stream
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        append()
+        attend()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(stop) / args.steps
+
+    # per-launch duration of the dominant entry point (split-K attention + its combine), events per launch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in evs:
+        append()
+        a.record()
+        attend()
+        b.record()
+    torch.cuda.synchronize()
+    attn_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    attn_mean_ms = sum(attn_ms) / len(attn_ms)
+
+    attn_b = attention_bytes(inp["ctx_lens"].tolist(), Hq, Hkv)
+    step_b = attn_b + append_bytes(B, Hq, Hkv)
+    value = step_b / (ms_step * 1e-3) / 1e9
+    achieved = attn_b / (attn_mean_ms * 1e-3) / 1e9
+    traffic = traffic_from_profiles("decode_attn", args.workload)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3 KV, bf16 MFMA, fp32 softmax",
+        "data": "synthetic (seeded N(0,1) bf16, 1% 8-sigma outliers, random-permutation block table)",
+        "config": {"workload": f"{w.name}: {w.description}", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+                   "keys_per_seq": inp["max_seq_len"], "page_size": 16, "step": "fused QK-norm/RoPE fp8 append + "
+                   "split-K decode attention", "pages_per_split": args.pages_per_split or "auto"},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "decode_tokens_per_s_per_layer": round(B / (ms_step * 1e-3), 1),
+        "attn_ms_mean": round(attn_mean_ms, 5),
+        "attn_ms_p10_p50_p90": [round(attn_ms[len(attn_ms) // 10], 5), round(attn_ms[len(attn_ms) // 2], 5),
+                                round(attn_ms[9 * len(attn_ms) // 10], 5)],
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "nc_decode_attn_fp8 (decode_split_kernel + decode_combine_kernel)",
+                     "bytes_per_launch": attn_b},
+    }
+    if args.cpu_seqs > 0:
+        result["cpu_baseline"] = cpu_baseline(w, inp, args.cpu_seqs)
+        result["cpu_baseline"]["speedup_of_gpu"] = round(achieved / result["cpu_baseline"]["value"], 1)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -18,7 +18,8 @@ from .native import check, hip_library, pointer, stream
 
 def qk_norm_rope_append(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache, block_table: torch.Tensor,
                         start_pos: torch.Tensor, q_gain: torch.Tensor, k_gain: torch.Tensor, cos: torch.Tensor,
-                        sin: torch.Tensor, num_new: torch.Tensor | None = None) -> torch.Tensor:
+                        sin: torch.Tensor, num_new: torch.Tensor | None = None,
+                        q_out: torch.Tensor | None = None) -> torch.Tensor:
     """qkv bf16 [B, T, (Hq + 2 Hkv) * 128] (rows contiguous; token stride = qkv.stride(1)) -> q bf16
     [B, T, Hq, 128] normed and rotated; k (normed, rotated) and v are quantized into `cache` at positions
     start_pos[b] + t."""
@@ -36,7 +37,11 @@ def qk_norm_rope_append(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache
     if num_new is not None:
         _require(num_new, "num_new", torch.int32)
     cache.check_table(block_table)
-    q_out = torch.empty(B, T, num_q_heads, HEAD_DIM, dtype=torch.bfloat16, device=qkv.device)
+    if q_out is None:
+        q_out = torch.empty(B, T, num_q_heads, HEAD_DIM, dtype=torch.bfloat16, device=qkv.device)
+    _require(q_out, "q_out", torch.bfloat16)
+    if q_out.shape != (B, T, num_q_heads, HEAD_DIM):
+        raise ValueError(f"q_out must be [{B}, {T}, {num_q_heads}, {HEAD_DIM}]")
     check(hip_library().nc_qk_norm_rope_append_fp8(
         pointer(qkv), qkv.stride(1), B, T, num_q_heads, Hkv, pointer(start_pos),
         pointer(num_new) if num_new is not None else None, pointer(q_gain), pointer(k_gain), pointer(cos),

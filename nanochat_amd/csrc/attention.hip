@@ -75,11 +75,10 @@ __device__ __forceinline__ void load_q(const uint16_t *row, int g, bf16x8 (&qb)[
 /* Scores S^T (keys 4g + i of one page, column c) = K Q^T from one page's two K loads. */
 __device__ __forceinline__ f32x4 page_scores(const uint4 &k0, const uint4 &k1, const bf16x8 (&qb)[4]) {
     f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
-    bf16x8 a;
-    fp8x4_to_bf16(k0.x, a, 0); fp8x4_to_bf16(k0.y, a, 4); s = mfma16x16x32(a, qb[0], s);
-    fp8x4_to_bf16(k0.z, a, 0); fp8x4_to_bf16(k0.w, a, 4); s = mfma16x16x32(a, qb[1], s);
-    fp8x4_to_bf16(k1.x, a, 0); fp8x4_to_bf16(k1.y, a, 4); s = mfma16x16x32(a, qb[2], s);
-    fp8x4_to_bf16(k1.z, a, 0); fp8x4_to_bf16(k1.w, a, 4); s = mfma16x16x32(a, qb[3], s);
+    s = mfma16x16x32(fp8x8_to_bf16(k0.x, k0.y), qb[0], s);
+    s = mfma16x16x32(fp8x8_to_bf16(k0.z, k0.w), qb[1], s);
+    s = mfma16x16x32(fp8x8_to_bf16(k1.x, k1.y), qb[2], s);
+    s = mfma16x16x32(fp8x8_to_bf16(k1.z, k1.w), qb[3], s);
     return s;
 }
 
@@ -168,9 +167,7 @@ __device__ __forceinline__ void attend_pair(const AttnArgs &a, const int32_t *bt
 #pragma unroll
     for (int t = 0; t < 8; t++) {
         st.o[t] *= alpha;
-        bf16x8 va;
-        fp8x4_to_bf16(dword(t < 4 ? va0 : va1, t & 3), va, 0);
-        fp8x4_to_bf16(dword(t < 4 ? vb0 : vb1, t & 3), va, 4);
+        const bf16x8 va = fp8x8_to_bf16(dword(t < 4 ? va0 : va1, t & 3), dword(t < 4 ? vb0 : vb1, t & 3));
         st.o[t] = mfma16x16x32(va, pv, st.o[t]);
     }
 }

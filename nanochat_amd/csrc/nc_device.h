@@ -25,7 +25,6 @@ constexpr float FP8_MAX = 448.0f;
 constexpr float FLT_EPS = 1.1920928955078125e-07f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 /* bf16 bits -> fp32 (exact). */
@@ -79,14 +78,25 @@ __device__ __forceinline__ int v_page_offset(int slot, int dim) {
     return (t >> 2) * 1024 + (((slot >> 2) << 4) + (dim & 15)) * 16 + (t & 3) * 4 + (slot & 3);
 }
 
-/* Four e4m3fn codes (one dword) -> four bf16 (exact) as the low or high half of an MFMA operand. */
-__device__ __forceinline__ void fp8x4_to_bf16(uint32_t w, bf16x8 &dst, int at) {
-    const bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false);
-    const bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, true);
-    dst[at + 0] = lo[0];
-    dst[at + 1] = lo[1];
-    dst[at + 2] = hi[0];
-    dst[at + 3] = hi[1];
+/* Two e4m3fn codes (bytes 0-1, or 2-3 for the _hi form, of w) -> two bf16 (exact) packed in a dword, by one
+ * v_cvt_scalef32_pk_bf16_fp8 with scale 1. Inline asm on purpose: the compiler's model of the builtin's bf16x2
+ * result is wrong when an element is extracted (it packs element 0 twice), so the result is kept opaque as a
+ * whole dword and only ever reinterpreted as a full MFMA operand. */
+__device__ __forceinline__ uint32_t cvt_fp8x2_bf16_lo(uint32_t w) {
+    uint32_t r;
+    asm("v_cvt_scalef32_pk_bf16_fp8 %0, %1, 1.0" : "=v"(r) : "v"(w));
+    return r;
+}
+__device__ __forceinline__ uint32_t cvt_fp8x2_bf16_hi(uint32_t w) {
+    uint32_t r;
+    asm("v_cvt_scalef32_pk_bf16_fp8 %0, %1, 1.0 op_sel:[1,0,0]" : "=v"(r) : "v"(w));
+    return r;
+}
+
+/* Eight e4m3fn codes (dword a: codes 0-3, dword b: codes 4-7) -> an exact bf16x8 MFMA operand. */
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t a, uint32_t b) {
+    const uint4 u = {cvt_fp8x2_bf16_lo(a), cvt_fp8x2_bf16_hi(a), cvt_fp8x2_bf16_lo(b), cvt_fp8x2_bf16_hi(b)};
+    return __builtin_bit_cast(bf16x8, u);
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {

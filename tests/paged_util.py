@@ -19,7 +19,8 @@ def device_cache(inp: dict, kv_heads: int, device) -> tuple:
     table = inp["block_table"].to(device)
     ctx = inp["ctx_lens"].to(device)
     zeros = torch.zeros_like(ctx)
-    cache.append(inp["k_cache"].to(device), inp["v_cache"].to(device), zeros, table, num_new=ctx)
+    if inp["k_cache"].shape[1]:
+        cache.append(inp["k_cache"].to(device), inp["v_cache"].to(device), zeros, table, num_new=ctx)
     cache.append(inp["k_new"].to(device), inp["v_new"].to(device), ctx, table)
     torch.cuda.synchronize()
     return cache, table, ctx + 1
@@ -34,7 +35,8 @@ def oracle_cache(inp: dict, kv_heads: int, seqs) -> tuple:
     cache = PagedCache(table.size, kv_heads)
     for i, b in enumerate(seqs):
         n = lens[i] - 1
-        cache.append(table, i, np.arange(n), f32(inp["k_cache"][b, :n]), f32(inp["v_cache"][b, :n]))
+        if n:
+            cache.append(table, i, np.arange(n), f32(inp["k_cache"][b, :n]), f32(inp["v_cache"][b, :n]))
         cache.append(table, i, np.array([n]), f32(inp["k_new"][b]), f32(inp["v_new"][b]))
     return cache, table, np.array(lens)
 
@@ -63,3 +65,23 @@ def expected_codes(k_rows: np.ndarray, v_rows: np.ndarray):
 def attn_errors(got: torch.Tensor, want: np.ndarray) -> tuple[float, float]:
     d = np.abs(got.float().cpu().numpy().astype(np.float64) - want)
     return float(d.max()), float(d.mean())
+
+
+def magnitude_cache(cache: PagedCache) -> PagedCache:
+    """The same cache with every V code's sign cleared: attention over it gives sum_j p_j |v_j|."""
+    mag = PagedCache(cache.k.shape[0], cache.hkv)
+    mag.k, mag.ks, mag.vs = cache.k, cache.ks, cache.vs
+    mag.v = cache.v & np.uint8(0x7F)
+    return mag
+
+
+# Per-element bound relative to the attention-weighted magnitude sum_j p_j |v_j|: the kernel's bf16 rounding of
+# p * v_scale (2^-9), of q k products (none: fp32 accumulation of exact products) and of the output (2^-9)
+# stay far inside 2^-7; a dequantization error of one e4m3 mantissa step (2^-3) does not.
+REL_BOUND = 2.0 ** -7
+
+
+def check_relative(got: torch.Tensor, want: np.ndarray, want_mag: np.ndarray) -> None:
+    err = np.abs(got.float().cpu().numpy().astype(np.float64) - want)
+    worst = float((err - REL_BOUND * want_mag).max())
+    assert worst <= 1e-4, f"error exceeds 2^-7 of sum p|v| by {worst}"

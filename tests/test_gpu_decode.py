@@ -11,7 +11,7 @@ from nanochat_amd.attention import decode_attention
 from nanochat_amd.workloads import DECODE, DecodeWorkload, decode_inputs
 from oracle.attention import decode_attention as oracle_decode
 from tests.conftest import ATTN_MAX_ABS, ATTN_MEAN_ABS
-from tests.paged_util import attn_errors, device_cache, f32, oracle_cache
+from tests.paged_util import attn_errors, check_relative, device_cache, f32, magnitude_cache, oracle_cache
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).parent / "golden"
@@ -25,7 +25,9 @@ def run(w: DecodeWorkload, device, seed=0, window=-1, pps=0, seqs=None, inp=None
     torch.cuda.synchronize()
     seqs = range(w.batch) if seqs is None else seqs
     ocache, otable, olens = oracle_cache(inp, w.kv_heads, seqs)
-    want = oracle_decode(f32(inp["q"][list(seqs)]), ocache, otable, olens, window=window)
+    qs = f32(inp["q"][list(seqs)])
+    want = oracle_decode(qs, ocache, otable, olens, window=window)
+    check_relative(out[list(seqs)], want, oracle_decode(qs, magnitude_cache(ocache), otable, olens, window=window))
     return out, want, inp, (cache, table, lens, q)
 
 
@@ -111,3 +113,19 @@ def test_full_size_subset(device, name):
     mx, mean = attn_errors(out[seqs], want)
     assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
     assert torch.isfinite(out.float()).all()
+
+
+def test_single_key_returns_dequantized_value(device):
+    """One cached position: softmax weight 1, so out = bf16(code * bf16(v_scale)) elementwise."""
+    w = DecodeWorkload("one-key", 4, 8, 2, 0, paged=True, outliers=0.05)
+    inp = decode_inputs(w, 4)
+    out, want, _, _ = run(w, device, inp=inp)
+    v = want.astype(np.float32)          # the dequantized value itself
+    got = out.float().cpu().numpy()
+    assert np.all(np.abs(got - v) <= np.abs(v) * 2.0 ** -7 + 1e-30)
+
+
+@pytest.mark.parametrize("n", [2, 3, 5, 8, 17, 33])
+def test_few_keys(device, n):
+    w = DecodeWorkload(f"few{n}", 6, 16, 4, n - 1, paged=True, outliers=0.02)
+    run(w, device, seed=n, pps=2)

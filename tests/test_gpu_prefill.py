@@ -13,7 +13,7 @@ from oracle.layout import PAGE, PagedCache
 from oracle.numerics import bf16_round
 from oracle.rope import qk_norm_rope
 from tests.conftest import ATTN_MAX_ABS, ATTN_MEAN_ABS
-from tests.paged_util import attn_errors, f32
+from tests.paged_util import attn_errors, check_relative, f32, magnitude_cache
 
 pytestmark = pytest.mark.gpu
 
@@ -72,6 +72,8 @@ def test_prefill_matches_oracle(device, w, window):
     seqs = list(range(w.batch))
     oq, ocache, otable = oracle_for(w, inp, seqs, cos, sin)
     want = oracle_prefill(oq, ocache, otable, np.full(len(seqs), w.ctx), window=window)
+    check_relative(out, want, oracle_prefill(oq, magnitude_cache(ocache), otable, np.full(len(seqs), w.ctx),
+                                             window=window))
     mx, mean = attn_errors(out, want)
     assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
 
@@ -94,6 +96,7 @@ def test_config4_full_size_subset(device):
     oq, ocache, otable = oracle_for(w, inp, seqs, cos, sin)
     assert np.array_equal(bf16_round(oq), q[seqs].float().cpu().numpy())
     want = oracle_prefill(oq, ocache, otable, np.full(len(seqs), w.ctx))
+    check_relative(out[seqs], want, oracle_prefill(oq, magnitude_cache(ocache), otable, np.full(len(seqs), w.ctx)))
     mx, mean = attn_errors(out[seqs], want)
     assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
     assert torch.isfinite(out.float()).all()
