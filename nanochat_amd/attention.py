@@ -51,14 +51,26 @@ def qk_norm_rope_append(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache
     return q_out
 
 
+_WORKSPACES: dict = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A decode workspace of at least nbytes for this device, kept for reuse (every call rewrites what it reads)."""
+    ws = _WORKSPACES.get(device)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _WORKSPACES[device] = ws
+    return ws
+
+
 def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int, window: int = -1,
-                           pages_per_split: int = 0) -> int:
+                           pages_per_worker: int = 0) -> int:
     return hip_library().nc_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_seq_len, window,
-                                                   pages_per_split)
+                                                   pages_per_worker)
 
 
 def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Tensor, seq_lens: torch.Tensor,
-                     max_seq_len: int, window: int = -1, sm_scale: float | None = None, pages_per_split: int = 0,
+                     max_seq_len: int, window: int = -1, sm_scale: float | None = None, pages_per_worker: int = 0,
                      out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """q bf16 [B, Hq, 128] (the current token's, already appended) -> out bf16 [B, Hq, 128].
 
@@ -75,14 +87,16 @@ def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Te
         out = torch.empty_like(q)
     _require(out, "out", torch.bfloat16)
     lib = hip_library()
-    need = lib.nc_decode_workspace_bytes(B, Hq, cache.num_kv_heads, max_seq_len, window, pages_per_split)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    need = lib.nc_decode_workspace_bytes(B, Hq, cache.num_kv_heads, max_seq_len, window, pages_per_worker)
+    if need == 0:
+        raise ValueError(f"unsupported decode shape: B={B}, Hq={Hq}, Hkv={cache.num_kv_heads}")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = _workspace(q.device, need)
     check(lib.nc_decode_attn_fp8(
         pointer(q), pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.k_scale), pointer(cache.v_scale),
         pointer(block_table), block_table.size(1), cache.num_pages, pointer(seq_lens), max_seq_len, B, Hq,
-        cache.num_kv_heads, window, sm_scale, pages_per_split, pointer(out),
-        pointer(workspace) if need else None, need, stream()))
+        cache.num_kv_heads, window, sm_scale, pages_per_worker, pointer(out),
+        pointer(workspace), need, stream()))
     return out
 
 

@@ -25,6 +25,7 @@ namespace nc {
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int WAVES = 4;
 constexpr int O_PITCH = HEAD_DIM + 4;  /* LDS row pitch of a wave's merged output (floats) */
+constexpr float RESCALE_LOG2 = 8.0f;   /* lazy rescale threshold: exponentials stay <= 2^8 */
 
 struct AttnArgs {
     const uint16_t *q;        /* [B][T][Hq][128] bf16 (T = 1 in decode) */
@@ -36,16 +37,17 @@ struct AttnArgs {
     const int32_t *start_pos; /* prefill */
     int B, T, Hq, Hkv, G, window;
     float scale_log2;         /* sm_scale * log2(e) */
-    int pages_per_split, n_splits;
-    float *part_o;            /* [B][Hq][n_splits][128] */
-    float *part_ml;           /* [B][Hq][n_splits][2]: max (log2 domain), sum */
+    int workers;              /* decode: waves sharing the flattened page list */
+    float *part_o;            /* decode partials [B*Hkv + workers][G][128] */
+    float *part_ml;           /* [B*Hkv + workers][G][2]: reference max (log2 domain), sum */
+    int *meta;                /* [B*Hkv][2]: first partial slot and partial count of each (sequence, KV head) */
     uint16_t *out;            /* [B][T][Hq][128] bf16 */
 };
 
 /* A wave's running state for its 16 query columns; lane (g, c) = (lane >> 4, lane & 15) holds column c. */
 struct WaveState {
-    f32x4 o[8];  /* O^T tile t: dims 16t + 4g + i of column c */
-    float m;     /* running max of column c, log2 domain (equal in the four groups) */
+    f32x4 o[8];  /* O^T tile t: dims 16t + 4g + i of column c, scaled by 2^-m */
+    float m;     /* column c's reference max (log2 domain, equal in the four groups); exponentials use it */
     float l;     /* sum of exp2(s - m) over the keys this lane's group holds */
     bool bad;    /* a block-table entry fell outside the page pool */
 };
@@ -88,97 +90,168 @@ __device__ __forceinline__ uint32_t dword(const uint4 &u, int i) {
 
 __device__ __forceinline__ uint4 and4(const uint4 &u, uint32_t m) { return uint4{u.x & m, u.y & m, u.z & m, u.w & m}; }
 
-/*
- * One step over logical pages lpa and lpa + 1 (has_b: whether the second is in range) of KV head kvh of
- * sequence b. Keys of this lane's column outside [lo, hi] are masked; V codes of keys past written_hi (slots
- * the cache has not written, whose bytes may be anything) are zeroed before use.
- */
-__device__ __forceinline__ void attend_pair(const AttnArgs &a, const int32_t *bt, int kvh, int lpa, bool has_b, int lo,
-                                            int hi, int written_hi, const bf16x8 (&qb)[4], WaveState &st, int lane) {
-    const int g = lane >> 4;
+/* Two consecutive logical pages (lpa, lpa + 1) of one KV head: their (page, head) indices. Without a second
+ * page in range (has_b false) the first is read twice and every key of the copy is masked. */
+struct PairAddr {
+    long long ha, hb;
+    int lpa;
+    bool has_b;
+};
+
+__device__ __forceinline__ PairAddr pair_addr(const AttnArgs &a, const int32_t *bt, int kvh, int lpa, int end,
+                                              bool &bad) {
+    PairAddr p;
+    p.lpa = lpa;
+    p.has_b = lpa + 1 < end;
     int pa = bt[lpa];
-    int pb = has_b ? bt[lpa + 1] : 0;
-    if ((unsigned)pa >= (unsigned)a.num_pages) { st.bad = true; pa = 0; }
-    if ((unsigned)pb >= (unsigned)a.num_pages) { st.bad = true; pb = 0; }
-    const long long ha = (long long)pa * a.Hkv + kvh, hb = (long long)pb * a.Hkv + kvh;
-    const uint4 *kA = reinterpret_cast<const uint4 *>(a.k_pages + ha * PAGE_BYTES) + lane;
-    const uint4 *vA = reinterpret_cast<const uint4 *>(a.v_pages + ha * PAGE_BYTES) + lane;
-    const uint4 ka0 = kA[0], ka1 = kA[64];
-    uint4 va0 = vA[0], va1 = vA[64];
-    const float4 ksa = *reinterpret_cast<const float4 *>(a.k_scale + ha * PAGE + g * 4);
-    const float4 vsa = *reinterpret_cast<const float4 *>(a.v_scale + ha * PAGE + g * 4);
-    uint4 kb0 = {0u, 0u, 0u, 0u}, kb1 = kb0, vb0 = kb0, vb1 = kb0;
-    float4 ksb = {0.0f, 0.0f, 0.0f, 0.0f}, vsb = ksb;
-    if (has_b) {
-        const uint4 *kB = reinterpret_cast<const uint4 *>(a.k_pages + hb * PAGE_BYTES) + lane;
-        const uint4 *vB = reinterpret_cast<const uint4 *>(a.v_pages + hb * PAGE_BYTES) + lane;
-        kb0 = kB[0]; kb1 = kB[64];
-        vb0 = vB[0]; vb1 = vB[64];
-        ksb = *reinterpret_cast<const float4 *>(a.k_scale + hb * PAGE + g * 4);
-        vsb = *reinterpret_cast<const float4 *>(a.v_scale + hb * PAGE + g * 4);
-    }
-    /* the tail page(s): zero V codes of unwritten slots (a dword holds slots 4g..4g+3 of one dim) */
-    const int key_a = lpa * PAGE + g * 4, key_b = key_a + PAGE;
-    if (lpa * PAGE + PAGE - 1 > written_hi) {
-        const int n = min(max(written_hi - key_a + 1, 0), 4);
-        const uint32_t m = n >= 4 ? 0xFFFFFFFFu : ((1u << (8 * n)) - 1u);
-        va0 = and4(va0, m); va1 = and4(va1, m);
-    }
-    if (has_b && (lpa + 1) * PAGE + PAGE - 1 > written_hi) {
-        const int n = min(max(written_hi - key_b + 1, 0), 4);
-        const uint32_t m = n >= 4 ? 0xFFFFFFFFu : ((1u << (8 * n)) - 1u);
-        vb0 = and4(vb0, m); vb1 = and4(vb1, m);
-    }
+    int pb = p.has_b ? bt[lpa + 1] : pa;
+    if ((unsigned)pa >= (unsigned)a.num_pages) { bad = true; pa = 0; }
+    if ((unsigned)pb >= (unsigned)a.num_pages) { bad = true; pb = 0; }
+    p.ha = (long long)pa * a.Hkv + kvh;
+    p.hb = (long long)pb * a.Hkv + kvh;
+    return p;
+}
 
-    const f32x4 sa = page_scores(ka0, ka1, qb);
-    f32x4 sb = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (has_b) sb = page_scores(kb0, kb1, qb);
+/* One operand (K or V) of a page pair as this lane loads it: two 1 KiB-contiguous 16-byte loads per page and
+ * the four scales of the lane's keys 4g..4g+3. */
+struct PairRegs {
+    uint4 a0, a1, b0, b1;
+    float4 sa, sb;
+};
 
+/* Page bytes are streamed once per launch: non-temporal loads (measured ~7 TB/s for a plain stream on MI355X,
+ * against ~6.4 TB/s for ordinary loads). */
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 load_nt(const uint8_t *p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return uint4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ __forceinline__ float4 load_nt(const float *p) {
+    const f32x4v v = __builtin_nontemporal_load(reinterpret_cast<const f32x4v *>(p));
+    return float4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ __forceinline__ void load_pair(const uint8_t *pages, const float *scales, const PairAddr &p, int lane,
+                                          PairRegs &r) {
+    const uint8_t *A = pages + p.ha * PAGE_BYTES + lane * 16;
+    const uint8_t *Bp = pages + p.hb * PAGE_BYTES + lane * 16;
+    r.a0 = load_nt(A);
+    r.a1 = load_nt(A + 1024);
+    r.b0 = load_nt(Bp);
+    r.b1 = load_nt(Bp + 1024);
+    r.sa = load_nt(scales + p.ha * PAGE + (lane >> 4) * 4);
+    r.sb = load_nt(scales + p.hb * PAGE + (lane >> 4) * 4);
+}
+
+/* Key bounds of a wave: a lane's column sees keys [lo, hi]; pairs inside [full_lo, full_hi] are unmasked for
+ * every column; V codes of keys past written_hi are not cache contents and are zeroed before use. */
+struct KeyBounds {
+    int lo, hi, full_lo, full_hi, written_hi;
+};
+
+/* Softmax update and PV of one pair from its scores: the lazy rescale moves the reference max only when a
+ * column's max grows past it by RESCALE_LOG2 (p <= 2^8 otherwise), decided for the whole wave at once. */
+template <bool MASKED>
+__device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p, const f32x4 &sa, const f32x4 &sb,
+                                            const float4 &ksa, const float4 &ksb, PairRegs &v, const KeyBounds &kb,
+                                            WaveState &st, int lane) {
+    const int g = lane >> 4;
+    const int key_a = p.lpa * PAGE + g * 4, key_b = key_a + PAGE;
+    if (MASKED) {
+        const int na = min(max(kb.written_hi - key_a + 1, 0), 4), nb = p.has_b ? min(max(kb.written_hi - key_b + 1, 0), 4) : 0;
+        const uint32_t ma = na >= 4 ? 0xFFFFFFFFu : ((1u << (8 * na)) - 1u);
+        const uint32_t mb = nb >= 4 ? 0xFFFFFFFFu : ((1u << (8 * nb)) - 1u);
+        v.a0 = and4(v.a0, ma); v.a1 = and4(v.a1, ma);
+        v.b0 = and4(v.b0, mb); v.b1 = and4(v.b1, mb);
+    }
+    const float ks[8] = {ksa.x, ksa.y, ksa.z, ksa.w, ksb.x, ksb.y, ksb.z, ksb.w};
+    const float vs[8] = {v.sa.x, v.sa.y, v.sa.z, v.sa.w, v.sb.x, v.sb.y, v.sb.z, v.sb.w};
     float s[8];
-    const float ksA[4] = {ksa.x, ksa.y, ksa.z, ksa.w}, ksB[4] = {ksb.x, ksb.y, ksb.z, ksb.w};
-    const float vsA[4] = {vsa.x, vsa.y, vsa.z, vsa.w}, vsB[4] = {vsb.x, vsb.y, vsb.z, vsb.w};
     bool ok[8];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        ok[i] = key_a + i >= lo && key_a + i <= hi;
-        ok[4 + i] = has_b && key_b + i >= lo && key_b + i <= hi;
-        s[i] = ok[i] ? sa[i] * ksA[i] * a.scale_log2 : -INFINITY;
-        s[4 + i] = ok[4 + i] ? sb[i] * ksB[i] * a.scale_log2 : -INFINITY;
+    for (int i = 0; i < 8; i++) {
+        const float acc = i < 4 ? sa[i] : sb[i - 4];
+        if (MASKED) {
+            const int key = (i < 4 ? key_a : key_b) + (i & 3);
+            ok[i] = (i < 4 || p.has_b) && key >= kb.lo && key <= kb.hi;
+            s[i] = ok[i] ? acc * ks[i] * a.scale_log2 : -INFINITY;
+        } else {
+            ok[i] = true;
+            s[i] = acc * ks[i] * a.scale_log2;
+        }
     }
     float mt = s[0];
 #pragma unroll
     for (int i = 1; i < 8; i++) mt = fmaxf(mt, s[i]);
     mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
     mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
-    const float mn = fmaxf(st.m, mt);
-    const float ms = mn == -INFINITY ? 0.0f : mn;
-    const float alpha = __builtin_amdgcn_exp2f(st.m - ms);
+    const float mnew = fmaxf(st.m, mt);
+    if (__any(mnew > st.m + RESCALE_LOG2)) {
+        const float alpha = mnew == st.m ? 1.0f : __builtin_amdgcn_exp2f(st.m - mnew);
+#pragma unroll
+        for (int t = 0; t < 8; t++) st.o[t] *= alpha;
+        st.l *= alpha;
+        st.m = mnew;
+    }
+    const float mbase = st.m == -INFINITY ? 0.0f : st.m;  /* a column with no key yet: every s is -inf */
     float psum = 0.0f;
     bf16x8 pv;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float p = __builtin_amdgcn_exp2f(s[i] - ms);
-        psum += p;
-        const float w = ok[i] ? p * (i < 4 ? vsA[i] : vsB[i - 4]) : 0.0f;
-        pv[i] = (__bf16)w;
+        const float pr = __builtin_amdgcn_exp2f(s[i] - mbase);
+        psum += pr;
+        pv[i] = (__bf16)(ok[i] ? pr * vs[i] : 0.0f);
     }
-    st.l = st.l * alpha + psum;
-    st.m = mn;
+    st.l += psum;
 #pragma unroll
     for (int t = 0; t < 8; t++) {
-        st.o[t] *= alpha;
-        const bf16x8 va = fp8x8_to_bf16(dword(t < 4 ? va0 : va1, t & 3), dword(t < 4 ? vb0 : vb1, t & 3));
+        const bf16x8 va = fp8x8_to_bf16(dword(t < 4 ? v.a0 : v.a1, t & 3), dword(t < 4 ? v.b0 : v.b1, t & 3));
         st.o[t] = mfma16x16x32(va, pv, st.o[t]);
     }
 }
 
-/* Pages of sequence b's key range [begin, p]; sizing shared by the split and combine kernels. */
-__device__ __forceinline__ void decode_range(const AttnArgs &a, int L, int &begin, int &pg0, int &pg1, int &ns) {
+/*
+ * A wave's pass over the page pairs lpa0, lpa0 + step, ... below `end` (logical pages of KV head kvh through
+ * block-table row bt). Rolling prefetch: the next pair's K loads are issued as soon as this pair's scores are
+ * computed, its V loads as soon as this pair's PV is issued, so one pair is always in flight per wave.
+ */
+__device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *bt, int kvh, int lpa0, int step, int end,
+                                             const KeyBounds &kb, const bf16x8 (&qb)[4], WaveState &st, int lane) {
+    if (lpa0 >= end) return;
+    PairAddr cur = pair_addr(a, bt, kvh, lpa0, end, st.bad);
+    PairRegs kr, vr;
+    load_pair(a.k_pages, a.k_scale, cur, lane, kr);
+    load_pair(a.v_pages, a.v_scale, cur, lane, vr);
+    for (int lpa = lpa0; lpa < end; lpa += step) {
+        const bool more = lpa + step < end;
+        PairAddr nxt = cur;
+        if (more) nxt = pair_addr(a, bt, kvh, lpa + step, end, st.bad);
+        const f32x4 sa = page_scores(kr.a0, kr.a1, qb);
+        const f32x4 sb = page_scores(kr.b0, kr.b1, qb);
+        const float4 ksa = kr.sa, ksb = kr.sb;
+        if (more) load_pair(a.k_pages, a.k_scale, nxt, lane, kr);
+        const bool interior = cur.has_b && cur.lpa * PAGE >= kb.full_lo && cur.lpa * PAGE + 2 * PAGE - 1 <= kb.full_hi &&
+                              cur.lpa * PAGE + 2 * PAGE - 1 <= kb.written_hi;
+        if (interior)
+            pair_update<false>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
+        else
+            pair_update<true>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
+        if (more) load_pair(a.v_pages, a.v_scale, nxt, lane, vr);
+        cur = nxt;
+    }
+}
+
+/* Key range [begin, p] of a sequence of L keys and its logical pages [pg0, pg0 + npages); npages = 0 for an
+ * inactive sequence (L <= 0) or one the block table cannot hold (its output is NaN). */
+__device__ __forceinline__ int decode_pages(const AttnArgs &a, int L, int &begin, int &pg0) {
+    if (L <= 0 || L > a.max_pages * PAGE) return 0;
     const int p = L - 1;
     begin = a.window >= 0 ? max(p - a.window, 0) : 0;
     pg0 = begin / PAGE;
-    pg1 = p / PAGE + 1;
-    ns = (pg1 - pg0 + a.pages_per_split - 1) / a.pages_per_split;
+    return p / PAGE + 1 - pg0;
 }
 
 __device__ __forceinline__ void store_bf16x4(uint16_t *dst, const float *v) {
@@ -188,112 +261,147 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *dst, const float *v) {
     *reinterpret_cast<uint2 *>(dst) = u;
 }
 
-/* Grid (n_splits, Hkv, B), 4 waves: the split's page pairs go to the waves round-robin, the waves' states
- * merge in LDS, and the split writes either the final output (one split for this sequence) or a partial. */
-__global__ void __launch_bounds__(256) decode_split_kernel(AttnArgs a) {
-    __shared__ float sh_o[WAVES][16][O_PITCH];
-    __shared__ float sh_m[WAVES][16], sh_l[WAVES][16];
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+/* The worker owning flattened page x when P pages are shared by W workers, worker w taking
+ * [floor(w P / W), floor((w + 1) P / W)). */
+__device__ __forceinline__ long long worker_of(long long x, long long P, long long W) { return ((x + 1) * W - 1) / P; }
+
+constexpr int MAX_DECODE_BATCH = 4096;  /* sequences per decode launch (the LDS page prefix: 32 KiB) */
+
+/*
+ * Balanced split-K decode. The (sequence, KV head) units in order b * Hkv + kvh, each with the pages of its key
+ * range, form one flattened page list of P pages; `workers` waves (4 per work-group) take equal contiguous runs
+ * of it, so every wave streams the same number of pages whatever the sequence lengths. A wave walks the units
+ * its run touches: a unit entirely inside the run is finished in place (bf16 output), a unit cut by run
+ * boundaries leaves one partial per touching wave (slot meta[u][0] + j for its j-th wave) and its first wave
+ * records the slot range in meta[u] for decode_combine_kernel.
+ */
+__global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
+    extern __shared__ long long sh_cum[];  /* [B + 1]: pages of the units of sequences < b */
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
-    const int L = a.seq_lens[b];
-    if (L <= 0) {
-        if (split == 0 && a.n_splits == 1)
-            for (int e = threadIdx.x; e < a.G * HEAD_DIM; e += blockDim.x)
-                a.out[((long long)b * a.Hq + kvh * a.G) * HEAD_DIM + e] = 0;
-        return;
+    if (wave == 0) {  /* exclusive prefix over sequences of Hkv * pages, 64 sequences per step */
+        long long run = 0;
+        for (int b0 = 0; b0 < a.B; b0 += WAVE) {
+            int begin, pg0;
+            const int b = b0 + lane;
+            long long v = b < a.B ? (long long)a.Hkv * decode_pages(a, a.seq_lens[b], begin, pg0) : 0;
+#pragma unroll
+            for (int o = 1; o < WAVE; o <<= 1) {
+                const long long t = __shfl_up(v, o, WAVE);
+                if (lane >= o) v += t;
+            }
+            if (b < a.B) sh_cum[b + 1] = run + v;
+            run += __shfl(v, WAVE - 1, WAVE);
+        }
+        if (lane == 0) sh_cum[0] = 0;
     }
-    int begin, pg0, pg1, ns;
-    decode_range(a, L, begin, pg0, pg1, ns);
-    if (L > a.max_pages * PAGE || ns > a.n_splits) {  /* past the block table or the grid: NaN, no reads */
-        if (split == 0 && a.n_splits == 1)
-            for (int e = threadIdx.x; e < a.G * HEAD_DIM; e += blockDim.x)
-                a.out[((long long)b * a.Hq + kvh * a.G) * HEAD_DIM + e] = (uint16_t)0x7FC0;
-        return;
+    __syncthreads();
+    const long long P = sh_cum[a.B];
+    const long long W = min((long long)a.workers, P);  /* at most one wave per page: no run is empty */
+    const long long wid = (long long)blockIdx.x * WAVES + wave;
+    if (wid >= W) return;  /* the grid rounds the workers up to whole work-groups */
+    long long s = wid * P / W;
+    const long long e = (wid + 1) * P / W;
+    if (s >= e) return;
+    int lo_b = 0, hi_b = a.B - 1;  /* the sequence holding flattened page s: the last b with sh_cum[b] <= s */
+    while (lo_b < hi_b) {
+        const int mid = (lo_b + hi_b + 1) >> 1;
+        if (sh_cum[mid] <= s) lo_b = mid; else hi_b = mid - 1;
     }
-    if (split >= ns) return;
-    const int first = pg0 + split * a.pages_per_split;
-    const int last = min(pg1, first + a.pages_per_split);
-    const int npairs = (last - first + 1) / 2;
+    int b = lo_b;
+    while (s < e && b < a.B) {
+        const int L = a.seq_lens[b];
+        int begin = 0, pg0 = 0;
+        const int np = decode_pages(a, L, begin, pg0);
+        if (np == 0 || sh_cum[b + 1] <= s) { b++; continue; }
+        const int kvh = (int)((s - sh_cum[b]) / np);
+        const long long us = sh_cum[b] + (long long)kvh * np, ue = us + np;  /* this unit's flattened pages */
+        const long long seg_end = min(e, ue);
+        const int first = pg0 + (int)(s - us), last = pg0 + (int)(seg_end - us);
+        const long long row0 = (long long)b * a.Hq + kvh * a.G;
 
-    bf16x8 qb[4];
-    load_q(c < a.G ? a.q + ((long long)b * a.Hq + kvh * a.G + c) * HEAD_DIM : nullptr, g, qb);
-    WaveState st;
-    state_init(st);
-    const int32_t *bt = a.block_table + (long long)b * a.max_pages;
-    for (int k = wave; k < npairs; k += WAVES) {
-        const int lpa = first + 2 * k;
-        attend_pair(a, bt, kvh, lpa, lpa + 1 < last, begin, L - 1, L - 1, qb, st, lane);
-    }
-    st.l += __shfl_xor(st.l, 16, WAVE);
-    st.l += __shfl_xor(st.l, 32, WAVE);
-    if (c < a.G) {
+        bf16x8 qb[4];
+        load_q(c < a.G ? a.q + (row0 + c) * HEAD_DIM : nullptr, g, qb);
+        WaveState st;
+        state_init(st);
+        const KeyBounds kb = {begin, L - 1, begin, L - 1, L - 1};
+        attend_pages(a, a.block_table + (long long)b * a.max_pages, kvh, first, 2, last, kb, qb, st, lane);
+        st.l += __shfl_xor(st.l, 16, WAVE);
+        st.l += __shfl_xor(st.l, 32, WAVE);
+        const long long w0 = worker_of(us, P, W), w1 = worker_of(ue - 1, P, W);
+        const int u = b * a.Hkv + kvh;
+        if (w0 == w1) {  /* the whole unit is in this run */
+            if (c < a.G) {
+                uint16_t *dst = a.out + (row0 + c) * HEAD_DIM;
+                const float inv = 1.0f / st.l;
 #pragma unroll
-        for (int t = 0; t < 8; t++)
+                for (int t = 0; t < 8; t++) {
+                    float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) sh_o[wave][c][16 * t + 4 * g + i] = st.o[t][i];
-        if (g == 0) {
-            sh_m[wave][c] = st.m;
-            sh_l[wave][c] = st.l;
-        }
-    }
-    const int bad = __syncthreads_or(st.bad ? 1 : 0);
-    for (int e = threadIdx.x; e < a.G * HEAD_DIM; e += blockDim.x) {
-        const int col = e / HEAD_DIM, d = e % HEAD_DIM;
-        float M = sh_m[0][col];
-        for (int w = 1; w < WAVES; w++) M = fmaxf(M, sh_m[w][col]);
-        float ls = 0.0f, o = 0.0f;
-        for (int w = 0; w < WAVES; w++) {
-            const float f = __builtin_amdgcn_exp2f(sh_m[w][col] - M);
-            ls += sh_l[w][col] * f;
-            o += sh_o[w][col][d] * f;
-        }
-        const long long row = (long long)b * a.Hq + kvh * a.G + col;
-        if (ns == 1 || a.n_splits == 1) {
-            a.out[row * HEAD_DIM + d] = bad ? (uint16_t)0x7FC0 : f32_to_bf16(o / ls);
+                    for (int i = 0; i < 4; i++) v[i] = st.bad ? NAN : st.o[t][i] * inv;
+                    store_bf16x4(dst + 16 * t + 4 * g, v);
+                }
+            }
         } else {
-            const long long at = row * a.n_splits + split;
-            a.part_o[at * HEAD_DIM + d] = bad ? NAN : o;
-            if (d == 0) {
-                a.part_ml[at * 2] = bad ? NAN : M;
-                a.part_ml[at * 2 + 1] = ls;
+            const long long slot = u + wid;  /* = meta[u][0] + (wid - w0) */
+            if (c < a.G) {
+                float *po = a.part_o + (slot * a.G + c) * HEAD_DIM;
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const f32x4 o = st.o[t];
+                    *reinterpret_cast<float4 *>(po + 16 * t + 4 * g) =
+                        float4{st.bad ? NAN : o[0], o[1], o[2], o[3]};
+                }
+                if (g == 0) {
+                    a.part_ml[(slot * a.G + c) * 2] = st.bad ? NAN : st.m;
+                    a.part_ml[(slot * a.G + c) * 2 + 1] = st.l;
+                }
             }
         }
+        if (wid == w0 && lane == 0) {  /* the unit's first wave: where its partials are, how many */
+            a.meta[2 * u] = (int)(u + w0);
+            a.meta[2 * u + 1] = (int)(w1 - w0 + 1);
+        }
+        s = seg_end;
     }
 }
 
-/* Grid B*Hq, 128 threads (one per dim): merges a sequence's split partials (log-sum-exp in base 2). */
+/* Grid B*Hq, 128 threads (one per dim): zeros for inactive sequences, NaN for ones past the block table, and
+ * the log-sum-exp (base 2) merge of a unit's partials when more than one wave worked on it. */
 __global__ void __launch_bounds__(HEAD_DIM) decode_combine_kernel(AttnArgs a) {
-    const int b = blockIdx.x / a.Hq, d = threadIdx.x;
+    const int b = blockIdx.x / a.Hq, h = blockIdx.x % a.Hq, d = threadIdx.x;
     const long long row = blockIdx.x;
     const int L = a.seq_lens[b];
     if (L <= 0) {
         a.out[row * HEAD_DIM + d] = 0;
         return;
     }
-    int begin, pg0, pg1, ns;
-    decode_range(a, L, begin, pg0, pg1, ns);
-    if (L > a.max_pages * PAGE || ns > a.n_splits) {
+    int begin, pg0;
+    if (decode_pages(a, L, begin, pg0) == 0) {
         a.out[row * HEAD_DIM + d] = (uint16_t)0x7FC0;
         return;
     }
-    if (ns <= 1) return;
-    const float *ml = a.part_ml + row * a.n_splits * 2;
-    const float *po = a.part_o + row * a.n_splits * HEAD_DIM + d;
+    const int u = b * a.Hkv + h / a.G, c = h % a.G;
+    const int first = a.meta[2 * u], count = a.meta[2 * u + 1];
+    if (count <= 1) return;  /* finished by its only wave */
+    const float *ml = a.part_ml + ((long long)first * a.G + c) * 2;
+    const float *po = a.part_o + ((long long)first * a.G + c) * HEAD_DIM + d;
+    const long long step = (long long)a.G;
     float M = ml[0];
-    for (int s = 1; s < ns; s++) M = fmaxf(M, ml[2 * s]);
+    for (int j = 1; j < count; j++) M = fmaxf(M, ml[2 * step * j]);
     float ls = 0.0f, o = 0.0f;
-    for (int s = 0; s < ns; s++) {
-        const float f = __builtin_amdgcn_exp2f(ml[2 * s] - M);
-        ls += ml[2 * s + 1] * f;
-        o += po[(long long)s * HEAD_DIM] * f;
+    for (int j = 0; j < count; j++) {
+        const float mj = ml[2 * step * j];
+        const float f = mj == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj - M);
+        ls += ml[2 * step * j + 1] * f;
+        o += po[step * HEAD_DIM * j] * f;
     }
     a.out[row * HEAD_DIM + d] = f32_to_bf16(o / ls);
 }
 
 /* Grid (ceil(T / (4 tpt)), Hkv, B), 4 waves; wave w owns tile blockIdx.x*4 + w of tpt = 16 / G consecutive
  * tokens x G heads (column c = token (c / G), head (c % G)) and streams every page its rows can see. */
-__global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     const int kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
@@ -302,29 +410,29 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     if (t0 >= a.T) return;
     const int tl = c / a.G, hg = c % a.G;
     const bool live = c < tpt * a.G && t0 + tl < a.T;
+    const long long qrow = ((long long)b * a.T + t0 + tl) * a.Hq + kvh * a.G + hg;
     const int start = a.start_pos[b];
     if (start < 0 || (long long)start + a.T > (long long)a.max_pages * PAGE) {  /* past the block table: NaN */
-        if (c < tpt * a.G && t0 + tl < a.T) {
-            uint16_t *dst = a.out + (((long long)b * a.T + t0 + tl) * a.Hq + kvh * a.G + hg) * HEAD_DIM;
-            for (int d = g * 32; d < g * 32 + 32; d++) dst[d] = (uint16_t)0x7FC0;
-        }
+        if (live)
+            for (int d = g * 32; d < g * 32 + 32; d++) a.out[qrow * HEAD_DIM + d] = (uint16_t)0x7FC0;
         return;
     }
+    const int t_last = min(t0 + tpt, a.T) - 1;   /* the wave's last token */
     const int pos = start + t0 + tl;
-    const int hi = live ? pos : -1;
-    const int lo = live ? (a.window >= 0 ? max(pos - a.window, 0) : 0) : 0;
-    const int written_hi = start + a.T - 1;
-    const int w_hi = start + min(t0 + tpt, a.T) - 1;
+    KeyBounds kb;
+    kb.hi = live ? pos : -1;
+    kb.lo = live ? (a.window >= 0 ? max(pos - a.window, 0) : 0) : 0;
+    kb.full_hi = start + t0;                                                   /* the wave's first row */
+    kb.full_lo = a.window >= 0 ? max(start + t_last - a.window, 0) : 0;       /* its last row's window start */
+    kb.written_hi = start + a.T - 1;
     const int w_lo = a.window >= 0 ? max(start + t0 - a.window, 0) : 0;
-    const int pg0 = w_lo / PAGE, pg1 = w_hi / PAGE + 1;
+    const int pg0 = w_lo / PAGE, pg1 = (start + t_last) / PAGE + 1;
 
     bf16x8 qb[4];
-    const long long qrow = ((long long)b * a.T + t0 + tl) * a.Hq + kvh * a.G + hg;
     load_q(live ? a.q + qrow * HEAD_DIM : nullptr, g, qb);
     WaveState st;
     state_init(st);
-    const int32_t *bt = a.block_table + (long long)b * a.max_pages;
-    for (int lpa = pg0; lpa < pg1; lpa += 2) attend_pair(a, bt, kvh, lpa, lpa + 1 < pg1, lo, hi, written_hi, qb, st, lane);
+    attend_pages(a, a.block_table + (long long)b * a.max_pages, kvh, pg0, 2, pg1, kb, qb, st, lane);
     st.l += __shfl_xor(st.l, 16, WAVE);
     st.l += __shfl_xor(st.l, 32, WAVE);
     if (!live) return;
@@ -339,45 +447,65 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     }
 }
 
-/* Pages per split when the caller passes 0: about 2048 work-groups in total, at least 8 pages. */
-static int auto_pages_per_split(int units, int max_range_pages) {
-    long long pps = ((long long)max_range_pages * units + 2047) / 2048;
-    if (pps < 8) pps = 8;
-    if (pps > 512) pps = 512;
-    return (int)((pps + 1) & ~1LL);
+/* Decode workers (waves). Automatic: every wave slot the device holds at the kernel's occupancy, so one
+ * balanced round covers the whole page list; at most one wave per MIN_WORKER_PAGES pages, at most
+ * MAX_WORKERS. pages_per_worker > 0 asks for that many pages per wave instead. */
+constexpr int MIN_WORKER_PAGES = 16;
+constexpr int MAX_WORKERS = 4096;
+
+static long long max_unit_pages(int max_seq_len, int window) {
+    long long n = (max_seq_len + PAGE - 1) / PAGE;
+    if (window >= 0) n = min(n, (long long)(window / PAGE + 2));
+    return n;
 }
 
-static int max_range_pages(int max_seq_len, int window) {
-    int n = (max_seq_len + PAGE - 1) / PAGE;
-    if (window >= 0) n = min(n, window / PAGE + 2);
-    return n;
+static int worker_bound(int B, int Hkv, int max_seq_len, int window, int pages_per_worker) {
+    const long long pages = (long long)B * Hkv * max_unit_pages(max_seq_len, window);
+    long long w = (pages + MIN_WORKER_PAGES - 1) / MIN_WORKER_PAGES;
+    if (pages_per_worker > 0) w = min(w, (pages + pages_per_worker - 1) / pages_per_worker);
+    return (int)max(1LL, min(w, (long long)MAX_WORKERS));
+}
+
+static int device_wave_slots() {
+    static int slots[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MAX_WORKERS;
+    if (!slots[dev]) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, 256,
+                                                         (MAX_DECODE_BATCH + 1) * sizeof(long long)) != hipSuccess)
+            return MAX_WORKERS;
+        slots[dev] = max(1, cus * per_cu * WAVES);
+    }
+    return slots[dev];
+}
+
+/* Workspace layout: partial O [B*Hkv + W][G][128] fp32, partial (max, sum) [B*Hkv + W][G][2] fp32, then
+ * meta [B*Hkv][2] int32, W = worker_bound(...). Every launch rewrites what it later reads. */
+static size_t workspace_bytes_for(int B, int Hq, int Hkv, int W) {
+    const size_t slots = (size_t)B * Hkv + W, G = Hq / Hkv;
+    return slots * G * (HEAD_DIM + 2) * sizeof(float) + (size_t)B * Hkv * 2 * sizeof(int);
 }
 
 }  // namespace nc
 
 using namespace nc;
 
-static int decode_splits(int B, int Hkv, int max_seq_len, int window, int pages_per_split, int &pps) {
-    const int range = max_range_pages(max_seq_len, window);
-    pps = pages_per_split > 0 ? ((pages_per_split + 1) & ~1) : auto_pages_per_split(B * Hkv, range);
-    return (range + pps - 1) / pps;
-}
-
-extern "C" size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window, int pages_per_split) {
-    if (B <= 0 || Hq <= 0 || Hkv <= 0 || max_seq_len <= 0) return 0;
-    int pps;
-    const int splits = decode_splits(B, Hkv, max_seq_len, window, pages_per_split, pps);
-    return splits > 1 ? (size_t)B * Hq * splits * (HEAD_DIM + 2) * sizeof(float) : 0;
+extern "C" size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window, int pages_per_worker) {
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || max_seq_len <= 0) return 0;
+    return workspace_bytes_for(B, Hq, Hkv, worker_bound(B, Hkv, max_seq_len, window, pages_per_worker));
 }
 
 extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *k_scale,
                                   const float *v_scale, const int32_t *block_table, int max_pages, int num_pages,
                                   const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window,
-                                  float sm_scale, int pages_per_split, void *out, void *workspace,
+                                  float sm_scale, int pages_per_worker, void *out, void *workspace,
                                   size_t workspace_bytes, void *stream) {
-    if (!q || !k_pages || !v_pages || !k_scale || !v_scale || !block_table || !seq_lens || !out) return NC_ERR_NULL;
+    if (!q || !k_pages || !v_pages || !k_scale || !v_scale || !block_table || !seq_lens || !out || !workspace)
+        return NC_ERR_NULL;
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || max_pages <= 0 || num_pages <= 0 ||
-        max_seq_len <= 0 || (long long)max_seq_len > (long long)max_pages * PAGE || B > 65535 || Hkv > 65535)
+        max_seq_len <= 0 || (long long)max_seq_len > (long long)max_pages * PAGE || B > MAX_DECODE_BATCH)
         return NC_ERR_SHAPE;
     AttnArgs a = {};
     a.q = (const uint16_t *)q;
@@ -387,20 +515,18 @@ extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void
     a.seq_lens = seq_lens;
     a.B = B; a.T = 1; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.window = window;
     a.scale_log2 = sm_scale * LOG2E;
-    int pps;
-    a.n_splits = decode_splits(B, Hkv, max_seq_len, window, pages_per_split, pps);
-    a.pages_per_split = pps;
+    const int bound = worker_bound(B, Hkv, max_seq_len, window, pages_per_worker);
+    a.workers = pages_per_worker > 0 ? bound : min(bound, device_wave_slots());
     a.out = (uint16_t *)out;
-    if (a.n_splits > 1) {
-        const size_t need = (size_t)B * Hq * a.n_splits * (HEAD_DIM + 2) * sizeof(float);
-        if (!workspace) return NC_ERR_NULL;
-        if (workspace_bytes < need) return NC_ERR_WORKSPACE;
-        a.part_o = (float *)workspace;
-        a.part_ml = a.part_o + (size_t)B * Hq * a.n_splits * HEAD_DIM;
-    }
-    hipLaunchKernelGGL(decode_split_kernel, dim3(a.n_splits, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
-    if (a.n_splits > 1)
-        hipLaunchKernelGGL(decode_combine_kernel, dim3(B * Hq), dim3(HEAD_DIM), 0, (hipStream_t)stream, a);
+    const size_t need = workspace_bytes_for(B, Hq, Hkv, bound);
+    if (workspace_bytes < need) return NC_ERR_WORKSPACE;
+    const size_t slots = (size_t)B * Hkv + bound;
+    a.part_o = (float *)workspace;
+    a.part_ml = a.part_o + slots * a.G * HEAD_DIM;
+    a.meta = (int *)(a.part_ml + slots * a.G * 2);
+    const int grid = (a.workers + WAVES - 1) / WAVES;
+    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(256), (B + 1) * sizeof(long long), (hipStream_t)stream, a);
+    hipLaunchKernelGGL(decode_combine_kernel, dim3(B * Hq), dim3(HEAD_DIM), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 

@@ -54,12 +54,30 @@ def test_small_workspace_rejected(lib):
                                   need - 1, None) == -3
 
 
-def test_workspace_sizes(lib):
-    # one split per sequence needs no workspace; a window caps the pages a split range covers
-    assert lib.nc_decode_workspace_bytes(1, 4, 4, 16, -1, 64) == 0
-    full = lib.nc_decode_workspace_bytes(8, 16, 4, 8193, -1, 16)
-    assert full == 8 * 16 * ((8193 + 15) // 16 + 15) // 16 * 130 * 4
-    assert lib.nc_decode_workspace_bytes(8, 16, 4, 8193, 512, 16) < full
+def expected_workspace(B, Hq, Hkv, max_seq, window, pps):
+    """The documented layout: fp32 partials (O [128] + max, sum) for B*Hkv + W slots of G heads, then int32
+    meta [B*Hkv][2]; W = one wave per 16 pages of the largest possible page list (at most 4096), or per `pps`."""
+    unit_pages = -(-max_seq // 16)
+    if window >= 0:
+        unit_pages = min(unit_pages, window // 16 + 2)
+    pages = B * Hkv * unit_pages
+    w = -(-pages // 16)
+    if pps > 0:
+        w = min(w, -(-pages // pps))
+    w = max(1, min(w, 4096))
+    return (B * Hkv + w) * (Hq // Hkv) * 130 * 4 + B * Hkv * 2 * 4
+
+
+@pytest.mark.parametrize("args", [(1, 4, 4, 16, -1, 64), (8, 16, 4, 8193, -1, 0), (8, 16, 4, 8193, 512, 0),
+                                  (64, 16, 4, 8193, -1, 0), (64, 16, 4, 8193, -1, 258), (32, 10, 10, 4097, -1, 0)])
+def test_workspace_sizes(lib, args):
+    assert lib.nc_decode_workspace_bytes(*args) == expected_workspace(*args)
+
+
+def test_workspace_window_and_bad_sizes(lib):
+    assert lib.nc_decode_workspace_bytes(8, 16, 4, 8193, 512, 0) < lib.nc_decode_workspace_bytes(8, 16, 4, 8193, -1, 0)
+    assert lib.nc_decode_workspace_bytes(0, 16, 4, 8193, -1, 0) == 0
+    assert lib.nc_decode_workspace_bytes(8, 6, 4, 8193, -1, 0) == 0
 
 
 def test_bad_append_shapes_rejected(lib):

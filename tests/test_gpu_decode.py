@@ -21,7 +21,7 @@ def run(w: DecodeWorkload, device, seed=0, window=-1, pps=0, seqs=None, inp=None
     inp = inp or decode_inputs(w, seed)
     cache, table, lens = device_cache(inp, w.kv_heads, device)
     q = inp["q"].to(device)
-    out = decode_attention(q, cache, table, lens, inp["max_seq_len"], window=window, pages_per_split=pps)
+    out = decode_attention(q, cache, table, lens, inp["max_seq_len"], window=window, pages_per_worker=pps)
     torch.cuda.synchronize()
     seqs = range(w.batch) if seqs is None else seqs
     ocache, otable, olens = oracle_cache(inp, w.kv_heads, seqs)
@@ -82,9 +82,9 @@ def test_split_count_independence(device):
     inp = decode_inputs(w, 2)
     cache, table, lens = device_cache(inp, w.kv_heads, device)
     q = inp["q"].to(device)
-    ref = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_split=1000).float()
+    ref = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_worker=1000).float()
     for pps in (2, 8, 32, 0):
-        o = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_split=pps).float()
+        o = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_worker=pps).float()
         assert (o - ref).abs().max().item() <= 1e-2
 
 
@@ -95,12 +95,12 @@ def test_inactive_and_bad_pages(device):
     lens[1] = 0
     q = inp["q"].to(device)
     for pps in (2, 0):
-        out = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_split=pps)
+        out = decode_attention(q, cache, table, lens, inp["max_seq_len"], pages_per_worker=pps)
         assert out[1].abs().sum().item() == 0 and torch.isfinite(out.float()).all()
     bad = table.clone()
     bad[2, 1] = cache.num_pages + 5
     for pps in (2, 0):
-        out = decode_attention(q, cache, bad, lens, inp["max_seq_len"], pages_per_split=pps).float()
+        out = decode_attention(q, cache, bad, lens, inp["max_seq_len"], pages_per_worker=pps).float()
         assert torch.isnan(out[2]).all() and torch.isfinite(out[0]).all()
 
 
@@ -129,3 +129,14 @@ def test_single_key_returns_dequantized_value(device):
 def test_few_keys(device, n):
     w = DecodeWorkload(f"few{n}", 6, 16, 4, n - 1, paged=True, outliers=0.02)
     run(w, device, seed=n, pps=2)
+
+
+def test_workspace_reuse_across_shapes(device):
+    """Calls with different (B, Hkv) in a row sharing the cached workspace, each checked."""
+    shapes = [DecodeWorkload("wsA", 8, 16, 4, 900, paged=True), DecodeWorkload("wsB", 6, 10, 10, 1200),
+              DecodeWorkload("wsA", 8, 16, 4, 900, paged=True), DecodeWorkload("wsC", 3, 8, 2, 2000, ctx_min=100)]
+    for i, w in enumerate(shapes):
+        for pps in (4, 0):
+            out, want, _, _ = run(w, device, seed=i, pps=pps)
+            mx, mean = attn_errors(out, want)
+            assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (w.name, pps, mx, mean)
