@@ -186,7 +186,7 @@ def main():
                                 round(attn_ms[9 * len(attn_ms) // 10], 5)],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "nc_decode_attn_fp8 (decode_split_kernel + decode_combine_kernel)",
+                     "kernel": "nc_decode_attn_fp8 (decode_kernel + decode_combine_kernel)",
                      "bytes_per_launch": attn_b},
     }
     if args.cpu_seqs > 0:

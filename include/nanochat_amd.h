@@ -10,7 +10,8 @@
  *   bf16             raw 16-bit patterns (torch.bfloat16 storage)
  *   k_pages, v_pages uint8 [num_pages][Hkv][2048]: one 16-token page of one KV head, OCP e4m3fn codes in
  *                    the MFMA tiling documented in nanochat_amd/csrc/nc_device.h (k/v_page_offset)
- *   k_scale, v_scale fp32 [num_pages][Hkv][16]: one absmax/448 scale per (token, KV head)
+ *   kv_scale         fp32 [num_pages][Hkv][2][16]: one absmax/448 scale per (token, KV head), K scales then
+ *                    V scales of a page's 16 slots (one 128-byte line per page and head)
  *   block_table      int32 [B][max_pages]: position p of sequence b is slot p % 16 of page
  *                    block_table[b][p / 16]
  * Query head h reads KV head h / (Hq / Hkv); Hq must be a multiple of Hkv with Hq / Hkv <= 16.
@@ -63,7 +64,7 @@ int nc_last_error(void);
  */
 int nc_kv_append_fp8(const void *k, const void *v, long long token_stride, int B, int T, int Hkv,
                      const int32_t *start_pos, const int32_t *num_new, const int32_t *block_table, int max_pages,
-                     void *k_pages, void *v_pages, float *k_scale, float *v_scale, int num_pages, void *stream);
+                     void *k_pages, void *v_pages, float *kv_scale, int num_pages, void *stream);
 
 /*
  * The fused append of a decode or prefill step: the reference's attn_prologue q/k math
@@ -78,7 +79,7 @@ int nc_qk_norm_rope_append_fp8(const void *qkv, long long token_stride, int B, i
                                const int32_t *start_pos, const int32_t *num_new, const float *q_gain,
                                const float *k_gain, const float *cos, const float *sin, int rope_len, void *q_out,
                                const int32_t *block_table, int max_pages, void *k_pages, void *v_pages,
-                               float *k_scale, float *v_scale, int num_pages, void *stream);
+                               float *kv_scale, int num_pages, void *stream);
 
 /* Workspace bytes nc_decode_attn_fp8 needs for these sizes (0 for unsupported sizes): fp32 partial results and
  * per-(sequence, KV head) metadata, rewritten by every call before it is read (no initialization needed). */
@@ -98,8 +99,8 @@ size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int wi
  * A block-table entry outside [0, num_pages) makes that sequence's output NaN instead of reading outside
  * the pool.
  */
-int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *k_scale,
-                       const float *v_scale, const int32_t *block_table, int max_pages, int num_pages,
+int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
+                       const int32_t *block_table, int max_pages, int num_pages,
                        const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window, float sm_scale,
                        int pages_per_worker, void *out, void *workspace, size_t workspace_bytes, void *stream);
 
@@ -109,8 +110,8 @@ int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, 
  * sequence b sits at position start_pos[b] + t and attends keys [max(p - window, 0), p]; the chunk must
  * already be appended. q, out: bf16 [B][T][Hq][128].
  */
-int nc_prefill_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *k_scale,
-                        const float *v_scale, const int32_t *block_table, int max_pages, int num_pages,
+int nc_prefill_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
+                        const int32_t *block_table, int max_pages, int num_pages,
                         const int32_t *start_pos, int B, int T, int Hq, int Hkv, int window, float sm_scale,
                         void *out, void *stream);
 

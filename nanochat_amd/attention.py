@@ -46,8 +46,7 @@ def qk_norm_rope_append(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache
         pointer(qkv), qkv.stride(1), B, T, num_q_heads, Hkv, pointer(start_pos),
         pointer(num_new) if num_new is not None else None, pointer(q_gain), pointer(k_gain), pointer(cos),
         pointer(sin), cos.size(0), pointer(q_out), pointer(block_table), block_table.size(1),
-        pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.k_scale), pointer(cache.v_scale),
-        cache.num_pages, stream()))
+        pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.kv_scale), cache.num_pages, stream()))
     return q_out
 
 
@@ -93,7 +92,7 @@ def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Te
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = _workspace(q.device, need)
     check(lib.nc_decode_attn_fp8(
-        pointer(q), pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.k_scale), pointer(cache.v_scale),
+        pointer(q), pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.kv_scale),
         pointer(block_table), block_table.size(1), cache.num_pages, pointer(seq_lens), max_seq_len, B, Hq,
         cache.num_kv_heads, window, sm_scale, pages_per_worker, pointer(out),
         pointer(workspace), need, stream()))
@@ -115,7 +114,7 @@ def prefill_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.T
         out = torch.empty_like(q)
     _require(out, "out", torch.bfloat16)
     check(hip_library().nc_prefill_attn_fp8(
-        pointer(q), pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.k_scale), pointer(cache.v_scale),
+        pointer(q), pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.kv_scale),
         pointer(block_table), block_table.size(1), cache.num_pages, pointer(start_pos), B, T, Hq, cache.num_kv_heads,
         window, sm_scale, pointer(out), stream()))
     return out

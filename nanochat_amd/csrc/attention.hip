@@ -30,7 +30,7 @@ constexpr float RESCALE_LOG2 = 8.0f;   /* lazy rescale threshold: exponentials s
 struct AttnArgs {
     const uint16_t *q;        /* [B][T][Hq][128] bf16 (T = 1 in decode) */
     const uint8_t *k_pages, *v_pages;
-    const float *k_scale, *v_scale;
+    const float *kv_scale;    /* [num_pages][Hkv][2][16]: K scales, then V scales */
     const int32_t *block_table;
     int max_pages, num_pages;
     const int32_t *seq_lens;  /* decode */
@@ -134,6 +134,7 @@ __device__ __forceinline__ float4 load_nt(const float *p) {
     return float4{v[0], v[1], v[2], v[3]};
 }
 
+/* scales: the K (or V) half of kv_scale, i.e. kv_scale (+ 16 for V); a (page, head)'s scales are 32 floats apart. */
 __device__ __forceinline__ void load_pair(const uint8_t *pages, const float *scales, const PairAddr &p, int lane,
                                           PairRegs &r) {
     const uint8_t *A = pages + p.ha * PAGE_BYTES + lane * 16;
@@ -142,8 +143,8 @@ __device__ __forceinline__ void load_pair(const uint8_t *pages, const float *sca
     r.a1 = load_nt(A + 1024);
     r.b0 = load_nt(Bp);
     r.b1 = load_nt(Bp + 1024);
-    r.sa = load_nt(scales + p.ha * PAGE + (lane >> 4) * 4);
-    r.sb = load_nt(scales + p.hb * PAGE + (lane >> 4) * 4);
+    r.sa = load_nt(scales + p.ha * 2 * PAGE + (lane >> 4) * 4);
+    r.sb = load_nt(scales + p.hb * 2 * PAGE + (lane >> 4) * 4);
 }
 
 /* Key bounds of a wave: a lane's column sees keys [lo, hi]; pairs inside [full_lo, full_hi] are unmasked for
@@ -223,8 +224,8 @@ __device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *b
     if (lpa0 >= end) return;
     PairAddr cur = pair_addr(a, bt, kvh, lpa0, end, st.bad);
     PairRegs kr, vr;
-    load_pair(a.k_pages, a.k_scale, cur, lane, kr);
-    load_pair(a.v_pages, a.v_scale, cur, lane, vr);
+    load_pair(a.k_pages, a.kv_scale, cur, lane, kr);
+    load_pair(a.v_pages, a.kv_scale + PAGE, cur, lane, vr);
     for (int lpa = lpa0; lpa < end; lpa += step) {
         const bool more = lpa + step < end;
         PairAddr nxt = cur;
@@ -232,14 +233,14 @@ __device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *b
         const f32x4 sa = page_scores(kr.a0, kr.a1, qb);
         const f32x4 sb = page_scores(kr.b0, kr.b1, qb);
         const float4 ksa = kr.sa, ksb = kr.sb;
-        if (more) load_pair(a.k_pages, a.k_scale, nxt, lane, kr);
+        if (more) load_pair(a.k_pages, a.kv_scale, nxt, lane, kr);
         const bool interior = cur.has_b && cur.lpa * PAGE >= kb.full_lo && cur.lpa * PAGE + 2 * PAGE - 1 <= kb.full_hi &&
                               cur.lpa * PAGE + 2 * PAGE - 1 <= kb.written_hi;
         if (interior)
             pair_update<false>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
         else
             pair_update<true>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
-        if (more) load_pair(a.v_pages, a.v_scale, nxt, lane, vr);
+        if (more) load_pair(a.v_pages, a.kv_scale + PAGE, nxt, lane, vr);
         cur = nxt;
     }
 }
@@ -387,14 +388,17 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_combine_kernel(AttnArgs a) {
     const float *ml = a.part_ml + ((long long)first * a.G + c) * 2;
     const float *po = a.part_o + ((long long)first * a.G + c) * HEAD_DIM + d;
     const long long step = (long long)a.G;
-    float M = ml[0];
-    for (int j = 1; j < count; j++) M = fmaxf(M, ml[2 * step * j]);
-    float ls = 0.0f, o = 0.0f;
+    /* one pass, online: no load depends on the running state, so unrolled iterations issue together */
+    float m = -INFINITY, ls = 0.0f, o = 0.0f;
+#pragma unroll 4
     for (int j = 0; j < count; j++) {
-        const float mj = ml[2 * step * j];
-        const float f = mj == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj - M);
-        ls += ml[2 * step * j + 1] * f;
-        o += po[step * HEAD_DIM * j] * f;
+        const float mj = ml[2 * step * j], lj = ml[2 * step * j + 1], oj = po[step * HEAD_DIM * j];
+        const float mn = fmaxf(m, mj);
+        const float fo = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+        const float fn = mj == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj - mn);
+        ls = ls * fo + lj * fn;
+        o = o * fo + oj * fn;
+        m = mn;
     }
     a.out[row * HEAD_DIM + d] = f32_to_bf16(o / ls);
 }
@@ -497,12 +501,12 @@ extern "C" size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_
     return workspace_bytes_for(B, Hq, Hkv, worker_bound(B, Hkv, max_seq_len, window, pages_per_worker));
 }
 
-extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *k_scale,
-                                  const float *v_scale, const int32_t *block_table, int max_pages, int num_pages,
+extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
+                                  const int32_t *block_table, int max_pages, int num_pages,
                                   const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window,
                                   float sm_scale, int pages_per_worker, void *out, void *workspace,
                                   size_t workspace_bytes, void *stream) {
-    if (!q || !k_pages || !v_pages || !k_scale || !v_scale || !block_table || !seq_lens || !out || !workspace)
+    if (!q || !k_pages || !v_pages || !kv_scale || !block_table || !seq_lens || !out || !workspace)
         return NC_ERR_NULL;
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || max_pages <= 0 || num_pages <= 0 ||
         max_seq_len <= 0 || (long long)max_seq_len > (long long)max_pages * PAGE || B > MAX_DECODE_BATCH)
@@ -510,7 +514,7 @@ extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void
     AttnArgs a = {};
     a.q = (const uint16_t *)q;
     a.k_pages = (const uint8_t *)k_pages; a.v_pages = (const uint8_t *)v_pages;
-    a.k_scale = k_scale; a.v_scale = v_scale;
+    a.kv_scale = kv_scale;
     a.block_table = block_table; a.max_pages = max_pages; a.num_pages = num_pages;
     a.seq_lens = seq_lens;
     a.B = B; a.T = 1; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.window = window;
@@ -530,18 +534,18 @@ extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void
     return (int)hipGetLastError();
 }
 
-extern "C" int nc_prefill_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *k_scale,
-                                   const float *v_scale, const int32_t *block_table, int max_pages, int num_pages,
+extern "C" int nc_prefill_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
+                                   const int32_t *block_table, int max_pages, int num_pages,
                                    const int32_t *start_pos, int B, int T, int Hq, int Hkv, int window,
                                    float sm_scale, void *out, void *stream) {
-    if (!q || !k_pages || !v_pages || !k_scale || !v_scale || !block_table || !start_pos || !out) return NC_ERR_NULL;
+    if (!q || !k_pages || !v_pages || !kv_scale || !block_table || !start_pos || !out) return NC_ERR_NULL;
     if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || max_pages <= 0 || num_pages <= 0 ||
         B > 65535 || Hkv > 65535)
         return NC_ERR_SHAPE;
     AttnArgs a = {};
     a.q = (const uint16_t *)q;
     a.k_pages = (const uint8_t *)k_pages; a.v_pages = (const uint8_t *)v_pages;
-    a.k_scale = k_scale; a.v_scale = v_scale;
+    a.kv_scale = kv_scale;
     a.block_table = block_table; a.max_pages = max_pages; a.num_pages = num_pages;
     a.start_pos = start_pos;
     a.B = B; a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.window = window;

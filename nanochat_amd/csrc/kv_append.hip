@@ -54,7 +54,7 @@ struct AppendArgs {
     const int32_t *block_table;
     int max_pages;
     uint8_t *k_pages, *v_pages;
-    float *k_scale, *v_scale;
+    float *kv_scale;          /* [num_pages][Hkv][2][16]: K scales, then V scales */
     int num_pages;
 };
 
@@ -104,9 +104,9 @@ __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
         k1 = bf16_to_f32(f32_to_bf16(y1));
         k2 = bf16_to_f32(f32_to_bf16(y2));
     }
-    quantize_store<k_page_offset>(k1, k2, a.k_pages + at * PAGE_BYTES, a.k_scale + at * PAGE + slot, slot, lane);
+    quantize_store<k_page_offset>(k1, k2, a.k_pages + at * PAGE_BYTES, a.kv_scale + at * 2 * PAGE + slot, slot, lane);
     quantize_store<v_page_offset>(bf16_to_f32(vx[lane]), bf16_to_f32(vx[lane + HALF]), a.v_pages + at * PAGE_BYTES,
-                                  a.v_scale + at * PAGE + slot, slot, lane);
+                                  a.kv_scale + (at * 2 + 1) * PAGE + slot, slot, lane);
 }
 
 /* The training-form prologue (reference model/kernels/qk_prologue.cu:8-32): token p = blockIdx.x of rows/H,
@@ -149,9 +149,9 @@ using namespace nc;
 
 extern "C" int nc_kv_append_fp8(const void *k, const void *v, long long token_stride, int B, int T, int Hkv,
                                 const int32_t *start_pos, const int32_t *num_new, const int32_t *block_table,
-                                int max_pages, void *k_pages, void *v_pages, float *k_scale, float *v_scale,
-                                int num_pages, void *stream) {
-    if (!k || !v || !start_pos || !block_table || !k_pages || !v_pages || !k_scale || !v_scale) return NC_ERR_NULL;
+                                int max_pages, void *k_pages, void *v_pages, float *kv_scale, int num_pages,
+                                void *stream) {
+    if (!k || !v || !start_pos || !block_table || !k_pages || !v_pages || !kv_scale) return NC_ERR_NULL;
     if (B <= 0 || T <= 0 || Hkv <= 0 || max_pages <= 0 || num_pages <= 0 || token_stride < (long long)Hkv * HEAD_DIM)
         return NC_ERR_SHAPE;
     if ((long long)B * T > 0x7FFFFFFFLL) return NC_ERR_SHAPE;
@@ -163,7 +163,7 @@ extern "C" int nc_kv_append_fp8(const void *k, const void *v, long long token_st
     a.start_pos = start_pos; a.num_new = num_new;
     a.block_table = block_table; a.max_pages = max_pages;
     a.k_pages = (uint8_t *)k_pages; a.v_pages = (uint8_t *)v_pages;
-    a.k_scale = k_scale; a.v_scale = v_scale; a.num_pages = num_pages;
+    a.kv_scale = kv_scale; a.num_pages = num_pages;
     return launch_append(a, false, (hipStream_t)stream);
 }
 
@@ -171,10 +171,9 @@ extern "C" int nc_qk_norm_rope_append_fp8(const void *qkv, long long token_strid
                                           const int32_t *start_pos, const int32_t *num_new, const float *q_gain,
                                           const float *k_gain, const float *cos, const float *sin, int rope_len,
                                           void *q_out, const int32_t *block_table, int max_pages, void *k_pages,
-                                          void *v_pages, float *k_scale, float *v_scale, int num_pages,
-                                          void *stream) {
+                                          void *v_pages, float *kv_scale, int num_pages, void *stream) {
     if (!qkv || !start_pos || !q_gain || !k_gain || !cos || !sin || !q_out || !block_table || !k_pages || !v_pages ||
-        !k_scale || !v_scale)
+        !kv_scale)
         return NC_ERR_NULL;
     if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || max_pages <= 0 || num_pages <= 0 || rope_len <= 0 ||
         token_stride < (long long)(Hq + 2 * Hkv) * HEAD_DIM)
@@ -189,7 +188,7 @@ extern "C" int nc_qk_norm_rope_append_fp8(const void *qkv, long long token_strid
     a.q_out = (uint16_t *)q_out;
     a.block_table = block_table; a.max_pages = max_pages;
     a.k_pages = (uint8_t *)k_pages; a.v_pages = (uint8_t *)v_pages;
-    a.k_scale = k_scale; a.v_scale = v_scale; a.num_pages = num_pages;
+    a.kv_scale = kv_scale; a.num_pages = num_pages;
     return launch_append(a, true, (hipStream_t)stream);
 }
 
@@ -222,4 +221,4 @@ extern "C" const char *nc_status_string(int status) {
     }
 }
 
-extern "C" int nc_abi_version(void) { return 1; }
+extern "C" int nc_abi_version(void) { return 2; }

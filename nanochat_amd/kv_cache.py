@@ -3,9 +3,10 @@
 The reference keeps one contiguous bf16 cache per slot, `[L][max_len][C]` (model/kernels/decode.cu:726,
 740-763). Here one layer's cache is a pool of pages shared by all sequences:
 
-    k_pages, v_pages  uint8 [num_pages, Hkv, 2048]  e4m3fn codes of 16 tokens of one KV head, in the MFMA
-                                                    tiling of nanochat_amd/csrc/nc_device.h
-    k_scale, v_scale  fp32  [num_pages, Hkv, 16]    one absmax/448 scale per (token, KV head)
+    k_pages, v_pages  uint8 [num_pages, Hkv, 2048]   e4m3fn codes of 16 tokens of one KV head, in the MFMA
+                                                     tiling of nanochat_amd/csrc/nc_device.h
+    kv_scale          fp32  [num_pages, Hkv, 2, 16]  one absmax/448 scale per (token, KV head): K, then V
+                                                     (k_scale and v_scale are views of its two halves)
 
 and a sequence reaches its pages through an int32 block table row (position p -> page
 table[b, p // 16], slot p % 16). A contiguous cache is the identity table.
@@ -48,15 +49,15 @@ class PagedKVCache:
         self.num_pages, self.num_kv_heads = num_pages, num_kv_heads
         self.k_pages = torch.zeros(num_pages, num_kv_heads, PAGE_BYTES, dtype=torch.uint8, device=device)
         self.v_pages = torch.zeros_like(self.k_pages)
-        self.k_scale = torch.zeros(num_pages, num_kv_heads, PAGE_SIZE, dtype=torch.float32, device=device)
-        self.v_scale = torch.zeros_like(self.k_scale)
-        for name in ("k_pages", "v_pages", "k_scale", "v_scale"):
+        self.kv_scale = torch.zeros(num_pages, num_kv_heads, 2, PAGE_SIZE, dtype=torch.float32, device=device)
+        self.k_scale, self.v_scale = self.kv_scale[:, :, 0], self.kv_scale[:, :, 1]
+        for name in ("k_pages", "v_pages", "kv_scale"):
             t = getattr(self, name)
             _require(t, name, t.dtype)
 
     @property
     def nbytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in (self.k_pages, self.v_pages, self.k_scale, self.v_scale))
+        return sum(t.numel() * t.element_size() for t in (self.k_pages, self.v_pages, self.kv_scale))
 
     def check_table(self, block_table: torch.Tensor) -> None:
         _require(block_table, "block_table", torch.int32)
@@ -84,5 +85,4 @@ class PagedKVCache:
         check(hip_library().nc_kv_append_fp8(
             pointer(k), pointer(v), k.stride(1), B, T, H, pointer(start_pos),
             pointer(num_new) if num_new is not None else None, pointer(block_table), block_table.size(1),
-            pointer(self.k_pages), pointer(self.v_pages), pointer(self.k_scale), pointer(self.v_scale),
-            self.num_pages, stream()))
+            pointer(self.k_pages), pointer(self.v_pages), pointer(self.kv_scale), self.num_pages, stream()))

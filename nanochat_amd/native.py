@@ -59,16 +59,15 @@ SIGNATURES = {
     "nc_last_error": ([], c_int),
     "qkp_forward": ([c_void_p] * 8 + [c_longlong, c_int, c_int, c_void_p], None),
     "nc_kv_append_fp8": ([c_void_p, c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
-                          c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p], c_int),
+                          c_void_p, c_void_p, c_void_p, c_int, c_void_p], c_int),
     "nc_qk_norm_rope_append_fp8": ([c_void_p, c_longlong, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
-                                    c_void_p, c_void_p, c_int, c_void_p], c_int),
+                                    c_void_p, c_int, c_void_p], c_int),
     "nc_decode_workspace_bytes": ([c_int, c_int, c_int, c_int, c_int, c_int], c_size_t),
-    "nc_decode_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int,
-                            c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_size_t, c_void_p],
-                           c_int),
-    "nc_prefill_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int,
-                             c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p], c_int),
+    "nc_decode_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
+                            c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_size_t, c_void_p], c_int),
+    "nc_prefill_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
+                             c_int, c_int, c_int, c_float, c_void_p, c_void_p], c_int),
 }
 
 

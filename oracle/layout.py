@@ -4,7 +4,8 @@ The reference cache is contiguous bf16 `[slot][L][max_len][C]` (model/kernels/de
 with a head's keys at stride C (decode.cu:577-579). The build's cache is paged:
 
     K, V pages    uint8 [num_pages][Hkv][2048]   one 16-token page of one KV head, fp8 codes
-    K, V scales   fp32  [num_pages][Hkv][16]     one scale per (token, KV head)
+    K, V scales   fp32  [num_pages][Hkv][16]     one scale per (token, KV head); on the device the two are
+                                                 interleaved as kv_scale [num_pages][Hkv][2][16] (K, then V)
     block table   int32 [B][max_pages]           position p of sequence b lives in page
                                                  table[b][p // 16], slot p % 16
 

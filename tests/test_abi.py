@@ -24,7 +24,7 @@ def test_header_and_binding_agree():
 def test_library_exports_every_declared_symbol(lib):
     for name in declared():
         assert hasattr(lib, name), name
-    assert lib.nc_abi_version() == 1
+    assert lib.nc_abi_version() == 2
 
 
 def test_status_strings(lib):
@@ -34,23 +34,23 @@ def test_status_strings(lib):
 
 
 def test_null_pointers_rejected(lib):
-    assert lib.nc_kv_append_fp8(None, None, 512, 1, 1, 4, None, None, None, 1, None, None, None, None, 1, None) == -1
-    assert lib.nc_decode_attn_fp8(None, *([DUMMY] * 5), 1, 1, DUMMY, 16, 1, 4, 4, -1, 0.1, 0, DUMMY, None, 0,
+    assert lib.nc_kv_append_fp8(None, None, 512, 1, 1, 4, None, None, None, 1, None, None, None, 1, None) == -1
+    assert lib.nc_decode_attn_fp8(None, *([DUMMY] * 4), 1, 1, DUMMY, 16, 1, 4, 4, -1, 0.1, 0, DUMMY, None, 0,
                                   None) == -1
-    assert lib.nc_prefill_attn_fp8(DUMMY, *([DUMMY] * 5), 1, 1, None, 1, 1, 4, 4, -1, 0.1, DUMMY, None) == -1
+    assert lib.nc_prefill_attn_fp8(DUMMY, *([DUMMY] * 4), 1, 1, None, 1, 1, 4, 4, -1, 0.1, DUMMY, None) == -1
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,max_seq,max_pages", [
     (0, 4, 4, 16, 1), (1, 6, 4, 16, 1), (1, 34, 2, 16, 1), (1, 4, 4, 17, 1), (1, 4, 4, 0, 1), (1, 4, 0, 16, 1)])
 def test_bad_decode_shapes_rejected(lib, B, Hq, Hkv, max_seq, max_pages):
-    assert lib.nc_decode_attn_fp8(*([DUMMY] * 6), max_pages, 4, DUMMY, max_seq, B, Hq, Hkv, -1, 0.1, 0, DUMMY,
+    assert lib.nc_decode_attn_fp8(*([DUMMY] * 5), max_pages, 4, DUMMY, max_seq, B, Hq, Hkv, -1, 0.1, 0, DUMMY,
                                   DUMMY, 1 << 30, None) == -2
 
 
 def test_small_workspace_rejected(lib):
     need = lib.nc_decode_workspace_bytes(64, 16, 4, 8193, -1, 0)
     assert need > 0
-    assert lib.nc_decode_attn_fp8(*([DUMMY] * 6), 513, 64 * 513, DUMMY, 8193, 64, 16, 4, -1, 0.1, 0, DUMMY, DUMMY,
+    assert lib.nc_decode_attn_fp8(*([DUMMY] * 5), 513, 64 * 513, DUMMY, 8193, 64, 16, 4, -1, 0.1, 0, DUMMY, DUMMY,
                                   need - 1, None) == -3
 
 
@@ -81,9 +81,9 @@ def test_workspace_window_and_bad_sizes(lib):
 
 
 def test_bad_append_shapes_rejected(lib):
-    assert lib.nc_kv_append_fp8(*([DUMMY] * 2), 100, 1, 1, 4, *([DUMMY] * 3), 1, *([DUMMY] * 4), 1, None) == -2
+    assert lib.nc_kv_append_fp8(*([DUMMY] * 2), 100, 1, 1, 4, *([DUMMY] * 3), 1, *([DUMMY] * 3), 1, None) == -2
     assert lib.nc_qk_norm_rope_append_fp8(DUMMY, 128 * 5, 1, 1, 4, 1, *([DUMMY] * 6), 0, DUMMY, DUMMY, 1,
-                                          *([DUMMY] * 4), 1, None) == -2
+                                          *([DUMMY] * 3), 1, None) == -2
 
 
 def test_qkp_forward_reports_errors(lib):
