@@ -10,7 +10,9 @@ value = algorithmic HBM bytes of the step / step time (GB/s). Attention bytes pe
 (n + 1) * 264 (fp8 K + V and two fp32 scales per key) + G * 128 * 2 * 2 (q in, out) + ceil((n + 1) / 16) * 4
 (block table); the append adds (Hq + 2 Hkv) * 256 read and Hq * 256 + Hkv * 264 written per token.
 
-    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2] [--pages-per-worker P] [--cpu-seqs S]
+    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4] [--pages-per-worker P] [--cpu-seqs S]
+
+--workload c4 times the chunked-prefill step instead (TFLOP/s against the 2.5 PFLOP/s bf16 dense MFMA peak).
 """
 import argparse
 import json
@@ -24,6 +26,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "decode-attn HBM GB/s (% of peak) + decode tokens/sec, bs64 ctx8K"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 PROFILES = ROOT / "profiles"
 
 
@@ -80,6 +83,75 @@ def cpu_baseline(w, inp, seqs):
                       f"({sum(lens)} keys), {dt:.2f} s"}
 
 
+def prefill_flops(ctx, chunk, batch, q_heads):
+    """Causal-useful FLOPs of chunked prefill: 4 * D per (query row, visible key), rows at ctx + i see ctx + i + 1."""
+    keys = sum(ctx + i + 1 for i in range(chunk))
+    return 4 * 128 * keys * batch * q_heads
+
+
+def bench_prefill(args, w):
+    """One chunked-prefill step of workload w (fused QK-norm/RoPE fp8 append of the chunk, then MFMA attention)."""
+    import torch
+
+    from nanochat_amd.attention import prefill_attention, qk_norm_rope_append
+    from nanochat_amd.kv_cache import PagedKVCache
+    from nanochat_amd.rotary import rotary_tables
+    from nanochat_amd.workloads import prefill_inputs
+
+    dev = torch.device("cuda:0")
+    inp = prefill_inputs(w, seed=0)
+    cache = PagedKVCache(inp["num_pages"], w.kv_heads, dev)
+    table, start = inp["block_table"].to(dev), inp["start_pos"].to(dev)
+    cache.append(inp["k_cache"].to(dev), inp["v_cache"].to(dev), torch.zeros_like(start), table, num_new=start)
+    qkv = inp["qkv"].to(dev)
+    qg, kg = inp["q_gain"].to(dev), inp["k_gain"].to(dev)
+    cos, sin = rotary_tables(w.ctx + w.chunk, w.theta, dev)
+    q = torch.empty(w.batch, w.chunk, w.q_heads, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.empty_like(q)
+
+    def append():
+        qk_norm_rope_append(qkv, w.q_heads, cache, table, start, qg, kg, cos, sin, q_out=q)
+
+    def attend():
+        prefill_attention(q, cache, table, start, out=out)
+
+    for _ in range(args.warmup):
+        append()
+        attend()
+    torch.cuda.synchronize()
+    start_ev, stop_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start_ev.record()
+    for _ in range(args.steps):
+        append()
+        attend()
+    stop_ev.record()
+    torch.cuda.synchronize()
+    ms_step = start_ev.elapsed_time(stop_ev) / args.steps
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in evs:
+        append()
+        a.record()
+        attend()
+        b.record()
+    torch.cuda.synchronize()
+    attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    flops = prefill_flops(w.ctx, w.chunk, w.batch, w.q_heads)
+    achieved = flops / (attn_ms * 1e-3) / 1e12
+    return {
+        "metric": "chunked-prefill attention TFLOP/s over the fp8 cache (MFMA)", "value": round(achieved, 2),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 KV, bf16 MFMA, fp32 softmax",
+        "data": "synthetic (seeded N(0,1) bf16 chunk and cache, random-permutation block table)",
+        "config": {"workload": f"{w.name}: {w.description}", "batch": w.batch, "q_heads": w.q_heads,
+                   "kv_heads": w.kv_heads, "cached": w.ctx, "chunk": w.chunk, "rope_theta": w.theta},
+        "attn_ms_mean": round(attn_ms, 5), "flops_per_launch": flops,
+        "tokens_per_s": round(w.batch * w.chunk / (ms_step * 1e-3), 1),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "nc_prefill_attn_fp8 (prefill_kernel)"},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +176,11 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    from nanochat_amd.workloads import PREFILL
+
+    if args.workload in PREFILL:
+        print(json.dumps(bench_prefill(args, PREFILL[args.workload])), flush=True)
+        return
     dev = torch.device("cuda:0")
     w = DECODE[args.workload]
     inp = decode_inputs(w, seed=0)

@@ -44,19 +44,25 @@ struct AttnArgs {
     uint16_t *out;            /* [B][T][Hq][128] bf16 */
 };
 
-/* A wave's running state for its 16 query columns; lane (g, c) = (lane >> 4, lane & 15) holds column c. */
+/* A wave's running state for NT tiles of 16 query columns; lane (g, c) = (lane >> 4, lane & 15) holds column c
+ * of every tile. */
+template <int NT>
 struct WaveState {
-    f32x4 o[8];  /* O^T tile t: dims 16t + 4g + i of column c, scaled by 2^-m */
-    float m;     /* column c's reference max (log2 domain, equal in the four groups); exponentials use it */
-    float l;     /* sum of exp2(s - m) over the keys this lane's group holds */
-    bool bad;    /* a block-table entry fell outside the page pool */
+    f32x4 o[NT][8];  /* O^T tile d: dims 16d + 4g + i of column c, scaled by 2^-m */
+    float m[NT];     /* column c's reference max (log2 domain, equal in the four groups); exponentials use it */
+    float l[NT];     /* sum of exp2(s - m) over the keys this lane's group holds */
+    bool bad;        /* a block-table entry fell outside the page pool */
 };
 
-__device__ __forceinline__ void state_init(WaveState &st) {
+template <int NT>
+__device__ __forceinline__ void state_init(WaveState<NT> &st) {
 #pragma unroll
-    for (int t = 0; t < 8; t++) st.o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    st.m = -INFINITY;
-    st.l = 0.0f;
+    for (int t = 0; t < NT; t++) {
+#pragma unroll
+        for (int d = 0; d < 8; d++) st.o[t][d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        st.m[t] = -INFINITY;
+        st.l[t] = 0.0f;
+    }
     st.bad = false;
 }
 
@@ -74,14 +80,19 @@ __device__ __forceinline__ void load_q(const uint16_t *row, int g, bf16x8 (&qb)[
     }
 }
 
-/* Scores S^T (keys 4g + i of one page, column c) = K Q^T from one page's two K loads. */
-__device__ __forceinline__ f32x4 page_scores(const uint4 &k0, const uint4 &k1, const bf16x8 (&qb)[4]) {
-    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
-    s = mfma16x16x32(fp8x8_to_bf16(k0.x, k0.y), qb[0], s);
-    s = mfma16x16x32(fp8x8_to_bf16(k0.z, k0.w), qb[1], s);
-    s = mfma16x16x32(fp8x8_to_bf16(k1.x, k1.y), qb[2], s);
-    s = mfma16x16x32(fp8x8_to_bf16(k1.z, k1.w), qb[3], s);
-    return s;
+/* Scores S^T (keys 4g + i of one page, column c of tile t) = K Q^T for every tile from one page's two K loads:
+ * each converted K operand feeds NT MFMAs. */
+template <int NT>
+__device__ __forceinline__ void page_scores(const uint4 &k0, const uint4 &k1, const bf16x8 (&qb)[NT][4],
+                                            f32x4 (&s)[NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) s[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const bf16x8 k[4] = {fp8x8_to_bf16(k0.x, k0.y), fp8x8_to_bf16(k0.z, k0.w), fp8x8_to_bf16(k1.x, k1.y),
+                         fp8x8_to_bf16(k1.z, k1.w)};
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) s[t] = mfma16x16x32(k[cc], qb[t][cc], s[t]);
 }
 
 __device__ __forceinline__ uint32_t dword(const uint4 &u, int i) {
@@ -147,18 +158,21 @@ __device__ __forceinline__ void load_pair(const uint8_t *pages, const float *sca
     r.sb = load_nt(scales + p.hb * 2 * PAGE + (lane >> 4) * 4);
 }
 
-/* Key bounds of a wave: a lane's column sees keys [lo, hi]; pairs inside [full_lo, full_hi] are unmasked for
- * every column; V codes of keys past written_hi are not cache contents and are zeroed before use. */
+/* Key bounds of a wave: in tile t a lane's column sees keys [lo[t], hi[t]]; pairs inside [full_lo, full_hi]
+ * are unmasked for every column; V codes of keys past written_hi are not cache contents and are zeroed. */
+template <int NT>
 struct KeyBounds {
-    int lo, hi, full_lo, full_hi, written_hi;
+    int lo[NT], hi[NT];
+    int full_lo, full_hi, written_hi;
 };
 
-/* Softmax update and PV of one pair from its scores: the lazy rescale moves the reference max only when a
- * column's max grows past it by RESCALE_LOG2 (p <= 2^8 otherwise), decided for the whole wave at once. */
-template <bool MASKED>
-__device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p, const f32x4 &sa, const f32x4 &sb,
-                                            const float4 &ksa, const float4 &ksb, PairRegs &v, const KeyBounds &kb,
-                                            WaveState &st, int lane) {
+/* Softmax update and PV of one pair from its scores: per tile, the lazy rescale moves the reference max only
+ * when a column's max grows past it by RESCALE_LOG2 (p <= 2^8 otherwise), decided for the whole wave at once;
+ * each converted V operand feeds NT MFMAs. */
+template <int NT, bool MASKED>
+__device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p, const f32x4 (&sa)[NT],
+                                            const f32x4 (&sb)[NT], const float4 &ksa, const float4 &ksb, PairRegs &v,
+                                            const KeyBounds<NT> &kb, WaveState<NT> &st, int lane) {
     const int g = lane >> 4;
     const int key_a = p.lpa * PAGE + g * 4, key_b = key_a + PAGE;
     if (MASKED) {
@@ -168,80 +182,108 @@ __device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p
         v.a0 = and4(v.a0, ma); v.a1 = and4(v.a1, ma);
         v.b0 = and4(v.b0, mb); v.b1 = and4(v.b1, mb);
     }
-    const float ks[8] = {ksa.x, ksa.y, ksa.z, ksa.w, ksb.x, ksb.y, ksb.z, ksb.w};
+    const float ks[8] = {ksa.x * a.scale_log2, ksa.y * a.scale_log2, ksa.z * a.scale_log2, ksa.w * a.scale_log2,
+                         ksb.x * a.scale_log2, ksb.y * a.scale_log2, ksb.z * a.scale_log2, ksb.w * a.scale_log2};
     const float vs[8] = {v.sa.x, v.sa.y, v.sa.z, v.sa.w, v.sb.x, v.sb.y, v.sb.z, v.sb.w};
-    float s[8];
-    bool ok[8];
+    bf16x8 pv[NT];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float acc = i < 4 ? sa[i] : sb[i - 4];
-        if (MASKED) {
-            const int key = (i < 4 ? key_a : key_b) + (i & 3);
-            ok[i] = (i < 4 || p.has_b) && key >= kb.lo && key <= kb.hi;
-            s[i] = ok[i] ? acc * ks[i] * a.scale_log2 : -INFINITY;
-        } else {
-            ok[i] = true;
-            s[i] = acc * ks[i] * a.scale_log2;
+    for (int t = 0; t < NT; t++) {
+        float s[8];
+        bool ok[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float acc = i < 4 ? sa[t][i] : sb[t][i - 4];
+            if (MASKED) {
+                const int key = (i < 4 ? key_a : key_b) + (i & 3);
+                ok[i] = (i < 4 || p.has_b) && key >= kb.lo[t] && key <= kb.hi[t];
+                s[i] = ok[i] ? acc * ks[i] : -INFINITY;
+            } else {
+                ok[i] = true;
+                s[i] = acc * ks[i];
+            }
         }
-    }
-    float mt = s[0];
+        float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+        mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+        const float mnew = fmaxf(st.m[t], mt);
+        if (__any(mnew > st.m[t] + RESCALE_LOG2)) {
+            const float alpha = mnew == st.m[t] ? 1.0f : __builtin_amdgcn_exp2f(st.m[t] - mnew);
 #pragma unroll
-    for (int i = 1; i < 8; i++) mt = fmaxf(mt, s[i]);
-    mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
-    const float mnew = fmaxf(st.m, mt);
-    if (__any(mnew > st.m + RESCALE_LOG2)) {
-        const float alpha = mnew == st.m ? 1.0f : __builtin_amdgcn_exp2f(st.m - mnew);
+            for (int d = 0; d < 8; d++) st.o[t][d] *= alpha;
+            st.l[t] *= alpha;
+            st.m[t] = mnew;
+        }
+        const float mbase = st.m[t] == -INFINITY ? 0.0f : st.m[t];  /* no key yet: every s is -inf */
+        float psum = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 8; t++) st.o[t] *= alpha;
-        st.l *= alpha;
-        st.m = mnew;
+        for (int i = 0; i < 8; i++) {
+            const float pr = __builtin_amdgcn_exp2f(s[i] - mbase);
+            psum += pr;
+            pv[t][i] = (__bf16)(ok[i] ? pr * vs[i] : 0.0f);
+        }
+        st.l[t] += psum;
     }
-    const float mbase = st.m == -INFINITY ? 0.0f : st.m;  /* a column with no key yet: every s is -inf */
-    float psum = 0.0f;
-    bf16x8 pv;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float pr = __builtin_amdgcn_exp2f(s[i] - mbase);
-        psum += pr;
-        pv[i] = (__bf16)(ok[i] ? pr * vs[i] : 0.0f);
-    }
-    st.l += psum;
+    for (int d = 0; d < 8; d++) {
+        const bf16x8 va = fp8x8_to_bf16(dword(d < 4 ? v.a0 : v.a1, d & 3), dword(d < 4 ? v.b0 : v.b1, d & 3));
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-        const bf16x8 va = fp8x8_to_bf16(dword(t < 4 ? v.a0 : v.a1, t & 3), dword(t < 4 ? v.b0 : v.b1, t & 3));
-        st.o[t] = mfma16x16x32(va, pv, st.o[t]);
+        for (int t = 0; t < NT; t++) st.o[t][d] = mfma16x16x32(va, pv[t], st.o[t][d]);
     }
+}
+
+template <int NT>
+__device__ __forceinline__ void pair_step(const AttnArgs &a, const PairAddr &cur, const f32x4 (&sa)[NT],
+                                          const f32x4 (&sb)[NT], const float4 &ksa, const float4 &ksb, PairRegs &vr,
+                                          const KeyBounds<NT> &kb, WaveState<NT> &st, int lane) {
+    const bool interior = cur.has_b && cur.lpa * PAGE >= kb.full_lo && cur.lpa * PAGE + 2 * PAGE - 1 <= kb.full_hi &&
+                          cur.lpa * PAGE + 2 * PAGE - 1 <= kb.written_hi;
+    if (interior)
+        pair_update<NT, false>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
+    else
+        pair_update<NT, true>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
 }
 
 /*
  * A wave's pass over the page pairs lpa0, lpa0 + step, ... below `end` (logical pages of KV head kvh through
- * block-table row bt). Rolling prefetch: the next pair's K loads are issued as soon as this pair's scores are
- * computed, its V loads as soon as this pair's PV is issued, so one pair is always in flight per wave.
+ * block-table row bt). PREFETCH (the memory-bound decode): the next pair's K loads are issued as soon as this
+ * pair's scores are computed, its V loads as soon as this pair's PV is issued, so one pair is always in flight
+ * per wave. Without it (the MFMA-bound prefill) a pair's loads are issued at the top of its step, which keeps
+ * registers for more query columns.
  */
+template <int NT, bool PREFETCH>
 __device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *bt, int kvh, int lpa0, int step, int end,
-                                             const KeyBounds &kb, const bf16x8 (&qb)[4], WaveState &st, int lane) {
+                                             const KeyBounds<NT> &kb, const bf16x8 (&qb)[NT][4], WaveState<NT> &st,
+                                             int lane) {
     if (lpa0 >= end) return;
-    PairAddr cur = pair_addr(a, bt, kvh, lpa0, end, st.bad);
-    PairRegs kr, vr;
-    load_pair(a.k_pages, a.kv_scale, cur, lane, kr);
-    load_pair(a.v_pages, a.kv_scale + PAGE, cur, lane, vr);
-    for (int lpa = lpa0; lpa < end; lpa += step) {
-        const bool more = lpa + step < end;
-        PairAddr nxt = cur;
-        if (more) nxt = pair_addr(a, bt, kvh, lpa + step, end, st.bad);
-        const f32x4 sa = page_scores(kr.a0, kr.a1, qb);
-        const f32x4 sb = page_scores(kr.b0, kr.b1, qb);
-        const float4 ksa = kr.sa, ksb = kr.sb;
-        if (more) load_pair(a.k_pages, a.kv_scale, nxt, lane, kr);
-        const bool interior = cur.has_b && cur.lpa * PAGE >= kb.full_lo && cur.lpa * PAGE + 2 * PAGE - 1 <= kb.full_hi &&
-                              cur.lpa * PAGE + 2 * PAGE - 1 <= kb.written_hi;
-        if (interior)
-            pair_update<false>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
-        else
-            pair_update<true>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
-        if (more) load_pair(a.v_pages, a.kv_scale + PAGE, nxt, lane, vr);
-        cur = nxt;
+    if (PREFETCH) {
+        PairAddr cur = pair_addr(a, bt, kvh, lpa0, end, st.bad);
+        PairRegs kr, vr;
+        load_pair(a.k_pages, a.kv_scale, cur, lane, kr);
+        load_pair(a.v_pages, a.kv_scale + PAGE, cur, lane, vr);
+        for (int lpa = lpa0; lpa < end; lpa += step) {
+            const bool more = lpa + step < end;
+            PairAddr nxt = cur;
+            if (more) nxt = pair_addr(a, bt, kvh, lpa + step, end, st.bad);
+            f32x4 sa[NT], sb[NT];
+            page_scores<NT>(kr.a0, kr.a1, qb, sa);
+            page_scores<NT>(kr.b0, kr.b1, qb, sb);
+            const float4 ksa = kr.sa, ksb = kr.sb;
+            if (more) load_pair(a.k_pages, a.kv_scale, nxt, lane, kr);
+            pair_step<NT>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
+            if (more) load_pair(a.v_pages, a.kv_scale + PAGE, nxt, lane, vr);
+            cur = nxt;
+        }
+    } else {
+        for (int lpa = lpa0; lpa < end; lpa += step) {
+            const PairAddr cur = pair_addr(a, bt, kvh, lpa, end, st.bad);
+            PairRegs kr, vr;
+            load_pair(a.k_pages, a.kv_scale, cur, lane, kr);
+            load_pair(a.v_pages, a.kv_scale + PAGE, cur, lane, vr);
+            f32x4 sa[NT], sb[NT];
+            page_scores<NT>(kr.a0, kr.a1, qb, sa);
+            page_scores<NT>(kr.b0, kr.b1, qb, sb);
+            pair_step<NT>(a, cur, sa, sb, kr.sa, kr.sb, vr, kb, st, lane);
+        }
     }
 }
 
@@ -321,25 +363,27 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         const int first = pg0 + (int)(s - us), last = pg0 + (int)(seg_end - us);
         const long long row0 = (long long)b * a.Hq + kvh * a.G;
 
-        bf16x8 qb[4];
-        load_q(c < a.G ? a.q + (row0 + c) * HEAD_DIM : nullptr, g, qb);
-        WaveState st;
+        bf16x8 qb[1][4];
+        load_q(c < a.G ? a.q + (row0 + c) * HEAD_DIM : nullptr, g, qb[0]);
+        WaveState<1> st;
         state_init(st);
-        const KeyBounds kb = {begin, L - 1, begin, L - 1, L - 1};
-        attend_pages(a, a.block_table + (long long)b * a.max_pages, kvh, first, 2, last, kb, qb, st, lane);
-        st.l += __shfl_xor(st.l, 16, WAVE);
-        st.l += __shfl_xor(st.l, 32, WAVE);
+        KeyBounds<1> kb;
+        kb.lo[0] = kb.full_lo = begin;
+        kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
+        attend_pages<1, true>(a, a.block_table + (long long)b * a.max_pages, kvh, first, 2, last, kb, qb, st, lane);
+        st.l[0] += __shfl_xor(st.l[0], 16, WAVE);
+        st.l[0] += __shfl_xor(st.l[0], 32, WAVE);
         const long long w0 = worker_of(us, P, W), w1 = worker_of(ue - 1, P, W);
         const int u = b * a.Hkv + kvh;
         if (w0 == w1) {  /* the whole unit is in this run */
             if (c < a.G) {
                 uint16_t *dst = a.out + (row0 + c) * HEAD_DIM;
-                const float inv = 1.0f / st.l;
+                const float inv = 1.0f / st.l[0];
 #pragma unroll
                 for (int t = 0; t < 8; t++) {
                     float v[4];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) v[i] = st.bad ? NAN : st.o[t][i] * inv;
+                    for (int i = 0; i < 4; i++) v[i] = st.bad ? NAN : st.o[0][t][i] * inv;
                     store_bf16x4(dst + 16 * t + 4 * g, v);
                 }
             }
@@ -349,13 +393,13 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
                 float *po = a.part_o + (slot * a.G + c) * HEAD_DIM;
 #pragma unroll
                 for (int t = 0; t < 8; t++) {
-                    const f32x4 o = st.o[t];
+                    const f32x4 o = st.o[0][t];
                     *reinterpret_cast<float4 *>(po + 16 * t + 4 * g) =
                         float4{st.bad ? NAN : o[0], o[1], o[2], o[3]};
                 }
                 if (g == 0) {
-                    a.part_ml[(slot * a.G + c) * 2] = st.bad ? NAN : st.m;
-                    a.part_ml[(slot * a.G + c) * 2 + 1] = st.l;
+                    a.part_ml[(slot * a.G + c) * 2] = st.bad ? NAN : st.m[0];
+                    a.part_ml[(slot * a.G + c) * 2 + 1] = st.l[0];
                 }
             }
         }
@@ -403,53 +447,72 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_combine_kernel(AttnArgs a) {
     a.out[row * HEAD_DIM + d] = f32_to_bf16(o / ls);
 }
 
-/* Grid (ceil(T / (4 tpt)), Hkv, B), 4 waves; wave w owns tile blockIdx.x*4 + w of tpt = 16 / G consecutive
- * tokens x G heads (column c = token (c / G), head (c % G)) and streams every page its rows can see. */
+/* Grid (ceil(T / (4 NT tpt)), Hkv, B), 4 waves. A wave owns NT tiles of 16 columns, each tile tpt = 16 / G
+ * consecutive tokens x G heads (column c = token c / G, head c % G), and streams every page its rows can see;
+ * each K/V operand it converts feeds its NT tiles. */
+template <int NT>
 __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     const int kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
-    const int tpt = 16 / a.G;
-    const int t0 = (blockIdx.x * WAVES + wave) * tpt;
+    const int tpt = 16 / a.G, tpw = tpt * NT;
+    const int t0 = (blockIdx.x * WAVES + wave) * tpw;
     if (t0 >= a.T) return;
-    const int tl = c / a.G, hg = c % a.G;
-    const bool live = c < tpt * a.G && t0 + tl < a.T;
-    const long long qrow = ((long long)b * a.T + t0 + tl) * a.Hq + kvh * a.G + hg;
     const int start = a.start_pos[b];
+    const int hg = c % a.G;
+    bool live[NT];
+    long long qrow[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int tok = t0 + t * tpt + c / a.G;
+        live[t] = c < tpt * a.G && tok < a.T;
+        qrow[t] = ((long long)b * a.T + tok) * a.Hq + kvh * a.G + hg;
+    }
     if (start < 0 || (long long)start + a.T > (long long)a.max_pages * PAGE) {  /* past the block table: NaN */
-        if (live)
-            for (int d = g * 32; d < g * 32 + 32; d++) a.out[qrow * HEAD_DIM + d] = (uint16_t)0x7FC0;
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            if (live[t])
+                for (int d = g * 32; d < g * 32 + 32; d++) a.out[qrow[t] * HEAD_DIM + d] = (uint16_t)0x7FC0;
         return;
     }
-    const int t_last = min(t0 + tpt, a.T) - 1;   /* the wave's last token */
-    const int pos = start + t0 + tl;
-    KeyBounds kb;
-    kb.hi = live ? pos : -1;
-    kb.lo = live ? (a.window >= 0 ? max(pos - a.window, 0) : 0) : 0;
+    const int t_last = min(t0 + tpw, a.T) - 1;   /* the wave's last token */
+    KeyBounds<NT> kb;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int pos = start + t0 + t * tpt + c / a.G;
+        kb.hi[t] = live[t] ? pos : -1;
+        kb.lo[t] = live[t] ? (a.window >= 0 ? max(pos - a.window, 0) : 0) : 0;
+    }
     kb.full_hi = start + t0;                                                   /* the wave's first row */
     kb.full_lo = a.window >= 0 ? max(start + t_last - a.window, 0) : 0;       /* its last row's window start */
     kb.written_hi = start + a.T - 1;
     const int w_lo = a.window >= 0 ? max(start + t0 - a.window, 0) : 0;
     const int pg0 = w_lo / PAGE, pg1 = (start + t_last) / PAGE + 1;
 
-    bf16x8 qb[4];
-    load_q(live ? a.q + qrow * HEAD_DIM : nullptr, g, qb);
-    WaveState st;
+    bf16x8 qb[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++) load_q(live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr, g, qb[t]);
+    WaveState<NT> st;
     state_init(st);
-    attend_pages(a, a.block_table + (long long)b * a.max_pages, kvh, pg0, 2, pg1, kb, qb, st, lane);
-    st.l += __shfl_xor(st.l, 16, WAVE);
-    st.l += __shfl_xor(st.l, 32, WAVE);
-    if (!live) return;
-    uint16_t *dst = a.out + qrow * HEAD_DIM;
-    const float inv = 1.0f / st.l;
+    attend_pages<NT, false>(a, a.block_table + (long long)b * a.max_pages, kvh, pg0, 2, pg1, kb, qb, st, lane);
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-        float v[4];
+    for (int t = 0; t < NT; t++) {
+        st.l[t] += __shfl_xor(st.l[t], 16, WAVE);
+        st.l[t] += __shfl_xor(st.l[t], 32, WAVE);
+        if (!live[t]) continue;
+        uint16_t *dst = a.out + qrow[t] * HEAD_DIM;
+        const float inv = 1.0f / st.l[t];
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = st.bad ? NAN : st.o[t][i] * inv;
-        store_bf16x4(dst + 16 * t + 4 * g, v);
+        for (int d = 0; d < 8; d++) {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = st.bad ? NAN : st.o[t][d][i] * inv;
+            store_bf16x4(dst + 16 * d + 4 * g, v);
+        }
     }
 }
+
+constexpr int PREFILL_TILES = 2;  /* 16-column tiles per prefill wave */
 
 /* Decode workers (waves). Automatic: every wave slot the device holds at the kernel's occupancy, so one
  * balanced round covers the whole page list; at most one wave per MIN_WORKER_PAGES pages, at most
@@ -551,8 +614,8 @@ extern "C" int nc_prefill_attn_fp8(const void *q, const void *k_pages, const voi
     a.B = B; a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.window = window;
     a.scale_log2 = sm_scale * LOG2E;
     a.out = (uint16_t *)out;
-    const int tpt = 16 / a.G;
-    const int tiles = (T + tpt - 1) / tpt;
-    hipLaunchKernelGGL(prefill_kernel, dim3((tiles + WAVES - 1) / WAVES, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
+    const int tokens_per_block = WAVES * PREFILL_TILES * (16 / a.G);
+    hipLaunchKernelGGL(prefill_kernel<PREFILL_TILES>, dim3((T + tokens_per_block - 1) / tokens_per_block, Hkv, B),
+                       dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }

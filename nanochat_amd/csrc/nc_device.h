@@ -79,18 +79,16 @@ __device__ __forceinline__ int v_page_offset(int slot, int dim) {
 }
 
 /* Two e4m3fn codes (bytes 0-1, or 2-3 for the _hi form, of w) -> two bf16 (exact) packed in a dword, by one
- * v_cvt_scalef32_pk_bf16_fp8 with scale 1. Inline asm on purpose: the compiler's model of the builtin's bf16x2
- * result is wrong when an element is extracted (it packs element 0 twice), so the result is kept opaque as a
- * whole dword and only ever reinterpreted as a full MFMA operand. */
+ * v_cvt_scalef32_pk_bf16_fp8 with scale 1. The builtin's 2-element result is only ever reinterpreted whole: the
+ * compiler mis-models an extracted element (it packs element 0 twice), while as a whole dword it emits the bare
+ * instruction. It must stay a builtin (not inline asm) so the compiler sees a VALU write and inserts the wait
+ * states an in-flight MFMA reading the same registers needs. */
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t cvt_fp8x2_bf16_lo(uint32_t w) {
-    uint32_t r;
-    asm("v_cvt_scalef32_pk_bf16_fp8 %0, %1, 1.0" : "=v"(r) : "v"(w));
-    return r;
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false));
 }
 __device__ __forceinline__ uint32_t cvt_fp8x2_bf16_hi(uint32_t w) {
-    uint32_t r;
-    asm("v_cvt_scalef32_pk_bf16_fp8 %0, %1, 1.0 op_sel:[1,0,0]" : "=v"(r) : "v"(w));
-    return r;
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, true));
 }
 
 /* Eight e4m3fn codes (dword a: codes 0-3, dword b: codes 4-7) -> an exact bf16x8 MFMA operand. */
