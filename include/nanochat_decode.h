@@ -1,0 +1,83 @@
+/*
+ * nanochat_amd decoder runtime (libnanochat_decode.so): the 14 dec_* symbols of the reference's decoder ABI,
+ * model/kernels/decode.cu:904-1131, with the argument lists inference/decoder.py:132-148 binds, over an fp8
+ * (e4m3fn) paged KV cache on gfx950. Every call is stream-ordered on the stream given to dec_create except
+ * dec_create (synchronous allocation) and dec_tokens (synchronizes). A failed HIP or rocBLAS call, or an argument
+ * out of range, aborts with a message, as in the reference (decode.cu:47-53, 926-931).
+ *
+ * Differences from the reference, by design: the KV cache is fp8 with one scale per (token, head) (the reference
+ * caches bf16); the prompt store lives in device memory, as pages of the same pools (the reference: pinned host
+ * memory); dec_prefill takes up to 8192 rows (the reference: 1024); steps are launched eagerly, not as graphs.
+ */
+#ifndef NANOCHAT_DECODE_H
+#define NANOCHAT_DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* cfg [7]: L, C, F, vocab, max_len, store (prompt-store positions), lazy (the BOS row a host may reject).
+ * ptrs [4 + 8 L]: wte fp32 [vocab][C], cos, sin fp32 [>= max_len][64], lm_head bf16 [vocab][C]; per layer qkv bf16
+ * [3C][C], o [C][C], fc [F][C], proj [C][F], ve table (must be 0), ve gate (must be 0), q norm, k norm fp32 [128].
+ * scal [2L + 1]: per layer (resid, x0) lambdas, then the logit cap. window [L]: keys before a query per layer.
+ * Reference: decode.cu:950-1023. */
+void *dec_create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream);
+
+/* Slots (decode.cu:948). */
+int dec_batch(void *handle);
+
+/* Start slot b at its prompt's last token `token`, position `last` (decode.cu:1026-1035). */
+void dec_set_prompt(void *handle, int b, int32_t token, int32_t last, float temperature, float top_p,
+                    unsigned long long seed);
+
+/* Rows per dec_prefill call (decode.cu:1037). */
+int dec_prefill_rows(void *handle);
+
+/* Run n rows (host int32 [3][n]: token, position, slot; a slot's rows at consecutive positions) through the body,
+ * caching each row's K and V, each row attending to its slot's positions up to its own (decode.cu:1041-1051). */
+void dec_prefill(void *handle, int n, const int32_t *rows);
+
+/* Copy slot b's positions [at, at + n) to / from prompt-store position store_at (decode.cu:1069-1075). */
+void dec_save_prompt(void *handle, int b, int at, int store_at, int n);
+void dec_load_prompt(void *handle, int b, int at, int store_at, int n);
+
+/* Pinned host allowed-token masks [B][vocab / 32] (decode.cu:1079). */
+uint32_t *dec_masks(void *handle);
+
+/* Active and masked slots, host uint64 [2][ceil(B / 64)] (decode.cu:1083-1105). */
+void dec_set_active(void *handle, const unsigned long long *slots);
+
+/* One step: the body (embedding, layers), then the head (final norm, lm_head, choice, commit)
+ * (decode.cu:1107-1116). */
+void dec_launch_body(void *handle);
+void dec_launch_head(void *handle);
+
+/* Wait for the step; out [2B]: each slot's token, then its alternative (decode.cu:1120-1124). */
+void dec_tokens(void *handle, int32_t *out);
+
+/* Slot b's next input becomes its alternative (decode.cu:1128-1131). */
+void dec_take_alt(void *handle, int b);
+
+/* Free everything dec_create allocated (decode.cu:904-924). */
+void dec_destroy(void *handle);
+
+/* --- Extensions with no counterpart in the reference. */
+
+/* dec_create with at most max_slots slots (1..1024): for callers that share the device with other work. dec_create
+ * is dec_create_slots(..., 1024). */
+void *dec_create_slots(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream,
+                       int max_slots);
+
+/* Test hooks (synchronize, then copy to host): the last head's fp32 logits of slots [0, rows), out [rows][vocab];
+ * and the cached rows of slot b (b = -1: the prompt store) at positions [at, at + n) of one layer, k and v as
+ * e4m3fn codes [n][H][128], scales [n][H][2] (K, V). */
+void dec_debug_logits(void *handle, float *out, int rows);
+void dec_debug_cache(void *handle, int layer, int b, int at, int n, uint8_t *k, uint8_t *v, float *scales);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOCHAT_DECODE_H */

@@ -19,6 +19,7 @@
 
 #include "nc_device.h"
 #include "nanochat_amd.h"
+#include "nc_internal.h"
 
 namespace nc {
 
@@ -34,7 +35,10 @@ struct AttnArgs {
     const int32_t *block_table;
     int max_pages, num_pages;
     const int32_t *seq_lens;  /* decode */
-    const int32_t *start_pos; /* prefill */
+    const int32_t *start_pos; /* prefill: the first position of each sequence's (or run's) rows */
+    const int32_t *run_row0;  /* NULL, or prefill runs: run b's rows are q/out rows run_row0[b] .. + run_count[b] */
+    const int32_t *run_count;
+    const int32_t *run_slot;  /* run b's block-table row */
     int B, T, Hq, Hkv, G, window;
     float scale_log2;         /* sm_scale * log2(e) */
     int workers;              /* decode: waves sharing the flattened page list */
@@ -245,10 +249,10 @@ __device__ __forceinline__ void pair_step(const AttnArgs &a, const PairAddr &cur
 
 /*
  * A wave's pass over the page pairs lpa0, lpa0 + step, ... below `end` (logical pages of KV head kvh through
- * block-table row bt). PREFETCH (the memory-bound decode): the next pair's K loads are issued as soon as this
- * pair's scores are computed, its V loads as soon as this pair's PV is issued, so one pair is always in flight
- * per wave. Without it (the MFMA-bound prefill) a pair's loads are issued at the top of its step, which keeps
- * registers for more query columns.
+ * block-table row bt). PREFETCH: the next pair's K loads are issued as soon as this pair's scores are computed,
+ * its V loads as soon as this pair's PV is issued, so one pair is always in flight per wave (both kernels use it;
+ * measured 6% faster for prefill at two column tiles). Without it a pair's loads are issued at the top of its
+ * step, which needs fewer registers.
  */
 template <int NT, bool PREFETCH>
 __device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *bt, int kvh, int lpa0, int step, int end,
@@ -457,7 +461,10 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     const int c = lane & 15, g = lane >> 4;
     const int tpt = 16 / a.G, tpw = tpt * NT;
     const int t0 = (blockIdx.x * WAVES + wave) * tpw;
-    if (t0 >= a.T) return;
+    const int T = a.run_row0 ? a.run_count[b] : a.T;          /* this sequence's (run's) rows */
+    if (t0 >= T) return;
+    const long long row0 = a.run_row0 ? a.run_row0[b] : (long long)b * a.T;
+    const int trow = a.run_row0 ? a.run_slot[b] : b;          /* its block-table row */
     const int start = a.start_pos[b];
     const int hg = c % a.G;
     bool live[NT];
@@ -465,17 +472,17 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const int tok = t0 + t * tpt + c / a.G;
-        live[t] = c < tpt * a.G && tok < a.T;
-        qrow[t] = ((long long)b * a.T + tok) * a.Hq + kvh * a.G + hg;
+        live[t] = c < tpt * a.G && tok < T;
+        qrow[t] = (row0 + tok) * a.Hq + kvh * a.G + hg;
     }
-    if (start < 0 || (long long)start + a.T > (long long)a.max_pages * PAGE) {  /* past the block table: NaN */
+    if (start < 0 || (long long)start + T > (long long)a.max_pages * PAGE) {  /* past the block table: NaN */
 #pragma unroll
         for (int t = 0; t < NT; t++)
             if (live[t])
                 for (int d = g * 32; d < g * 32 + 32; d++) a.out[qrow[t] * HEAD_DIM + d] = (uint16_t)0x7FC0;
         return;
     }
-    const int t_last = min(t0 + tpw, a.T) - 1;   /* the wave's last token */
+    const int t_last = min(t0 + tpw, T) - 1;     /* the wave's last token */
     KeyBounds<NT> kb;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -485,7 +492,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     }
     kb.full_hi = start + t0;                                                   /* the wave's first row */
     kb.full_lo = a.window >= 0 ? max(start + t_last - a.window, 0) : 0;       /* its last row's window start */
-    kb.written_hi = start + a.T - 1;
+    kb.written_hi = start + T - 1;
     const int w_lo = a.window >= 0 ? max(start + t0 - a.window, 0) : 0;
     const int pg0 = w_lo / PAGE, pg1 = (start + t_last) / PAGE + 1;
 
@@ -494,7 +501,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     for (int t = 0; t < NT; t++) load_q(live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr, g, qb[t]);
     WaveState<NT> st;
     state_init(st);
-    attend_pages<NT, false>(a, a.block_table + (long long)b * a.max_pages, kvh, pg0, 2, pg1, kb, qb, st, lane);
+    attend_pages<NT, true>(a, a.block_table + (long long)trow * a.max_pages, kvh, pg0, 2, pg1, kb, qb, st, lane);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         st.l[t] += __shfl_xor(st.l[t], 16, WAVE);
@@ -513,6 +520,29 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
 }
 
 constexpr int PREFILL_TILES = 2;  /* 16-column tiles per prefill wave */
+
+/* Prefill over runs for the decoder runtime: run b = rows run_row0[b] .. + run_count[b] of q/out ([rows][Hq][128])
+ * at positions start_pos[b] + t of block-table row run_slot[b]; max_count bounds run_count. Arguments are checked
+ * by the caller. */
+int prefill_runs(const uint16_t *q, const uint8_t *k_pages, const uint8_t *v_pages, const float *kv_scale,
+                 const int32_t *block_table, int max_pages, int num_pages, const int32_t *start_pos,
+                 const int32_t *run_row0, const int32_t *run_count, const int32_t *run_slot, int runs, int max_count,
+                 int Hq, int Hkv, int window, float sm_scale, uint16_t *out, hipStream_t stream) {
+    AttnArgs a = {};
+    a.q = q;
+    a.k_pages = k_pages; a.v_pages = v_pages; a.kv_scale = kv_scale;
+    a.block_table = block_table; a.max_pages = max_pages; a.num_pages = num_pages;
+    a.start_pos = start_pos;
+    a.run_row0 = run_row0; a.run_count = run_count; a.run_slot = run_slot;
+    a.B = runs; a.T = max_count; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.window = window;
+    a.scale_log2 = sm_scale * LOG2E;
+    a.out = out;
+    const int tokens_per_block = WAVES * PREFILL_TILES * (16 / a.G);
+    hipLaunchKernelGGL(prefill_kernel<PREFILL_TILES>, dim3((max_count + tokens_per_block - 1) / tokens_per_block, Hkv,
+                                                           runs),
+                       dim3(256), 0, stream, a);
+    return (int)hipGetLastError();
+}
 
 /* Decode workers (waves). Automatic: every wave slot the device holds at the kernel's occupancy, so one
  * balanced round covers the whole page list; at most one wave per MIN_WORKER_PAGES pages, at most

@@ -1,0 +1,855 @@
+/*
+ * The decoder runtime on gfx950: the reference's dec_* ABI (model/kernels/decode.cu:904-1131, bound by
+ * inference/decoder.py:132-148) over an fp8 paged KV cache.
+ *
+ * A step is a stream of kernels on the caller's stream, launched eagerly:
+ *   body   norm_kernel(EMBED) -> per layer { norm_kernel(RESID), qkv GEMM (bf16 out), the fused q/k norm + RoPE +
+ *          value-embedding + fp8 append (kv_append.hip), split-K decode attention (attention.hip), o GEMM (fp32 out),
+ *          resid_rstd_kernel, fc GEMM (fp32 out), relu2_kernel, proj GEMM (bf16(s + xo) by beta = 1) }
+ *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
+ *          the allowed tokens, then the commit), the tokens to pinned host memory.
+ * GEMMs are rocBLAS gemm_ex, bf16 operands with fp32 accumulation, atomics off (deterministic). Every kernel covers
+ * the slots up to the highest active one (dec_set_active) and skips inactive slots.
+ *
+ * Numerics, op by op as decode.cu: the epilogues round once (bf16(s + residual)); the MLP reads the un-normed stream
+ * scaled by its rstd; every RMS norm is 1 / sqrt(mean x^2 + FLT_EPSILON), correctly rounded (the reference: rsqrtf).
+ * The KV cache is fp8 e4m3fn with one absmax scale per (token, head) (the reference caches bf16); a step's own key
+ * is read back from the cache like the others.
+ *
+ * Memory: one allocation per role, sized at dec_create. The KV pool of layer l is pages [0, B max_pages) for the
+ * slots (slot b owns pages b max_pages + i, the identity block table) followed by the prompt store's pages (store
+ * position s at page B max_pages + s / 16, slot s % 16), so saving and loading a prompt are page-to-page copies
+ * inside one pool.
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include <rocblas/rocblas.h>
+
+#include "nc_device.h"
+#include "nanochat_amd.h"
+#include "nanochat_decode.h"
+#include "nc_internal.h"
+
+namespace nc {
+namespace dec {
+
+constexpr int MAX_BATCH = 1024;            /* slots (the reference's limit, decode.cu:27-29) */
+constexpr int MASK_BITS = 64;              /* slots per word of a slot mask */
+constexpr int MASK_WORDS = MAX_BATCH / MASK_BITS;
+constexpr int WORD_BITS = 32;              /* tokens per word of an allowed-token mask */
+constexpr int PREFILL_ROWS = 8192;         /* rows per dec_prefill call */
+constexpr int GLOBAL_PTRS = 4, LAYER_PTRS = 8;
+constexpr int CHOICE_THREADS = 1024, CHOICE_WAVES = CHOICE_THREADS / WAVE;
+constexpr float SM_SCALE = 0.08838834764831845f;  /* 1 / sqrt(128) */
+
+/* A failed HIP or rocBLAS call aborts, naming it: never silently wrong tokens (decode.cu:47-53). */
+[[noreturn]] static void die(const char *what, const char *detail, int line) {
+    fprintf(stderr, "decoder.hip:%d: %s: %s\n", line, what, detail);
+    abort();
+}
+#define HIP_CHECK(call)                                                        \
+    do {                                                                       \
+        const hipError_t e_ = (call);                                          \
+        if (e_ != hipSuccess) ::nc::dec::die(#call, hipGetErrorString(e_), __LINE__);    \
+    } while (0)
+#define BLAS_CHECK(call)                                                                \
+    do {                                                                                \
+        const rocblas_status s_ = (call);                                               \
+        if (s_ != rocblas_status_success) ::nc::dec::die(#call, rocblas_status_to_string(s_), __LINE__); \
+    } while (0)
+#define NC_CHECK(call)                                                         \
+    do {                                                                       \
+        const int s_ = (call);                                                 \
+        if (s_ != 0) ::nc::dec::die(#call, nc_status_string(s_), __LINE__);              \
+    } while (0)
+#define REQUIRE(cond, msg) \
+    do {                   \
+        if (!(cond)) ::nc::dec::die("dec_create", msg, __LINE__); \
+    } while (0)
+
+__device__ __forceinline__ bool live(const unsigned long long *mask, int b) {
+    return (mask[b / MASK_BITS] >> (b % MASK_BITS)) & 1ull;
+}
+
+/* ---------------------------------------------------------------- norms and epilogues (a wave per row) */
+
+enum { NORM_FINAL, NORM_RESID, NORM_EMBED };
+
+struct NormArgs {
+    int kind;
+    const uint16_t *in;       /* RESID: the stream x (NULL at layer 0: x0 itself), FINAL: x */
+    const float *wte;         /* EMBED: [vocab][C] fp32 */
+    float *x0;                /* [rows][C] fp32: EMBED writes, RESID reads */
+    int32_t *tokens;          /* EMBED: a token outside [0, vocab) is replaced by 0 here (embedded and read by
+                                 the layers' value embeddings as 0), so no kernel reads outside a table */
+    int vocab;
+    float l1, l2;             /* RESID: resid and x0 lambdas */
+    uint16_t *mixed, *out;    /* RESID: mixed = bf16(v); out = bf16(v r) */
+    const unsigned long long *active;  /* NULL: every row */
+    int rows, C;
+    const int32_t *pos;       /* EMBED in a step: seq_lens = pos + 1 and num_new = 1 for active slots, else 0 */
+    int32_t *seq_lens, *num_new;
+};
+
+/* RMS norm of a row (decode.cu:413-443): EMBED x0 = wte[token] r in fp32; RESID v = fma(l1, h, x0 l2), mixed =
+ * bf16(v), out = bf16(v r); FINAL out = bf16(x r); r = 1 / sqrt(sum v^2 / C + FLT_EPSILON), the sum a lane-strided
+ * FMA chain then the butterfly. */
+__global__ void __launch_bounds__(256) norm_kernel(NormArgs a) {
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & (WAVE - 1);
+    if (b >= a.rows) return;
+    const bool on = !a.active || live(a.active, b);
+    if (a.seq_lens && lane == 0) {
+        a.seq_lens[b] = on ? a.pos[b] + 1 : 0;
+        a.num_new[b] = on ? 1 : 0;
+    }
+    if (!on) return;
+    const long long row = (long long)b * a.C;
+    const float *emb = nullptr;
+    if (a.kind == NORM_EMBED) {
+        int token = a.tokens[b];
+        if (token < 0 || token >= a.vocab) {
+            token = 0;
+            if (lane == 0) a.tokens[b] = 0;
+        }
+        emb = a.wte + (long long)token * a.C;
+    }
+    auto value = [&](int i) -> float {
+        if (a.kind == NORM_EMBED) return emb[i];
+        if (a.kind == NORM_FINAL) return bf16_to_f32(a.in[row + i]);
+        const float x0 = a.x0[row + i];
+        const float h = a.in ? bf16_to_f32(a.in[row + i]) : x0;
+        return __builtin_fmaf(a.l1, h, x0 * a.l2);
+    };
+    float ss = 0.0f;
+    for (int i = lane; i < a.C; i += WAVE) {
+        const float v = value(i);
+        ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = wave_sum_butterfly(ss);
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)a.C + FLT_EPS);
+    for (int i = lane; i < a.C; i += WAVE) {
+        const float v = value(i);
+        if (a.kind == NORM_EMBED) {
+            a.x0[row + i] = v * r;
+        } else {
+            if (a.kind == NORM_RESID) a.mixed[row + i] = f32_to_bf16(v);
+            a.out[row + i] = f32_to_bf16(v * r);
+        }
+    }
+}
+
+/* o_proj's epilogue and the MLP's rstd (decode.cu:149-154, 445-456): x = s + xm (fp32), xo = bf16(x),
+ * rstd = 1 / sqrt(sum x^2 (1 / C) + FLT_EPSILON). */
+__global__ void __launch_bounds__(256) resid_rstd_kernel(const float *s, const uint16_t *xm, uint16_t *xo, float *rstd,
+                                                         const unsigned long long *active, int rows, int C) {
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & (WAVE - 1);
+    if (b >= rows || (active && !live(active, b))) return;
+    const long long row = (long long)b * C;
+    float ss = 0.0f;
+    for (int i = lane; i < C; i += WAVE) {
+        const float x = s[row + i] + bf16_to_f32(xm[row + i]);
+        xo[row + i] = f32_to_bf16(x);
+        ss = __builtin_fmaf(x, x, ss);
+    }
+    ss = wave_sum_butterfly(ss);
+    if (lane == 0) rstd[b] = 1.0f / __builtin_sqrtf(ss * (1.0f / (float)C) + FLT_EPS);
+}
+
+/* fc's epilogue (decode.cu:144-148): u = bf16(relu(p) p), p = s rstd[row]; four columns a thread. */
+__global__ void __launch_bounds__(256) relu2_kernel(const float *s, const float *rstd, uint16_t *u,
+                                                    const unsigned long long *active, int F) {
+    const int b = blockIdx.y;
+    if (active && !live(active, b)) return;
+    const int j = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (j >= F) return;
+    const long long at = (long long)b * F + j;
+    const float4 v = *reinterpret_cast<const float4 *>(s + at);
+    const float r = rstd[b];
+    const float p[4] = {v.x * r, v.y * r, v.z * r, v.w * r};
+    uint16_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = f32_to_bf16(fmaxf(p[i], 0.0f) * p[i]);
+    *reinterpret_cast<uint2 *>(u + at) = make_uint2((uint32_t)o[0] | (uint32_t)o[1] << 16,
+                                                   (uint32_t)o[2] | (uint32_t)o[3] << 16);
+}
+
+/* ---------------------------------------------------------------- the choice */
+
+/* Philox4x32-10 (Salmon et al., "Parallel random numbers: as easy as 1, 2, 3", SC'11; the Random123 constants):
+ * ten rounds of two 32x32->64 multiplies, the key bumped by the Weyl constants between rounds. */
+__host__ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+    for (int r = 0; r < 10; r++) {
+        if (r) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c[0], p1 = (uint64_t)0xCD9E8D57u * c[2];
+        const uint32_t y0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0, y1 = (uint32_t)p1;
+        const uint32_t y2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1, y3 = (uint32_t)p0;
+        c[0] = y0; c[1] = y1; c[2] = y2; c[3] = y3;
+    }
+}
+
+/* Gumbel noise -log(-log(u)) for row `row` of generated position i under seed (decode.cu:98-105): Philox at counter
+ * (row, i, 0, 0), key (seed low, seed high); the first two words give 52 bits r, u = (2 r + 1) 2^-53 in (0, 1);
+ * the logs in fp64. */
+__device__ __forceinline__ float gumbel(unsigned long long seed, int i, int row) {
+    uint32_t c[4] = {(uint32_t)row, (uint32_t)i, 0u, 0u};
+    philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    const unsigned long long r = ((unsigned long long)c[0] << 32 | c[1]) >> 12;
+    const double u = ldexp(2.0 * (double)r + 1.0, -53);
+    return (float)-log(-log(u));
+}
+
+/* The choice order (decode.cu:90-96): the score's bits mapped to an unsigned order, then ~row, so the largest key
+ * has the largest score and, among equal scores, the lowest row. Key 0 means none. */
+__device__ __forceinline__ unsigned long long choice_key(float score, int row) {
+    const uint32_t bits = __float_as_uint(score);
+    const uint32_t ordered = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+    return ((unsigned long long)ordered << 32) | (0xFFFFFFFFu - (uint32_t)row);
+}
+
+struct ChoiceArgs {
+    const float *logits;       /* [B][vocab] fp32 */
+    float *probs;              /* [B][vocab]: the nucleus path's exp(z / T - max) */
+    const unsigned long long *active;  /* [2][MASK_WORDS]: active slots, then masked slots */
+    const uint32_t *allow;     /* [B][vocab / 32] */
+    const float *temperature, *top_p;
+    const unsigned long long *seed;
+    const int32_t *first;
+    int32_t *tokens, *alt_tokens, *pos;
+    float softcap;
+    int vocab, lazy;
+};
+
+/* Fixed-order block reductions: the wave butterfly, then the waves in order; every thread gets the result. */
+__device__ float block_sum(float v, float *scratch) {
+    v = wave_sum_butterfly(v);
+    __syncthreads();
+    if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int w = 0; w < CHOICE_WAVES; w++) s = s + scratch[w];
+    return s;
+}
+
+__device__ float block_max(float v, float *scratch) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = -INFINITY;
+    for (int w = 0; w < CHOICE_WAVES; w++) m = fmaxf(m, scratch[w]);
+    return m;
+}
+
+__device__ unsigned long long block_max_key(unsigned long long v, unsigned long long *scratch) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        const unsigned long long other = __shfl_xor(v, o, WAVE);
+        v = other > v ? other : v;
+    }
+    __syncthreads();
+    if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    unsigned long long m = 0;
+    for (int w = 0; w < CHOICE_WAVES; w++) m = scratch[w] > m ? scratch[w] : m;
+    return m;
+}
+
+/* A block per slot: its token among the allowed rows of its logits, then the commit (decode.cu:170-229, 361-411,
+ * 677-688). Temperature 0: the largest logit. T > 0: the largest z / T + gumbel, z = c tanh(s / c) (Gumbel-max
+ * sampling of softmax(z / T)). T > 0 and top_p < 1: the nucleus of transformers' TopPLogitsWarper (keep
+ * e >= e*, the least e with C(e) > (1 - top_p) sum e, C(x) the sum of e <= x, e = exp(z / T - max z / T), found by
+ * bisection on e's bits), then Gumbel-max within it. The alternative is the best key but the lazy row's (none for a
+ * nucleus slot). */
+__global__ void __launch_bounds__(CHOICE_THREADS) choose_kernel(ChoiceArgs c) {
+    __shared__ float fscratch[CHOICE_WAVES];
+    __shared__ unsigned long long kscratch[CHOICE_WAVES];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    if (!live(c.active, b)) return;
+    const float *s = c.logits + (long long)b * c.vocab;
+    const float T = c.temperature[b], top_p = c.top_p[b];
+    const bool masked = live(c.active + MASK_WORDS, b);
+    const uint32_t *allow = c.allow + (long long)b * (c.vocab / WORD_BITS);
+    const int gen = c.pos[b] - c.first[b];
+    const unsigned long long seed = c.seed[b];
+    auto allowed = [&](int r) { return !masked || ((allow[r / WORD_BITS] >> (r % WORD_BITS)) & 1u); };
+    auto capped = [&](int r) { return c.softcap * tanhf(s[r] / c.softcap); };
+    unsigned long long best = 0, alt = 0;
+    if (T > 0.0f && top_p < 1.0f) {
+        float *e = c.probs + (long long)b * c.vocab;  /* a thread reads back only the rows it wrote */
+        float m = -INFINITY;
+        for (int r = tid; r < c.vocab; r += CHOICE_THREADS)
+            if (allowed(r)) m = fmaxf(m, capped(r) / T);
+        m = block_max(m, fscratch);
+        float sum = 0.0f;
+        for (int r = tid; r < c.vocab; r += CHOICE_THREADS) {
+            e[r] = allowed(r) ? expf(capped(r) / T - m) : 0.0f;
+            sum = sum + e[r];
+        }
+        const float drop = (1.0f - top_p) * block_sum(sum, fscratch);
+        uint32_t lo = 0u, hi = __float_as_uint(1.0f);
+        while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            const float x = __uint_as_float(mid);
+            float below = 0.0f;
+            for (int r = tid; r < c.vocab; r += CHOICE_THREADS)
+                if (e[r] <= x) below = below + e[r];
+            if (block_sum(below, fscratch) > drop) hi = mid; else lo = mid + 1;
+        }
+        const float least = __uint_as_float(lo);
+        for (int r = tid; r < c.vocab; r += CHOICE_THREADS) {
+            if (e[r] < least || e[r] == 0.0f) continue;
+            const unsigned long long key = choice_key(capped(r) / T + gumbel(seed, gen, r), r);
+            best = key > best ? key : best;
+        }
+    } else {
+        for (int r = tid; r < c.vocab; r += CHOICE_THREADS) {
+            if (!allowed(r)) continue;
+            const float score = T > 0.0f ? capped(r) / T + gumbel(seed, gen, r) : s[r];
+            const unsigned long long key = choice_key(score, r);
+            best = key > best ? key : best;
+            if (r != c.lazy) alt = key > alt ? key : alt;
+        }
+    }
+    best = block_max_key(best, kscratch);
+    alt = block_max_key(alt, kscratch);
+    if (tid == 0) {
+        c.tokens[b] = (int32_t)(0xFFFFFFFFu - (uint32_t)best);   /* key 0 (nothing allowed) gives -1 */
+        c.alt_tokens[b] = (int32_t)(0xFFFFFFFFu - (uint32_t)alt);
+        c.pos[b] += 1;
+    }
+}
+
+/* ---------------------------------------------------------------- small state kernels */
+
+__global__ void set_slot_kernel(int32_t *tokens, int32_t *pos, int32_t *first, float *temperature, float *top_p,
+                                unsigned long long *seeds, int b, int32_t token, int32_t last, float t, float p,
+                                unsigned long long seed) {
+    tokens[b] = token;
+    pos[b] = last;
+    first[b] = last;
+    temperature[b] = t;
+    top_p[b] = p;
+    seeds[b] = seed;
+}
+
+struct SlotMasks {
+    unsigned long long w[2 * MASK_WORDS];
+};
+
+__global__ void set_active_kernel(unsigned long long *active, SlotMasks m) {
+    if (threadIdx.x < 2 * MASK_WORDS) active[threadIdx.x] = m.w[threadIdx.x];
+}
+
+__global__ void take_alt_kernel(int32_t *tokens, const int32_t *alt_tokens, int b) { tokens[b] = alt_tokens[b]; }
+
+/* Copy n positions of every layer and head between two places of the same pools: (page src_page0 + (src_pos + i) / 16,
+ * slot (src_pos + i) % 16) -> likewise at dst; codes keep their tile layout, both scales move. A wave per
+ * (position, layer, head); lane l moves dims l and l + 64 of K and of V. */
+__global__ void __launch_bounds__(256) copy_positions_kernel(uint8_t *k_pages, uint8_t *v_pages, float *kv_scale,
+                                                             long long layer_pages, int H, int L, long long src_page0,
+                                                             int src_pos, long long dst_page0, int dst_pos, int n) {
+    const long long unit = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & (WAVE - 1);
+    if (unit >= (long long)n * L * H) return;
+    const int h = (int)(unit % H), l = (int)(unit / H % L), i = (int)(unit / ((long long)H * L));
+    const int sp = src_pos + i, dp = dst_pos + i;
+    const long long sa = ((long long)l * layer_pages + src_page0 + sp / PAGE) * H + h;
+    const long long da = ((long long)l * layer_pages + dst_page0 + dp / PAGE) * H + h;
+    const int ss = sp % PAGE, ds = dp % PAGE;
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        const int dim = lane + half * HALF;
+        k_pages[da * PAGE_BYTES + k_page_offset(ds, dim)] = k_pages[sa * PAGE_BYTES + k_page_offset(ss, dim)];
+        v_pages[da * PAGE_BYTES + v_page_offset(ds, dim)] = v_pages[sa * PAGE_BYTES + v_page_offset(ss, dim)];
+    }
+    if (lane < 2) kv_scale[(da * 2 + lane) * PAGE + ds] = kv_scale[(sa * 2 + lane) * PAGE + ss];
+}
+
+__global__ void identity_table_kernel(int32_t *table, long long n) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) table[i] = (int32_t)i;
+}
+
+/* ---------------------------------------------------------------- the decoder */
+
+struct Layer {
+    const uint16_t *qkv, *o, *fc, *proj, *ve;  /* bf16 [3C][C], [C][C], [F][C], [C][F]; ve [vocab][C] or NULL */
+    const float *ve_gate, *q_gain, *k_gain;   /* [H][C] or NULL; [128]; [128] */
+    float resid, x0;
+    int window;
+};
+
+/* Per-row activations of a step (slots) or of a prefill call (rows). */
+struct Acts {
+    float *x0;                 /* [rows][C] fp32 */
+    uint16_t *x, *xm, *h, *hn, *qkv, *q, *att, *xo, *u;  /* bf16 [rows][C] (qkv [3C], u [F]) */
+    float *acc;                /* [rows][max(C, F)]: fp32 GEMM outputs */
+    float *rstd;               /* [rows] */
+};
+
+struct Decoder {
+    int B, L, C, F, H, vocab, max_len, store, lazy, max_pages;
+    long long slot_pages, layer_pages;   /* pages of the slots; pages of a layer's pool (slots + store) */
+    float softcap;
+    const float *wte, *cos, *sin;
+    const uint16_t *lm_head;
+    std::vector<Layer> layer;
+    hipStream_t stream;
+    rocblas_handle blas;
+    uint8_t *k_pages, *v_pages;          /* [L][layer_pages][H][2048] */
+    float *kv_scale;                     /* [L][layer_pages][H][2][16] */
+    int32_t *block_table;                /* [B][max_pages], identity */
+    int32_t *tokens, *alt_tokens, *pos, *first, *seq_lens, *num_new;  /* [B] */
+    float *temperature, *top_p;
+    unsigned long long *seed;
+    unsigned long long *active;          /* [2][MASK_WORDS] */
+    uint32_t *allow;                     /* [B][vocab / 32] */
+    float *logits, *probs;               /* [B][vocab] */
+    Acts slot, row;
+    void *workspace;
+    size_t workspace_bytes;
+    int32_t *rows;                       /* device [7][PREFILL_ROWS]: token, position, slot; run row0, count, slot,
+                                            start */
+    int32_t *staging;                    /* pinned host, as rows */
+    hipEvent_t staged;                   /* the last upload of staging has been read */
+    int32_t *host_tokens;                /* pinned [2][B] */
+    uint32_t *host_allow;                /* pinned [B][vocab / 32] */
+    int narrow;                          /* a step's rows: the highest active slot + 1 */
+    std::vector<void *> device_blocks;
+};
+
+static void *device_alloc(Decoder *d, size_t bytes) {
+    void *p = nullptr;
+    if (!bytes) return nullptr;
+    HIP_CHECK(hipMalloc(&p, bytes));
+    HIP_CHECK(hipMemsetAsync(p, 0, bytes, d->stream));
+    d->device_blocks.push_back(p);
+    return p;
+}
+
+static size_t acts_bytes(const Decoder *d, size_t rows) {
+    const size_t C = d->C, F = d->F, W = F > C ? F : C;
+    return rows * (C * 4 + 7 * C * 2 + 3 * C * 2 + F * 2 + W * 4 + 4) + 16 * 256;
+}
+
+static Acts carve_acts(Decoder *d, size_t rows) {
+    const size_t C = d->C, F = d->F, W = F > C ? F : C;
+    unsigned char *p = (unsigned char *)device_alloc(d, acts_bytes(d, rows));
+    auto take = [&](size_t bytes) {
+        void *q = p;
+        p += (bytes + 255) / 256 * 256;
+        return q;
+    };
+    Acts a;
+    a.x0 = (float *)take(rows * C * 4);
+    a.x = (uint16_t *)take(rows * C * 2);
+    a.xm = (uint16_t *)take(rows * C * 2);
+    a.h = (uint16_t *)take(rows * C * 2);
+    a.hn = (uint16_t *)take(rows * C * 2);
+    a.q = (uint16_t *)take(rows * C * 2);
+    a.att = (uint16_t *)take(rows * C * 2);
+    a.xo = (uint16_t *)take(rows * C * 2);
+    a.qkv = (uint16_t *)take(rows * 3 * C * 2);
+    a.u = (uint16_t *)take(rows * F * 2);
+    a.acc = (float *)take(rows * W * 4);
+    a.rstd = (float *)take(rows * 4);
+    return a;
+}
+
+/* out[n][rows] = in[n][cols] . W[rows][cols]^T: column-major rows x n = (W as cols x rows)^T (cols x n). resid
+ * non-NULL: out = bf16(s + resid) by beta = 1 (one rounding of the fp32 sum). */
+static void gemm(Decoder *d, const uint16_t *w, int rows, int cols, const uint16_t *in, int n, void *out, bool f32,
+                 const uint16_t *resid = nullptr) {
+    if (n <= 0) return;
+    const float alpha = 1.0f, beta = resid ? 1.0f : 0.0f;
+    const rocblas_datatype ot = f32 ? rocblas_datatype_f32_r : rocblas_datatype_bf16_r;
+    BLAS_CHECK(rocblas_gemm_ex(d->blas, rocblas_operation_transpose, rocblas_operation_none, rows, n, cols, &alpha, w,
+                               rocblas_datatype_bf16_r, cols, in, rocblas_datatype_bf16_r, cols, &beta,
+                               resid ? (const void *)resid : out, ot, rows, out, ot, rows, rocblas_datatype_f32_r,
+                               rocblas_gemm_algo_standard, 0, 0));
+}
+
+static NormArgs norm_args(Decoder *d, int kind, const Acts &a, int rows, int32_t *tokens,
+                          const unsigned long long *active) {
+    NormArgs n = {};
+    n.kind = kind;
+    n.wte = d->wte;
+    n.x0 = a.x0;
+    n.tokens = tokens;
+    n.vocab = d->vocab;
+    n.active = active;
+    n.rows = rows;
+    n.C = d->C;
+    return n;
+}
+
+static void launch_norm(Decoder *d, const NormArgs &n) {
+    hipLaunchKernelGGL(norm_kernel, dim3((n.rows + 3) / 4), dim3(256), 0, d->stream, n);
+}
+
+static uint8_t *layer_k(Decoder *d, int l) { return d->k_pages + (size_t)l * d->layer_pages * d->H * PAGE_BYTES; }
+static uint8_t *layer_v(Decoder *d, int l) { return d->v_pages + (size_t)l * d->layer_pages * d->H * PAGE_BYTES; }
+static float *layer_s(Decoder *d, int l) { return d->kv_scale + (size_t)l * d->layer_pages * d->H * 2 * PAGE; }
+
+/* The rest of a layer after its attention: o_proj + residual, the MLP. */
+static void mlp(Decoder *d, const Layer &ly, const Acts &a, int n, const unsigned long long *active) {
+    const int C = d->C, F = d->F;
+    gemm(d, ly.o, C, C, a.att, n, a.acc, true);
+    hipLaunchKernelGGL(resid_rstd_kernel, dim3((n + 3) / 4), dim3(256), 0, d->stream, a.acc, a.xm, a.xo, a.rstd,
+                       active, n, C);
+    gemm(d, ly.fc, F, C, a.xo, n, a.acc, true);
+    hipLaunchKernelGGL(relu2_kernel, dim3((F / 4 + 255) / 256, n), dim3(256), 0, d->stream, a.acc, a.rstd, a.u, active,
+                       F);
+    gemm(d, ly.proj, C, F, a.u, n, a.x, false, a.xo);
+}
+
+static void enqueue_body(Decoder *d) {
+    const int R = d->narrow, C = d->C;
+    if (R <= 0) return;
+    const Acts &a = d->slot;
+    NormArgs n = norm_args(d, NORM_EMBED, a, R, d->tokens, d->active);
+    n.pos = d->pos;
+    n.seq_lens = d->seq_lens;
+    n.num_new = d->num_new;
+    launch_norm(d, n);
+    for (int l = 0; l < d->L; l++) {
+        const Layer &ly = d->layer[l];
+        NormArgs r = norm_args(d, NORM_RESID, a, R, d->tokens, d->active);
+        r.in = l == 0 ? nullptr : a.x;
+        r.l1 = ly.resid;
+        r.l2 = ly.x0;
+        r.mixed = a.xm;
+        r.out = a.h;
+        launch_norm(d, r);
+        gemm(d, ly.qkv, 3 * C, C, a.h, R, a.qkv, false);
+        NC_CHECK(append_rows(a.qkv, 3LL * C, R, d->H, d->H, d->pos, d->num_new, nullptr, ly.q_gain, ly.k_gain, d->cos,
+                             d->sin, d->max_len, a.q, d->block_table, d->max_pages, layer_k(d, l), layer_v(d, l),
+                             layer_s(d, l), (int)d->layer_pages, a.h, ly.ve, ly.ve_gate, d->tokens, C, d->stream));
+        NC_CHECK(nc_decode_attn_fp8(a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table, d->max_pages,
+                                    (int)d->layer_pages, d->seq_lens, d->max_len, R, d->H, d->H, ly.window, SM_SCALE, 0,
+                                    a.att, d->workspace, d->workspace_bytes, d->stream));
+        mlp(d, ly, a, R, d->active);
+    }
+}
+
+static void enqueue_head(Decoder *d) {
+    const int R = d->narrow;
+    if (R > 0) {
+        const Acts &a = d->slot;
+        NormArgs n = norm_args(d, NORM_FINAL, a, R, d->tokens, d->active);
+        n.in = a.x;
+        n.out = a.hn;
+        launch_norm(d, n);
+        gemm(d, d->lm_head, d->vocab, d->C, a.hn, R, d->logits, true);
+        ChoiceArgs c = {d->logits, d->probs, d->active, d->allow, d->temperature, d->top_p, d->seed, d->first,
+                        d->tokens, d->alt_tokens, d->pos, d->softcap, d->vocab, d->lazy};
+        hipLaunchKernelGGL(choose_kernel, dim3(R), dim3(CHOICE_THREADS), 0, d->stream, c);
+    }
+    HIP_CHECK(hipMemcpyAsync(d->host_tokens, d->tokens, (size_t)d->B * 4, hipMemcpyDeviceToHost, d->stream));
+    HIP_CHECK(hipMemcpyAsync(d->host_tokens + d->B, d->alt_tokens, (size_t)d->B * 4, hipMemcpyDeviceToHost, d->stream));
+}
+
+static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream,
+                       int max_slots) {
+    Decoder *d = new Decoder();
+    d->L = cfg[0]; d->C = cfg[1]; d->F = cfg[2]; d->vocab = cfg[3]; d->max_len = cfg[4]; d->store = cfg[5];
+    d->lazy = cfg[6];
+    REQUIRE(d->L > 0 && d->C > 0 && d->C % HEAD_DIM == 0, "C must be a positive multiple of 128");
+    REQUIRE(d->F > 0 && d->F % 4 == 0, "F must be a positive multiple of 4");
+    REQUIRE(d->vocab > 0 && d->vocab % WORD_BITS == 0, "vocab must be a positive multiple of 32");
+    REQUIRE(d->max_len > 0 && d->store >= 0, "max_len must be positive, store non-negative");
+    REQUIRE(max_slots > 0 && max_slots <= MAX_BATCH, "slots must be in [1, 1024]");
+    d->H = d->C / HEAD_DIM;
+    d->max_pages = (d->max_len + PAGE - 1) / PAGE;
+    d->wte = (const float *)ptrs[0];
+    d->cos = (const float *)ptrs[1];
+    d->sin = (const float *)ptrs[2];
+    d->lm_head = (const uint16_t *)ptrs[3];
+    REQUIRE(d->wte && d->cos && d->sin && d->lm_head, "null embedding, rotary table or lm_head");
+    d->softcap = scal[2 * d->L];
+    d->stream = (hipStream_t)stream;
+    for (int l = 0; l < d->L; l++) {
+        const uint64_t *p = ptrs + GLOBAL_PTRS + LAYER_PTRS * l;
+        Layer ly = {(const uint16_t *)p[0], (const uint16_t *)p[1], (const uint16_t *)p[2], (const uint16_t *)p[3],
+                    (const uint16_t *)p[4], (const float *)p[5], (const float *)p[6], (const float *)p[7],
+                    scal[2 * l], scal[2 * l + 1], window[l]};
+        REQUIRE(ly.qkv && ly.o && ly.fc && ly.proj && ly.q_gain && ly.k_gain, "null layer weight");
+        REQUIRE(!ly.ve == !ly.ve_gate, "a value-embedding table needs its gate, and the gate its table");
+        d->layer.push_back(ly);
+    }
+    BLAS_CHECK(rocblas_create_handle(&d->blas));
+    BLAS_CHECK(rocblas_set_stream(d->blas, d->stream));
+    BLAS_CHECK(rocblas_set_atomics_mode(d->blas, rocblas_atomics_not_allowed));
+
+    /* fixed blocks first (prefill rows, masks, store pages' share is per layer below), then the slots: B, the most
+     * slots (<= max_slots) whose KV pages, activations and choice buffers fit the free memory less a reserve */
+    const size_t store_pages = ((size_t)d->store + PAGE - 1) / PAGE;
+    const size_t page_set = (size_t)d->H * (2 * PAGE_BYTES + 2 * PAGE * sizeof(float));  /* a page of every head */
+    const size_t per_slot = (size_t)d->L * d->max_pages * page_set + acts_bytes(d, 1) + (size_t)d->vocab * 8 +
+                            (size_t)d->vocab / 8 + (size_t)d->max_pages * 4 + 64 +
+                            (size_t)d->H * (HEAD_DIM + 2) * 4 + (size_t)d->H * 8;
+    d->row = carve_acts(d, PREFILL_ROWS);
+    d->rows = (int32_t *)device_alloc(d, 7 * PREFILL_ROWS * sizeof(int32_t));
+    d->active = (unsigned long long *)device_alloc(d, 2 * MASK_WORDS * sizeof(unsigned long long));
+    size_t free_bytes = 0, total_bytes = 0;
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    HIP_CHECK(hipMemGetInfo(&free_bytes, &total_bytes));
+    const size_t fixed = (size_t)d->L * store_pages * page_set + (size_t)4096 * d->H * (HEAD_DIM + 2) * 4;
+    const size_t reserve = (size_t)2 << 30 > total_bytes / 64 ? (size_t)2 << 30 : total_bytes / 64;
+    REQUIRE(free_bytes > fixed + reserve + per_slot, "no slot fits in free device memory");
+    const size_t fit = (free_bytes - fixed - reserve) / per_slot;
+    d->B = (int)(fit < (size_t)max_slots ? fit : (size_t)max_slots);
+
+    d->slot_pages = (long long)d->B * d->max_pages;
+    d->layer_pages = d->slot_pages + (long long)store_pages;
+    REQUIRE(d->layer_pages < (1LL << 31), "a layer's pool exceeds 2^31 pages");
+    d->k_pages = (uint8_t *)device_alloc(d, (size_t)d->L * d->layer_pages * d->H * PAGE_BYTES);
+    d->v_pages = (uint8_t *)device_alloc(d, (size_t)d->L * d->layer_pages * d->H * PAGE_BYTES);
+    d->kv_scale = (float *)device_alloc(d, (size_t)d->L * d->layer_pages * d->H * 2 * PAGE * sizeof(float));
+    d->block_table = (int32_t *)device_alloc(d, (size_t)d->slot_pages * sizeof(int32_t));
+    hipLaunchKernelGGL(identity_table_kernel, dim3((unsigned)((d->slot_pages + 255) / 256)), dim3(256), 0, d->stream,
+                       d->block_table, d->slot_pages);
+    const size_t B = d->B;
+    int32_t *state = (int32_t *)device_alloc(d, B * 6 * sizeof(int32_t));
+    d->tokens = state; d->alt_tokens = state + B; d->pos = state + 2 * B; d->first = state + 3 * B;
+    d->seq_lens = state + 4 * B; d->num_new = state + 5 * B;
+    d->temperature = (float *)device_alloc(d, B * sizeof(float));
+    d->top_p = (float *)device_alloc(d, B * sizeof(float));
+    d->seed = (unsigned long long *)device_alloc(d, B * sizeof(unsigned long long));
+    d->allow = (uint32_t *)device_alloc(d, B * (d->vocab / WORD_BITS) * sizeof(uint32_t));
+    d->logits = (float *)device_alloc(d, B * d->vocab * sizeof(float));
+    d->probs = (float *)device_alloc(d, B * d->vocab * sizeof(float));
+    d->slot = carve_acts(d, B);
+    d->workspace_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1, 0);
+    REQUIRE(d->workspace_bytes > 0, "decode attention workspace");
+    d->workspace = device_alloc(d, d->workspace_bytes);
+    HIP_CHECK(hipHostMalloc((void **)&d->staging, 7 * PREFILL_ROWS * sizeof(int32_t), hipHostMallocDefault));
+    HIP_CHECK(hipHostMalloc((void **)&d->host_tokens, 2 * B * sizeof(int32_t), hipHostMallocDefault));
+    HIP_CHECK(hipHostMalloc((void **)&d->host_allow, B * (d->vocab / WORD_BITS) * sizeof(uint32_t),
+                            hipHostMallocDefault));
+    memset(d->host_tokens, 0, 2 * B * sizeof(int32_t));
+    memset(d->host_allow, 0, B * (d->vocab / WORD_BITS) * sizeof(uint32_t));
+    HIP_CHECK(hipEventCreateWithFlags(&d->staged, hipEventDisableTiming));
+    HIP_CHECK(hipEventRecord(d->staged, d->stream));
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    d->narrow = 0;
+    return d;
+}
+
+/* Slot b's positions [at, at + n) <-> store positions [store_at, store_at + n), every layer. */
+static void prompt_copy(Decoder *d, int b, int at, int store_at, int n, bool to_store) {
+    if (n <= 0) return;
+    if (b < 0 || b >= d->B || at < 0 || at + n > d->max_len || store_at < 0 || store_at + n > d->store)
+        die("dec_save_prompt/dec_load_prompt", "slot or position range out of bounds", __LINE__);
+    const long long slot_page0 = (long long)b * d->max_pages, store_page0 = d->slot_pages;
+    const long long units = (long long)n * d->L * d->H;
+    hipLaunchKernelGGL(copy_positions_kernel, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, d->stream, d->k_pages,
+                       d->v_pages, d->kv_scale, d->layer_pages, d->H, d->L, to_store ? slot_page0 : store_page0,
+                       to_store ? at : store_at, to_store ? store_page0 : slot_page0, to_store ? store_at : at, n);
+    HIP_CHECK(hipGetLastError());
+}
+
+static void prefill(Decoder *d, int n, const int32_t *rows) {
+    if (n <= 0) return;
+    if (n > PREFILL_ROWS) die("dec_prefill", "more rows than dec_prefill_rows", __LINE__);
+    const int32_t *tok = rows, *pos = rows + n, *slot = rows + 2 * n;
+    for (int r = 0; r < n; r++)
+        if (slot[r] < 0 || slot[r] >= d->B || pos[r] < 0 || pos[r] >= d->max_len || tok[r] < 0 || tok[r] >= d->vocab)
+            die("dec_prefill", "row with a slot, position or token out of range", __LINE__);
+    HIP_CHECK(hipEventSynchronize(d->staged));  /* the previous upload has been read */
+    int32_t *s = d->staging;
+    memcpy(s, tok, n * sizeof(int32_t));
+    memcpy(s + PREFILL_ROWS, pos, n * sizeof(int32_t));
+    memcpy(s + 2 * PREFILL_ROWS, slot, n * sizeof(int32_t));
+    /* runs: maximal stretches of rows of one slot at consecutive positions */
+    int32_t *row0 = s + 3 * PREFILL_ROWS, *count = s + 4 * PREFILL_ROWS, *rslot = s + 5 * PREFILL_ROWS,
+            *start = s + 6 * PREFILL_ROWS;
+    int runs = 0, max_count = 0;
+    for (int r = 0; r < n; r++) {
+        if (r == 0 || slot[r] != slot[r - 1] || pos[r] != pos[r - 1] + 1) {
+            row0[runs] = r;
+            count[runs] = 0;
+            rslot[runs] = slot[r];
+            start[runs] = pos[r];
+            runs++;
+        }
+        count[runs - 1]++;
+        if (count[runs - 1] > max_count) max_count = count[runs - 1];
+    }
+    HIP_CHECK(hipMemcpyAsync(d->rows, s, 7 * PREFILL_ROWS * sizeof(int32_t), hipMemcpyHostToDevice, d->stream));
+    HIP_CHECK(hipEventRecord(d->staged, d->stream));
+    int32_t *dtok = d->rows;
+    const int32_t *dpos = d->rows + PREFILL_ROWS, *dslot = d->rows + 2 * PREFILL_ROWS;
+    const int32_t *drow0 = d->rows + 3 * PREFILL_ROWS, *dcount = d->rows + 4 * PREFILL_ROWS,
+                  *drslot = d->rows + 5 * PREFILL_ROWS, *dstart = d->rows + 6 * PREFILL_ROWS;
+    const int C = d->C;
+    const Acts &a = d->row;
+    launch_norm(d, norm_args(d, NORM_EMBED, a, n, dtok, nullptr));
+    for (int l = 0; l < d->L; l++) {
+        const Layer &ly = d->layer[l];
+        NormArgs r = norm_args(d, NORM_RESID, a, n, dtok, nullptr);
+        r.in = l == 0 ? nullptr : a.x;
+        r.l1 = ly.resid;
+        r.l2 = ly.x0;
+        r.mixed = a.xm;
+        r.out = a.h;
+        launch_norm(d, r);
+        gemm(d, ly.qkv, 3 * C, C, a.h, n, a.qkv, false);
+        NC_CHECK(append_rows(a.qkv, 3LL * C, n, d->H, d->H, dpos, nullptr, dslot, ly.q_gain, ly.k_gain, d->cos, d->sin,
+                             d->max_len, a.q, d->block_table, d->max_pages, layer_k(d, l), layer_v(d, l), layer_s(d, l),
+                             (int)d->layer_pages, a.h, ly.ve, ly.ve_gate, dtok, C, d->stream));
+        if (l == d->L - 1) break;  /* no row chooses a token: the last layer only caches its K and V */
+        NC_CHECK(prefill_runs(a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table, d->max_pages,
+                              (int)d->layer_pages, dstart, drow0, dcount, drslot, runs, max_count, d->H, d->H, ly.window,
+                              SM_SCALE, a.att, d->stream));
+        mlp(d, ly, a, n, nullptr);
+    }
+}
+
+static void destroy(Decoder *d) {
+    hipStreamSynchronize(d->stream);
+    for (void *p : d->device_blocks) hipFree(p);
+    hipHostFree(d->staging);
+    hipHostFree(d->host_tokens);
+    hipHostFree(d->host_allow);
+    hipEventDestroy(d->staged);
+    rocblas_destroy_handle(d->blas);
+    delete d;
+}
+
+}  // namespace dec
+}  // namespace nc
+
+using nc::dec::Decoder;
+
+extern "C" void *dec_create_slots(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window,
+                                  void *stream, int max_slots) {
+    return nc::dec::create(cfg, ptrs, scal, window, stream, max_slots);
+}
+
+extern "C" void *dec_create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream) {
+    return nc::dec::create(cfg, ptrs, scal, window, stream, nc::dec::MAX_BATCH);
+}
+
+extern "C" int dec_batch(void *handle) { return ((Decoder *)handle)->B; }
+
+extern "C" void dec_set_prompt(void *handle, int b, int32_t token, int32_t last, float temperature, float top_p,
+                               unsigned long long seed) {
+    Decoder *d = (Decoder *)handle;
+    if (b < 0 || b >= d->B || token < 0 || token >= d->vocab || last < 0 || last >= d->max_len)
+        nc::dec::die("dec_set_prompt", "slot, token or position out of range", __LINE__);
+    hipLaunchKernelGGL(nc::dec::set_slot_kernel, dim3(1), dim3(1), 0, d->stream, d->tokens, d->pos, d->first,
+                       d->temperature, d->top_p, d->seed, b, token, last, temperature, top_p, seed);
+    HIP_CHECK(hipGetLastError());
+}
+
+extern "C" int dec_prefill_rows(void *) { return nc::dec::PREFILL_ROWS; }
+
+extern "C" void dec_prefill(void *handle, int n, const int32_t *rows) { nc::dec::prefill((Decoder *)handle, n, rows); }
+
+extern "C" void dec_save_prompt(void *handle, int b, int at, int store_at, int n) {
+    nc::dec::prompt_copy((Decoder *)handle, b, at, store_at, n, true);
+}
+
+extern "C" void dec_load_prompt(void *handle, int b, int at, int store_at, int n) {
+    nc::dec::prompt_copy((Decoder *)handle, b, at, store_at, n, false);
+}
+
+extern "C" uint32_t *dec_masks(void *handle) { return ((Decoder *)handle)->host_allow; }
+
+extern "C" void dec_set_active(void *handle, const unsigned long long *slots) {
+    using namespace nc::dec;
+    Decoder *d = (Decoder *)handle;
+    const int words = (d->B + MASK_BITS - 1) / MASK_BITS;
+    SlotMasks m = {};
+    int high = -1, lo = -1, hi = -1;
+    for (int w = 0; w < words; w++) {
+        m.w[w] = slots[w];
+        m.w[MASK_WORDS + w] = slots[words + w];
+        if (slots[w]) high = w * MASK_BITS + MASK_BITS - 1 - __builtin_clzll(slots[w]);
+        if (slots[words + w]) {
+            if (lo < 0) lo = w * MASK_BITS + __builtin_ctzll(slots[words + w]);
+            hi = w * MASK_BITS + MASK_BITS - 1 - __builtin_clzll(slots[words + w]);
+        }
+    }
+    if (high >= d->B) die("dec_set_active", "active slot beyond dec_batch", __LINE__);
+    if (hi >= d->B) die("dec_set_active", "masked slot beyond dec_batch", __LINE__);
+    hipLaunchKernelGGL(set_active_kernel, dim3(1), dim3(64), 0, d->stream, d->active, m);
+    HIP_CHECK(hipGetLastError());
+    d->narrow = high + 1;
+    if (lo >= 0) {
+        const size_t n = d->vocab / WORD_BITS;
+        HIP_CHECK(hipMemcpyAsync(d->allow + lo * n, d->host_allow + lo * n, (hi + 1 - lo) * n * sizeof(uint32_t),
+                                 hipMemcpyHostToDevice, d->stream));
+    }
+}
+
+extern "C" void dec_launch_body(void *handle) {
+    nc::dec::enqueue_body((Decoder *)handle);
+    HIP_CHECK(hipGetLastError());
+}
+
+extern "C" void dec_launch_head(void *handle) {
+    nc::dec::enqueue_head((Decoder *)handle);
+    HIP_CHECK(hipGetLastError());
+}
+
+extern "C" void dec_tokens(void *handle, int32_t *out) {
+    Decoder *d = (Decoder *)handle;
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    memcpy(out, d->host_tokens, 2 * (size_t)d->B * sizeof(int32_t));
+}
+
+extern "C" void dec_take_alt(void *handle, int b) {
+    Decoder *d = (Decoder *)handle;
+    if (b < 0 || b >= d->B) nc::dec::die("dec_take_alt", "slot out of range", __LINE__);
+    hipLaunchKernelGGL(nc::dec::take_alt_kernel, dim3(1), dim3(1), 0, d->stream, d->tokens, d->alt_tokens, b);
+    HIP_CHECK(hipGetLastError());
+}
+
+extern "C" void dec_destroy(void *handle) { nc::dec::destroy((Decoder *)handle); }
+
+extern "C" void dec_debug_logits(void *handle, float *out, int rows) {
+    Decoder *d = (Decoder *)handle;
+    if (rows < 0 || rows > d->B) nc::dec::die("dec_debug_logits", "rows out of range", __LINE__);
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    HIP_CHECK(hipMemcpy(out, d->logits, (size_t)rows * d->vocab * sizeof(float), hipMemcpyDeviceToHost));
+}
+
+extern "C" void dec_debug_cache(void *handle, int layer, int b, int at, int n, uint8_t *k, uint8_t *v, float *scales) {
+    using namespace nc;
+    Decoder *d = (Decoder *)handle;
+    const int limit = b < 0 ? d->store : d->max_len;
+    if (layer < 0 || layer >= d->L || b >= d->B || at < 0 || n < 0 || at + n > limit)
+        dec::die("dec_debug_cache", "layer, slot or position range out of bounds", __LINE__);
+    if (n == 0) return;
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    const long long page0 = b < 0 ? d->slot_pages : (long long)b * d->max_pages;
+    const int first = at / PAGE, last = (at + n - 1) / PAGE, pages = last - first + 1, H = d->H;
+    std::vector<uint8_t> kp((size_t)pages * H * PAGE_BYTES), vp(kp.size());
+    std::vector<float> sp((size_t)pages * H * 2 * PAGE);
+    const size_t base = (size_t)(d->layer_pages * layer + page0 + first) * H;
+    HIP_CHECK(hipMemcpy(kp.data(), d->k_pages + base * PAGE_BYTES, kp.size(), hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(vp.data(), d->v_pages + base * PAGE_BYTES, vp.size(), hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(sp.data(), d->kv_scale + base * 2 * PAGE, sp.size() * sizeof(float), hipMemcpyDeviceToHost));
+    for (int i = 0; i < n; i++) {
+        const int p = at + i, pg = p / PAGE - first, slot = p % PAGE;
+        for (int h = 0; h < H; h++) {
+            const size_t unit = (size_t)pg * H + h;
+            for (int dim = 0; dim < HEAD_DIM; dim++) {
+                k[((size_t)i * H + h) * HEAD_DIM + dim] = kp[unit * PAGE_BYTES + k_page_offset(slot, dim)];
+                v[((size_t)i * H + h) * HEAD_DIM + dim] = vp[unit * PAGE_BYTES + v_page_offset(slot, dim)];
+            }
+            scales[((size_t)i * H + h) * 2] = sp[(unit * 2) * PAGE + slot];
+            scales[((size_t)i * H + h) * 2 + 1] = sp[(unit * 2 + 1) * PAGE + slot];
+        }
+    }
+}

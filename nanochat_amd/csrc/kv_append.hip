@@ -11,6 +11,7 @@
  */
 #include "nc_device.h"
 #include "nanochat_amd.h"
+#include "nc_internal.h"
 
 namespace nc {
 
@@ -52,6 +53,12 @@ struct AppendArgs {
     int rope_len;
     uint16_t *q_out;           /* [B][T][Hq][128] */
     const int32_t *block_table;
+    const int32_t *seq_slot;   /* NULL, or sequence b's block-table row (the decoder's prefill rows) */
+    /* value embeddings (fused append, NULL ve: none): v += 2 sigmoid(ve_gate[head] . h) ve[tokens[token]] */
+    const uint16_t *ve_h, *ve;  /* h: [B T][C] the layer's normed input; ve: [vocab][C] */
+    const float *ve_gate;       /* [Hkv][C] */
+    const int32_t *ve_tokens;   /* [B T] */
+    int C;
     int max_pages;
     uint8_t *k_pages, *v_pages;
     float *kv_scale;          /* [num_pages][Hkv][2][16]: K scales, then V scales */
@@ -91,7 +98,8 @@ __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
     const int kvh = FUSED ? row - a.Hq : row;
     const int lp = p / PAGE;
     if (lp >= a.max_pages) return;
-    const int page = a.block_table[(long long)b * a.max_pages + lp];
+    const int trow = a.seq_slot ? a.seq_slot[b] : b;
+    const int page = a.block_table[(long long)trow * a.max_pages + lp];
     if (page < 0 || page >= a.num_pages) return;
     const int slot = p % PAGE;
     const long long at = (long long)page * a.Hkv + kvh;
@@ -105,8 +113,22 @@ __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
         k2 = bf16_to_f32(f32_to_bf16(y2));
     }
     quantize_store<k_page_offset>(k1, k2, a.k_pages + at * PAGE_BYTES, a.kv_scale + at * 2 * PAGE + slot, slot, lane);
-    quantize_store<v_page_offset>(bf16_to_f32(vx[lane]), bf16_to_f32(vx[lane + HALF]), a.v_pages + at * PAGE_BYTES,
-                                  a.kv_scale + (at * 2 + 1) * PAGE + slot, slot, lane);
+    float v1 = bf16_to_f32(vx[lane]), v2 = bf16_to_f32(vx[lane + HALF]);
+    if (FUSED && a.ve) {
+        /* reference decode.cu:481-494: g = 2 sigmoid(ve_gate[head] . h) (lane-strided FMAs, then the butterfly),
+         * v = bf16(v + g ve[token]) */
+        const uint16_t *h = a.ve_h + tok * a.C;
+        const float *w = a.ve_gate + (long long)kvh * a.C;
+        float d = 0.0f;
+        for (int i = lane; i < a.C; i += WAVE) d = __builtin_fmaf(bf16_to_f32(h[i]), w[i], d);
+        d = wave_sum_butterfly(d);
+        const float g = 2.0f * (1.0f / (1.0f + expf(-d)));
+        const uint16_t *e = a.ve + (long long)a.ve_tokens[tok] * a.C + kvh * HEAD_DIM;
+        v1 = bf16_to_f32(f32_to_bf16(v1 + g * bf16_to_f32(e[lane])));
+        v2 = bf16_to_f32(f32_to_bf16(v2 + g * bf16_to_f32(e[lane + HALF])));
+    }
+    quantize_store<v_page_offset>(v1, v2, a.v_pages + at * PAGE_BYTES, a.kv_scale + (at * 2 + 1) * PAGE + slot, slot,
+                                  lane);
 }
 
 /* The training-form prologue (reference model/kernels/qk_prologue.cu:8-32): token p = blockIdx.x of rows/H,
@@ -141,6 +163,29 @@ static int launch_append(const AppendArgs &a, bool fused, hipStream_t stream) {
     else
         hipLaunchKernelGGL(append_kernel<false>, grid, dim3(256), 0, stream, a);
     return (int)hipGetLastError();
+}
+
+/* The fused append for the decoder runtime: as nc_qk_norm_rope_append_fp8 with T = 1, sequence b (a slot or a
+ * prefill row) at position pos[b], using block-table row seq_slot[b] (NULL: b) and skipping b when
+ * num_new[b] == 0 (NULL: none skipped); with ve non-NULL, v gets the layer's value embedding. Arguments are
+ * checked by the caller. */
+int append_rows(const uint16_t *qkv, long long token_stride, int n, int Hq, int Hkv, const int32_t *pos,
+                const int32_t *num_new, const int32_t *seq_slot, const float *q_gain, const float *k_gain,
+                const float *cos, const float *sin, int rope_len, uint16_t *q_out, const int32_t *block_table,
+                int max_pages, uint8_t *k_pages, uint8_t *v_pages, float *kv_scale, int num_pages,
+                const uint16_t *ve_h, const uint16_t *ve, const float *ve_gate, const int32_t *tokens, int C,
+                hipStream_t stream) {
+    AppendArgs a = {};
+    a.qkv = qkv;
+    a.token_stride = token_stride;
+    a.B = n; a.T = 1; a.Hq = Hq; a.Hkv = Hkv;
+    a.start_pos = pos; a.num_new = num_new; a.seq_slot = seq_slot;
+    a.q_gain = q_gain; a.k_gain = k_gain; a.cos = cos; a.sin = sin; a.rope_len = rope_len;
+    a.q_out = q_out;
+    a.block_table = block_table; a.max_pages = max_pages;
+    a.k_pages = k_pages; a.v_pages = v_pages; a.kv_scale = kv_scale; a.num_pages = num_pages;
+    a.ve_h = ve_h; a.ve = ve; a.ve_gate = ve_gate; a.ve_tokens = tokens; a.C = C;
+    return launch_append(a, true, stream);
 }
 
 }  // namespace nc

@@ -67,13 +67,13 @@ __device__ __forceinline__ float wave_max(float v) {
 
 /* Byte offset of (slot, dim) inside a K page: the 16x16x32 MFMA A-operand tiling (lane = group*16 + slot
  * holds dims group*32 + h*16 .. +15 at h*1024 + lane*16). */
-__device__ __forceinline__ int k_page_offset(int slot, int dim) {
+__host__ __device__ __forceinline__ int k_page_offset(int slot, int dim) {
     return ((dim & 31) >> 4) * 1024 + (((dim >> 5) << 4) + slot) * 16 + (dim & 15);
 }
 
 /* Byte offset of (slot, dim) inside a V page: the transposed A-operand tiling of the PV MFMA (lane =
  * (slot/4)*16 + dim%16 holds, for tiles t = 4h..4h+3, the 4 slots of its group at dim 16t + dim%16). */
-__device__ __forceinline__ int v_page_offset(int slot, int dim) {
+__host__ __device__ __forceinline__ int v_page_offset(int slot, int dim) {
     const int t = dim >> 4;
     return (t >> 2) * 1024 + (((slot >> 2) << 4) + (dim & 15)) * 16 + (t & 3) * 4 + (slot & 3);
 }

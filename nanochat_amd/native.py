@@ -1,9 +1,14 @@
-"""The HIP library of the fp8 KV path: its hipcc build for gfx950 and its ctypes binding.
+"""The HIP libraries of the fp8 KV path: their hipcc build for gfx950 and their ctypes bindings.
 
 Mirrors the reference's loader (native.py:43-65: `pointer`, `stream`, `cuda_library`) with one
-difference in build policy: the library is compiled ahead of time into the package
-(`nanochat_amd/lib/libnanochat_kv.so`, by `build()` or `python -m nanochat_amd.native`) and only
-loaded at run time, so a GPU host never compiles. Loading a missing library builds it once.
+difference in build policy: the libraries are compiled ahead of time into the package (by `build()` or
+`python -m nanochat_amd.native`) and only loaded at run time, so a GPU host never compiles. Loading a
+missing library builds both once.
+
+    libnanochat_kv.so      the kernel entry points of include/nanochat_amd.h
+    libnanochat_decode.so  the decoder runtime of include/nanochat_decode.h (the same kernels, plus the
+                           dec_* runtime and rocBLAS GEMMs); hip_library("decode") loads it, as the
+                           reference's cuda_library("decode") loads decode.cu
 """
 
 import ctypes
@@ -19,14 +24,17 @@ CSRC = PACKAGE / "csrc"
 INCLUDE = PACKAGE.parent / "include"
 LIB_DIR = PACKAGE / "lib"
 LIBRARY = LIB_DIR / "libnanochat_kv.so"
-SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip"]
-HEADERS = [CSRC / "nc_device.h", INCLUDE / "nanochat_amd.h"]
+DECODE_LIBRARY = LIB_DIR / "libnanochat_decode.so"
+KERNEL_SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip"]
+DECODE_SOURCES = [CSRC / "decoder.hip"]
+SOURCES = KERNEL_SOURCES + DECODE_SOURCES
+HEADERS = [CSRC / "nc_device.h", CSRC / "nc_internal.h", INCLUDE / "nanochat_amd.h", INCLUDE / "nanochat_decode.h"]
 HEAD_DIM = 128
 
 # -ffp-contract=off: the append's fp32 order is part of its bit-exact contract (no implicit FMAs).
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in any kernel.
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-DHEAD_DIM={HEAD_DIM}", f"-I{INCLUDE}",
 ]
 
@@ -36,17 +44,29 @@ def hipcc() -> str:
     return str(Path(rocm) / "bin" / "hipcc")
 
 
-def build(output: Path = LIBRARY) -> Path:
-    """Compile every kernel source into one shared library (written to a temporary file, then renamed)."""
-    output.parent.mkdir(parents=True, exist_ok=True)
-    with tempfile.TemporaryDirectory(dir=output.parent) as tmp:
-        built = Path(tmp) / output.name
-        cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(built), *map(str, SOURCES)]
-        result = subprocess.run(cmd, capture_output=True, text=True)
-        if result.returncode != 0:
-            raise RuntimeError(f"hipcc failed ({result.returncode}):\n{' '.join(cmd)}\n{result.stderr}")
-        built.replace(output)
-    return output
+def _run(cmd: list[str]) -> None:
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({result.returncode}):\n{' '.join(cmd)}\n{result.stderr}")
+
+
+def build() -> tuple[Path, Path]:
+    """Compile every source once, then link both libraries (each written to a temporary file, then renamed)."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    rocm_lib = Path(hipcc()).parent.parent / "lib"
+    with tempfile.TemporaryDirectory(dir=LIB_DIR) as tmp:
+        objects = {}
+        for src in SOURCES:
+            objects[src] = Path(tmp) / (src.stem + ".o")
+            _run([hipcc(), *HIPCC_FLAGS, "-c", "-o", str(objects[src]), str(src)])
+        for output, sources, libs in ((LIBRARY, KERNEL_SOURCES, []),
+                                      (DECODE_LIBRARY, KERNEL_SOURCES + DECODE_SOURCES,
+                                       [f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lrocblas"])):
+            built = Path(tmp) / output.name
+            _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(built),
+                  *(str(objects[s]) for s in sources), *libs])
+            built.replace(output)
+    return LIBRARY, DECODE_LIBRARY
 
 
 c_void_p, c_int, c_longlong, c_float, c_size_t = (ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float,
@@ -71,15 +91,41 @@ SIGNATURES = {
 }
 
 
+# argtypes of every entry point of include/nanochat_decode.h (the reference's binding: decoder.py:132-148)
+DECODE_SIGNATURES = {
+    "dec_create": ([c_void_p] * 5, c_void_p),
+    "dec_create_slots": ([c_void_p] * 5 + [c_int], c_void_p),
+    "dec_batch": ([c_void_p], c_int),
+    "dec_set_prompt": ([c_void_p, c_int, ctypes.c_int32, ctypes.c_int32, c_float, c_float, ctypes.c_ulonglong], None),
+    "dec_prefill_rows": ([c_void_p], c_int),
+    "dec_prefill": ([c_void_p, c_int, c_void_p], None),
+    "dec_save_prompt": ([c_void_p, c_int, c_int, c_int, c_int], None),
+    "dec_load_prompt": ([c_void_p, c_int, c_int, c_int, c_int], None),
+    "dec_masks": ([c_void_p], ctypes.POINTER(ctypes.c_uint32)),
+    "dec_set_active": ([c_void_p, c_void_p], None),
+    "dec_launch_body": ([c_void_p], None),
+    "dec_launch_head": ([c_void_p], None),
+    "dec_tokens": ([c_void_p, c_void_p], None),
+    "dec_take_alt": ([c_void_p, c_int], None),
+    "dec_destroy": ([c_void_p], None),
+    "dec_debug_logits": ([c_void_p, c_void_p, c_int], None),
+    "dec_debug_cache": ([c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p], None),
+}
+
+LIBRARIES = {"nanochat_kv": (LIBRARY, SIGNATURES), "decode": (DECODE_LIBRARY, DECODE_SIGNATURES)}
+
+
 @functools.cache
 def hip_library(name: str = "nanochat_kv") -> ctypes.CDLL:
-    """The prebuilt library (built here first if absent), with every entry point's argtypes set; once per process."""
-    if name != "nanochat_kv":
-        raise ValueError(f"unknown library {name!r}: the fp8 KV path ships one library, 'nanochat_kv'")
-    if not LIBRARY.exists():
+    """A prebuilt library (both built here first if absent) with every entry point's argtypes set; once per process.
+    "nanochat_kv": the kernel entry points; "decode": the dec_* decoder runtime."""
+    if name not in LIBRARIES:
+        raise ValueError(f"unknown library {name!r}: expected one of {sorted(LIBRARIES)}")
+    path, signatures = LIBRARIES[name]
+    if not path.exists():
         build()
-    lib = ctypes.CDLL(str(LIBRARY))
-    for symbol, (argtypes, restype) in SIGNATURES.items():
+    lib = ctypes.CDLL(str(path))
+    for symbol, (argtypes, restype) in signatures.items():
         fn = getattr(lib, symbol)
         fn.argtypes = argtypes
         fn.restype = restype

@@ -11,12 +11,16 @@ Decode (configs 1-3 and the derived headline 3u), order of draws:
   4. paged only: randperm of B * max_pages pages, assigned in order (max_pages = pages of ctx + 1)
 Chunked prefill (config 4), order of draws: qkv [B, T, (Hq + 2 Hkv) * 128], k_cache, v_cache
 [B, ctx, Hkv, 128], q_gain and k_gain = 1 + 0.1 * randn(128), then the block-table permutation.
+End-to-end decoding (config 5), random-init weights (model_tensors), order of draws: wte [vocab, C] (fp32),
+lm_head [vocab, C]; per layer qkv [3C, C], o [C, C], fc [F, C], proj [C, F], q_norm and k_norm = 1 + 0.1 randn(128),
+then on value-embedding layers ve [vocab, C] and ve_gate [H, C]; every matrix std * randn (bf16 but wte and ve_gate);
+then the prompts (prompt_tokens): randint(1, vocab, (B, prompt)) with BOS (0) first.
 """
 from dataclasses import dataclass
 
 import torch
 
-from .config import HEAD_DIM
+from .config import HEAD_DIM, ROPE_THETA
 from .kv_cache import pages_for
 
 
@@ -110,3 +114,72 @@ def prefill_inputs(w: PrefillWorkload, seed: int = 0) -> dict:
         table = torch.arange(B * max_pages, dtype=torch.int32).view(B, max_pages)
     return dict(qkv=qkv, k_cache=k_cache, v_cache=v_cache, q_gain=q_gain, k_gain=k_gain, block_table=table,
                 num_pages=B * max_pages, start_pos=torch.full((B,), w.ctx, dtype=torch.int32))
+
+
+@dataclass(frozen=True)
+class ModelWorkload:
+    name: str
+    layers: int
+    hidden: int
+    ffn: int
+    vocab: int
+    batch: int             # slots decoding together
+    prompt: int            # tokens of each prompt, BOS included (all but the last are prefilled)
+    steps: int             # greedy decode steps (tokens generated per slot)
+    std: float = 0.02      # weight init N(0, std)
+    theta: float = ROPE_THETA
+    softcap: float = 15.0
+    description: str = ""
+
+    @property
+    def max_length(self) -> int:
+        """Cache positions a slot needs: the prompt but its last token, then one per step."""
+        return self.prompt - 1 + self.steps
+
+
+MODELS = {
+    "c5": ModelWorkload("c5", 26, 1664, 4 * 1664, 65536, 128, 2048, 512,
+                        description="end-to-end greedy decode: 26 layers, d1664, 13 heads, vocab 65536, B=128, "
+                                    "2048-token prompts, 512 steps"),
+}
+
+
+def model_tensors(layers: int, hidden: int, ffn: int, vocab: int, max_length: int, *, seed: int = 0,
+                  std: float = 0.02, theta: float = ROPE_THETA, softcap: float = 15.0, ve_layers=(), windows=None,
+                  resid_lambda: float = 1.0, x0_lambda: float = 0.1, device=None, generator_device="cpu"):
+    """Random-init decoder inputs (a decoder.ModelTensors on `device`), drawn in the order the module docstring
+    lists from a generator on generator_device ("cpu": the bytes a CPU oracle can redraw; a GPU generator draws
+    the large models fast). windows: keys before a query per layer (None: max_length, full attention)."""
+    from .decoder import LayerTensors, ModelTensors
+    from .rotary import rotary_tables
+
+    gen = torch.Generator(device=generator_device).manual_seed(seed)
+
+    def draw(*shape, dtype=torch.bfloat16, scale=std):
+        x = torch.randn(*shape, generator=gen, device=generator_device, dtype=torch.float32) * scale
+        return x.to(dtype).to(device).contiguous()
+
+    C, H = hidden, hidden // HEAD_DIM
+    wte = draw(vocab, C, dtype=torch.float32)
+    lm_head = draw(vocab, C)
+    lys = []
+    for i in range(layers):
+        ly = LayerTensors(qkv=draw(3 * C, C), o=draw(C, C), fc=draw(ffn, C), proj=draw(C, ffn),
+                          q_norm=(1.0 + draw(HEAD_DIM, dtype=torch.float32, scale=0.1)),
+                          k_norm=(1.0 + draw(HEAD_DIM, dtype=torch.float32, scale=0.1)))
+        if i in ve_layers:
+            ly.ve = draw(vocab, C)
+            ly.ve_gate = draw(H, C, dtype=torch.float32)
+        lys.append(ly)
+    cos, sin = rotary_tables(max_length, theta, device)
+    return ModelTensors(wte=wte, cos=cos, sin=sin, lm_head=lm_head, layers=lys,
+                        resid_lambdas=[resid_lambda] * layers, x0_lambdas=[x0_lambda] * layers,
+                        windows=list(windows) if windows is not None else [max_length] * layers, softcap=softcap)
+
+
+def prompt_tokens(batch: int, prompt: int, vocab: int, seed: int = 0, bos: int = 0) -> torch.Tensor:
+    """Random prompts [batch, prompt] int64: BOS, then tokens in [1, vocab)."""
+    gen = torch.Generator().manual_seed(seed)
+    ids = torch.randint(1, vocab, (batch, prompt), generator=gen)
+    ids[:, 0] = bos
+    return ids

@@ -91,3 +91,55 @@ def test_qkp_forward_reports_errors(lib):
     assert lib.nc_last_error() == -1
     lib.qkp_forward(*([DUMMY] * 8), 7, 6, 1, None)
     assert lib.nc_last_error() == -2
+
+
+DECODE_HEADER = HEADER.parent / "nanochat_decode.h"
+
+# the reference's decoder ABI (decode.cu:904-1131): every symbol inference/decoder.py binds
+REFERENCE_DEC = {"dec_create", "dec_batch", "dec_set_prompt", "dec_prefill_rows", "dec_prefill", "dec_save_prompt",
+                 "dec_load_prompt", "dec_masks", "dec_set_active", "dec_launch_body", "dec_launch_head", "dec_tokens",
+                 "dec_take_alt", "dec_destroy"}
+
+
+def decode_declared():
+    text = re.sub(r"/\*.*?\*/", "", DECODE_HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b([A-Za-z_]\w*)\s*\([^;{]*\)\s*;", text))
+
+
+def test_decode_header_covers_the_reference_abi():
+    from nanochat_amd.native import DECODE_SIGNATURES
+
+    assert REFERENCE_DEC <= decode_declared()
+    assert decode_declared() == set(DECODE_SIGNATURES)
+
+
+def test_decode_library_exports_every_declared_symbol():
+    from nanochat_amd.native import DECODE_LIBRARY, hip_library
+
+    if not DECODE_LIBRARY.exists():
+        pytest.fail(f"{DECODE_LIBRARY} is not built: run python -m nanochat_amd.native")
+    dec = hip_library("decode")
+    for name in decode_declared():
+        assert hasattr(dec, name), name
+    # the kernel entry points ride along in the decoder library
+    for name in declared():
+        assert hasattr(dec, name), name
+    assert dec.dec_prefill_rows(None) == 8192
+
+
+def test_decode_argtypes_match_the_reference_binding():
+    """decoder.py:132-148's argtypes for the 14 symbols, restated as ctypes types."""
+    from nanochat_amd.native import DECODE_SIGNATURES
+
+    P, I = ctypes.c_void_p, ctypes.c_int
+    expected = {
+        "dec_create": [P] * 5, "dec_batch": [P],
+        "dec_set_prompt": [P, I, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, ctypes.c_float, ctypes.c_ulonglong],
+        "dec_prefill_rows": [P], "dec_prefill": [P, I, P], "dec_save_prompt": [P, I, I, I, I],
+        "dec_load_prompt": [P, I, I, I, I], "dec_masks": [P], "dec_set_active": [P, P], "dec_launch_body": [P],
+        "dec_launch_head": [P], "dec_destroy": [P], "dec_tokens": [P, P], "dec_take_alt": [P, I],
+    }
+    for name, argtypes in expected.items():
+        assert DECODE_SIGNATURES[name][0] == argtypes, name
+    assert DECODE_SIGNATURES["dec_create"][1] is P
+    assert DECODE_SIGNATURES["dec_masks"][1] == ctypes.POINTER(ctypes.c_uint32)

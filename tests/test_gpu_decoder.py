@@ -1,0 +1,286 @@
+"""The decoder runtime (libnanochat_decode.so through the dec_* ABI) against the CPU oracle: prefill caches, step
+logits, the choice (greedy, masks, alternative, Gumbel-max, nucleus), the prompt store, inactive slots and
+continuous batching. Logits are compared teacher-forced: each step's inputs are the tokens the device chose."""
+import numpy as np
+import pytest
+import torch
+
+from nanochat_amd.decoder import PagedDecoder, Request
+from nanochat_amd.workloads import model_tensors
+from oracle import model as om
+from oracle import sampling
+
+pytestmark = pytest.mark.gpu
+
+# tiny: 3 layers (a 40-key window on layer 0, value embeddings on layers 0 and 2); wide: the config-5 width
+SHAPES = {
+    "tiny": dict(layers=3, hidden=256, ffn=1024, vocab=2048, max_length=160, windows=[40, 160, 160], ve_layers=(0, 2)),
+    "wide": dict(layers=2, hidden=1664, ffn=6656, vocab=4096, max_length=96, windows=[96, 96], ve_layers=()),
+}
+# logits against the float64 oracle on the same inputs, relative to the largest |logit|: fp32 GEMM accumulation
+# flips bf16 roundings of intermediate activations and fp8 codes downstream (fp32 GEMMs alone move the oracle's
+# own logits by ~0.6% max, ~0.08% mean of that scale); the device's attention adds bf16 probabilities in PV
+LOGIT_MAX_REL = 2e-2
+LOGIT_MEAN_REL = 3e-3
+# a choice may differ from the oracle's only between scores this close (relative)
+NEAR_TIE = 1e-5
+
+
+def build(device, shape, seed=0):
+    s = dict(SHAPES[shape])
+    max_length = s.pop("max_length")
+    m = model_tensors(s["layers"], s["hidden"], s["ffn"], s["vocab"], max_length, seed=seed, std=0.05,
+                      theta=10000.0, ve_layers=s["ve_layers"], windows=s["windows"], device=device)
+    return m, om.weights_from_tensors(m), max_length
+
+
+def prompts(lengths, vocab, seed):
+    rng = np.random.default_rng(seed)
+    return [[0] + list(rng.integers(1, vocab, n - 1)) for n in lengths]
+
+
+def check_logits(got, want, label):
+    """Returns the absolute max-error bound used, for near-argmax checks."""
+    err = np.abs(got.astype(np.float64) - want)
+    scale = np.abs(want).max()
+    print(f"{label}: logits max abs {err.max():.3e} mean abs {err.mean():.3e} (scale {scale:.2f})", flush=True)
+    assert err.max() <= LOGIT_MAX_REL * scale and err.mean() <= LOGIT_MEAN_REL * scale, label
+    return LOGIT_MAX_REL * scale
+
+
+def check_cache(dec, orc, layer, b, n, label):
+    """Layer 0's rows come from exact inputs: codes equal but for rare neighbours (an fp32-accumulated GEMM output
+    rounding to the other bf16). Deeper layers inherit the accumulated rounding noise of the layers before (fp32
+    GEMMs alone move the oracle's own deeper-layer values by ~1% RMS), so they are compared as values."""
+    from oracle.quant import dequantize_rows
+
+    k, v, s = dec.cache_rows(layer, b, 0, n)
+    c = orc.codes[b]
+    for name, got, want, i in (("k", k, c["k"][layer, :n], 0), ("v", v, c["v"][layer, :n], 1)):
+        x = dequantize_rows(got, s[..., i]).astype(np.float64)
+        y = dequantize_rows(want, c["scale"][layer, :n, :, i]).astype(np.float64)
+        if layer == 0:
+            same = np.mean(got == want)
+            assert same >= 0.995, f"{label} {name}: {same:.4f} of the codes equal"
+            # a differing value is within one e4m3 step of the oracle's plus a bf16 ulp of the row's absmax
+            # (448 scale): an element that is a near-cancellation of row-sized terms moves by the latter
+            step = np.maximum(np.abs(x), np.abs(y)) * 2 ** -3 + 448 * s[..., i, None] * 2 ** -7
+            far = np.argwhere(np.abs(x - y) > step)
+            detail = [(tuple(f), int(got[tuple(f)]), int(want[tuple(f)]), float(x[tuple(f)]), float(y[tuple(f)]),
+                       float(s[f[0], f[1], i]), float(c["scale"][layer, f[0], f[1], i])) for f in far[:8]]
+            assert len(far) == 0, f"{label} {name}: {len(far)} far codes (pos, head, dim), got, want: {detail}"
+            rel = np.abs(s[..., i] - c["scale"][layer, :n, :, i]) / np.maximum(c["scale"][layer, :n, :, i], 1e-30)
+            assert rel.max() <= 2 ** -7, f"{label} {name} scales: {rel.max():.3e}"
+        rms = np.sqrt(np.mean((x - y) ** 2) / np.mean(y ** 2))
+        worst = np.abs(x - y).max() / np.abs(y).max()
+        print(f"{label} {name}: rel rms {rms:.2e} rel max {worst:.2e}", flush=True)
+        assert rms <= 0.04 and worst <= 0.2, f"{label} {name}: rel rms {rms:.3e}, rel max {worst:.3e}"
+
+
+def run_steps(dec, orc, inputs, positions, slots, steps, label, temperature=None):
+    """Greedy steps over `slots` (all active), checking logits, choice and alternative; returns the new inputs."""
+    inputs, positions = list(inputs), list(positions)
+    rows = max(slots) + 1
+    for step in range(steps):
+        tokens = dec.step()
+        got = dec.logits(rows)
+        want = orc.head(orc.body(inputs, positions, slots))
+        bound = check_logits(got[slots], want, f"{label} step {step}")
+        for i, b in enumerate(slots):
+            tok, alt = sampling.choose(got[b], lazy=dec.bos)
+            assert tokens[b] == tok and dec.tokens[dec.batch + b] == alt, (label, step, b)
+            # the device's choice is also (nearly) the oracle's best
+            assert want[i][tok] >= want[i].max() - 2 * bound
+        inputs = [int(tokens[b]) for b in slots]
+        positions = [p + 1 for p in positions]
+    return inputs, positions
+
+
+@pytest.mark.parametrize("shape", ["tiny", "wide"])
+def test_prefill_and_greedy_steps_match_oracle(device, shape):
+    m, w, max_length = build(device, shape)
+    lengths = [23, 64, 5, 81] if shape == "tiny" else [17, 40, 3]
+    ids = prompts(lengths, m.vocab, seed=1)
+    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+    try:
+        orc = om.DecoderOracle(w, max_length)
+        slots = list(range(len(ids)))
+        for b in slots:
+            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=8))
+        dec.prefill()
+        rows = [(t, p, b) for b in slots for p, t in enumerate(ids[b][:-1])]
+        orc.body(*map(list, zip(*rows)), cache_only_last=True)
+        for layer in range(len(m.layers)):
+            for b in slots:
+                check_cache(dec, orc, layer, b, len(ids[b]) - 1, f"{shape} layer {layer} slot {b}")
+        dec.flags[0, slots] = True
+        dec.set_active()
+        run_steps(dec, orc, [i[-1] for i in ids], [len(i) - 1 for i in ids], slots, 6, shape)
+    finally:
+        dec.close()
+
+
+def test_prompt_store_round_trip_and_reuse(device):
+    m, w, max_length = build(device, "tiny")
+    ids = prompts([50, 30], m.vocab, seed=2)
+    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=200, max_slots=8)
+    try:
+        for b in (0, 1):
+            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+        dec.prefill()                                  # prefills, then saves both prompts (store positions 0, 49)
+        assert dec.stored == {tuple(ids[0]): 0, tuple(ids[1]): 49}
+        dec.start(5, 2, Request(input_ids=ids[0], max_new_tokens=4))   # loaded from the store, not prefilled
+        assert not dec.pending
+        n = len(ids[0]) - 1
+        for layer in range(len(m.layers)):
+            a, s_ = dec.cache_rows(layer, 0, 0, n), dec.cache_rows(layer, -1, 0, n)
+            c = dec.cache_rows(layer, 5, 0, n)
+            for x, y, z in zip(a, s_, c):
+                assert np.array_equal(x, y) and np.array_equal(x, z), layer
+            t1 = dec.cache_rows(layer, -1, 49, len(ids[1]) - 1)
+            for x, y in zip(dec.cache_rows(layer, 1, 0, len(ids[1]) - 1), t1):
+                assert np.array_equal(x, y), layer
+        dec.flags[0, [0, 1, 5]] = True
+        dec.set_active()
+        tokens = dec.step()
+        got = dec.logits(6)
+        # same cache bytes and inputs; the split-K schedule partitions the two slots' keys differently, so their
+        # fp32 sums (and downstream bf16 roundings) may differ: equal within the logit tolerance
+        assert tokens[0] == tokens[5]
+        assert np.abs(got[0] - got[5]).max() <= LOGIT_MAX_REL * np.abs(got[0]).max()
+    finally:
+        dec.close()
+
+
+def test_masks_and_alternative(device):
+    m, w, max_length = build(device, "tiny")
+    ids = prompts([12, 20, 9], m.vocab, seed=3)
+    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+    try:
+        for b in range(3):
+            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+        dec.prefill()
+        rng = np.random.default_rng(4)
+        allowed = rng.random(m.vocab) < 0.05
+        dec.masks[1] = np.packbits(allowed, bitorder="little").view("<u4")
+        dec.masks[2] = 0
+        dec.masks[2, 0] = 1                       # slot 2 may choose only BOS: its alternative is none (-1)
+        dec.flags[0, :3] = True
+        dec.flags[1, [1, 2]] = True
+        dec.set_active()
+        tokens = dec.step()
+        got = dec.logits(3)
+        B = dec.batch
+        for b in range(3):
+            tok, alt = sampling.choose(got[b], allow=None if b == 0 else dec.masks[b], lazy=0)
+            assert tokens[b] == tok and dec.tokens[B + b] == alt, b
+        assert allowed[tokens[1]]
+        assert tokens[2] == 0 and dec.tokens[B + 2] == -1
+        # take the alternative of slot 1: its next input is the alternative token
+        alt1 = int(dec.tokens[B + 1])
+        dec.lib.dec_take_alt(dec.handle, 1)
+        dec.flags[1] = False
+        dec.set_active()
+        orc = om.DecoderOracle(w, max_length)
+        rows = [(t, p, b) for b in range(3) for p, t in enumerate(ids[b][:-1])]
+        orc.body(*map(list, zip(*rows)), cache_only_last=True)
+        orc.body([i[-1] for i in ids], [len(i) - 1 for i in ids], [0, 1, 2])
+        inputs = [int(tokens[0]), alt1, int(tokens[2])]
+        run_steps(dec, orc, inputs, [len(i) for i in ids], [0, 1, 2], 1, "after take_alt")
+    finally:
+        dec.close()
+
+
+def near_tie_ok(got_tok, want_tok, scores):
+    return got_tok == want_tok or abs(scores[got_tok] - scores[want_tok]) <= NEAR_TIE * max(1.0, abs(scores[want_tok]))
+
+
+def test_sampling_matches_oracle_choice(device):
+    m, w, max_length = build(device, "tiny")
+    ids = prompts([10, 14, 18, 22], m.vocab, seed=5)
+    params = [(0.9, 1.0, 7), (0.7, 0.8, 123456789012345), (1.3, 0.5, 2 ** 63 + 5), (0.0, 0.5, 1)]
+    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+    try:
+        for b, (T, p, seed) in enumerate(params):
+            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=6, temperature=T, top_p=p, seed=seed))
+        dec.prefill()
+        dec.flags[0, :4] = True
+        dec.set_active()
+        B = dec.batch
+        for step in range(5):
+            tokens = dec.step()
+            got = dec.logits(4)
+            for b, (T, p, seed) in enumerate(params):
+                tok, alt = sampling.choose(got[b], temperature=T, top_p=p, seed=seed, gen=step, lazy=0,
+                                           softcap=m.softcap)
+                if T > 0:
+                    z = sampling.capped(got[b], m.softcap)
+                    scores = (z / np.float32(T)).astype(np.float32) + sampling.gumbel(seed, step, np.arange(m.vocab))
+                    if p < 1:
+                        keep, e = sampling.nucleus_keep(z, T, p, np.ones(m.vocab, bool))
+                        if not keep[tokens[b]]:   # only a row at the nucleus boundary may differ
+                            kept = e[keep]
+                            assert abs(e[tokens[b]] - kept.min()) <= 1e-5 * kept.min(), (step, b)
+                        else:
+                            assert near_tie_ok(int(tokens[b]), tok, scores), (step, b)
+                        assert dec.tokens[B + b] == -1
+                    else:
+                        assert near_tie_ok(int(tokens[b]), tok, scores), (step, b)
+                        assert near_tie_ok(int(dec.tokens[B + b]), alt, scores), (step, b)
+                else:
+                    assert tokens[b] == tok and dec.tokens[B + b] == alt
+    finally:
+        dec.close()
+
+
+def test_inactive_slot_holds_still(device):
+    m, w, max_length = build(device, "tiny")
+    ids = prompts([15, 25, 35], m.vocab, seed=6)
+    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+    try:
+        for b in range(3):
+            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+        dec.prefill()
+        orc = om.DecoderOracle(w, max_length)
+        rows = [(t, p, b) for b in range(3) for p, t in enumerate(ids[b][:-1])]
+        orc.body(*map(list, zip(*rows)), cache_only_last=True)
+        dec.flags[0, [0, 2]] = True                    # slot 1 idles this step
+        dec.set_active()
+        inputs, pos = run_steps(dec, orc, [ids[0][-1], ids[2][-1]], [14, 34], [0, 2], 1, "slot 1 idle")
+        _, _, s = dec.cache_rows(0, 1, len(ids[1]) - 1, 1)
+        assert np.all(s == 0)                          # its next position was not written
+        dec.flags[0, 1] = True
+        dec.set_active()
+        run_steps(dec, orc, [inputs[0], ids[1][-1], inputs[1]], [pos[0], 24, pos[1]], [0, 1, 2], 2, "slot 1 back")
+    finally:
+        dec.close()
+
+
+def test_generate_continuous_batching(device):
+    """generate() over more requests than slots: every output token is (nearly) the oracle's greedy choice given the
+    tokens before it; stopping criteria and max_new_tokens end requests; slots are refilled."""
+    m, w, max_length = build(device, "tiny")
+    ids = prompts([9, 30, 12, 44, 7], m.vocab, seed=7)
+    stop_after = {3: 2}
+    requests = [Request(input_ids=ids[i], max_new_tokens=5,
+                        stopping_criteria=(lambda out, k=stop_after.get(i): k is not None and len(out) >= k))
+                for i in range(5)]
+    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=300, max_slots=2)
+    try:
+        assert dec.batch == 2
+        done = dict(dec.generate(requests))
+        assert sorted(done) == list(range(5))
+        assert sorted(dec.timings) == list(range(5))
+        for i, out in done.items():
+            assert 1 <= len(out) <= 5
+            if i == 3:
+                assert len(out) == 2
+            orc = om.DecoderOracle(w, max_length)
+            seq = ids[i] + out
+            n = len(ids[i]) - 1
+            orc.body(seq[:n], list(range(n)), [0] * n, cache_only_last=True)
+            for j, tok in enumerate(out):
+                want = orc.head(orc.body([seq[n + j]], [n + j], [0]))[0]
+                assert want[tok] >= want.max() - 2 * LOGIT_MAX_REL * np.abs(want).max(), (i, j)
+    finally:
+        dec.close()
