@@ -13,6 +13,8 @@ value = algorithmic HBM bytes of the step / step time (GB/s). Attention bytes pe
     python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4] [--pages-per-worker P] [--cpu-seqs S]
 
 --workload c4 times the chunked-prefill step instead (TFLOP/s against the 2.5 PFLOP/s bf16 dense MFMA peak).
+--workload c5 runs the end-to-end decoder (libnanochat_decode.so through the dec_* ABI): a random-init 26-layer
+d1664 model, 128 random 2048-token prompts prefilled, then 512 greedy steps; value = decode tokens/s.
 """
 import argparse
 import json
@@ -152,6 +154,115 @@ def bench_prefill(args, w):
     }
 
 
+def model_decode_bytes(w, positions):
+    """HBM bytes a decode step must read: every slot's cached keys (264 B per key per head per layer, positions
+    0..p), the GEMM weights and lm_head in bf16."""
+    H = w.hidden // 128
+    kv = sum(p + 1 for p in positions) * w.layers * H * 264
+    weights = 2 * (w.layers * (4 * w.hidden * w.hidden + 2 * w.hidden * w.ffn) + w.vocab * w.hidden)
+    return kv + weights
+
+
+def model_cpu_baseline(w, model, slots=8, seed=0):
+    """The CPU oracle (float64 numpy, oracle/model.py) on a bounded sample of config 5: one decode step of `slots`
+    slots at the prompt's full context, over caches filled with seeded random fp8 rows (the step's work does not
+    depend on the cached values); tokens/s = slots / step time."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import model as om
+
+    cores = min(16, os.cpu_count() or 1)
+    weights = om.weights_from_tensors(model)
+    n = w.prompt - 1
+    orc = om.DecoderOracle(weights, n + 1)
+    rng = np.random.default_rng(seed)
+    for b in range(slots):
+        k, v = orc._slot(b)
+        k[:, :n] = rng.standard_normal(k[:, :n].shape, dtype=np.float32)
+        v[:, :n] = rng.standard_normal(v[:, :n].shape, dtype=np.float32)
+    tokens = rng.integers(1, w.vocab, slots)
+    with threadpool_limits(cores):
+        orc.head(orc.body(tokens[:1], [n], [0]))   # warm-up: the oracle's one-time float64 weight copies
+        t0 = time.perf_counter()
+        orc.head(orc.body(tokens, [n] * slots, list(range(slots))))
+        dt = time.perf_counter() - t0
+    return {"value": round(slots / dt, 3), "unit": "decode tokens/s", "cores": cores, "kind": "port",
+            "sample": f"one decode step of {slots} slots at context {n + 1} (caches pre-filled), float64 numpy oracle",
+            "seconds": round(dt, 3)}
+
+
+def bench_model(args, w, cpu_slots=8):
+    """Config 5 end to end through the decoder runtime."""
+    import torch
+
+    from nanochat_amd.decoder import PagedDecoder, Request
+    from nanochat_amd.workloads import model_tensors, prompt_tokens
+
+    dev = torch.device("cuda:0")
+    model = model_tensors(w.layers, w.hidden, w.ffn, w.vocab, w.max_length, seed=0, std=w.std, theta=w.theta,
+                          softcap=w.softcap, device=dev, generator_device="cuda")
+    ids = prompt_tokens(w.batch, w.prompt, w.vocab, seed=0).tolist()
+    dec = PagedDecoder(model, bos_token_id=0, max_length=w.max_length, prompt_store=0, max_slots=w.batch)
+    try:
+        if dec.batch < w.batch:
+            raise RuntimeError(f"only {dec.batch} slots fit, the workload needs {w.batch}")
+        # warm-up: a short prompt per slot and a few steps (rocBLAS loads its kernels on first use)
+        for b in range(w.batch):
+            dec.start(b, b, Request(input_ids=ids[b][:32], max_new_tokens=1))
+        dec.prefill()
+        dec.flags[0, :w.batch] = True
+        dec.set_active()
+        for _ in range(max(1, min(args.warmup, 5))):
+            dec.step()
+        torch.cuda.synchronize()
+        # prefill: every prompt but its last token (the first step's input), dec_prefill_rows rows a call
+        t0 = time.perf_counter()
+        for b in range(w.batch):
+            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=w.steps))
+        dec.prefill()
+        dec.stream.synchronize()
+        prefill_s = time.perf_counter() - t0
+        # decode: `steps` greedy steps of every slot, each ending with the tokens on the host (dec_tokens)
+        positions = [w.prompt - 1] * w.batch
+        step_bytes = 0
+        t0 = time.perf_counter()
+        for i in range(w.steps):
+            dec.step()
+            step_bytes += model_decode_bytes(w, [p + i for p in positions])
+        decode_s = time.perf_counter() - t0
+    finally:
+        dec.close()
+    tokens = w.batch * w.steps
+    tok_s = tokens / decode_s
+    roof_tok_s = tokens / (step_bytes / (HBM_PEAK_GBS * 1e9))
+    prefill_rows = w.batch * (w.prompt - 1)
+    H = w.hidden // 128
+    prefill_flops_ = 2 * prefill_rows * (w.layers * (4 * w.hidden * w.hidden + 2 * w.hidden * w.ffn)) + \
+        4 * 128 * H * w.batch * (w.layers - 1) * sum(range(1, w.prompt))
+    result = {
+        "metric": "end-to-end decode tokens/s (config 5)", "value": round(tok_s, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": w.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * decode_s / w.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 weights/activations, fp8e4m3 KV, fp32 accumulation",
+        "data": "synthetic (random-init N(0, 0.02) weights, random-token prompts, seeded)",
+        "config": {"workload": f"{w.name}: {w.description}", "layers": w.layers, "hidden": w.hidden,
+                   "heads": H, "ffn": w.ffn, "vocab": w.vocab, "batch": w.batch, "prompt": w.prompt,
+                   "steps": w.steps, "rope_theta": w.theta},
+        "prefill_s": round(prefill_s, 4), "prefill_tokens_per_s": round(prefill_rows / prefill_s, 1),
+        "prefill_tflops": round(prefill_flops_ / prefill_s / 1e12, 2),
+        "decode_s": round(decode_s, 4), "end_to_end_tokens_per_s": round(tokens / (prefill_s + decode_s), 1),
+        "roofline": {"bound": "hbm", "achieved": round(step_bytes / decode_s / 1e9, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(tok_s / roof_tok_s, 4), "traffic": None,
+                     "kernel": "whole decode step (KV + weights per step)",
+                     "roofline_tokens_per_s": round(roof_tok_s, 1)},
+    }
+    if cpu_slots > 0:
+        result["cpu_baseline"] = model_cpu_baseline(w, model, cpu_slots)
+        result["cpu_baseline"]["speedup_of_gpu"] = round(tok_s / result["cpu_baseline"]["value"], 1)
+    return result
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -176,10 +287,13 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
-    from nanochat_amd.workloads import PREFILL
+    from nanochat_amd.workloads import MODELS, PREFILL
 
     if args.workload in PREFILL:
         print(json.dumps(bench_prefill(args, PREFILL[args.workload])), flush=True)
+        return
+    if args.workload in MODELS:
+        print(json.dumps(bench_model(args, MODELS[args.workload], cpu_slots=args.cpu_seqs)), flush=True)
         return
     dev = torch.device("cuda:0")
     w = DECODE[args.workload]

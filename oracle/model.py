@@ -94,6 +94,14 @@ class DecoderOracle:
         self.v = {}
         self.codes = {}   # slot -> dict of raw codes/scales per layer for byte comparisons
         self.L, self.H = L, H
+        self._f64 = {}    # id(weight) -> its float64 copy, converted once
+
+    def _mm(self, x, w):
+        """x (n, K) @ w (R, K)^T in float64, w converted once per oracle."""
+        key = id(w)
+        if key not in self._f64:
+            self._f64[key] = (w, w.astype(np.float64))
+        return x.astype(np.float64) @ self._f64[key][1].T
 
     def _slot(self, b):
         if b not in self.k:
@@ -122,13 +130,13 @@ class DecoderOracle:
             v = v.astype(np.float32)
             xm = bf16_round(v)
             hn = bf16_round((v * rms_scale(v)).astype(np.float32))
-            qkv = bf16_round(matmul_t(hn, ly.qkv).astype(np.float32)).reshape(n, 3, H, HEAD_DIM)
+            qkv = bf16_round(self._mm(hn, ly.qkv).astype(np.float32)).reshape(n, 3, H, HEAD_DIM)
             cos, sin = w.cos[positions][:, None, :], w.sin[positions][:, None, :]
             q = qk_norm_rope(qkv[:, 0], ly.q_gain, cos, sin)
             k = qk_norm_rope(qkv[:, 1], ly.k_gain, cos, sin)
             val = qkv[:, 2]
             if ly.ve is not None:
-                d = matmul_t(hn, ly.ve_gate)                              # (n, H)
+                d = self._mm(hn, ly.ve_gate)                              # (n, H)
                 g = (2.0 / (1.0 + np.exp(-d))).astype(np.float32)[:, :, None]
                 e = _f32(ly.ve[tokens]).reshape(n, H, HEAD_DIM)
                 val = bf16_round((val + (g * e).astype(np.float32)).astype(np.float32))
@@ -155,18 +163,18 @@ class DecoderOracle:
                 s = np.exp(s - s.max(axis=-1, keepdims=True))
                 att[r] = np.einsum("hm,mhd->hd", s / s.sum(axis=-1, keepdims=True), vv)
             att = bf16_round(att.astype(np.float32)).reshape(n, C)
-            xs = (matmul_t(att, ly.o) + xm.astype(np.float64)).astype(np.float32)
+            xs = (self._mm(att, ly.o) + xm.astype(np.float64)).astype(np.float32)
             xo = bf16_round(xs)
             rstd = rms_scale(xs, divide=False)
-            p_ = (matmul_t(xo, ly.fc).astype(np.float32) * rstd).astype(np.float32)
+            p_ = (self._mm(xo, ly.fc).astype(np.float32) * rstd).astype(np.float32)
             u = bf16_round((np.maximum(p_, 0) * p_).astype(np.float32))
-            x = bf16_round((matmul_t(u, ly.proj) + xo.astype(np.float64)).astype(np.float32))
+            x = bf16_round((self._mm(u, ly.proj) + xo.astype(np.float64)).astype(np.float32))
         return x
 
     def head(self, x):
         """Final norm and lm_head: logits (n, vocab) float64."""
         hn = bf16_round((x * rms_scale(x)).astype(np.float32))
-        return matmul_t(hn, self.w.lm_head)
+        return self._mm(hn, self.w.lm_head)
 
 
 def weights_from_tensors(model):
