@@ -76,6 +76,16 @@ void *dec_create_slots(const int *cfg, const uint64_t *ptrs, const float *scal, 
 void dec_debug_logits(void *handle, float *out, int rows);
 void dec_debug_cache(void *handle, int layer, int b, int at, int n, uint8_t *k, uint8_t *v, float *scales);
 
+/* The decode step's skinny GEMM alone: out[n][r] = epilogue(sum_k x[n][k] w[r][k]), bf16 w [R][K] and x [N][K],
+ * epi 0 bf16(s), 1 x = s + res: bf16 out and fp32 out_f32, 2 bf16(relu(p) p) with p = s rstd[n], 3 bf16(s + res),
+ * 4 fp32 out_f32 = s; split over `slices` K-slices (0: the decoder's choice, dec_debug_gemm_slices) whose partial
+ * sums go to part (fp32 [slices][N][R]) and are added in slice order. Returns 0, a hipError_t, -2 when (R, K, N)
+ * does not fit (N <= 128, K % 128 == 0, R % 4 == 0), or -3 while the kernel is switched off (it is: its first GPU
+ * run faulted and the cause is not yet found). Stream-ordered. */
+int dec_debug_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out, float *out_f32,
+                   const void *res, const float *rstd, int slices, float *part, void *stream);
+int dec_debug_gemm_slices(int R, int K);
+
 #ifdef __cplusplus
 }
 #endif

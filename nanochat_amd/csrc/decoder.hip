@@ -3,13 +3,15 @@
  * inference/decoder.py:132-148) over an fp8 paged KV cache.
  *
  * A step is a stream of kernels on the caller's stream, launched eagerly:
- *   body   norm_kernel(EMBED) -> per layer { norm_kernel(RESID), qkv GEMM (bf16 out), the fused q/k norm + RoPE +
- *          value-embedding + fp8 append (kv_append.hip), split-K decode attention (attention.hip), o GEMM (fp32 out),
- *          resid_rstd_kernel, fc GEMM (fp32 out), relu2_kernel, proj GEMM (bf16(s + xo) by beta = 1) }
+ *   body   norm_kernel(EMBED) -> per layer { norm_kernel(RESID), qkv GEMM, the fused q/k norm + RoPE + value-embedding
+ *          + fp8 append (kv_append.hip), split-K decode attention (attention.hip), o GEMM (+ residual, fp32 sum kept),
+ *          rstd_kernel, fc GEMM (+ ReLU^2 of the rstd-scaled sum), proj GEMM (+ residual) }
  *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
  *          the allowed tokens, then the commit), the tokens to pinned host memory.
- * GEMMs are rocBLAS gemm_ex, bf16 operands with fp32 accumulation, atomics off (deterministic). Every kernel covers
- * the slots up to the highest active one (dec_set_active) and skips inactive slots.
+ * GEMMs are rocBLAS gemm_ex (bf16 operands, fp32 accumulation, atomics off) followed by the epilogue kernels.
+ * skinny_gemm.hip's weight-streaming MFMA kernels for a step's few slots are built but switched off (Decoder::skinny):
+ * their first GPU test run faulted and the cause is not yet found. Every kernel covers the slots up to the highest active one (dec_set_active) and skips inactive
+ * slots.
  *
  * Numerics, op by op as decode.cu: the epilogues round once (bf16(s + residual)); the MLP reads the un-normed stream
  * scaled by its rstd; every RMS norm is 1 / sqrt(mean x^2 + FLT_EPSILON), correctly rounded (the reference: rsqrtf).
@@ -96,14 +98,23 @@ struct NormArgs {
     int32_t *seq_lens, *num_new;
 };
 
-/* RMS norm of a row (decode.cu:413-443): EMBED x0 = wte[token] r in fp32; RESID v = fma(l1, h, x0 l2), mixed =
- * bf16(v), out = bf16(v r); FINAL out = bf16(x r); r = 1 / sqrt(sum v^2 / C + FLT_EPSILON), the sum a lane-strided
- * FMA chain then the butterfly. */
+/* Sum over a 256-thread block in a fixed order (the wave butterfly, then the four waves in order); every thread
+ * gets the result. scratch: 4 floats of LDS. */
+__device__ __forceinline__ float block4_sum(float v, float *scratch) {
+    v = wave_sum_butterfly(v);
+    if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((scratch[0] + scratch[1]) + scratch[2]) + scratch[3];
+}
+
+/* RMS norm of a row, a 256-thread block per row (decode.cu:413-443): EMBED x0 = wte[token] r in fp32; RESID
+ * v = fma(l1, h, x0 l2), mixed = bf16(v), out = bf16(v r); FINAL out = bf16(x r); r = 1 / sqrt(sum v^2 / C +
+ * FLT_EPSILON), the sum a thread-strided FMA chain, then block4_sum. */
 __global__ void __launch_bounds__(256) norm_kernel(NormArgs a) {
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & (WAVE - 1);
-    if (b >= a.rows) return;
+    __shared__ float scratch[4];
+    const int b = blockIdx.x, tid = threadIdx.x;
     const bool on = !a.active || live(a.active, b);
-    if (a.seq_lens && lane == 0) {
+    if (a.seq_lens && tid == 0) {
         a.seq_lens[b] = on ? a.pos[b] + 1 : 0;
         a.num_new[b] = on ? 1 : 0;
     }
@@ -114,7 +125,8 @@ __global__ void __launch_bounds__(256) norm_kernel(NormArgs a) {
         int token = a.tokens[b];
         if (token < 0 || token >= a.vocab) {
             token = 0;
-            if (lane == 0) a.tokens[b] = 0;
+            __syncthreads();   /* every thread has read tokens[b] */
+            if (tid == 0) a.tokens[b] = 0;
         }
         emb = a.wte + (long long)token * a.C;
     }
@@ -126,13 +138,15 @@ __global__ void __launch_bounds__(256) norm_kernel(NormArgs a) {
         return __builtin_fmaf(a.l1, h, x0 * a.l2);
     };
     float ss = 0.0f;
-    for (int i = lane; i < a.C; i += WAVE) {
+#pragma unroll 4
+    for (int i = tid; i < a.C; i += 256) {
         const float v = value(i);
         ss = __builtin_fmaf(v, v, ss);
     }
-    ss = wave_sum_butterfly(ss);
+    ss = block4_sum(ss, scratch);
     const float r = 1.0f / __builtin_sqrtf(ss / (float)a.C + FLT_EPS);
-    for (int i = lane; i < a.C; i += WAVE) {
+#pragma unroll 4
+    for (int i = tid; i < a.C; i += 256) {
         const float v = value(i);
         if (a.kind == NORM_EMBED) {
             a.x0[row + i] = v * r;
@@ -143,21 +157,27 @@ __global__ void __launch_bounds__(256) norm_kernel(NormArgs a) {
     }
 }
 
-/* o_proj's epilogue and the MLP's rstd (decode.cu:149-154, 445-456): x = s + xm (fp32), xo = bf16(x),
- * rstd = 1 / sqrt(sum x^2 (1 / C) + FLT_EPSILON). */
-__global__ void __launch_bounds__(256) resid_rstd_kernel(const float *s, const uint16_t *xm, uint16_t *xo, float *rstd,
-                                                         const unsigned long long *active, int rows, int C) {
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & (WAVE - 1);
-    if (b >= rows || (active && !live(active, b))) return;
+/* The MLP's rstd of o_proj's fp32 residual sum (decode.cu:149-154, 445-456), a block per row: x = s + xm when xm is
+ * given (then xo = bf16(x) is written here), else x = s (the GEMM wrote xo and x); rstd = 1 / sqrt(sum x^2 (1 / C)
+ * + FLT_EPSILON). */
+__global__ void __launch_bounds__(256) rstd_kernel(const float *s, const uint16_t *xm, uint16_t *xo, float *rstd,
+                                                   const unsigned long long *active, int C) {
+    __shared__ float scratch[4];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    if (active && !live(active, b)) return;
     const long long row = (long long)b * C;
     float ss = 0.0f;
-    for (int i = lane; i < C; i += WAVE) {
-        const float x = s[row + i] + bf16_to_f32(xm[row + i]);
-        xo[row + i] = f32_to_bf16(x);
+#pragma unroll 4
+    for (int i = tid; i < C; i += 256) {
+        float x = s[row + i];
+        if (xm) {
+            x = x + bf16_to_f32(xm[row + i]);
+            xo[row + i] = f32_to_bf16(x);
+        }
         ss = __builtin_fmaf(x, x, ss);
     }
-    ss = wave_sum_butterfly(ss);
-    if (lane == 0) rstd[b] = 1.0f / __builtin_sqrtf(ss * (1.0f / (float)C) + FLT_EPS);
+    ss = block4_sum(ss, scratch);
+    if (tid == 0) rstd[b] = 1.0f / __builtin_sqrtf(ss * (1.0f / (float)C) + FLT_EPS);
 }
 
 /* fc's epilogue (decode.cu:144-148): u = bf16(relu(p) p), p = s rstd[row]; four columns a thread. */
@@ -423,6 +443,8 @@ struct Decoder {
     int32_t *host_tokens;                /* pinned [2][B] */
     uint32_t *host_allow;                /* pinned [B][vocab / 32] */
     int narrow;                          /* a step's rows: the highest active slot + 1 */
+    bool skinny;                         /* decode-step GEMMs by skinny_gemm (else rocBLAS) */
+    float *part;                         /* the skinny GEMMs' split-K partial sums */
     std::vector<void *> device_blocks;
 };
 
@@ -492,23 +514,50 @@ static NormArgs norm_args(Decoder *d, int kind, const Acts &a, int rows, int32_t
 }
 
 static void launch_norm(Decoder *d, const NormArgs &n) {
-    hipLaunchKernelGGL(norm_kernel, dim3((n.rows + 3) / 4), dim3(256), 0, d->stream, n);
+    hipLaunchKernelGGL(norm_kernel, dim3(n.rows), dim3(256), 0, d->stream, n);
 }
 
 static uint8_t *layer_k(Decoder *d, int l) { return d->k_pages + (size_t)l * d->layer_pages * d->H * PAGE_BYTES; }
 static uint8_t *layer_v(Decoder *d, int l) { return d->v_pages + (size_t)l * d->layer_pages * d->H * PAGE_BYTES; }
 static float *layer_s(Decoder *d, int l) { return d->kv_scale + (size_t)l * d->layer_pages * d->H * 2 * PAGE; }
 
+/* A GEMM with its epilogue: the skinny MFMA GEMM when the rows fit it (a decode step's few slots), else rocBLAS
+ * into fp32 or bf16 and the epilogue kernels. */
+static void gemm_epi(Decoder *d, int epi, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
+                     uint16_t *out, float *out_f32, const uint16_t *res, const float *rstd,
+                     const unsigned long long *active) {
+    if (n <= 0) return;
+    if (d->skinny && skinny_gemm_fits(rows, cols, n)) {
+        const int S = skinny_gemm_slices(rows, cols);
+        SkinnyGemm g = {w, in, rows, cols, n, out, out_f32, res, rstd, active};
+        NC_CHECK(skinny_gemm(g, epi, d->part, S, d->stream));
+        if (S > 1) NC_CHECK(skinny_gemm_reduce(g, epi, d->part, S, d->stream));
+        return;
+    }
+    switch (epi) {
+    case SG_STORE: gemm(d, w, rows, cols, in, n, out, false); break;
+    case SG_RESID: gemm(d, w, rows, cols, in, n, out, false, res); break;
+    case SG_F32: gemm(d, w, rows, cols, in, n, out_f32, true); break;
+    case SG_RESID2:  /* fp32 s; the rstd kernel adds the residual and writes out */
+        gemm(d, w, rows, cols, in, n, out_f32, true);
+        break;
+    case SG_RELU2:
+        gemm(d, w, rows, cols, in, n, out_f32, true);
+        hipLaunchKernelGGL(relu2_kernel, dim3((rows / 4 + 255) / 256, n), dim3(256), 0, d->stream, out_f32, rstd, out,
+                           active, rows);
+        break;
+    }
+}
+
 /* The rest of a layer after its attention: o_proj + residual, the MLP. */
 static void mlp(Decoder *d, const Layer &ly, const Acts &a, int n, const unsigned long long *active) {
     const int C = d->C, F = d->F;
-    gemm(d, ly.o, C, C, a.att, n, a.acc, true);
-    hipLaunchKernelGGL(resid_rstd_kernel, dim3((n + 3) / 4), dim3(256), 0, d->stream, a.acc, a.xm, a.xo, a.rstd,
-                       active, n, C);
-    gemm(d, ly.fc, F, C, a.xo, n, a.acc, true);
-    hipLaunchKernelGGL(relu2_kernel, dim3((F / 4 + 255) / 256, n), dim3(256), 0, d->stream, a.acc, a.rstd, a.u, active,
-                       F);
-    gemm(d, ly.proj, C, F, a.u, n, a.x, false, a.xo);
+    const bool fused = d->skinny && skinny_gemm_fits(C, C, n);
+    gemm_epi(d, SG_RESID2, ly.o, C, C, a.att, n, a.xo, a.acc, a.xm, nullptr, active);
+    hipLaunchKernelGGL(rstd_kernel, dim3(n), dim3(256), 0, d->stream, a.acc, fused ? nullptr : a.xm, a.xo, a.rstd,
+                       active, C);
+    gemm_epi(d, SG_RELU2, ly.fc, F, C, a.xo, n, a.u, a.acc, nullptr, a.rstd, active);
+    gemm_epi(d, SG_RESID, ly.proj, C, F, a.u, n, a.x, nullptr, a.xo, nullptr, active);
 }
 
 static void enqueue_body(Decoder *d) {
@@ -529,7 +578,7 @@ static void enqueue_body(Decoder *d) {
         r.mixed = a.xm;
         r.out = a.h;
         launch_norm(d, r);
-        gemm(d, ly.qkv, 3 * C, C, a.h, R, a.qkv, false);
+        gemm_epi(d, SG_STORE, ly.qkv, 3 * C, C, a.h, R, a.qkv, nullptr, nullptr, nullptr, d->active);
         NC_CHECK(append_rows(a.qkv, 3LL * C, R, d->H, d->H, d->pos, d->num_new, nullptr, ly.q_gain, ly.k_gain, d->cos,
                              d->sin, d->max_len, a.q, d->block_table, d->max_pages, layer_k(d, l), layer_v(d, l),
                              layer_s(d, l), (int)d->layer_pages, a.h, ly.ve, ly.ve_gate, d->tokens, C, d->stream));
@@ -548,7 +597,7 @@ static void enqueue_head(Decoder *d) {
         n.in = a.x;
         n.out = a.hn;
         launch_norm(d, n);
-        gemm(d, d->lm_head, d->vocab, d->C, a.hn, R, d->logits, true);
+        gemm_epi(d, SG_F32, d->lm_head, d->vocab, d->C, a.hn, R, nullptr, d->logits, nullptr, nullptr, d->active);
         ChoiceArgs c = {d->logits, d->probs, d->active, d->allow, d->temperature, d->top_p, d->seed, d->first,
                         d->tokens, d->alt_tokens, d->pos, d->softcap, d->vocab, d->lazy};
         hipLaunchKernelGGL(choose_kernel, dim3(R), dim3(CHOICE_THREADS), 0, d->stream, c);
@@ -628,6 +677,15 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     d->logits = (float *)device_alloc(d, B * d->vocab * sizeof(float));
     d->probs = (float *)device_alloc(d, B * d->vocab * sizeof(float));
     d->slot = carve_acts(d, B);
+    size_t part_bytes = 0;
+    const int C = d->C, F = d->F, N = d->B < SG_MAX_N ? d->B : SG_MAX_N;
+    const int shapes[5][2] = {{3 * C, C}, {C, C}, {F, C}, {C, F}, {d->vocab, C}};
+    for (const auto &rk : shapes)
+        if (skinny_gemm_fits(rk[0], rk[1], N)) {
+            const size_t bytes = (size_t)skinny_gemm_slices(rk[0], rk[1]) * N * rk[0] * sizeof(float);
+            part_bytes = bytes > part_bytes ? bytes : part_bytes;
+        }
+    d->part = (float *)device_alloc(d, part_bytes > 0 ? part_bytes : 256);
     d->workspace_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1, 0);
     REQUIRE(d->workspace_bytes > 0, "decode attention workspace");
     d->workspace = device_alloc(d, d->workspace_bytes);
@@ -641,6 +699,9 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     HIP_CHECK(hipEventRecord(d->staged, d->stream));
     HIP_CHECK(hipStreamSynchronize(d->stream));
     d->narrow = 0;
+    /* the skinny GEMM path is switched off: its first test run faulted the GPU and the cause is not found (every
+     * access replays in bounds on the CPU); the step uses rocBLAS until it is */
+    d->skinny = false;
     return d;
 }
 
@@ -853,3 +914,19 @@ extern "C" void dec_debug_cache(void *handle, int layer, int b, int at, int n, u
         }
     }
 }
+
+static const bool skinny_enabled = false;
+
+extern "C" int dec_debug_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out, float *out_f32,
+                              const void *res, const float *rstd, int slices, float *part, void *stream) {
+    nc::SkinnyGemm g = {(const uint16_t *)w, (const uint16_t *)x, R, K, N, (uint16_t *)out, out_f32,
+                        (const uint16_t *)res, rstd, nullptr};
+    if (!nc::skinny_gemm_fits(R, K, N)) return -2;
+    if (!skinny_enabled) return -3;   /* switched off, see dec_create */
+    const int S = slices > 0 ? slices : nc::skinny_gemm_slices(R, K);
+    const int e = nc::skinny_gemm(g, epi, part, S, (hipStream_t)stream);
+    if (e != 0 || S == 1) return e;
+    return nc::skinny_gemm_reduce(g, epi, part, S, (hipStream_t)stream);
+}
+
+extern "C" int dec_debug_gemm_slices(int R, int K) { return nc::skinny_gemm_slices(R, K); }
