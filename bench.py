@@ -10,7 +10,11 @@ value = algorithmic HBM bytes of the step / step time (GB/s). Attention bytes pe
 (n + 1) * 264 (fp8 K + V and two fp32 scales per key) + G * 128 * 2 * 2 (q in, out) + ceil((n + 1) / 16) * 4
 (block table); the append adds (Hq + 2 Hkv) * 256 read and Hq * 256 + Hkv * 264 written per token.
 
-    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4] [--pages-per-worker P] [--cpu-seqs S]
+    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4|c5] [--pages-per-worker P] [--cpu-seqs S]
+                    [--no-e2e]
+
+A decode workload's line also carries the metric's second half, `decode_tokens_per_s`: config 5 end to end
+(below), unless --no-e2e.
 
 --workload c4 times the chunked-prefill step instead (TFLOP/s against the 2.5 PFLOP/s bf16 dense MFMA peak).
 --workload c5 runs the end-to-end decoder (libnanochat_decode.so through the dec_* ABI): a random-init 26-layer
@@ -271,6 +275,8 @@ def main():
     ap.add_argument("--workload", default="c3u")
     ap.add_argument("--pages-per-worker", type=int, default=0)
     ap.add_argument("--cpu-seqs", type=int, default=6, help="sequences in the CPU baseline sample (0: skip)")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="decode workloads: skip the config-5 end-to-end decode tokens/s part of the metric")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: the fp8 KV decode path is single-GPU by design (asked for {args.gpus})",
@@ -383,6 +389,15 @@ def main():
     if args.cpu_seqs > 0:
         result["cpu_baseline"] = cpu_baseline(w, inp, args.cpu_seqs)
         result["cpu_baseline"]["speedup_of_gpu"] = round(achieved / result["cpu_baseline"]["value"], 1)
+    if not args.no_e2e:
+        # the metric's second half: end-to-end decode tokens/s of config 5 through the decoder runtime
+        del cache, ws, qkv, q_out, out
+        torch.cuda.empty_cache()
+        e2e = bench_model(args, MODELS["c5"], cpu_slots=8 if args.cpu_seqs > 0 else 0)
+        result["decode_tokens_per_s"] = e2e["value"]
+        keep = ("metric", "value", "unit", "ms_per_step", "config", "prefill_s", "prefill_tokens_per_s",
+                "prefill_tflops", "decode_s", "end_to_end_tokens_per_s", "roofline", "cpu_baseline")
+        result["end_to_end"] = {k: e2e[k] for k in keep if k in e2e}
     print(json.dumps(result), flush=True)
 
 
