@@ -50,6 +50,18 @@ int nc_abi_version(void);
 void qkp_forward(const void *q, const void *k, const void *gq, const void *gk, void *qo, void *ko, const void *cos,
                  const void *sin, long long rows, int H, int T, void *stream);
 
+/* The prologue's backward: the reference's qkp_backward (model/kernels/qk_prologue.cu:128-136), same arguments.
+ * q, k as for qkp_forward; dqo, dko: the outputs' gradients, contiguous [rows][128] bf16; dq, dk: the inputs'
+ * gradients at q's and k's strides (token stride 3 H 128); dgq, dgk: the gains' gradients fp32 [128], summed in a
+ * fixed order (bitwise reproducible); part: fp32 [2 qkp_backward_blocks()][128] scratch. rows = 0 is allowed (the
+ * gain gradients are zero). Returns nothing; nc_last_error() reports the status. */
+void qkp_backward(const void *q, const void *k, const void *gq, const void *gk, const void *dqo, const void *dko,
+                  void *dq, void *dk, void *dgq, void *dgk, void *part, const void *cos, const void *sin,
+                  long long rows, int H, int T, void *stream);
+
+/* Blocks per tensor of qkp_backward's partial gain gradients (reference qk_prologue.cu:120-125): fixed. */
+int qkp_backward_blocks(void);
+
 /* Status of the last void entry point's launch on this host thread (NC_OK or a hipError_t). */
 int nc_last_error(void);
 

@@ -8,7 +8,8 @@
  *          rstd_kernel, fc GEMM (+ ReLU^2 of the rstd-scaled sum), proj GEMM (+ residual) }
  *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
  *          the allowed tokens, then the commit), the tokens to pinned host memory.
- * GEMMs are rocBLAS gemm_ex (bf16 operands, fp32 accumulation, atomics off) followed by the epilogue kernels.
+ * GEMMs are hipBLASLt matmuls (bf16 operands, fp32 accumulation; a plan per shape and slot count, the heuristic's
+ * first algorithm; rocBLAS gemm_ex when hipBLASLt offers none) followed by the epilogue kernels.
  * skinny_gemm.hip's weight-streaming MFMA kernels for a step's few slots are built but switched off (Decoder::skinny):
  * their first GPU test run faulted and the cause is not yet found. Every kernel covers the slots up to the highest active one (dec_set_active) and skips inactive
  * slots.
@@ -28,8 +29,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <map>
+#include <tuple>
 #include <vector>
 
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
 #include "nc_device.h"
@@ -424,6 +428,9 @@ struct Decoder {
     std::vector<Layer> layer;
     hipStream_t stream;
     rocblas_handle blas;
+    hipblasLtHandle_t lt;                /* hipBLASLt: the GEMMs' first choice (rocBLAS when it has no plan) */
+    void *lt_ws;
+    size_t lt_ws_bytes;
     uint8_t *k_pages, *v_pages;          /* [L][layer_pages][H][2048] */
     float *kv_scale;                     /* [L][layer_pages][H][2][16] */
     int32_t *block_table;                /* [B][max_pages], identity */
@@ -486,12 +493,84 @@ static Acts carve_acts(Decoder *d, size_t rows) {
     return a;
 }
 
+/* A hipBLASLt plan for one GEMM shape: column-major D (rows x n) = W^T (W stored [rows][cols], so a cols x rows
+ * column-major matrix, transposed) x X (cols x n), fp32 compute; the heuristic's first algorithm. */
+struct LtPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo;
+    bool ok = false;
+};
+
+static std::map<std::tuple<Decoder *, int, int, int, int>, LtPlan> &lt_plans() {
+    static std::map<std::tuple<Decoder *, int, int, int, int>, LtPlan> plans;
+    return plans;
+}
+
+static const LtPlan &lt_plan(Decoder *d, int rows, int cols, int n, bool f32) {
+    LtPlan &p = lt_plans()[std::make_tuple(d, rows, cols, n, (int)f32)];
+    if (p.desc) return p;
+    const hipDataType ot = f32 ? HIP_R_32F : HIP_R_16BF;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, cols, rows, cols) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, cols, n, cols) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.c, ot, rows, n, rows) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    if (ok) {
+        const uint64_t ws = d->lt_ws_bytes;
+        ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+             hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof ws) ==
+                 HIPBLAS_STATUS_SUCCESS;
+    }
+    if (ok) {
+        hipblasLtMatmulHeuristicResult_t r[1];
+        int got = 0;
+        ok = hipblasLtMatmulAlgoGetHeuristic(d->lt, p.desc, p.a, p.b, p.c, p.c, pref, 1, r, &got) ==
+                 HIPBLAS_STATUS_SUCCESS &&
+             got > 0 && r[0].state == HIPBLAS_STATUS_SUCCESS && r[0].workspaceSize <= d->lt_ws_bytes;
+        if (ok) p.algo = r[0].algo;
+    }
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    p.ok = ok;
+    return p;
+}
+
+static void lt_release(Decoder *d) {
+    auto &plans = lt_plans();
+    for (auto it = plans.begin(); it != plans.end();) {
+        if (std::get<0>(it->first) != d) {
+            ++it;
+            continue;
+        }
+        LtPlan &p = it->second;
+        if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
+        if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
+        if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
+        if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+        it = plans.erase(it);
+    }
+}
+
 /* out[n][rows] = in[n][cols] . W[rows][cols]^T: column-major rows x n = (W as cols x rows)^T (cols x n). resid
- * non-NULL: out = bf16(s + resid) by beta = 1 (one rounding of the fp32 sum). */
+ * non-NULL: out = bf16(s + resid) by beta = 1 (one rounding of the fp32 sum). hipBLASLt's plan for the shape,
+ * else rocBLAS gemm_ex. */
 static void gemm(Decoder *d, const uint16_t *w, int rows, int cols, const uint16_t *in, int n, void *out, bool f32,
                  const uint16_t *resid = nullptr) {
     if (n <= 0) return;
     const float alpha = 1.0f, beta = resid ? 1.0f : 0.0f;
+    const LtPlan &p = lt_plan(d, rows, cols, n, f32);
+    if (p.ok) {
+        const hipblasStatus_t st = hipblasLtMatmul(d->lt, p.desc, &alpha, w, p.a, in, p.b, &beta,
+                                                   resid ? (const void *)resid : out, p.c, out, p.c, &p.algo,
+                                                   d->lt_ws, d->lt_ws_bytes, d->stream);
+        if (st != HIPBLAS_STATUS_SUCCESS) die("hipblasLtMatmul", "failed", __LINE__);
+        return;
+    }
     const rocblas_datatype ot = f32 ? rocblas_datatype_f32_r : rocblas_datatype_bf16_r;
     BLAS_CHECK(rocblas_gemm_ex(d->blas, rocblas_operation_transpose, rocblas_operation_none, rows, n, cols, &alpha, w,
                                rocblas_datatype_bf16_r, cols, in, rocblas_datatype_bf16_r, cols, &beta,
@@ -637,6 +716,8 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     BLAS_CHECK(rocblas_create_handle(&d->blas));
     BLAS_CHECK(rocblas_set_stream(d->blas, d->stream));
     BLAS_CHECK(rocblas_set_atomics_mode(d->blas, rocblas_atomics_not_allowed));
+    if (hipblasLtCreate(&d->lt) != HIPBLAS_STATUS_SUCCESS) die("hipblasLtCreate", "failed", __LINE__);
+    d->lt_ws_bytes = (size_t)32 << 20;
 
     /* fixed blocks first (prefill rows, masks, store pages' share is per layer below), then the slots: B, the most
      * slots (<= max_slots) whose KV pages, activations and choice buffers fit the free memory less a reserve */
@@ -686,6 +767,7 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
             part_bytes = bytes > part_bytes ? bytes : part_bytes;
         }
     d->part = (float *)device_alloc(d, part_bytes > 0 ? part_bytes : 256);
+    d->lt_ws = device_alloc(d, d->lt_ws_bytes);
     d->workspace_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1, 0);
     REQUIRE(d->workspace_bytes > 0, "decode attention workspace");
     d->workspace = device_alloc(d, d->workspace_bytes);
@@ -782,6 +864,8 @@ static void destroy(Decoder *d) {
     hipHostFree(d->host_tokens);
     hipHostFree(d->host_allow);
     hipEventDestroy(d->staged);
+    lt_release(d);
+    hipblasLtDestroy(d->lt);
     rocblas_destroy_handle(d->blas);
     delete d;
 }

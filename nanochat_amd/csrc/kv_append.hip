@@ -153,6 +153,61 @@ __global__ void __launch_bounds__(256) qkp_forward_kernel(const uint16_t *q, con
     y[lane + HALF] = f32_to_bf16(y2);
 }
 
+/* The training-form prologue's backward (reference model/kernels/qk_prologue.cu:36-90): per (token, head) row, a
+ * wave with lane l on dims l and l + 64, recomputing n = x r; the rotation's transpose gives dm (dm1 = dy1 c - dy2 s,
+ * dm2 = dy1 s + dy2 c); dn = dm g; dx = r (dn - n b), b = sum(dn n) / 128 (the butterfly); the gain gradient
+ * sum_rows dm n accumulates per lane in row order. Grid: QKB_BLOCKS blocks per tensor (q's, then k's), wave w of
+ * block j taking rows j 4 + w, + QKB_BLOCKS 4, ...; each block writes its partial [128] (waves added in order). */
+constexpr int QKB_BLOCKS = 512;   /* fixed, so the gain gradient's summation order is fixed */
+
+__global__ void __launch_bounds__(256) qkp_backward_kernel(const uint16_t *q, const uint16_t *k, const float *gq,
+                                                           const float *gk, const uint16_t *dqo, const uint16_t *dko,
+                                                           uint16_t *dq, uint16_t *dk, const float *cos,
+                                                           const float *sin, float *part, long long rows, int H,
+                                                           int T) {
+    __shared__ float wpart[4][HEAD_DIM];
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const bool isq = blockIdx.x < QKB_BLOCKS;
+    const long long first = (isq ? blockIdx.x : blockIdx.x - QKB_BLOCKS) * 4 + wave;
+    const uint16_t *xin = isq ? q : k, *dyin = isq ? dqo : dko;
+    uint16_t *dxout = isq ? dq : dk;
+    const float *g = isq ? gq : gk;
+    const float g1 = g[lane], g2 = g[lane + HALF];
+    float a1 = 0.0f, a2 = 0.0f;
+    for (long long i = first; i < rows; i += (long long)QKB_BLOCKS * 4) {
+        const long long t = i / H, at = t * 3 * H * HEAD_DIM + (i % H) * HEAD_DIM;
+        const long long tab = (t % T) * HALF + lane;
+        const float x1 = bf16_to_f32(xin[at + lane]), x2 = bf16_to_f32(xin[at + lane + HALF]);
+        const float d1 = bf16_to_f32(dyin[i * HEAD_DIM + lane]), d2 = bf16_to_f32(dyin[i * HEAD_DIM + lane + HALF]);
+        const float c = cos[tab], s = sin[tab];
+        const float ss = wave_sum_butterfly(x1 * x1 + x2 * x2);
+        const float r = 1.0f / __builtin_sqrtf(ss / 128.0f + FLT_EPS);
+        const float n1 = x1 * r, n2 = x2 * r;
+        const float dm1 = d1 * c - d2 * s, dm2 = d1 * s + d2 * c;
+        a1 = a1 + dm1 * n1;
+        a2 = a2 + dm2 * n2;
+        const float dn1 = dm1 * g1, dn2 = dm2 * g2;
+        const float b = wave_sum_butterfly(dn1 * n1 + dn2 * n2) / 128.0f;
+        dxout[at + lane] = f32_to_bf16(r * (dn1 - n1 * b));
+        dxout[at + lane + HALF] = f32_to_bf16(r * (dn2 - n2 * b));
+    }
+    wpart[wave][lane] = a1;
+    wpart[wave][lane + HALF] = a2;
+    __syncthreads();
+    if (threadIdx.x < HEAD_DIM)
+        part[(long long)blockIdx.x * HEAD_DIM + threadIdx.x] =
+            ((wpart[0][threadIdx.x] + wpart[1][threadIdx.x]) + wpart[2][threadIdx.x]) + wpart[3][threadIdx.x];
+}
+
+/* Block 0: q's gain gradient, block 1: k's; thread d adds dim d of the QKB_BLOCKS partials in block order
+ * (reference qk_prologue.cu:92-97). */
+__global__ void __launch_bounds__(HEAD_DIM) qkp_gain_sum_kernel(const float *part, float *dgq, float *dgk) {
+    const float *p = part + (long long)blockIdx.x * QKB_BLOCKS * HEAD_DIM + threadIdx.x;
+    float sum = 0.0f;
+    for (int j = 0; j < QKB_BLOCKS; j++) sum = sum + p[(long long)j * HEAD_DIM];
+    (blockIdx.x ? dgk : dgq)[threadIdx.x] = sum;
+}
+
 static thread_local int last_error = NC_OK;
 
 static int launch_append(const AppendArgs &a, bool fused, hipStream_t stream) {
@@ -235,6 +290,28 @@ extern "C" int nc_qk_norm_rope_append_fp8(const void *qkv, long long token_strid
     a.k_pages = (uint8_t *)k_pages; a.v_pages = (uint8_t *)v_pages;
     a.kv_scale = kv_scale; a.num_pages = num_pages;
     return launch_append(a, true, (hipStream_t)stream);
+}
+
+extern "C" int qkp_backward_blocks() { return QKB_BLOCKS; }
+
+extern "C" void qkp_backward(const void *q, const void *k, const void *gq, const void *gk, const void *dqo,
+                             const void *dko, void *dq, void *dk, void *dgq, void *dgk, void *part, const void *cos,
+                             const void *sin, long long rows, int H, int T, void *stream) {
+    if (!q || !k || !gq || !gk || !dqo || !dko || !dq || !dk || !dgq || !dgk || !part || !cos || !sin) {
+        last_error = NC_ERR_NULL;
+        return;
+    }
+    if (H <= 0 || T <= 0 || rows < 0 || rows % H) {
+        last_error = NC_ERR_SHAPE;
+        return;
+    }
+    hipLaunchKernelGGL(qkp_backward_kernel, dim3(2 * QKB_BLOCKS), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)q, (const uint16_t *)k, (const float *)gq, (const float *)gk,
+                       (const uint16_t *)dqo, (const uint16_t *)dko, (uint16_t *)dq, (uint16_t *)dk,
+                       (const float *)cos, (const float *)sin, (float *)part, rows, H, T);
+    hipLaunchKernelGGL(qkp_gain_sum_kernel, dim3(2), dim3(HEAD_DIM), 0, (hipStream_t)stream, (const float *)part,
+                       (float *)dgq, (float *)dgk);
+    last_error = (int)hipGetLastError();
 }
 
 extern "C" void qkp_forward(const void *q, const void *k, const void *gq, const void *gk, void *qo, void *ko,

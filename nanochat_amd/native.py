@@ -61,7 +61,7 @@ def build() -> tuple[Path, Path]:
             _run([hipcc(), *HIPCC_FLAGS, "-c", "-o", str(objects[src]), str(src)])
         for output, sources, libs in ((LIBRARY, KERNEL_SOURCES, []),
                                       (DECODE_LIBRARY, KERNEL_SOURCES + DECODE_SOURCES,
-                                       [f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lrocblas"])):
+                                       [f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lhipblaslt", "-lrocblas"])):
             built = Path(tmp) / output.name
             _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(built),
                   *(str(objects[s]) for s in sources), *libs])
@@ -78,6 +78,8 @@ SIGNATURES = {
     "nc_abi_version": ([], c_int),
     "nc_last_error": ([], c_int),
     "qkp_forward": ([c_void_p] * 8 + [c_longlong, c_int, c_int, c_void_p], None),
+    "qkp_backward": ([c_void_p] * 13 + [c_longlong, c_int, c_int, c_void_p], None),
+    "qkp_backward_blocks": ([], c_int),
     "nc_kv_append_fp8": ([c_void_p, c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
                           c_void_p, c_void_p, c_void_p, c_int, c_void_p], c_int),
     "nc_qk_norm_rope_append_fp8": ([c_void_p, c_longlong, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,

@@ -1,4 +1,5 @@
-"""Fused q/k prologue, training form: drop-in for the reference's model/ops/qk_prologue.py:13-21.
+"""Fused q/k prologue, training form: drop-in for the reference's model/ops/qk_prologue.py (qk_forward :13-21,
+qk_backward :24-36).
 
 Per (token, head) row of q and k: RMS norm (eps FLT_EPSILON), fp32 per-dimension gain and the -theta
 rotation (reference model/kernels/qk_row.cuh:26-41), fp32 math and one bf16 rounding. q, k are
@@ -33,3 +34,33 @@ def qk_forward(q: Tensor, k: Tensor, q_norm_weight: Tensor, k_norm_weight: Tenso
     if status:
         raise NativeError(f"qkp_forward: {lib.nc_status_string(status).decode()}")
     return q_out, k_out
+
+
+def qk_backward(q: Tensor, k: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, dq_out: Tensor, dk_out: Tensor,
+                cos: Tensor, sin: Tensor, dq: Tensor, dk: Tensor) -> tuple[Tensor, Tensor]:
+    """Write q's and k's gradients into dq, dk (views shaped and strided like q, k); return the gains' gradients,
+    summed in a fixed order (bitwise reproducible). dq_out, dk_out: the forward outputs' gradients, contiguous."""
+    B, T, H, D = q.shape
+    for name, t in (("q", q), ("k", k), ("dq", dq), ("dk", dk)):
+        if not t.is_cuda or t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be a bf16 device tensor")
+        if t.shape != (B, T, H, HEAD_DIM) or t.stride() != (T * 3 * H * HEAD_DIM, 3 * H * HEAD_DIM, HEAD_DIM, 1):
+            raise ValueError(f"{name} must be a (B, T, H, {HEAD_DIM}) view of a fused qkv tensor")
+    for name, t in (("dq_out", dq_out), ("dk_out", dk_out)):
+        if not t.is_cuda or t.dtype != torch.bfloat16 or t.shape != q.shape or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bf16 device tensor shaped like q")
+    for name, t in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight), ("cos", cos), ("sin", sin)):
+        if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous fp32 device tensor")
+    if cos.shape[0] < T or sin.shape[0] < T:
+        raise ValueError(f"cos/sin need {T} positions")
+    dq_norm_weight, dk_norm_weight = torch.empty_like(q_norm_weight), torch.empty_like(k_norm_weight)
+    lib = hip_library()
+    part = q_norm_weight.new_empty((2 * lib.qkp_backward_blocks(), D))
+    lib.qkp_backward(pointer(q), pointer(k), pointer(q_norm_weight), pointer(k_norm_weight), pointer(dq_out),
+                     pointer(dk_out), pointer(dq), pointer(dk), pointer(dq_norm_weight), pointer(dk_norm_weight),
+                     pointer(part), pointer(cos), pointer(sin), B * T * H, H, T, stream())
+    status = lib.nc_last_error()
+    if status:
+        raise NativeError(f"qkp_backward: {lib.nc_status_string(status).decode()}")
+    return dq_norm_weight, dk_norm_weight

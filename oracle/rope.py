@@ -18,10 +18,15 @@ The reference's rsqrtf is an approximation whose bits cannot be reproduced here 
 the correctly rounded 1/sqrt is the build's choice; the HF restatement's torch.rsqrt is the same
 division of a correctly rounded sqrt.
 
+qk_norm_rope_backward restates the backward of model/kernels/qk_prologue.cu:36-97 (k_backward, k_gain_sum) exactly
+(float64): n = x r, dm1 = dy1 cos - dy2 sin, dm2 = dy1 sin + dy2 cos, dgain = sum over rows of dm n,
+dn = dm gain, dx = r (dn - n mean(dn n)).
+
 Pinned by tests/test_oracle_rope.py: cos^2+sin^2 ~ 1 and t = 0 -> (1, 0); the position-0 case with unit
 gains reduces to the textbook RMS norm (torch.nn.functional.rms_norm, fp64) within half a bf16 ulp;
 a 90-degree rotation swaps the halves with a sign; a zero row gives zeros; the butterfly sum equals
-math.fsum within fp32 accumulation error; and float64 brute force within one bf16 ulp everywhere.
+math.fsum within fp32 accumulation error; and float64 brute force within one bf16 ulp everywhere. The backward
+equals torch autograd of the float64 forward (rms_norm, gain, rotation) within 1e-12.
 """
 import numpy as np
 
@@ -67,3 +72,21 @@ def qk_norm_rope(x, gain, cos, sin):
     y1 = (n1 * c + n2 * s).astype(np.float32)
     y2 = (n2 * c - n1 * s).astype(np.float32)
     return bf16_round(np.concatenate([y1, y2], axis=-1))
+
+
+def qk_norm_rope_backward(x, gain, cos, sin, dy):
+    """x (rows, 128) bf16 values, gain (128,), cos, sin broadcastable to (rows, 64), dy (rows, 128) -> (dx float64
+    (rows, 128), dgain float64 (128,)), exact float64 math."""
+    x = np.asarray(x, np.float64)
+    g = np.asarray(gain, np.float64)
+    c = np.asarray(cos, np.float64)
+    s = np.asarray(sin, np.float64)
+    dy = np.asarray(dy, np.float64)
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + float(FLT_EPSILON))
+    n = x * r
+    d1, d2 = dy[..., :HALF], dy[..., HALF:]
+    dm = np.concatenate([d1 * c - d2 * s, d1 * s + d2 * c], axis=-1)
+    dgain = np.sum(dm * n, axis=tuple(range(dm.ndim - 1)))
+    dn = dm * g
+    b = np.mean(dn * n, axis=-1, keepdims=True)
+    return r * (dn - n * b), dgain

@@ -93,6 +93,16 @@ def test_qkp_forward_reports_errors(lib):
     assert lib.nc_last_error() == -2
 
 
+def test_qkp_backward_reports_errors(lib):
+    assert lib.qkp_backward_blocks() == 512
+    lib.qkp_backward(*([DUMMY] * 10), None, DUMMY, DUMMY, 6, 6, 1, None)
+    assert lib.nc_last_error() == -1
+    lib.qkp_backward(*([DUMMY] * 13), 7, 6, 1, None)
+    assert lib.nc_last_error() == -2
+    lib.qkp_backward(*([DUMMY] * 13), 6, 6, 0, None)
+    assert lib.nc_last_error() == -2
+
+
 DECODE_HEADER = HEADER.parent / "nanochat_decode.h"
 
 # the reference's decoder ABI (decode.cu:904-1131): every symbol inference/decoder.py binds

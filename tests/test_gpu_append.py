@@ -127,3 +127,49 @@ def test_append_skips_out_of_range_pages(device):
     assert cache.k_scale[1, 0, 15].item() == pytest.approx(1 / 448)
     assert int(cache.k_pages[0].count_nonzero()) == 0 and cache.k_scale[0].abs().sum().item() == 0
     assert int(cache.k_pages[1].count_nonzero()) == 128
+
+
+@pytest.mark.parametrize("B,T,H", [(2, 33, 6), (4, 512, 6), (1, 1, 1)])
+def test_qk_backward_matches_oracle(device, B, T, H):
+    """dq, dk within one bf16 rounding of the float64 backward plus fp32 error; the gains' gradients within the
+    rigorous bound of their fp32 summation depth; bitwise repeatable; the v third of the gradient buffer untouched."""
+    from nanochat_amd.qk_prologue import qk_backward
+    from oracle.rope import qk_norm_rope_backward
+
+    gen = torch.Generator().manual_seed(B * 100 + T + H)
+    qkv = torch.randn(B, T, 3, H, 128, generator=gen).to(torch.bfloat16)
+    dout = torch.randn(2, B, T, H, 128, generator=gen).to(torch.bfloat16)
+    gains = 1 + 0.1 * torch.randn(2, 128, generator=gen)
+    cos, sin = rotary_tables(T, 1e4, device)
+    qkv_d, dout_d, g_d = qkv.to(device), dout.to(device), gains.to(device)
+
+    def run():
+        dqkv = torch.full_like(qkv_d, 7.0)
+        dgq, dgk = qk_backward(qkv_d[:, :, 0], qkv_d[:, :, 1], g_d[0], g_d[1], dout_d[0], dout_d[1], cos, sin,
+                               dqkv[:, :, 0], dqkv[:, :, 1])
+        torch.cuda.synchronize()
+        return dqkv.cpu(), dgq.cpu(), dgk.cpu()
+
+    dqkv, dgq, dgk = run()
+    again = run()
+    assert all(torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a, b.view(torch.int16) if
+                           b.dtype == torch.bfloat16 else b) for a, b in zip((dqkv, dgq, dgk), again))
+    assert bool((dqkv[:, :, 2] == 7.0).all())
+    rows = B * T * H
+    c = cos.cpu().numpy()[None, :, None].astype(np.float64)
+    s = sin.cpu().numpy()[None, :, None].astype(np.float64)
+    for j, dg in ((0, dgq), (1, dgk)):
+        x = qkv[:, :, j].double().numpy()
+        dy = dout[j].double().numpy()
+        dx, want_dg = qk_norm_rope_backward(x, gains[j].double().numpy(), c, s, dy)
+        got = dqkv[:, :, j].double().numpy()
+        row_scale = np.abs(dx).max(axis=-1, keepdims=True)
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(dx), 2.0 ** -126))) - 7)
+        assert np.all(np.abs(got - dx) <= ulp + 1e-5 * row_scale)
+        # |dm n| summed over rows: the scale of the fp32 summation error, depth rows/2048 + 4 + QKB_BLOCKS
+        d1, d2 = dy[..., :64], dy[..., 64:]
+        dm = np.concatenate([d1 * c - d2 * s, d1 * s + d2 * c], axis=-1)
+        n = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + 2.0 ** -23)
+        mag = np.abs(dm * n).reshape(-1, 128).sum(axis=0)
+        depth = rows // 2048 + 4 + 512
+        assert np.all(np.abs(dg.double().numpy() - want_dg) <= depth * 2.0 ** -24 * mag + 1e-30)

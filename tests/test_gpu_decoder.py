@@ -284,3 +284,27 @@ def test_generate_continuous_batching(device):
                 assert want[tok] >= want.max() - 2 * LOGIT_MAX_REL * np.abs(want).max(), (i, j)
     finally:
         dec.close()
+
+
+def test_steps_are_deterministic(device):
+    """Two decoders fed the same prompts give bit-identical logits: no GEMM or attention kernel the step runs sums
+    in a run-dependent order."""
+    m, w, max_length = build(device, "wide")
+    ids = prompts([20, 33, 7], m.vocab, seed=9)
+    out = []
+    for _ in range(2):
+        dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+        try:
+            for b in range(3):
+                dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+            dec.prefill()
+            dec.flags[0, :3] = True
+            dec.set_active()
+            logits = []
+            for _ in range(3):
+                dec.step()
+                logits.append(dec.logits(3))
+            out.append(np.stack(logits))
+        finally:
+            dec.close()
+    assert np.array_equal(out[0], out[1])

@@ -82,3 +82,29 @@ def test_brute_force_float64():
     # one bf16 rounding (half an ulp) plus fp32 arithmetic error: within one bf16 ulp of the exact value
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
     assert np.all(np.abs(y - ref) <= ulp + 1e-6)
+
+
+def test_backward_equals_torch_autograd():
+    """oracle.rope.qk_norm_rope_backward against autograd of the float64 forward: rms_norm (eps FLT_EPSILON), gain,
+    the -theta rotation of halves (reference qk_row.cuh:33-41)."""
+    import torch
+
+    from oracle.rope import FLT_EPSILON, qk_norm_rope_backward, rotary_tables
+
+    rng = np.random.default_rng(0)
+    rows, T = 40, 16
+    x = rng.standard_normal((rows, 128))
+    g = 1 + 0.2 * rng.standard_normal(128)
+    dy = rng.standard_normal((rows, 128))
+    cos, sin = rotary_tables(T, 10000.0)
+    pos = np.arange(rows) % T
+    c, s = cos[pos].astype(np.float64), sin[pos].astype(np.float64)
+    xt = torch.tensor(x, requires_grad=True)
+    gt = torch.tensor(g, requires_grad=True)
+    n = torch.nn.functional.rms_norm(xt, (128,), eps=float(FLT_EPSILON)) * gt
+    ct, st = torch.tensor(c), torch.tensor(s)
+    y = torch.cat([n[:, :64] * ct + n[:, 64:] * st, n[:, 64:] * ct - n[:, :64] * st], dim=1)
+    y.backward(torch.tensor(dy))
+    dx, dg = qk_norm_rope_backward(x, g, c, s, dy)
+    assert np.abs(dx - xt.grad.numpy()).max() <= 1e-12 * max(1.0, np.abs(dx).max())
+    assert np.abs(dg - gt.grad.numpy()).max() <= 1e-12 * max(1.0, np.abs(dg).max())
