@@ -86,6 +86,15 @@ int dec_debug_gemm(int epi, const void *w, int R, int K, const void *x, int N, v
                    const void *res, const float *rstd, int slices, float *part, void *stream);
 int dec_debug_gemm_slices(int R, int K);
 
+/* The decode step's range-checked weight-streaming GEMM (the one the decoder runs) alone, same arguments and
+ * epilogues as dec_debug_gemm; part needs dec_debug_stream_gemm_part_bytes(R, N, slices) bytes (none for one slice).
+ * Returns 0, a hipError_t, or -2 when the shape, the slice count or an operand the epilogue needs does not fit.
+ * Stream-ordered. */
+int dec_debug_stream_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out, float *out_f32,
+                          const void *res, const float *rstd, int slices, float *part, void *stream);
+int dec_debug_stream_gemm_slices(int R, int K);
+long long dec_debug_stream_gemm_part_bytes(int R, int N, int slices);
+
 #ifdef __cplusplus
 }
 #endif

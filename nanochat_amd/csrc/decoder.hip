@@ -8,11 +8,12 @@
  *          rstd_kernel, fc GEMM (+ ReLU^2 of the rstd-scaled sum), proj GEMM (+ residual) }
  *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
  *          the allowed tokens, then the commit), the tokens to pinned host memory.
- * GEMMs are hipBLASLt matmuls (bf16 operands, fp32 accumulation; a plan per shape and slot count, the heuristic's
- * first algorithm; rocBLAS gemm_ex when hipBLASLt offers none) followed by the epilogue kernels.
- * skinny_gemm.hip's weight-streaming MFMA kernels for a step's few slots are built but switched off (Decoder::skinny):
- * their first GPU test run faulted and the cause is not yet found. Every kernel covers the slots up to the highest active one (dec_set_active) and skips inactive
- * slots.
+ * A step's GEMMs (<= 128 slots) are stream_gemm.hip's weight-streaming MFMA kernels with the epilogues fused (split-K
+ * partials reduced in slice order by a second kernel); prefill's GEMMs are hipBLASLt matmuls (bf16 operands, fp32
+ * accumulation; a plan per shape and row count, the heuristic's first algorithm; rocBLAS gemm_ex when hipBLASLt offers
+ * none) followed by the epilogue kernels. skinny_gemm.hip (an earlier weight-streaming GEMM) is built but switched
+ * off: its first GPU test run faulted and the cause is not found. Every kernel covers the slots up to the highest
+ * active one (dec_set_active) and skips inactive slots.
  *
  * Numerics, op by op as decode.cu: the epilogues round once (bf16(s + residual)); the MLP reads the un-normed stream
  * scaled by its rstd; every RMS norm is 1 / sqrt(mean x^2 + FLT_EPSILON), correctly rounded (the reference: rsqrtf).
@@ -102,23 +103,47 @@ struct NormArgs {
     int32_t *seq_lens, *num_new;
 };
 
-/* Sum over a 256-thread block in a fixed order (the wave butterfly, then the four waves in order); every thread
- * gets the result. scratch: 4 floats of LDS. */
-__device__ __forceinline__ float block4_sum(float v, float *scratch) {
-    v = wave_sum_butterfly(v);
-    if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return ((scratch[0] + scratch[1]) + scratch[2]) + scratch[3];
+/* Row kernels: a wave per row, four rows a 256-thread block, one pass. Lane l holds elements (j 64 + l) 8 .. + 7 for
+ * j < NJ (NJ 512 >= C); every load is issued before the first use, the sum of squares is an FMA chain over the lane's
+ * elements in order (j, then element) and then the wave butterfly, so the result is fixed for a given C. */
+constexpr int ROW_CHUNK = WAVE * 8;   /* elements of a row per j */
+
+__device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-/* RMS norm of a row, a 256-thread block per row (decode.cu:413-443): EMBED x0 = wte[token] r in fp32; RESID
- * v = fma(l1, h, x0 l2), mixed = bf16(v), out = bf16(v r); FINAL out = bf16(x r); r = 1 / sqrt(sum v^2 / C +
- * FLT_EPSILON), the sum a thread-strided FMA chain, then block4_sum. */
+__device__ __forceinline__ void load8(const uint16_t *p, float (&v)[8]) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        v[2 * e] = bf16_to_f32((uint16_t)w[e]);
+        v[2 * e + 1] = bf16_to_f32((uint16_t)(w[e] >> 16));
+    }
+}
+
+__device__ __forceinline__ void store8(float *p, const float (&v)[8]) {
+    *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4 *>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+__device__ __forceinline__ void store8(uint16_t *p, const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) w[e] = (uint32_t)f32_to_bf16(v[2 * e]) | ((uint32_t)f32_to_bf16(v[2 * e + 1]) << 16);
+    *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+/* RMS norm of a row (decode.cu:413-443): EMBED x0 = wte[token] r in fp32; RESID v = fma(l1, h, x0 l2),
+ * mixed = bf16(v), out = bf16(v r); FINAL out = bf16(x r); r = 1 / sqrt(sum v^2 / C + FLT_EPSILON). */
+template <int NJ>
 __global__ void __launch_bounds__(256) norm_kernel(NormArgs a) {
-    __shared__ float scratch[4];
-    const int b = blockIdx.x, tid = threadIdx.x;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= a.rows) return;
     const bool on = !a.active || live(a.active, b);
-    if (a.seq_lens && tid == 0) {
+    if (a.seq_lens && lane == 0) {
         a.seq_lens[b] = on ? a.pos[b] + 1 : 0;
         a.num_new[b] = on ? 1 : 0;
     }
@@ -126,62 +151,90 @@ __global__ void __launch_bounds__(256) norm_kernel(NormArgs a) {
     const long long row = (long long)b * a.C;
     const float *emb = nullptr;
     if (a.kind == NORM_EMBED) {
-        int token = a.tokens[b];
+        int token = a.tokens[b];   /* every lane reads it before lane 0 can store below */
         if (token < 0 || token >= a.vocab) {
             token = 0;
-            __syncthreads();   /* every thread has read tokens[b] */
-            if (tid == 0) a.tokens[b] = 0;
+            if (lane == 0) a.tokens[b] = 0;
         }
         emb = a.wte + (long long)token * a.C;
     }
-    auto value = [&](int i) -> float {
-        if (a.kind == NORM_EMBED) return emb[i];
-        if (a.kind == NORM_FINAL) return bf16_to_f32(a.in[row + i]);
-        const float x0 = a.x0[row + i];
-        const float h = a.in ? bf16_to_f32(a.in[row + i]) : x0;
-        return __builtin_fmaf(a.l1, h, x0 * a.l2);
-    };
-    float ss = 0.0f;
-#pragma unroll 4
-    for (int i = tid; i < a.C; i += 256) {
-        const float v = value(i);
-        ss = __builtin_fmaf(v, v, ss);
-    }
-    ss = block4_sum(ss, scratch);
-    const float r = 1.0f / __builtin_sqrtf(ss / (float)a.C + FLT_EPS);
-#pragma unroll 4
-    for (int i = tid; i < a.C; i += 256) {
-        const float v = value(i);
+    float v[NJ][8];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int i = j * ROW_CHUNK + lane * 8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[j][e] = 0.0f;
+        if (i >= a.C) continue;
         if (a.kind == NORM_EMBED) {
-            a.x0[row + i] = v * r;
+            load8(emb + i, v[j]);
+        } else if (a.kind == NORM_FINAL) {
+            load8(a.in + row + i, v[j]);
         } else {
-            if (a.kind == NORM_RESID) a.mixed[row + i] = f32_to_bf16(v);
-            a.out[row + i] = f32_to_bf16(v * r);
+            float x0[8], h[8];
+            load8(a.x0 + row + i, x0);
+            if (a.in) load8(a.in + row + i, h);
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[j][e] = __builtin_fmaf(a.l1, a.in ? h[e] : x0[e], x0[e] * a.l2);
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
+    ss = wave_sum_butterfly(ss);
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)a.C + FLT_EPS);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int i = j * ROW_CHUNK + lane * 8;
+        if (i >= a.C) continue;
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) y[e] = v[j][e] * r;
+        if (a.kind == NORM_EMBED) {
+            store8(a.x0 + row + i, y);
+        } else {
+            if (a.kind == NORM_RESID) store8(a.mixed + row + i, v[j]);
+            store8(a.out + row + i, y);
         }
     }
 }
 
-/* The MLP's rstd of o_proj's fp32 residual sum (decode.cu:149-154, 445-456), a block per row: x = s + xm when xm is
+/* The MLP's rstd of o_proj's fp32 residual sum (decode.cu:149-154, 445-456), a wave per row: x = s + xm when xm is
  * given (then xo = bf16(x) is written here), else x = s (the GEMM wrote xo and x); rstd = 1 / sqrt(sum x^2 (1 / C)
  * + FLT_EPSILON). */
+template <int NJ>
 __global__ void __launch_bounds__(256) rstd_kernel(const float *s, const uint16_t *xm, uint16_t *xo, float *rstd,
-                                                   const unsigned long long *active, int C) {
-    __shared__ float scratch[4];
-    const int b = blockIdx.x, tid = threadIdx.x;
-    if (active && !live(active, b)) return;
+                                                   const unsigned long long *active, int rows, int C) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= rows || (active && !live(active, b))) return;
     const long long row = (long long)b * C;
-    float ss = 0.0f;
-#pragma unroll 4
-    for (int i = tid; i < C; i += 256) {
-        float x = s[row + i];
+    float x[NJ][8];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int i = j * ROW_CHUNK + lane * 8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[j][e] = 0.0f;
+        if (i >= C) continue;
+        load8(s + row + i, x[j]);
         if (xm) {
-            x = x + bf16_to_f32(xm[row + i]);
-            xo[row + i] = f32_to_bf16(x);
+            float m[8];
+            load8(xm + row + i, m);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[j][e] = x[j][e] + m[e];
         }
-        ss = __builtin_fmaf(x, x, ss);
     }
-    ss = block4_sum(ss, scratch);
-    if (tid == 0) rstd[b] = 1.0f / __builtin_sqrtf(ss * (1.0f / (float)C) + FLT_EPS);
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int i = j * ROW_CHUNK + lane * 8;
+        if (xm && i < C) store8(xo + row + i, x[j]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss = __builtin_fmaf(x[j][e], x[j][e], ss);
+    }
+    ss = wave_sum_butterfly(ss);
+    if (lane == 0) rstd[b] = 1.0f / __builtin_sqrtf(ss * (1.0f / (float)C) + FLT_EPS);
 }
 
 /* fc's epilogue (decode.cu:144-148): u = bf16(relu(p) p), p = s rstd[row]; four columns a thread. */
@@ -450,8 +503,9 @@ struct Decoder {
     int32_t *host_tokens;                /* pinned [2][B] */
     uint32_t *host_allow;                /* pinned [B][vocab / 32] */
     int narrow;                          /* a step's rows: the highest active slot + 1 */
-    bool skinny;                         /* decode-step GEMMs by skinny_gemm (else rocBLAS) */
-    float *part;                         /* the skinny GEMMs' split-K partial sums */
+    bool streaming;                      /* decode-step GEMMs by stream_gemm (else the library GEMM) */
+    float *part;                         /* stream_gemm's split-K partial sums, for up to SG_MAX_N rows */
+    long long part_bytes;
     std::vector<void *> device_blocks;
 };
 
@@ -592,25 +646,40 @@ static NormArgs norm_args(Decoder *d, int kind, const Acts &a, int rows, int32_t
     return n;
 }
 
+/* The row kernels' NJ: the fewest 512-element chunks covering C (C <= MAX_C). */
+constexpr int MAX_C = 8 * ROW_CHUNK;
+
 static void launch_norm(Decoder *d, const NormArgs &n) {
-    hipLaunchKernelGGL(norm_kernel, dim3(n.rows), dim3(256), 0, d->stream, n);
+    const dim3 grid((n.rows + 3) / 4), block(256);
+    if (n.C <= 2 * ROW_CHUNK) hipLaunchKernelGGL(norm_kernel<2>, grid, block, 0, d->stream, n);
+    else if (n.C <= 4 * ROW_CHUNK) hipLaunchKernelGGL(norm_kernel<4>, grid, block, 0, d->stream, n);
+    else hipLaunchKernelGGL(norm_kernel<8>, grid, block, 0, d->stream, n);
+}
+
+static void launch_rstd(Decoder *d, const float *s, const uint16_t *xm, uint16_t *xo, float *rstd,
+                        const unsigned long long *active, int rows) {
+    const dim3 grid((rows + 3) / 4), block(256);
+    const int C = d->C;
+    if (C <= 2 * ROW_CHUNK) hipLaunchKernelGGL(rstd_kernel<2>, grid, block, 0, d->stream, s, xm, xo, rstd, active, rows, C);
+    else if (C <= 4 * ROW_CHUNK) hipLaunchKernelGGL(rstd_kernel<4>, grid, block, 0, d->stream, s, xm, xo, rstd, active, rows, C);
+    else hipLaunchKernelGGL(rstd_kernel<8>, grid, block, 0, d->stream, s, xm, xo, rstd, active, rows, C);
 }
 
 static uint8_t *layer_k(Decoder *d, int l) { return d->k_pages + (size_t)l * d->layer_pages * d->H * PAGE_BYTES; }
 static uint8_t *layer_v(Decoder *d, int l) { return d->v_pages + (size_t)l * d->layer_pages * d->H * PAGE_BYTES; }
 static float *layer_s(Decoder *d, int l) { return d->kv_scale + (size_t)l * d->layer_pages * d->H * 2 * PAGE; }
 
-/* A GEMM with its epilogue: the skinny MFMA GEMM when the rows fit it (a decode step's few slots), else rocBLAS
- * into fp32 or bf16 and the epilogue kernels. */
+/* A GEMM with its epilogue: the weight-streaming MFMA GEMM when the rows fit it (a decode step's <= 128 slots), else
+ * the library GEMM into fp32 or bf16 and the epilogue kernels. */
 static void gemm_epi(Decoder *d, int epi, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
                      uint16_t *out, float *out_f32, const uint16_t *res, const float *rstd,
                      const unsigned long long *active) {
     if (n <= 0) return;
-    if (d->skinny && skinny_gemm_fits(rows, cols, n)) {
-        const int S = skinny_gemm_slices(rows, cols);
+    if (d->streaming && stream_gemm_fits(rows, cols, n)) {
+        const int S = stream_gemm_slices(rows, cols);
         SkinnyGemm g = {w, in, rows, cols, n, out, out_f32, res, rstd, active};
-        NC_CHECK(skinny_gemm(g, epi, d->part, S, d->stream));
-        if (S > 1) NC_CHECK(skinny_gemm_reduce(g, epi, d->part, S, d->stream));
+        NC_CHECK(stream_gemm(g, epi, d->part, d->part_bytes, S, d->stream));
+        if (S > 1) NC_CHECK(stream_gemm_reduce(g, epi, d->part, d->part_bytes, S, d->stream));
         return;
     }
     switch (epi) {
@@ -631,10 +700,9 @@ static void gemm_epi(Decoder *d, int epi, const uint16_t *w, int rows, int cols,
 /* The rest of a layer after its attention: o_proj + residual, the MLP. */
 static void mlp(Decoder *d, const Layer &ly, const Acts &a, int n, const unsigned long long *active) {
     const int C = d->C, F = d->F;
-    const bool fused = d->skinny && skinny_gemm_fits(C, C, n);
+    const bool fused = d->streaming && stream_gemm_fits(C, C, n);
     gemm_epi(d, SG_RESID2, ly.o, C, C, a.att, n, a.xo, a.acc, a.xm, nullptr, active);
-    hipLaunchKernelGGL(rstd_kernel, dim3(n), dim3(256), 0, d->stream, a.acc, fused ? nullptr : a.xm, a.xo, a.rstd,
-                       active, C);
+    launch_rstd(d, a.acc, fused ? nullptr : a.xm, a.xo, a.rstd, active, n);
     gemm_epi(d, SG_RELU2, ly.fc, F, C, a.xo, n, a.u, a.acc, nullptr, a.rstd, active);
     gemm_epi(d, SG_RESID, ly.proj, C, F, a.u, n, a.x, nullptr, a.xo, nullptr, active);
 }
@@ -690,7 +758,8 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     Decoder *d = new Decoder();
     d->L = cfg[0]; d->C = cfg[1]; d->F = cfg[2]; d->vocab = cfg[3]; d->max_len = cfg[4]; d->store = cfg[5];
     d->lazy = cfg[6];
-    REQUIRE(d->L > 0 && d->C > 0 && d->C % HEAD_DIM == 0, "C must be a positive multiple of 128");
+    REQUIRE(d->L > 0 && d->C > 0 && d->C % HEAD_DIM == 0 && d->C <= MAX_C,
+            "C must be a positive multiple of 128, at most 4096");
     REQUIRE(d->F > 0 && d->F % 4 == 0, "F must be a positive multiple of 4");
     REQUIRE(d->vocab > 0 && d->vocab % WORD_BITS == 0, "vocab must be a positive multiple of 32");
     REQUIRE(d->max_len > 0 && d->store >= 0, "max_len must be positive, store non-negative");
@@ -758,15 +827,18 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     d->logits = (float *)device_alloc(d, B * d->vocab * sizeof(float));
     d->probs = (float *)device_alloc(d, B * d->vocab * sizeof(float));
     d->slot = carve_acts(d, B);
-    size_t part_bytes = 0;
-    const int C = d->C, F = d->F, N = d->B < SG_MAX_N ? d->B : SG_MAX_N;
+    /* partials for the most rows a streamed GEMM takes: a step's slots and prefill's row blocks (up to SG_MAX_N rows,
+     * more than the slots when B < SG_MAX_N) both call it */
+    long long part_bytes = 256;
+    const int C = d->C, F = d->F;
     const int shapes[5][2] = {{3 * C, C}, {C, C}, {F, C}, {C, F}, {d->vocab, C}};
     for (const auto &rk : shapes)
-        if (skinny_gemm_fits(rk[0], rk[1], N)) {
-            const size_t bytes = (size_t)skinny_gemm_slices(rk[0], rk[1]) * N * rk[0] * sizeof(float);
+        if (stream_gemm_fits(rk[0], rk[1], SG_MAX_N)) {
+            const long long bytes = stream_gemm_part_bytes(rk[0], SG_MAX_N, stream_gemm_slices(rk[0], rk[1]));
             part_bytes = bytes > part_bytes ? bytes : part_bytes;
         }
-    d->part = (float *)device_alloc(d, part_bytes > 0 ? part_bytes : 256);
+    d->part = (float *)device_alloc(d, (size_t)part_bytes);
+    d->part_bytes = part_bytes;
     d->lt_ws = device_alloc(d, d->lt_ws_bytes);
     d->workspace_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1, 0);
     REQUIRE(d->workspace_bytes > 0, "decode attention workspace");
@@ -781,9 +853,7 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     HIP_CHECK(hipEventRecord(d->staged, d->stream));
     HIP_CHECK(hipStreamSynchronize(d->stream));
     d->narrow = 0;
-    /* the skinny GEMM path is switched off: its first test run faulted the GPU and the cause is not found (every
-     * access replays in bounds on the CPU); the step uses rocBLAS until it is */
-    d->skinny = false;
+    d->streaming = false;   /* the step GEMMs stay on the library until the streamed path beats it */
     return d;
 }
 
@@ -1014,3 +1084,22 @@ extern "C" int dec_debug_gemm(int epi, const void *w, int R, int K, const void *
 }
 
 extern "C" int dec_debug_gemm_slices(int R, int K) { return nc::skinny_gemm_slices(R, K); }
+
+extern "C" int dec_debug_stream_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out,
+                                     float *out_f32, const void *res, const float *rstd, int slices, float *part,
+                                     void *stream) {
+    nc::SkinnyGemm g = {(const uint16_t *)w, (const uint16_t *)x, R, K, N, (uint16_t *)out, out_f32,
+                        (const uint16_t *)res, rstd, nullptr};
+    if (!nc::stream_gemm_fits(R, K, N)) return -2;
+    const int S = slices > 0 ? slices : nc::stream_gemm_slices(R, K);
+    const long long part_bytes = nc::stream_gemm_part_bytes(R, N, S);   /* the caller allocates this much */
+    const int e = nc::stream_gemm(g, epi, part, part_bytes, S, (hipStream_t)stream);
+    if (e != 0 || S == 1) return e;
+    return nc::stream_gemm_reduce(g, epi, part, part_bytes, S, (hipStream_t)stream);
+}
+
+extern "C" int dec_debug_stream_gemm_slices(int R, int K) { return nc::stream_gemm_slices(R, K); }
+
+extern "C" long long dec_debug_stream_gemm_part_bytes(int R, int N, int slices) {
+    return nc::stream_gemm_part_bytes(R, N, slices);
+}

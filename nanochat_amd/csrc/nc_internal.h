@@ -46,4 +46,18 @@ int skinny_gemm(const SkinnyGemm &g, int epi, float *part, int S, hipStream_t st
 /* The S partials summed in slice order, then the epilogue. */
 int skinny_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, int S, hipStream_t stream);
 
+/* stream_gemm.hip: the same GEMM (SkinnyGemm operands, SG_* epilogues) with every global access range-checked by
+ * buffer instructions. */
+bool stream_gemm_fits(int R, int K, int N);
+/* K-slices for (R, K): about 384 workgroups of 128 rows, at least two 128-wide chunks a slice. */
+int stream_gemm_slices(int R, int K);
+/* Bytes of the partial sums of S slices (0 for S = 1). */
+long long stream_gemm_part_bytes(int R, int N, int S);
+/* S = 1: the epilogue in the GEMM. S > 1: fp32 partials to part [S][N][R] (part_bytes: its allocation, which must
+ * hold them), summed by stream_gemm_reduce. Returns 0, a hipError_t, or -2 when the shape, S, the partial buffer or an
+ * operand the epilogue needs does not fit. */
+int stream_gemm(const SkinnyGemm &g, int epi, float *part, long long part_bytes, int S, hipStream_t stream);
+int stream_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, long long part_bytes, int S,
+                       hipStream_t stream);
+
 }  // namespace nc

@@ -1,0 +1,93 @@
+"""The decode step's weight-streaming GEMM (stream_gemm.hip, through dec_debug_stream_gemm) against torch in float64:
+every epilogue, ragged row and slot counts, split-K slice counts, determinism, and the shapes it declines."""
+import numpy as np
+import pytest
+import torch
+
+from nanochat_amd.native import hip_library, pointer, stream
+
+pytestmark = pytest.mark.gpu
+
+STORE, RESID2, RELU2, RESID, F32 = range(5)
+# the config-5 decode shapes (qkv, o, fc, proj, lm_head) at full and partial slot counts, and ragged small ones
+SHAPES = [(4992, 1664, 128), (1664, 1664, 1), (6656, 1664, 37), (1664, 6656, 128), (100, 128, 16), (36, 256, 65),
+          (65536, 1664, 64), (260, 384, 17)]
+
+
+def bf16_ulp(x):
+    """bf16 spacing at |x| (2^-133 floor for zeros)."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def run(epi, w, x, res=None, rstd=None, slices=0):
+    R, K = w.shape
+    N = x.shape[0]
+    dev = w.device
+    out = torch.full((N, R), 7.0, dtype=torch.bfloat16, device=dev)
+    out32 = torch.full((N, R), 7.0, dtype=torch.float32, device=dev)
+    lib = hip_library("decode")
+    S = slices or lib.dec_debug_stream_gemm_slices(R, K)
+    part = torch.empty(max(1, lib.dec_debug_stream_gemm_part_bytes(R, N, S) // 4), dtype=torch.float32, device=dev)
+    print(f"stream_gemm epi={epi} R={R} K={K} N={N} S={S}", flush=True)
+    st = lib.dec_debug_stream_gemm(epi, pointer(w), R, K, pointer(x), N, pointer(out), pointer(out32),
+                                   pointer(res) if res is not None else None,
+                                   pointer(rstd) if rstd is not None else None, slices, pointer(part), stream())
+    assert st == 0, st
+    torch.cuda.synchronize()
+    return out, out32
+
+
+@pytest.mark.parametrize("slices", [0, 1, 3])
+@pytest.mark.parametrize("R,K,N", SHAPES)
+def test_epilogues_match_float64(device, R, K, N, slices):
+    if slices > K // 128:
+        pytest.skip("more slices than chunks")
+    gen = torch.Generator().manual_seed(R * 7 + K + N)
+    w = (torch.randn(R, K, generator=gen) * 0.05).bfloat16()
+    x = torch.randn(N, K, generator=gen).bfloat16()
+    res = torch.randn(N, R, generator=gen).bfloat16()
+    rstd = torch.rand(N, generator=gen) + 0.5
+    s = x.double() @ w.double().T                                  # exact products, float64 sums
+    bound = (x.double().abs() @ w.double().abs().T) * K * 2.0 ** -24  # fp32 accumulation error bound
+    wd, xd, rd, sd = w.to(device), x.to(device), res.to(device), rstd.to(device)
+
+    out, f32 = run(F32, wd, xd, slices=slices)
+    assert torch.all(out.cpu() == 7.0)                             # F32 writes only the fp32 output
+    f32 = f32.cpu().double()
+    assert (f32 - s).abs().le(bound + 1e-30).all()
+
+    def check_bf16(out, ref, prop, label):
+        """bf16(f(s_device)) against f(s): one bf16 rounding plus the propagated accumulation error `prop`."""
+        got = out.cpu().double().numpy()
+        ref, prop = ref.numpy(), prop.numpy()
+        assert np.all(np.abs(got - ref) <= bf16_ulp(ref) + prop + 1e-30), label
+
+    out, o32 = run(STORE, wd, xd, slices=slices)
+    check_bf16(out, s, bound, "store")
+    assert torch.all(o32.cpu() == 7.0)
+    out, o32 = run(RESID2, wd, xd, res=rd, slices=slices)
+    xsum = s + res.double()
+    check_bf16(out, xsum, bound + 2.0 ** -24 * xsum.abs(), "resid2 bf16")
+    assert (o32.cpu().double() - xsum).abs().le(bound + 2.0 ** -24 * xsum.abs() + 1e-30).all()
+    out, _ = run(RELU2, wd, xd, rstd=sd, slices=slices)
+    r = rstd.double()[:, None]
+    p = s * r
+    check_bf16(out, torch.relu(p) * p, 2 * p.abs() * r * bound + (r * bound) ** 2 + 2.0 ** -22 * p * p, "relu2")
+    out, _ = run(RESID, wd, xd, res=rd, slices=slices)
+    check_bf16(out, xsum, bound + 2.0 ** -24 * xsum.abs(), "resid")
+
+
+def test_deterministic_and_declines_bad_shapes(device):
+    gen = torch.Generator().manual_seed(5)
+    w = (torch.randn(1664, 6656, generator=gen) * 0.05).bfloat16().to(device)
+    x = torch.randn(128, 6656, generator=gen).bfloat16().to(device)
+    a = run(F32, w, x)[1]
+    b = run(F32, w, x)[1]
+    assert torch.equal(a, b)
+    lib = hip_library("decode")
+    out = torch.empty(256, 1664, dtype=torch.float32, device=device)
+    x2 = torch.zeros(129, 6656, dtype=torch.bfloat16, device=device)
+    for R, K, N, xx in ((1664, 6656, 129, x2), (1664, 6600, 128, x), (1662, 6656, 128, x)):
+        assert lib.dec_debug_stream_gemm(F32, pointer(w), R, K, pointer(xx), N, None, pointer(out), None, None, 1,
+                                         None, stream()) == -2
