@@ -49,7 +49,9 @@ int skinny_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, int S, h
 /* stream_gemm.hip: the same GEMM (SkinnyGemm operands, SG_* epilogues) with every global access range-checked by
  * buffer instructions. */
 bool stream_gemm_fits(int R, int K, int N);
-/* K-slices for (R, K): about 384 workgroups of 128 rows, at least two 128-wide chunks a slice. */
+/* K-slices for (R, K): at least stream_gemm_min_slices(K) (slices of at most four 128-wide chunks), more up to about
+ * 128 workgroups of 128 rows. */
+int stream_gemm_min_slices(int K);
 int stream_gemm_slices(int R, int K);
 /* Bytes of the partial sums of S slices (0 for S = 1). */
 long long stream_gemm_part_bytes(int R, int N, int S);

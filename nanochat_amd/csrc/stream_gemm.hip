@@ -6,17 +6,18 @@
  * range check turns any access outside an operand into a zero read or a dropped write (never a fault); the stores'
  * row and slot masks keep ragged tiles out of the neighbouring rows of the same array.
  *
- * Grid (ceil(R / 128) row blocks, S K-slices), 4 waves. A wave owns 32 weight rows (two 16-row MFMA tiles) and all
- * CT * 16 slot columns over its K-slice, walked in 128-wide chunks:
- *   - weights stream from HBM into registers two chunks ahead: lane (g = lane / 16, i = lane % 16) of tile t holds
- *     row 32 w + 16 t + i, bytes 64 j + 16 g of the chunk's 256 (piece j), so load instruction j covers 64
- *     contiguous bytes of each of 16 rows and MFMA j (v_mfma_f32_16x16x32_bf16) contracts k = 32 j .. 32 j + 31;
- *   - the chunk of x (CT * 16 slots x 128 k) is staged once per workgroup in LDS (double buffered; loaded two chunks
- *     ahead) and read as the MFMAs' B operand: slot row n's 16-byte block b is stored at block b ^ (n % 16), so the
- *     16 rows of one operand read fall in distinct banks.
- * Registers rotate by name (weights over three buffers, staged x over two: the loop is unrolled by six), so no copy
- * waits on a load; vector-memory counters retire in issue order, so a chunk only waits for the loads issued two
- * steps before it.
+ * Grid (ceil(R / 128) row blocks, S K-slices of at most GM_KC 128-wide chunks), 4 waves. A workgroup loads its whole
+ * slice at once and waits once (a slab: no software pipeline, every load is in flight together):
+ *   - the slots' x over the slice (CT * 16 slots x up to 512 k, up to 128 KiB) goes straight to LDS by buffer loads
+ *     with the LDS destination (16 bytes a lane, 1 KiB an instruction); slot row n's 16-byte block b lands at block
+ *     b ^ (n % 16) (each lane picks the global block that belongs at its LDS position), so the 16 rows of one MFMA
+ *     operand read fall in distinct banks;
+ *   - a wave owns 32 weight rows (two 16-row MFMA tiles) and loads all of them for the slice into registers: lane
+ *     (g = lane / 16, i = lane % 16) of tile t holds row 32 w + 16 t + i, bytes 64 j + 16 g of each chunk's 256
+ *     (piece j), so load instruction j covers 64 contiguous bytes of each of 16 rows and MFMA j
+ *     (v_mfma_f32_16x16x32_bf16) contracts k = 32 j .. 32 j + 31 of the chunk.
+ * Chunks past the slice are read at GM_PAST, beyond every operand's range (zeros, no memory access), so no load is
+ * conditional; the chunks are added in order.
  *
  * S = 1: the workgroup applies the epilogue itself (SkinnyGemm's SG_* kinds, nc_internal.h). S > 1: fp32 partial
  * sums to part[s][n][r], reduced in slice order (deterministic) by stream_gemm_reduce before the same epilogue.
@@ -34,7 +35,9 @@ constexpr int GM_WAVE_ROWS = 32;                        /* two 16-row MFMA tiles
 constexpr int GM_ROWS = GM_WAVE_ROWS * GM_WAVES;        /* weight rows per workgroup */
 constexpr int GM_CHUNK = 128;                           /* k per pipeline step */
 constexpr int GM_XROW = GM_CHUNK * 2;                   /* bytes of one staged slot row */
-constexpr int GM_TARGET_WGS = 384;                      /* split K until about this many workgroups */
+constexpr int GM_KC = 4;                                /* chunks per slice at most (x: 128 KiB of LDS) */
+constexpr int GM_TARGET_WGS = 128;                      /* more slices than the minimum until this many workgroups */
+constexpr int GM_PAST = 0x7FFF0000;   /* a byte offset past every operand's range (operands stay below it) */
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -61,6 +64,8 @@ __device__ __forceinline__ bool gm_live(const unsigned long long *mask, int n) {
 struct WChunk {
     u32x4 v[2][4];
 };
+
+typedef __attribute__((address_space(3))) void LdsPtr;
 
 /* The operand views of one launch. */
 struct GemmViews {
@@ -116,88 +121,66 @@ template <int CT, int EPI>
 __global__ void __launch_bounds__(GM_THREADS) stream_gemm_kernel(SkinnyGemm g, float *part, long long part_bytes,
                                                                   int S) {
     constexpr int NP = 16 * CT;   /* staged slot rows (buffer reads past N return zeros) */
-    __shared__ __align__(16) unsigned char xs[2][NP * GM_XROW];
+    __shared__ __align__(16) unsigned char xs[GM_KC][NP * GM_XROW];
     const GemmViews v = views(g, part, part_bytes);
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const int i16 = lane & 15, grp = lane >> 4;
     const int r0 = blockIdx.x * GM_ROWS + wave * GM_WAVE_ROWS;
     const int chunks = g.K / GM_CHUNK, s = blockIdx.y;
-    const int c_begin = s * chunks / S, c_end = (s + 1) * chunks / S;
+    const int c_begin = s * chunks / S, c_end = (s + 1) * chunks / S;   /* at most GM_KC chunks (host-checked) */
     const int rowb = g.K * 2;   /* bytes of a weight or slot row */
+
+    /* x: instruction i of chunk q fills LDS bytes [1024 i, 1024 i + 1024) of xs[q], slot rows 4 i .. 4 i + 3; the
+     * four waves take i = wave, wave + 4, ... */
+#pragma unroll
+    for (int q = 0; q < GM_KC; q++) {
+        const int c = c_begin + q;
+#pragma unroll
+        for (int k = 0; k < CT; k++) {
+            const int i = wave + 4 * k, n = 4 * i + grp, lb = i16 ^ (n & 15);
+            const int off = c < c_end ? n * rowb + c * GM_XROW + lb * 16 : GM_PAST;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(v.x, (LdsPtr *)&xs[q][i * 1024], 16, off, 0, 0, 0);
+        }
+    }
+    /* weights: all of the slice's chunks in registers */
+    const int woff0 = (r0 + i16) * rowb + grp * 16;
+    const int woff1 = woff0 + 16 * rowb;
+    WChunk f[GM_KC];
+#pragma unroll
+    for (int q = 0; q < GM_KC; q++) {
+        const int c = c_begin + q;
+        const int o0 = c < c_end ? woff0 + c * GM_XROW : GM_PAST, o1 = c < c_end ? woff1 + c * GM_XROW : GM_PAST;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            f[q].v[0][j] = bload16(v.w, o0 + 64 * j);
+            f[q].v[1][j] = bload16(v.w, o1 + 64 * j);
+        }
+    }
 
     f32x4 acc[2][CT];
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int ct = 0; ct < CT; ct++) acc[t][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    /* byte offset of this lane's piece 0 of chunk 0 in tile t (rows past R read zeros) */
-    const int woff0 = (r0 + i16) * rowb + grp * 16;
-    const int woff1 = woff0 + 16 * rowb;
-    auto load_w = [&](int c, WChunk &f) {
+    __syncthreads();   /* waits for the LDS loads of every wave */
+#pragma unroll
+    for (int q = 0; q < GM_KC; q++) {
+        if (c_begin + q >= c_end) break;
+        const unsigned char *stage = xs[q];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            f.v[0][j] = bload16(v.w, woff0 + c * GM_XROW + 64 * j);
-            f.v[1][j] = bload16(v.w, woff1 + c * GM_XROW + 64 * j);
-        }
-    };
-    /* staging: piece p = tid + 256 q (q < CT) is slot row p / 16, block p % 16, stored at block (p % 16) ^ (row % 16) */
-    auto load_x = [&](int c, u32x4 *x) {
+            const int blk = (4 * j + grp) ^ i16;   /* k block 4 j + g of slot row ct 16 + i16 */
+            u32x4 b[CT];
 #pragma unroll
-        for (int q = 0; q < CT; q++) {
-            const int p = tid + GM_THREADS * q, n = p >> 4, blk = p & 15;
-            x[q] = bload16(v.x, n * rowb + c * GM_XROW + blk * 16);
-        }
-    };
-    auto store_x = [&](int buf, const u32x4 *x) {
+            for (int ct = 0; ct < CT; ct++)
+                b[ct] = *reinterpret_cast<const u32x4 *>(stage + (ct * 16 + i16) * GM_XROW + (blk << 4));
+            const bf16x8 a0 = __builtin_bit_cast(bf16x8, f[q].v[0][j]);
+            const bf16x8 a1 = __builtin_bit_cast(bf16x8, f[q].v[1][j]);
 #pragma unroll
-        for (int q = 0; q < CT; q++) {
-            const int p = tid + GM_THREADS * q, n = p >> 4, blk = p & 15;
-            *reinterpret_cast<u32x4 *>(&xs[buf][n * GM_XROW + ((blk ^ (n & 15)) << 4)]) = x[q];
-        }
-    };
-
-    if (c_begin < c_end) {
-        u32x4 xa[CT], xb[CT];
-        WChunk f0, f1, f2;
-        load_x(c_begin, xa);
-        load_w(c_begin, f0);
-        if (c_begin + 1 < c_end) {
-            load_x(c_begin + 1, xb);
-            load_w(c_begin + 1, f1);
-        }
-        store_x(c_begin & 1, xa);
-        __syncthreads();
-        /* step c: the staged x(c) is in LDS buffer c & 1, xcur holds x(c + 1), xnext receives x(c + 2) */
-        auto step = [&](int c, const WChunk &use, WChunk &fill, const u32x4 *xcur, u32x4 *xnext) {
-            if (c + 2 < c_end) {
-                load_x(c + 2, xnext);
-                load_w(c + 2, fill);
+            for (int ct = 0; ct < CT; ct++) {
+                acc[0][ct] = mfma16x16x32(a0, __builtin_bit_cast(bf16x8, b[ct]), acc[0][ct]);
+                acc[1][ct] = mfma16x16x32(a1, __builtin_bit_cast(bf16x8, b[ct]), acc[1][ct]);
             }
-            const unsigned char *stage = xs[c & 1];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int blk = (4 * j + grp) ^ i16;   /* k block 4 j + g of slot row ct 16 + i16 */
-                const bf16x8 a0 = __builtin_bit_cast(bf16x8, use.v[0][j]);
-                const bf16x8 a1 = __builtin_bit_cast(bf16x8, use.v[1][j]);
-#pragma unroll
-                for (int ct = 0; ct < CT; ct++) {
-                    const bf16x8 b = __builtin_bit_cast(
-                        bf16x8, *reinterpret_cast<const u32x4 *>(stage + (ct * 16 + i16) * GM_XROW + (blk << 4)));
-                    acc[0][ct] = mfma16x16x32(a0, b, acc[0][ct]);
-                    acc[1][ct] = mfma16x16x32(a1, b, acc[1][ct]);
-                }
-            }
-            if (c + 1 < c_end) store_x((c + 1) & 1, xcur);
-            __syncthreads();
-        };
-        for (int c = c_begin; c < c_end; c += 6) {
-            step(c, f0, f2, xb, xa);
-            if (c + 1 < c_end) step(c + 1, f1, f0, xa, xb);
-            if (c + 2 < c_end) step(c + 2, f2, f1, xb, xa);
-            if (c + 3 < c_end) step(c + 3, f0, f2, xa, xb);
-            if (c + 4 < c_end) step(c + 4, f1, f0, xb, xa);
-            if (c + 5 < c_end) step(c + 5, f2, f1, xa, xb);
         }
     }
 
@@ -264,15 +247,18 @@ static hipError_t gm_launch_ct(const SkinnyGemm &g, int epi, float *part, long l
 bool stream_gemm_fits(int R, int K, int N) {
     /* every byte offset, including those of the rows and slots past R and N a tile covers, fits an int */
     return N >= 1 && N <= SG_MAX_N && K >= GM_CHUNK && K % GM_CHUNK == 0 && R >= 1 && R % 4 == 0 &&
-           (long long)(R + GM_ROWS) * K * 2 < (1LL << 31) && (long long)SG_MAX_N * K * 2 < (1LL << 31) &&
-           (long long)N * R * 4 < (1LL << 31);
+           (long long)(R + GM_ROWS) * K * 2 <= GM_PAST && (long long)SG_MAX_N * K * 2 <= GM_PAST &&
+           (long long)N * R * 4 <= GM_PAST;
 }
+
+int stream_gemm_min_slices(int K) { return (K / GM_CHUNK + GM_KC - 1) / GM_KC; }
 
 int stream_gemm_slices(int R, int K) {
     const int blocks = (R + GM_ROWS - 1) / GM_ROWS, chunks = K / GM_CHUNK;
-    int S = (GM_TARGET_WGS + blocks - 1) / blocks;
-    S = S > chunks / 2 ? chunks / 2 : S;   /* at least two chunks a slice */
-    return S < 1 ? 1 : S;
+    int S = stream_gemm_min_slices(K);
+    const int want = (GM_TARGET_WGS + blocks - 1) / blocks;
+    if (want > S) S = want > chunks ? chunks : want;
+    return S;
 }
 
 long long stream_gemm_part_bytes(int R, int N, int S) { return S > 1 ? (long long)S * N * R * 4 : 0; }
@@ -284,7 +270,7 @@ static bool part_fits(const SkinnyGemm &g, const float *part, long long part_byt
 }
 
 int stream_gemm(const SkinnyGemm &g, int epi, float *part, long long part_bytes, int S, hipStream_t stream) {
-    if (!stream_gemm_fits(g.R, g.K, g.N) || S < 1 || S > g.K / GM_CHUNK) return -2;
+    if (!stream_gemm_fits(g.R, g.K, g.N) || S < stream_gemm_min_slices(g.K) || S > g.K / GM_CHUNK) return -2;
     if (S > 1 && !part_fits(g, part, part_bytes, S)) return -2;
     if (epi < SG_STORE || epi > SG_F32) return -2;
     if (S == 1) {

@@ -38,11 +38,11 @@ def run(epi, w, x, res=None, rstd=None, slices=0):
     return out, out32
 
 
-@pytest.mark.parametrize("slices", [0, 1, 3])
+@pytest.mark.parametrize("slices", [0, 1, 3, 13])
 @pytest.mark.parametrize("R,K,N", SHAPES)
 def test_epilogues_match_float64(device, R, K, N, slices):
-    if slices > K // 128:
-        pytest.skip("more slices than chunks")
+    if slices > K // 128 or (slices and slices * 4 < K // 128):
+        pytest.skip("more slices than chunks, or slices of more than four chunks")
     gen = torch.Generator().manual_seed(R * 7 + K + N)
     w = (torch.randn(R, K, generator=gen) * 0.05).bfloat16()
     x = torch.randn(N, K, generator=gen).bfloat16()
