@@ -76,6 +76,11 @@ void *dec_create_slots(const int *cfg, const uint64_t *ptrs, const float *scal, 
 void dec_debug_logits(void *handle, float *out, int rows);
 void dec_debug_cache(void *handle, int layer, int b, int at, int n, uint8_t *k, uint8_t *v, float *scales);
 
+/* Whether a step over more than 64 slots runs as two concurrent lanes or as one (the default); whether the step's
+ * body replays captured graphs or launches its kernels one by one (the default). Both synchronize. */
+void dec_debug_set_split(void *handle, int on);
+void dec_debug_set_graphs(void *handle, int on);
+
 /* The decode step's skinny GEMM alone: out[n][r] = epilogue(sum_k x[n][k] w[r][k]), bf16 w [R][K] and x [N][K],
  * epi 0 bf16(s), 1 x = s + res: bf16 out and fp32 out_f32, 2 bf16(relu(p) p) with p = s rstd[n], 3 bf16(s + res),
  * 4 fp32 out_f32 = s; split over `slices` K-slices (0: the decoder's choice, dec_debug_gemm_slices) whose partial

@@ -207,8 +207,7 @@ __device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p
             }
         }
         float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-        mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+        mt = pair_max32(pair_max16(mt));   /* the column's max over the four row groups */
         const float mnew = fmaxf(st.m[t], mt);
         if (__any(mnew > st.m[t] + RESCALE_LOG2)) {
             const float alpha = mnew == st.m[t] ? 1.0f : __builtin_amdgcn_exp2f(st.m[t] - mnew);
@@ -375,8 +374,7 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         kb.lo[0] = kb.full_lo = begin;
         kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
         attend_pages<1, true>(a, a.block_table + (long long)b * a.max_pages, kvh, first, 2, last, kb, qb, st, lane);
-        st.l[0] += __shfl_xor(st.l[0], 16, WAVE);
-        st.l[0] += __shfl_xor(st.l[0], 32, WAVE);
+        st.l[0] = pair_sum32(pair_sum16(st.l[0]));
         const long long w0 = worker_of(us, P, W), w1 = worker_of(ue - 1, P, W);
         const int u = b * a.Hkv + kvh;
         if (w0 == w1) {  /* the whole unit is in this run */
@@ -504,8 +502,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     attend_pages<NT, true>(a, a.block_table + (long long)trow * a.max_pages, kvh, pg0, 2, pg1, kb, qb, st, lane);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        st.l[t] += __shfl_xor(st.l[t], 16, WAVE);
-        st.l[t] += __shfl_xor(st.l[t], 32, WAVE);
+        st.l[t] = pair_sum32(pair_sum16(st.l[t]));
         if (!live[t]) continue;
         uint16_t *dst = a.out + qrow[t] * HEAD_DIM;
         const float inv = 1.0f / st.l[t];

@@ -50,6 +50,7 @@ constexpr int MASK_BITS = 64;              /* slots per word of a slot mask */
 constexpr int MASK_WORDS = MAX_BATCH / MASK_BITS;
 constexpr int WORD_BITS = 32;              /* tokens per word of an allowed-token mask */
 constexpr int PREFILL_ROWS = 8192;         /* rows per dec_prefill call */
+constexpr int SPLIT_SLOTS = 64;            /* a step over more slots runs as two lanes (enqueue_body) */
 constexpr int GLOBAL_PTRS = 4, LAYER_PTRS = 8;
 constexpr int CHOICE_THREADS = 1024, CHOICE_WAVES = CHOICE_THREADS / WAVE;
 constexpr float SM_SCALE = 0.08838834764831845f;  /* 1 / sqrt(128) */
@@ -472,6 +473,15 @@ struct Acts {
     float *rstd;               /* [rows] */
 };
 
+/* Where a stretch of work runs: a stream with its own library handle and scratch, so two lanes can run at once. */
+struct Lane {
+    hipStream_t stream;
+    rocblas_handle blas;
+    void *lt_ws;                         /* hipBLASLt workspace (Decoder::lt_ws_bytes) */
+    void *attn_ws;                       /* decode-attention partials (Decoder::attn_ws_bytes) */
+    float *part;                         /* stream_gemm's split-K partial sums (Decoder::part_bytes) */
+};
+
 struct Decoder {
     int B, L, C, F, H, vocab, max_len, store, lazy, max_pages;
     long long slot_pages, layer_pages;   /* pages of the slots; pages of a layer's pool (slots + store) */
@@ -479,10 +489,12 @@ struct Decoder {
     const float *wte, *cos, *sin;
     const uint16_t *lm_head;
     std::vector<Layer> layer;
-    hipStream_t stream;
-    rocblas_handle blas;
+    hipStream_t stream;                  /* the caller's stream: every call is ordered on it */
+    Lane lane[2];                        /* lane 0 runs on `stream`; lane 1 on the decoder's own stream, forked from
+                                            and joined back into `stream` within a step */
+    hipEvent_t fork, join;
+    std::vector<hipEvent_t> attn_done;   /* [2 L]: lane h's attention of layer l finished */
     hipblasLtHandle_t lt;                /* hipBLASLt: the GEMMs' first choice (rocBLAS when it has no plan) */
-    void *lt_ws;
     size_t lt_ws_bytes;
     uint8_t *k_pages, *v_pages;          /* [L][layer_pages][H][2048] */
     float *kv_scale;                     /* [L][layer_pages][H][2][16] */
@@ -494,8 +506,7 @@ struct Decoder {
     uint32_t *allow;                     /* [B][vocab / 32] */
     float *logits, *probs;               /* [B][vocab] */
     Acts slot, row;
-    void *workspace;
-    size_t workspace_bytes;
+    size_t attn_ws_bytes;
     int32_t *rows;                       /* device [7][PREFILL_ROWS]: token, position, slot; run row0, count, slot,
                                             start */
     int32_t *staging;                    /* pinned host, as rows */
@@ -504,8 +515,10 @@ struct Decoder {
     uint32_t *host_allow;                /* pinned [B][vocab / 32] */
     int narrow;                          /* a step's rows: the highest active slot + 1 */
     bool streaming;                      /* decode-step GEMMs by stream_gemm (else the library GEMM) */
-    float *part;                         /* stream_gemm's split-K partial sums, for up to SG_MAX_N rows */
-    long long part_bytes;
+    long long part_bytes;                /* each lane's stream_gemm partials, for up to SG_MAX_N rows */
+    bool split;                          /* a step of more than SPLIT_SLOTS slots runs as two lanes */
+    bool graphs;                         /* the body replays a captured graph per (narrow, split) */
+    std::map<std::pair<int, int>, hipGraphExec_t> body_graphs;  /* nullptr: seen once, run eagerly */
     std::vector<void *> device_blocks;
 };
 
@@ -545,6 +558,20 @@ static Acts carve_acts(Decoder *d, size_t rows) {
     a.acc = (float *)take(rows * W * 4);
     a.rstd = (float *)take(rows * 4);
     return a;
+}
+
+/* The activations of rows b0 .. of a. */
+static Acts acts_from(const Decoder *d, const Acts &a, size_t b0) {
+    const size_t C = d->C, F = d->F, W = F > C ? F : C;
+    Acts r = a;
+    r.x0 = a.x0 + b0 * C;
+    r.x = a.x + b0 * C; r.xm = a.xm + b0 * C; r.h = a.h + b0 * C; r.hn = a.hn + b0 * C;
+    r.q = a.q + b0 * C; r.att = a.att + b0 * C; r.xo = a.xo + b0 * C;
+    r.qkv = a.qkv + b0 * 3 * C;
+    r.u = a.u + b0 * F;
+    r.acc = a.acc + b0 * W;
+    r.rstd = a.rstd + b0;
+    return r;
 }
 
 /* A hipBLASLt plan for one GEMM shape: column-major D (rows x n) = W^T (W stored [rows][cols], so a cols x rows
@@ -613,20 +640,20 @@ static void lt_release(Decoder *d) {
 /* out[n][rows] = in[n][cols] . W[rows][cols]^T: column-major rows x n = (W as cols x rows)^T (cols x n). resid
  * non-NULL: out = bf16(s + resid) by beta = 1 (one rounding of the fp32 sum). hipBLASLt's plan for the shape,
  * else rocBLAS gemm_ex. */
-static void gemm(Decoder *d, const uint16_t *w, int rows, int cols, const uint16_t *in, int n, void *out, bool f32,
-                 const uint16_t *resid = nullptr) {
+static void gemm(Decoder *d, const Lane &ln, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
+                 void *out, bool f32, const uint16_t *resid = nullptr) {
     if (n <= 0) return;
     const float alpha = 1.0f, beta = resid ? 1.0f : 0.0f;
     const LtPlan &p = lt_plan(d, rows, cols, n, f32);
     if (p.ok) {
         const hipblasStatus_t st = hipblasLtMatmul(d->lt, p.desc, &alpha, w, p.a, in, p.b, &beta,
                                                    resid ? (const void *)resid : out, p.c, out, p.c, &p.algo,
-                                                   d->lt_ws, d->lt_ws_bytes, d->stream);
+                                                   ln.lt_ws, d->lt_ws_bytes, ln.stream);
         if (st != HIPBLAS_STATUS_SUCCESS) die("hipblasLtMatmul", "failed", __LINE__);
         return;
     }
     const rocblas_datatype ot = f32 ? rocblas_datatype_f32_r : rocblas_datatype_bf16_r;
-    BLAS_CHECK(rocblas_gemm_ex(d->blas, rocblas_operation_transpose, rocblas_operation_none, rows, n, cols, &alpha, w,
+    BLAS_CHECK(rocblas_gemm_ex(ln.blas, rocblas_operation_transpose, rocblas_operation_none, rows, n, cols, &alpha, w,
                                rocblas_datatype_bf16_r, cols, in, rocblas_datatype_bf16_r, cols, &beta,
                                resid ? (const void *)resid : out, ot, rows, out, ot, rows, rocblas_datatype_f32_r,
                                rocblas_gemm_algo_standard, 0, 0));
@@ -649,20 +676,23 @@ static NormArgs norm_args(Decoder *d, int kind, const Acts &a, int rows, int32_t
 /* The row kernels' NJ: the fewest 512-element chunks covering C (C <= MAX_C). */
 constexpr int MAX_C = 8 * ROW_CHUNK;
 
-static void launch_norm(Decoder *d, const NormArgs &n) {
+static void launch_norm(const Lane &ln, const NormArgs &n) {
     const dim3 grid((n.rows + 3) / 4), block(256);
-    if (n.C <= 2 * ROW_CHUNK) hipLaunchKernelGGL(norm_kernel<2>, grid, block, 0, d->stream, n);
-    else if (n.C <= 4 * ROW_CHUNK) hipLaunchKernelGGL(norm_kernel<4>, grid, block, 0, d->stream, n);
-    else hipLaunchKernelGGL(norm_kernel<8>, grid, block, 0, d->stream, n);
+    if (n.C <= 2 * ROW_CHUNK) hipLaunchKernelGGL(norm_kernel<2>, grid, block, 0, ln.stream, n);
+    else if (n.C <= 4 * ROW_CHUNK) hipLaunchKernelGGL(norm_kernel<4>, grid, block, 0, ln.stream, n);
+    else hipLaunchKernelGGL(norm_kernel<8>, grid, block, 0, ln.stream, n);
 }
 
-static void launch_rstd(Decoder *d, const float *s, const uint16_t *xm, uint16_t *xo, float *rstd,
+static void launch_rstd(Decoder *d, const Lane &ln, const float *s, const uint16_t *xm, uint16_t *xo, float *rstd,
                         const unsigned long long *active, int rows) {
     const dim3 grid((rows + 3) / 4), block(256);
     const int C = d->C;
-    if (C <= 2 * ROW_CHUNK) hipLaunchKernelGGL(rstd_kernel<2>, grid, block, 0, d->stream, s, xm, xo, rstd, active, rows, C);
-    else if (C <= 4 * ROW_CHUNK) hipLaunchKernelGGL(rstd_kernel<4>, grid, block, 0, d->stream, s, xm, xo, rstd, active, rows, C);
-    else hipLaunchKernelGGL(rstd_kernel<8>, grid, block, 0, d->stream, s, xm, xo, rstd, active, rows, C);
+    if (C <= 2 * ROW_CHUNK)
+        hipLaunchKernelGGL(rstd_kernel<2>, grid, block, 0, ln.stream, s, xm, xo, rstd, active, rows, C);
+    else if (C <= 4 * ROW_CHUNK)
+        hipLaunchKernelGGL(rstd_kernel<4>, grid, block, 0, ln.stream, s, xm, xo, rstd, active, rows, C);
+    else
+        hipLaunchKernelGGL(rstd_kernel<8>, grid, block, 0, ln.stream, s, xm, xo, rstd, active, rows, C);
 }
 
 static uint8_t *layer_k(Decoder *d, int l) { return d->k_pages + (size_t)l * d->layer_pages * d->H * PAGE_BYTES; }
@@ -671,69 +701,154 @@ static float *layer_s(Decoder *d, int l) { return d->kv_scale + (size_t)l * d->l
 
 /* A GEMM with its epilogue: the weight-streaming MFMA GEMM when the rows fit it (a decode step's <= 128 slots), else
  * the library GEMM into fp32 or bf16 and the epilogue kernels. */
-static void gemm_epi(Decoder *d, int epi, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
-                     uint16_t *out, float *out_f32, const uint16_t *res, const float *rstd,
+static void gemm_epi(Decoder *d, const Lane &ln, int epi, const uint16_t *w, int rows, int cols, const uint16_t *in,
+                     int n, uint16_t *out, float *out_f32, const uint16_t *res, const float *rstd,
                      const unsigned long long *active) {
     if (n <= 0) return;
     if (d->streaming && stream_gemm_fits(rows, cols, n)) {
         const int S = stream_gemm_slices(rows, cols);
         SkinnyGemm g = {w, in, rows, cols, n, out, out_f32, res, rstd, active};
-        NC_CHECK(stream_gemm(g, epi, d->part, d->part_bytes, S, d->stream));
-        if (S > 1) NC_CHECK(stream_gemm_reduce(g, epi, d->part, d->part_bytes, S, d->stream));
+        NC_CHECK(stream_gemm(g, epi, ln.part, d->part_bytes, S, ln.stream));
+        if (S > 1) NC_CHECK(stream_gemm_reduce(g, epi, ln.part, d->part_bytes, S, ln.stream));
         return;
     }
     switch (epi) {
-    case SG_STORE: gemm(d, w, rows, cols, in, n, out, false); break;
-    case SG_RESID: gemm(d, w, rows, cols, in, n, out, false, res); break;
-    case SG_F32: gemm(d, w, rows, cols, in, n, out_f32, true); break;
+    case SG_STORE: gemm(d, ln, w, rows, cols, in, n, out, false); break;
+    case SG_RESID: gemm(d, ln, w, rows, cols, in, n, out, false, res); break;
+    case SG_F32: gemm(d, ln, w, rows, cols, in, n, out_f32, true); break;
     case SG_RESID2:  /* fp32 s; the rstd kernel adds the residual and writes out */
-        gemm(d, w, rows, cols, in, n, out_f32, true);
+        gemm(d, ln, w, rows, cols, in, n, out_f32, true);
         break;
     case SG_RELU2:
-        gemm(d, w, rows, cols, in, n, out_f32, true);
-        hipLaunchKernelGGL(relu2_kernel, dim3((rows / 4 + 255) / 256, n), dim3(256), 0, d->stream, out_f32, rstd, out,
+        gemm(d, ln, w, rows, cols, in, n, out_f32, true);
+        hipLaunchKernelGGL(relu2_kernel, dim3((rows / 4 + 255) / 256, n), dim3(256), 0, ln.stream, out_f32, rstd, out,
                            active, rows);
         break;
     }
 }
 
 /* The rest of a layer after its attention: o_proj + residual, the MLP. */
-static void mlp(Decoder *d, const Layer &ly, const Acts &a, int n, const unsigned long long *active) {
+static void mlp(Decoder *d, const Lane &ln, const Layer &ly, const Acts &a, int n, const unsigned long long *active) {
     const int C = d->C, F = d->F;
     const bool fused = d->streaming && stream_gemm_fits(C, C, n);
-    gemm_epi(d, SG_RESID2, ly.o, C, C, a.att, n, a.xo, a.acc, a.xm, nullptr, active);
-    launch_rstd(d, a.acc, fused ? nullptr : a.xm, a.xo, a.rstd, active, n);
-    gemm_epi(d, SG_RELU2, ly.fc, F, C, a.xo, n, a.u, a.acc, nullptr, a.rstd, active);
-    gemm_epi(d, SG_RESID, ly.proj, C, F, a.u, n, a.x, nullptr, a.xo, nullptr, active);
+    gemm_epi(d, ln, SG_RESID2, ly.o, C, C, a.att, n, a.xo, a.acc, a.xm, nullptr, active);
+    launch_rstd(d, ln, a.acc, fused ? nullptr : a.xm, a.xo, a.rstd, active, n);
+    gemm_epi(d, ln, SG_RELU2, ly.fc, F, C, a.xo, n, a.u, a.acc, nullptr, a.rstd, active);
+    gemm_epi(d, ln, SG_RESID, ly.proj, C, F, a.u, n, a.x, nullptr, a.xo, nullptr, active);
 }
 
-static void enqueue_body(Decoder *d) {
-    const int R = d->narrow, C = d->C;
-    if (R <= 0) return;
-    const Acts &a = d->slot;
-    NormArgs n = norm_args(d, NORM_EMBED, a, R, d->tokens, d->active);
-    n.pos = d->pos;
-    n.seq_lens = d->seq_lens;
-    n.num_new = d->num_new;
-    launch_norm(d, n);
-    for (int l = 0; l < d->L; l++) {
-        const Layer &ly = d->layer[l];
-        NormArgs r = norm_args(d, NORM_RESID, a, R, d->tokens, d->active);
-        r.in = l == 0 ? nullptr : a.x;
-        r.l1 = ly.resid;
-        r.l2 = ly.x0;
-        r.mixed = a.xm;
-        r.out = a.h;
-        launch_norm(d, r);
-        gemm_epi(d, SG_STORE, ly.qkv, 3 * C, C, a.h, R, a.qkv, nullptr, nullptr, nullptr, d->active);
-        NC_CHECK(append_rows(a.qkv, 3LL * C, R, d->H, d->H, d->pos, d->num_new, nullptr, ly.q_gain, ly.k_gain, d->cos,
-                             d->sin, d->max_len, a.q, d->block_table, d->max_pages, layer_k(d, l), layer_v(d, l),
-                             layer_s(d, l), (int)d->layer_pages, a.h, ly.ve, ly.ve_gate, d->tokens, C, d->stream));
-        NC_CHECK(nc_decode_attn_fp8(a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table, d->max_pages,
-                                    (int)d->layer_pages, d->seq_lens, d->max_len, R, d->H, d->H, ly.window, SM_SCALE, 0,
-                                    a.att, d->workspace, d->workspace_bytes, d->stream));
-        mlp(d, ly, a, R, d->active);
+/* Slots [b0, b0 + n) of a step (b0 a multiple of 64, so their active mask starts at word b0 / 64). */
+struct Part {
+    int b0, n;
+    Acts a;
+    const unsigned long long *active;
+};
+
+static Part step_part(Decoder *d, int b0, int n) {
+    return Part{b0, n, acts_from(d, d->slot, b0), d->active + b0 / MASK_BITS};
+}
+
+static void body_embed(Decoder *d, const Lane &ln, const Part &p) {
+    NormArgs n = norm_args(d, NORM_EMBED, p.a, p.n, d->tokens + p.b0, p.active);
+    n.pos = d->pos + p.b0;
+    n.seq_lens = d->seq_lens + p.b0;
+    n.num_new = d->num_new + p.b0;
+    launch_norm(ln, n);
+}
+
+/* Layer l up to its attention: the residual norm, qkv, the fused q/k norm + RoPE + fp8 append. */
+static void body_pre(Decoder *d, const Lane &ln, const Part &p, int l) {
+    const Layer &ly = d->layer[l];
+    const Acts &a = p.a;
+    const int C = d->C;
+    NormArgs r = norm_args(d, NORM_RESID, a, p.n, d->tokens + p.b0, p.active);
+    r.in = l == 0 ? nullptr : a.x;
+    r.l1 = ly.resid;
+    r.l2 = ly.x0;
+    r.mixed = a.xm;
+    r.out = a.h;
+    launch_norm(ln, r);
+    gemm_epi(d, ln, SG_STORE, ly.qkv, 3 * C, C, a.h, p.n, a.qkv, nullptr, nullptr, nullptr, p.active);
+    NC_CHECK(append_rows(a.qkv, 3LL * C, p.n, d->H, d->H, d->pos + p.b0, d->num_new + p.b0, nullptr, ly.q_gain,
+                         ly.k_gain, d->cos, d->sin, d->max_len, a.q, d->block_table + (size_t)p.b0 * d->max_pages,
+                         d->max_pages, layer_k(d, l), layer_v(d, l), layer_s(d, l), (int)d->layer_pages, a.h, ly.ve,
+                         ly.ve_gate, d->tokens + p.b0, C, ln.stream));
+}
+
+static void body_attn(Decoder *d, const Lane &ln, const Part &p, int l) {
+    NC_CHECK(nc_decode_attn_fp8(p.a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l),
+                                d->block_table + (size_t)p.b0 * d->max_pages, d->max_pages, (int)d->layer_pages,
+                                d->seq_lens + p.b0, d->max_len, p.n, d->H, d->H, d->layer[l].window, SM_SCALE, 0,
+                                p.a.att, ln.attn_ws, d->attn_ws_bytes, ln.stream));
+}
+
+/* The step's body. Up to SPLIT_SLOTS slots, one lane. More: two lanes, slots [0, b1) on lane 0 and [b1, narrow) on
+ * lane 1, forked from and joined into the caller's stream, with their attentions alternating (lane 1's attention
+ * of layer l after lane 0's, lane 0's of layer l + 1 after lane 1's of layer l): attention is bound by HBM bandwidth
+ * and the rest of a layer (norms, GEMMs over few rows, epilogues) by latency, so each half's attention runs while
+ * the other half works through the rest of its layer. */
+static void record_body(Decoder *d) {
+    const int R = d->narrow;
+    if (!d->split || R <= SPLIT_SLOTS) {
+        const Part p = step_part(d, 0, R);
+        const Lane &ln = d->lane[0];
+        body_embed(d, ln, p);
+        for (int l = 0; l < d->L; l++) {
+            body_pre(d, ln, p, l);
+            body_attn(d, ln, p, l);
+            mlp(d, ln, d->layer[l], p.a, p.n, p.active);
+        }
+        return;
     }
+    const int b1 = (R + 2 * MASK_BITS - 1) / (2 * MASK_BITS) * MASK_BITS;   /* half the rows, a multiple of 64 */
+    const Part p[2] = {step_part(d, 0, b1), step_part(d, b1, R - b1)};
+    const Lane *ln = d->lane;
+    HIP_CHECK(hipEventRecord(d->fork, ln[0].stream));
+    HIP_CHECK(hipStreamWaitEvent(ln[1].stream, d->fork, 0));
+    for (int h = 0; h < 2; h++) body_embed(d, ln[h], p[h]);
+    for (int l = 0; l < d->L; l++) {
+        hipEvent_t *done = &d->attn_done[2 * l];
+        body_pre(d, ln[0], p[0], l);
+        if (l > 0) HIP_CHECK(hipStreamWaitEvent(ln[0].stream, d->attn_done[2 * l - 1], 0));
+        body_attn(d, ln[0], p[0], l);
+        HIP_CHECK(hipEventRecord(done[0], ln[0].stream));
+        body_pre(d, ln[1], p[1], l);
+        HIP_CHECK(hipStreamWaitEvent(ln[1].stream, done[0], 0));
+        body_attn(d, ln[1], p[1], l);
+        HIP_CHECK(hipEventRecord(done[1], ln[1].stream));
+        for (int h = 0; h < 2; h++) mlp(d, ln[h], d->layer[l], p[h].a, p[h].n, p[h].active);
+    }
+    HIP_CHECK(hipEventRecord(d->join, ln[1].stream));
+    HIP_CHECK(hipStreamWaitEvent(ln[0].stream, d->join, 0));
+}
+
+/* The body as a graph (the reference captures its step too, decode.cu:893-902): one launch instead of a few hundred
+ * (two lanes: ~530 kernels and ~100 event edges a step). The first step of a given (narrow, split) runs eagerly, so
+ * the library plans and occupancy queries it makes happen outside a capture; the second captures it (thread-local
+ * mode, on the caller's stream, lane 1 joined through the fork event) and every later one replays it. The body
+ * records no memset, and its kernels read every per-step value (tokens, positions, masks) from device memory. */
+static void enqueue_body(Decoder *d) {
+    if (d->narrow <= 0) return;
+    if (!d->graphs) {
+        record_body(d);
+        return;
+    }
+    const auto key = std::make_pair(d->narrow, (int)d->split);
+    auto it = d->body_graphs.find(key);
+    if (it == d->body_graphs.end()) {
+        d->body_graphs.emplace(key, nullptr);
+        record_body(d);
+        return;
+    }
+    if (!it->second) {
+        hipGraph_t g = nullptr;
+        HIP_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+        record_body(d);
+        HIP_CHECK(hipStreamEndCapture(d->stream, &g));
+        HIP_CHECK(hipGraphInstantiate(&it->second, g, nullptr, nullptr, 0));
+        HIP_CHECK(hipGraphDestroy(g));
+    }
+    HIP_CHECK(hipGraphLaunch(it->second, d->stream));
 }
 
 static void enqueue_head(Decoder *d) {
@@ -743,8 +858,9 @@ static void enqueue_head(Decoder *d) {
         NormArgs n = norm_args(d, NORM_FINAL, a, R, d->tokens, d->active);
         n.in = a.x;
         n.out = a.hn;
-        launch_norm(d, n);
-        gemm_epi(d, SG_F32, d->lm_head, d->vocab, d->C, a.hn, R, nullptr, d->logits, nullptr, nullptr, d->active);
+        launch_norm(d->lane[0], n);
+        gemm_epi(d, d->lane[0], SG_F32, d->lm_head, d->vocab, d->C, a.hn, R, nullptr, d->logits, nullptr, nullptr,
+                 d->active);
         ChoiceArgs c = {d->logits, d->probs, d->active, d->allow, d->temperature, d->top_p, d->seed, d->first,
                         d->tokens, d->alt_tokens, d->pos, d->softcap, d->vocab, d->lazy};
         hipLaunchKernelGGL(choose_kernel, dim3(R), dim3(CHOICE_THREADS), 0, d->stream, c);
@@ -782,9 +898,18 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
         REQUIRE(!ly.ve == !ly.ve_gate, "a value-embedding table needs its gate, and the gate its table");
         d->layer.push_back(ly);
     }
-    BLAS_CHECK(rocblas_create_handle(&d->blas));
-    BLAS_CHECK(rocblas_set_stream(d->blas, d->stream));
-    BLAS_CHECK(rocblas_set_atomics_mode(d->blas, rocblas_atomics_not_allowed));
+    /* lane 0 is the caller's stream; lane 1 a stream of the decoder's own (default priority) */
+    d->lane[0].stream = d->stream;
+    HIP_CHECK(hipStreamCreateWithFlags(&d->lane[1].stream, hipStreamNonBlocking));
+    for (Lane &ln : d->lane) {
+        BLAS_CHECK(rocblas_create_handle(&ln.blas));
+        BLAS_CHECK(rocblas_set_stream(ln.blas, ln.stream));
+        BLAS_CHECK(rocblas_set_atomics_mode(ln.blas, rocblas_atomics_not_allowed));
+    }
+    HIP_CHECK(hipEventCreateWithFlags(&d->fork, hipEventDisableTiming));
+    HIP_CHECK(hipEventCreateWithFlags(&d->join, hipEventDisableTiming));
+    d->attn_done.resize(2 * d->L);
+    for (hipEvent_t &e : d->attn_done) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     if (hipblasLtCreate(&d->lt) != HIPBLAS_STATUS_SUCCESS) die("hipblasLtCreate", "failed", __LINE__);
     d->lt_ws_bytes = (size_t)32 << 20;
 
@@ -829,20 +954,28 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     d->slot = carve_acts(d, B);
     /* partials for the most rows a streamed GEMM takes: a step's slots and prefill's row blocks (up to SG_MAX_N rows,
      * more than the slots when B < SG_MAX_N) both call it */
-    long long part_bytes = 256;
+    d->streaming = false;   /* the step GEMMs stay on the library until the streamed path beats it */
+    /* measured at config 5 (128 slots, 26 layers): one lane eager 6.12 ms a step, one lane with graphs 6.2-6.3 ms,
+     * two lanes with graphs 6.6 ms: attention fills every CU, so the other lane's GEMMs cannot run beside it, and
+     * the host stays ahead of a 6 ms step. Both stay available (dec_debug_set_split / dec_debug_set_graphs). */
+    d->split = false;
+    d->graphs = false;
+    long long part_bytes = 0;
     const int C = d->C, F = d->F;
     const int shapes[5][2] = {{3 * C, C}, {C, C}, {F, C}, {C, F}, {d->vocab, C}};
     for (const auto &rk : shapes)
-        if (stream_gemm_fits(rk[0], rk[1], SG_MAX_N)) {
+        if (d->streaming && stream_gemm_fits(rk[0], rk[1], SG_MAX_N)) {
             const long long bytes = stream_gemm_part_bytes(rk[0], SG_MAX_N, stream_gemm_slices(rk[0], rk[1]));
             part_bytes = bytes > part_bytes ? bytes : part_bytes;
         }
-    d->part = (float *)device_alloc(d, (size_t)part_bytes);
     d->part_bytes = part_bytes;
-    d->lt_ws = device_alloc(d, d->lt_ws_bytes);
-    d->workspace_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1, 0);
-    REQUIRE(d->workspace_bytes > 0, "decode attention workspace");
-    d->workspace = device_alloc(d, d->workspace_bytes);
+    d->attn_ws_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1, 0);
+    REQUIRE(d->attn_ws_bytes > 0, "decode attention workspace");
+    for (Lane &ln : d->lane) {
+        ln.part = (float *)device_alloc(d, (size_t)part_bytes);
+        ln.lt_ws = device_alloc(d, d->lt_ws_bytes);
+        ln.attn_ws = device_alloc(d, d->attn_ws_bytes);
+    }
     HIP_CHECK(hipHostMalloc((void **)&d->staging, 7 * PREFILL_ROWS * sizeof(int32_t), hipHostMallocDefault));
     HIP_CHECK(hipHostMalloc((void **)&d->host_tokens, 2 * B * sizeof(int32_t), hipHostMallocDefault));
     HIP_CHECK(hipHostMalloc((void **)&d->host_allow, B * (d->vocab / WORD_BITS) * sizeof(uint32_t),
@@ -853,7 +986,6 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     HIP_CHECK(hipEventRecord(d->staged, d->stream));
     HIP_CHECK(hipStreamSynchronize(d->stream));
     d->narrow = 0;
-    d->streaming = false;   /* the step GEMMs stay on the library until the streamed path beats it */
     return d;
 }
 
@@ -905,7 +1037,8 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
                   *drslot = d->rows + 5 * PREFILL_ROWS, *dstart = d->rows + 6 * PREFILL_ROWS;
     const int C = d->C;
     const Acts &a = d->row;
-    launch_norm(d, norm_args(d, NORM_EMBED, a, n, dtok, nullptr));
+    const Lane &ln = d->lane[0];
+    launch_norm(ln, norm_args(d, NORM_EMBED, a, n, dtok, nullptr));
     for (int l = 0; l < d->L; l++) {
         const Layer &ly = d->layer[l];
         NormArgs r = norm_args(d, NORM_RESID, a, n, dtok, nullptr);
@@ -914,8 +1047,8 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
         r.l2 = ly.x0;
         r.mixed = a.xm;
         r.out = a.h;
-        launch_norm(d, r);
-        gemm(d, ly.qkv, 3 * C, C, a.h, n, a.qkv, false);
+        launch_norm(ln, r);
+        gemm(d, ln, ly.qkv, 3 * C, C, a.h, n, a.qkv, false);
         NC_CHECK(append_rows(a.qkv, 3LL * C, n, d->H, d->H, dpos, nullptr, dslot, ly.q_gain, ly.k_gain, d->cos, d->sin,
                              d->max_len, a.q, d->block_table, d->max_pages, layer_k(d, l), layer_v(d, l), layer_s(d, l),
                              (int)d->layer_pages, a.h, ly.ve, ly.ve_gate, dtok, C, d->stream));
@@ -923,7 +1056,7 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
         NC_CHECK(prefill_runs(a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table, d->max_pages,
                               (int)d->layer_pages, dstart, drow0, dcount, drslot, runs, max_count, d->H, d->H, ly.window,
                               SM_SCALE, a.att, d->stream));
-        mlp(d, ly, a, n, nullptr);
+        mlp(d, ln, ly, a, n, nullptr);
     }
 }
 
@@ -934,9 +1067,16 @@ static void destroy(Decoder *d) {
     hipHostFree(d->host_tokens);
     hipHostFree(d->host_allow);
     hipEventDestroy(d->staged);
+    hipStreamSynchronize(d->lane[1].stream);
+    for (auto &kv : d->body_graphs)
+        if (kv.second) hipGraphExecDestroy(kv.second);
     lt_release(d);
     hipblasLtDestroy(d->lt);
-    rocblas_destroy_handle(d->blas);
+    for (Lane &ln : d->lane) rocblas_destroy_handle(ln.blas);
+    hipStreamDestroy(d->lane[1].stream);
+    hipEventDestroy(d->fork);
+    hipEventDestroy(d->join);
+    for (hipEvent_t e : d->attn_done) hipEventDestroy(e);
     delete d;
 }
 
@@ -1084,6 +1224,18 @@ extern "C" int dec_debug_gemm(int epi, const void *w, int R, int K, const void *
 }
 
 extern "C" int dec_debug_gemm_slices(int R, int K) { return nc::skinny_gemm_slices(R, K); }
+
+extern "C" void dec_debug_set_split(void *handle, int on) {
+    Decoder *d = (Decoder *)handle;
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    d->split = on != 0;
+}
+
+extern "C" void dec_debug_set_graphs(void *handle, int on) {
+    Decoder *d = (Decoder *)handle;
+    HIP_CHECK(hipStreamSynchronize(d->stream));
+    d->graphs = on != 0;
+}
 
 extern "C" int dec_debug_stream_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out,
                                      float *out_f32, const void *res, const float *rstd, int slices, float *part,

@@ -52,6 +52,26 @@ __device__ __forceinline__ uint32_t e4m3_encode(float x) {
     return code | sign;
 }
 
+/* The pair of lanes (L, L ^ 32), or (L, L ^ 16), combined by one v_permlane32_swap / v_permlane16_swap (VALU, no
+ * LDS round trip): the swap hands every lane both values of its pair, the lower lane's first, so the two lanes of a
+ * pair compute the same result from the same operands in the same order. */
+__device__ __forceinline__ float pair_max32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_max16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_sum16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 /* Sum over the wave by an xor butterfly (offsets 32, 16, ..., 1): every lane ends with the same value. */
 __device__ __forceinline__ float wave_sum_butterfly(float v) {
 #pragma unroll

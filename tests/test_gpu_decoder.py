@@ -308,3 +308,80 @@ def test_steps_are_deterministic(device):
         finally:
             dec.close()
     assert np.array_equal(out[0], out[1])
+
+
+def test_two_lane_steps_match_one_lane_and_oracle(device):
+    """A step over more than 64 slots runs as two concurrent lanes (slots [0, 64) on the caller's stream, the rest on
+    the decoder's own, their attentions alternating): slots of both lanes match the oracle teacher-forced, the logits
+    match the one-lane step's within the fp32-order tolerance (the lanes' GEMMs and split-K attention add in another
+    order), the choices agree but at near-ties, and two two-lane runs are bit-identical."""
+    m, w, max_length = build(device, "tiny")
+    n = 100
+    lengths = [4 + (13 * b) % 37 for b in range(n)]
+    ids = prompts(lengths, m.vocab, seed=11)
+    runs = []
+    for split in (0, 1, 1):
+        dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=128)
+        try:
+            assert dec.batch >= n
+            dec.lib.dec_debug_set_split(dec.handle, split)
+            for b in range(n):
+                dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+            dec.prefill()
+            dec.flags[0, :n] = True
+            dec.set_active()
+            steps = []
+            for _ in range(2):
+                tokens = dec.step()
+                steps.append((dec.logits(n), tokens[:n].copy()))
+            runs.append(steps)
+        finally:
+            dec.close()
+    one, two, again = runs
+    for (la, ta), (lb, tb) in zip(two, again):
+        assert np.array_equal(la, lb) and np.array_equal(ta, tb)
+    (l1, t1), (l2, t2) = one[0], two[0]
+    scale = np.abs(l1).max()
+    err = np.abs(l1.astype(np.float64) - l2)
+    print(f"one lane vs two lanes: max {err.max():.3e} mean {err.mean():.3e} (scale {scale:.2f})", flush=True)
+    # the same bound as against the oracle: reordered fp32 sums flip bf16 roundings and fp8 codes downstream
+    assert err.max() <= LOGIT_MAX_REL * scale and err.mean() <= LOGIT_MEAN_REL * scale
+    for b in range(n):
+        if t1[b] != t2[b]:
+            assert abs(l2[b][t1[b]] - l2[b][t2[b]]) <= 2 * err.max(), b
+    orc = om.DecoderOracle(w, max_length)
+    rows = [(t, p, b) for b in range(n) for p, t in enumerate(ids[b][:-1])]
+    orc.body(*map(list, zip(*rows)), cache_only_last=True)
+    sample = [0, 1, 63, 64, 65, 99]
+    want = orc.head(orc.body([ids[b][-1] for b in sample], [lengths[b] - 1 for b in sample], sample))
+    check_logits(l2[sample], want, "two lanes step 0")
+
+
+@pytest.mark.parametrize("slots", [3, 100])
+def test_graph_replays_match_eager_steps(device, slots):
+    """With graphs on, the step's body replays a captured graph from its third step on (the first runs eagerly, the
+    second captures): every replay, each after the host's own work and a synchronization (dec_tokens), gives logits
+    and tokens bit-identical to the same steps launched kernel by kernel; one lane (3 slots) and two lanes (100)."""
+    m, w, max_length = build(device, "tiny")
+    lengths = [4 + (13 * b) % 37 for b in range(slots)]
+    ids = prompts(lengths, m.vocab, seed=12)
+    runs = []
+    for graphs in (0, 1):
+        dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=128)
+        try:
+            dec.lib.dec_debug_set_graphs(dec.handle, graphs)
+            dec.lib.dec_debug_set_split(dec.handle, 1)
+            for b in range(slots):
+                dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=8))
+            dec.prefill()
+            dec.flags[0, :slots] = True
+            dec.set_active()
+            steps = []
+            for _ in range(6):
+                tokens = dec.step()
+                steps.append((dec.logits(slots), tokens[:slots].copy()))
+            runs.append(steps)
+        finally:
+            dec.close()
+    for i, ((le, te), (lg, tg)) in enumerate(zip(*runs)):
+        assert np.array_equal(le, lg) and np.array_equal(te, tg), f"step {i}"
