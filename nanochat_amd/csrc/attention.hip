@@ -516,7 +516,214 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     }
 }
 
+/*
+ * Chunked prefill with the workgroup's pages staged in LDS. The four waves of a workgroup serve the same (sequence, KV
+ * head) and walk the same page pairs, so each pair is fetched once per workgroup, straight into LDS by
+ * global_load_lds (K 4 KiB, V 4 KiB, the pair's scales 256 B; each wave fetches a quarter), PF_AHEAD pairs ahead of
+ * the one being computed, with no registers held for the prefetch. The stage buffers are distinct LDS objects used in
+ * a fixed rotation (the loop is unrolled by PF_BUFS), so the compiler's wait before reading a stage covers that
+ * stage's fetches only; before the workgroup barrier each wave waits for its own fetches of the stage (the
+ * PF_FETCHES (PF_AHEAD - 1) issued after them may stay in flight) and for its LDS reads of the stage it is about to
+ * refill. The workgroup's block-table segment is read once into LDS. Each wave then runs the register kernel's pair
+ * step (scores, online softmax, PV) on operands read from LDS. Pairs are aligned to the workgroup's first page; a
+ * wave skips the pairs outside its own key range.
+ */
+constexpr int PF_AHEAD = 3;                    /* pairs in flight */
+constexpr int PF_BUFS = PF_AHEAD + 1;          /* stage buffers */
+constexpr int PF_FETCHES = 3;                  /* fetch instructions per wave per stage: K, V, scales */
+constexpr int PF_SCALES = 2 * 2 * PAGE * 4;   /* a pair's scales: [page][K 16, V 16] fp32 */
+constexpr int PF_STAGE = 2 * 2 * PAGE_BYTES;  /* K, then V, of two pages */
+constexpr int PF_TAB = 4096;                   /* block-table entries a workgroup can stage (65,536 keys) */
+
+struct PfStage {
+    unsigned char b[PF_STAGE];
+};
+struct PfScales {
+    float f[WAVES][PF_SCALES / 4];   /* each wave's copy of the pair's scales */
+};
+typedef __attribute__((address_space(3))) void LdsVoid;
+
+/* s_waitcnt: this wave's fetches of the oldest stage landed (the later stages' may stay in flight) and its LDS
+ * reads completed. Encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8]. */
+__device__ __forceinline__ void pf_wait_stage() {
+    constexpr int n = PF_FETCHES * (PF_AHEAD - 1);
+    __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
+/* A workgroup barrier without a memory fence (a fence would drain every fetch in flight); the empty asm statements
+ * keep the compiler from moving memory accesses across it. */
+__device__ __forceinline__ void pf_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+/* The fetches of stage s (logical pages pg0 + 2 s, + 1) into buffer st: wave w fetches K bytes [1024 w, + 1024) of the
+ * pair (pages a, a, b, b), the same of V, and all 256 scale bytes into its own slot (4 bytes a lane: no lane is
+ * masked off, so the compiler can count the fetches). Past the page range (s >= the workgroup's stages) it fetches
+ * the last pair again, so every wave always issues PF_FETCHES. */
+__device__ __forceinline__ void pf_fetch(const AttnArgs &a, const int *tab, int npages, int kvh, int s, PfStage &st,
+                                         PfScales &sc, int wave, int lane) {
+    const int last = (npages - 1) / 2;
+    const int ps = min(s, last);
+    int la = 2 * ps, lb = la + 1 < npages ? la + 1 : la;
+    int pa = tab[la], pb = tab[lb];
+    pa = (unsigned)pa < (unsigned)a.num_pages ? pa : 0;
+    pb = (unsigned)pb < (unsigned)a.num_pages ? pb : 0;
+    const long long ph = (long long)(wave < 2 ? pa : pb) * a.Hkv + kvh;
+    const int half = (wave & 1) * 1024;
+    __builtin_amdgcn_global_load_lds((const void *)(a.k_pages + ph * PAGE_BYTES + half + lane * 16),
+                                     (LdsVoid *)(st.b + wave * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(a.v_pages + ph * PAGE_BYTES + half + lane * 16),
+                                     (LdsVoid *)(st.b + 2 * 2048 + wave * 1024), 16, 0, 0);
+    const long long sh = (long long)(lane < 32 ? pa : pb) * a.Hkv + kvh;
+    __builtin_amdgcn_global_load_lds((const void *)(a.kv_scale + sh * 2 * PAGE + (lane & 31)), (LdsVoid *)sc.f[wave], 4,
+                                     0, 0);
+}
+
+/* One wave's step over stage s (buffer st) when the pair meets its key range. */
+template <int NT>
+__device__ __forceinline__ void pf_compute(const AttnArgs &a, const int *tab, int pg0, int npages, int s,
+                                           const PfStage &st, const PfScales &scs, int wpg0, int wpg1,
+                                           const KeyBounds<NT> &kb,
+                                           const bf16x8 (&qb)[NT][4], WaveState<NT> &st_w, int lane) {
+    const int la = 2 * s;
+    if (la >= npages || pg0 + la + 1 < wpg0 || pg0 + la >= wpg1) return;
+    const bool has_b = la + 1 < npages;
+    if ((unsigned)tab[la] >= (unsigned)a.num_pages || (has_b && (unsigned)tab[la + 1] >= (unsigned)a.num_pages))
+        st_w.bad = true;
+    const int g = lane >> 4;
+    PairAddr cur;
+    cur.lpa = pg0 + la;
+    cur.has_b = has_b;
+    cur.ha = cur.hb = 0;
+    const uint4 *k4 = reinterpret_cast<const uint4 *>(st.b);
+    const uint4 k0 = k4[lane], k1 = k4[64 + lane], k2 = k4[128 + lane], k3 = k4[192 + lane];
+    const float *sc = scs.f[threadIdx.x >> 6];
+    const float4 ksa = *reinterpret_cast<const float4 *>(sc + g * 4);
+    const float4 ksb = *reinterpret_cast<const float4 *>(sc + 2 * PAGE + g * 4);
+    f32x4 sa[NT], sb[NT];
+    page_scores<NT>(k0, k1, qb, sa);
+    page_scores<NT>(k2, k3, qb, sb);
+    const uint4 *v4 = reinterpret_cast<const uint4 *>(st.b + 2 * 2048);
+    PairRegs vr;
+    vr.a0 = v4[lane]; vr.a1 = v4[64 + lane]; vr.b0 = v4[128 + lane]; vr.b1 = v4[192 + lane];
+    vr.sa = *reinterpret_cast<const float4 *>(sc + PAGE + g * 4);
+    vr.sb = *reinterpret_cast<const float4 *>(sc + 3 * PAGE + g * 4);
+    pair_step<NT>(a, cur, sa, sb, ksa, ksb, vr, kb, st_w, lane);
+}
+
+/* Grid and columns as prefill_kernel. */
+template <int NT>
+__global__ void __launch_bounds__(256, 2) prefill_lds_kernel(AttnArgs a) {
+    __shared__ __align__(16) PfStage pb0, pb1, pb2, pb3;
+    __shared__ __align__(16) PfScales ps0, ps1, ps2, ps3;
+    __shared__ int tab[PF_TAB];
+    static_assert(PF_BUFS == 4, "the loop below rotates four stage buffers");
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int tpt = 16 / a.G, tpw = tpt * NT;
+    const int T = a.run_row0 ? a.run_count[b] : a.T;          /* this sequence's (run's) rows */
+    const int wg_t0 = blockIdx.x * WAVES * tpw;
+    if (wg_t0 >= T) return;                                    /* the whole workgroup */
+    const int t0 = wg_t0 + wave * tpw;
+    const bool on = t0 < T;                                    /* this wave has rows */
+    const long long row0 = a.run_row0 ? a.run_row0[b] : (long long)b * a.T;
+    const int trow = a.run_row0 ? a.run_slot[b] : b;
+    const int start = a.start_pos[b];
+    const int hg = c % a.G;
+    bool live[NT];
+    long long qrow[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int tok = t0 + t * tpt + c / a.G;
+        live[t] = on && c < tpt * a.G && tok < T;
+        qrow[t] = (row0 + tok) * a.Hq + kvh * a.G + hg;
+    }
+    if (start < 0 || (long long)start + T > (long long)a.max_pages * PAGE) {  /* past the block table: NaN */
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            if (live[t])
+                for (int d = g * 32; d < g * 32 + 32; d++) a.out[qrow[t] * HEAD_DIM + d] = (uint16_t)0x7FC0;
+        return;
+    }
+    /* the workgroup's pages [pg0, pg0 + npages) and this wave's [wpg0, wpg1) */
+    const int wg_last = min(wg_t0 + WAVES * tpw, T) - 1;
+    const int pg0 = (a.window >= 0 ? max(start + wg_t0 - a.window, 0) : 0) / PAGE;
+    const int npages = (start + wg_last) / PAGE + 1 - pg0;
+    const int t_last = on ? min(t0 + tpw, T) - 1 : t0;
+    const int wpg0 = (a.window >= 0 ? max(start + t0 - a.window, 0) : 0) / PAGE;
+    const int wpg1 = on ? (start + t_last) / PAGE + 1 : 0;
+    KeyBounds<NT> kb;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int pos = start + t0 + t * tpt + c / a.G;
+        kb.hi[t] = live[t] ? pos : -1;
+        kb.lo[t] = live[t] ? (a.window >= 0 ? max(pos - a.window, 0) : 0) : 0;
+    }
+    kb.full_hi = start + t0;
+    kb.full_lo = a.window >= 0 ? max(start + t_last - a.window, 0) : 0;
+    kb.written_hi = start + T - 1;
+
+    const int32_t *bt = a.block_table + (long long)trow * a.max_pages + pg0;
+    for (int i = threadIdx.x; i < npages; i += 256) tab[i] = bt[i];
+    bf16x8 qb[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++) load_q(live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr, g, qb[t]);
+    WaveState<NT> st;
+    state_init(st);
+    __syncthreads();   /* the table is in LDS (no fetch is in flight yet, so this fence drains nothing) */
+
+    const int stages = (npages + 1) / 2;
+    pf_fetch(a, tab, npages, kvh, 0, pb0, ps0, wave, lane);
+    pf_fetch(a, tab, npages, kvh, 1, pb1, ps1, wave, lane);
+    pf_fetch(a, tab, npages, kvh, 2, pb2, ps2, wave, lane);
+    /* step s: wait for stage s, barrier, refill the buffer read at step s - 1 with stage s + 3, compute stage s */
+    for (int s = 0; s < stages; s += PF_BUFS) {
+        pf_wait_stage(); pf_barrier();
+        pf_fetch(a, tab, npages, kvh, s + 3, pb3, ps3, wave, lane);
+        pf_compute<NT>(a, tab, pg0, npages, s, pb0, ps0, wpg0, wpg1, kb, qb, st, lane);
+        pf_wait_stage(); pf_barrier();
+        pf_fetch(a, tab, npages, kvh, s + 4, pb0, ps0, wave, lane);
+        pf_compute<NT>(a, tab, pg0, npages, s + 1, pb1, ps1, wpg0, wpg1, kb, qb, st, lane);
+        pf_wait_stage(); pf_barrier();
+        pf_fetch(a, tab, npages, kvh, s + 5, pb1, ps1, wave, lane);
+        pf_compute<NT>(a, tab, pg0, npages, s + 2, pb2, ps2, wpg0, wpg1, kb, qb, st, lane);
+        pf_wait_stage(); pf_barrier();
+        pf_fetch(a, tab, npages, kvh, s + 6, pb2, ps2, wave, lane);
+        pf_compute<NT>(a, tab, pg0, npages, s + 3, pb3, ps3, wpg0, wpg1, kb, qb, st, lane);
+    }
+    __builtin_amdgcn_s_waitcnt(0);   /* no fetch may land in LDS after the workgroup ends */
+    pf_barrier();
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        st.l[t] = pair_sum32(pair_sum16(st.l[t]));
+        if (!live[t]) continue;
+        uint16_t *dst = a.out + qrow[t] * HEAD_DIM;
+        const float inv = 1.0f / st.l[t];
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = st.bad ? NAN : st.o[t][d][i] * inv;
+            store_bf16x4(dst + 16 * d + 4 * g, v);
+        }
+    }
+}
+
 constexpr int PREFILL_TILES = 2;  /* 16-column tiles per prefill wave */
+
+/* Chunked prefill of `rows` rows of `seqs` sequences (or runs): the LDS-staged kernel when a sequence's block-table
+ * row fits its LDS segment, else the register kernel. */
+static void launch_prefill(const AttnArgs &a, int rows, int seqs, hipStream_t stream) {
+    const int tokens_per_block = WAVES * PREFILL_TILES * (16 / a.G);
+    const dim3 grid((rows + tokens_per_block - 1) / tokens_per_block, a.Hkv, seqs), block(256);
+    if (a.max_pages <= PF_TAB)
+        hipLaunchKernelGGL(prefill_lds_kernel<PREFILL_TILES>, grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL(prefill_kernel<PREFILL_TILES>, grid, block, 0, stream, a);
+}
 
 /* Prefill over runs for the decoder runtime: run b = rows run_row0[b] .. + run_count[b] of q/out ([rows][Hq][128])
  * at positions start_pos[b] + t of block-table row run_slot[b]; max_count bounds run_count. Arguments are checked
@@ -534,10 +741,7 @@ int prefill_runs(const uint16_t *q, const uint8_t *k_pages, const uint8_t *v_pag
     a.B = runs; a.T = max_count; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.window = window;
     a.scale_log2 = sm_scale * LOG2E;
     a.out = out;
-    const int tokens_per_block = WAVES * PREFILL_TILES * (16 / a.G);
-    hipLaunchKernelGGL(prefill_kernel<PREFILL_TILES>, dim3((max_count + tokens_per_block - 1) / tokens_per_block, Hkv,
-                                                           runs),
-                       dim3(256), 0, stream, a);
+    launch_prefill(a, max_count, runs, stream);
     return (int)hipGetLastError();
 }
 
@@ -641,8 +845,6 @@ extern "C" int nc_prefill_attn_fp8(const void *q, const void *k_pages, const voi
     a.B = B; a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.window = window;
     a.scale_log2 = sm_scale * LOG2E;
     a.out = (uint16_t *)out;
-    const int tokens_per_block = WAVES * PREFILL_TILES * (16 / a.G);
-    hipLaunchKernelGGL(prefill_kernel<PREFILL_TILES>, dim3((T + tokens_per_block - 1) / tokens_per_block, Hkv, B),
-                       dim3(256), 0, (hipStream_t)stream, a);
+    launch_prefill(a, T, B, (hipStream_t)stream);
     return (int)hipGetLastError();
 }
