@@ -290,6 +290,84 @@ __device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *b
     }
 }
 
+/* The same pass with the page ids read from LDS (tab[i] is the page of logical page tab0 + i, staged by the caller)
+ * and the pages read through buffer descriptors. Inside the loop the only vector-memory loads are the K/V stream and
+ * none is conditional: after the last pair the prefetch goes through zero-range descriptors (zeros, no memory access),
+ * so every wait the compiler places counts only the stream (a conditional or table load in the loop made each pair
+ * wait for every load in flight). */
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+/* A descriptor over `bytes` bytes from p, p the same in every lane (its halves are read from the first lane, so the
+ * descriptor lives in scalar registers and no load needs a per-lane loop). */
+__device__ __forceinline__ Rsrc page_rsrc(const void *p, int bytes) {
+    const unsigned long long u = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u), hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+    void *q = (void *)(((unsigned long long)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+/* non-temporal (aux bit 1: nt): page bytes are streamed once per launch */
+__device__ __forceinline__ uint4 bload_nt(Rsrc r, int off) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+    return uint4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ __forceinline__ PairAddr pair_addr_lds(const AttnArgs &a, const int *tab, int tab0, int kvh, int lpa, int end,
+                                                  bool &bad) {
+    PairAddr p;
+    p.lpa = lpa;
+    p.has_b = lpa + 1 < end;
+    int pa = __builtin_amdgcn_readfirstlane(tab[lpa - tab0]);
+    int pb = p.has_b ? __builtin_amdgcn_readfirstlane(tab[lpa + 1 - tab0]) : pa;
+    if ((unsigned)pa >= (unsigned)a.num_pages) { bad = true; pa = 0; }
+    if ((unsigned)pb >= (unsigned)a.num_pages) { bad = true; pb = 0; }
+    p.ha = (long long)pa * a.Hkv + kvh;
+    p.hb = (long long)pb * a.Hkv + kvh;
+    return p;
+}
+
+/* load_pair through descriptors of one (page, head) each; live false: zero-range descriptors (zeros, no access). */
+__device__ __forceinline__ void load_pair_b(const uint8_t *pages, const float *scales, const PairAddr &p, bool live,
+                                            int lane, PairRegs &r) {
+    const int pb = live ? PAGE_BYTES : 0, sb = live ? PAGE * 4 : 0;
+    const Rsrc A = page_rsrc(pages + p.ha * PAGE_BYTES, pb), B = page_rsrc(pages + p.hb * PAGE_BYTES, pb);
+    r.a0 = bload_nt(A, lane * 16);
+    r.a1 = bload_nt(A, 1024 + lane * 16);
+    r.b0 = bload_nt(B, lane * 16);
+    r.b1 = bload_nt(B, 1024 + lane * 16);
+    const uint4 sa = bload_nt(page_rsrc(scales + p.ha * 2 * PAGE, sb), (lane >> 4) * 16);
+    const uint4 sbv = bload_nt(page_rsrc(scales + p.hb * 2 * PAGE, sb), (lane >> 4) * 16);
+    r.sa = float4{__uint_as_float(sa.x), __uint_as_float(sa.y), __uint_as_float(sa.z), __uint_as_float(sa.w)};
+    r.sb = float4{__uint_as_float(sbv.x), __uint_as_float(sbv.y), __uint_as_float(sbv.z), __uint_as_float(sbv.w)};
+}
+
+template <int NT>
+__device__ __forceinline__ void attend_pages_lds(const AttnArgs &a, const int *tab, int tab0, int kvh, int lpa0,
+                                                 int end, const KeyBounds<NT> &kb, const bf16x8 (&qb)[NT][4],
+                                                 WaveState<NT> &st, int lane) {
+    lpa0 = __builtin_amdgcn_readfirstlane(lpa0);
+    end = __builtin_amdgcn_readfirstlane(end);
+    if (lpa0 >= end) return;
+    PairAddr cur = pair_addr_lds(a, tab, tab0, kvh, lpa0, end, st.bad);
+    PairRegs kr, vr;
+    load_pair_b(a.k_pages, a.kv_scale, cur, true, lane, kr);
+    load_pair_b(a.v_pages, a.kv_scale + PAGE, cur, true, lane, vr);
+    for (int lpa = lpa0; lpa < end; lpa += 2) {
+        const bool more = lpa + 2 < end;
+        const PairAddr nxt = pair_addr_lds(a, tab, tab0, kvh, more ? lpa + 2 : lpa, end, st.bad);
+        f32x4 sa[NT], sb[NT];
+        page_scores<NT>(kr.a0, kr.a1, qb, sa);
+        page_scores<NT>(kr.b0, kr.b1, qb, sb);
+        const float4 ksa = kr.sa, ksb = kr.sb;
+        load_pair_b(a.k_pages, a.kv_scale, nxt, more, lane, kr);
+        pair_step<NT>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
+        load_pair_b(a.v_pages, a.kv_scale + PAGE, nxt, more, lane, vr);
+        cur = nxt;
+    }
+}
+
+constexpr int DEC_TAB = 256;   /* block-table entries a decode wave stages at a time */
+
 /* Key range [begin, p] of a sequence of L keys and its logical pages [pg0, pg0 + npages); npages = 0 for an
  * inactive sequence (L <= 0) or one the block table cannot hold (its output is NaN). */
 __device__ __forceinline__ int decode_pages(const AttnArgs &a, int L, int &begin, int &pg0) {
@@ -323,6 +401,7 @@ constexpr int MAX_DECODE_BATCH = 4096;  /* sequences per decode launch (the LDS 
  */
 __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
     extern __shared__ long long sh_cum[];  /* [B + 1]: pages of the units of sequences < b */
+    __shared__ int dec_tab[WAVES][DEC_TAB];  /* each wave's staged block-table entries */
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     if (wave == 0) {  /* exclusive prefix over sequences of Hkv * pages, 64 sequences per step */
@@ -373,7 +452,15 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         KeyBounds<1> kb;
         kb.lo[0] = kb.full_lo = begin;
         kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
-        attend_pages<1, true>(a, a.block_table + (long long)b * a.max_pages, kvh, first, 2, last, kb, qb, st, lane);
+        const int32_t *bt = a.block_table + (long long)b * a.max_pages;
+        int *tab = dec_tab[wave];
+        for (int c0 = first; c0 < last; c0 += DEC_TAB) {   /* stage the table entries, then stream the pages */
+            const int c1 = min(c0 + DEC_TAB, last);
+#pragma unroll
+            for (int i = 0; i < DEC_TAB / WAVE; i++)
+                if (c0 + i * WAVE + lane < c1) tab[i * WAVE + lane] = bt[c0 + i * WAVE + lane];
+            attend_pages_lds<1>(a, tab, c0, kvh, c0, c1, kb, qb, st, lane);
+        }
         st.l[0] = pair_sum32(pair_sum16(st.l[0]));
         const long long w0 = worker_of(us, P, W), w1 = worker_of(ue - 1, P, W);
         const int u = b * a.Hkv + kvh;
