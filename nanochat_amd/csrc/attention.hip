@@ -290,7 +290,7 @@ __device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *b
     }
 }
 
-/* The same pass with the page ids read from LDS (tab[i] is the page of logical page tab0 + i, staged by the caller)
+/* The same pass with the page ids staged in registers by the caller (entry i is the page of logical page tab0 + i)
  * and the pages read through buffer descriptors. Inside the loop the only vector-memory loads are the K/V stream and
  * none is conditional: after the last pair the prefetch goes through zero-range descriptors (zeros, no memory access),
  * so every wait the compiler places counts only the stream (a conditional or table load in the loop made each pair
@@ -312,13 +312,26 @@ __device__ __forceinline__ uint4 bload_nt(Rsrc r, int off) {
     return uint4{v[0], v[1], v[2], v[3]};
 }
 
-__device__ __forceinline__ PairAddr pair_addr_lds(const AttnArgs &a, const int *tab, int tab0, int kvh, int lpa, int end,
-                                                  bool &bad) {
+/* A wave's staged block-table entries: lane j of v[q] holds entry 64 q + j (DEC_TAB = 256 entries). Entry e is read
+ * by v_readlane into a scalar register: no vector register or LDS access in the pair loop. */
+struct TabRegs {
+    int v[4];
+};
+
+__device__ __forceinline__ int tab_entry(const TabRegs &t, int e) {
+    const int j = e & (WAVE - 1), q = e >> 6;
+    const int r0 = __builtin_amdgcn_readlane(t.v[0], j), r1 = __builtin_amdgcn_readlane(t.v[1], j);
+    const int r2 = __builtin_amdgcn_readlane(t.v[2], j), r3 = __builtin_amdgcn_readlane(t.v[3], j);
+    return q == 0 ? r0 : q == 1 ? r1 : q == 2 ? r2 : r3;
+}
+
+__device__ __forceinline__ PairAddr pair_addr_tab(const AttnArgs &a, const TabRegs &tab, int tab0, int kvh, int lpa,
+                                                  int end, bool &bad) {
     PairAddr p;
     p.lpa = lpa;
     p.has_b = lpa + 1 < end;
-    int pa = __builtin_amdgcn_readfirstlane(tab[lpa - tab0]);
-    int pb = p.has_b ? __builtin_amdgcn_readfirstlane(tab[lpa + 1 - tab0]) : pa;
+    int pa = tab_entry(tab, lpa - tab0);
+    int pb = p.has_b ? tab_entry(tab, lpa + 1 - tab0) : pa;
     if ((unsigned)pa >= (unsigned)a.num_pages) { bad = true; pa = 0; }
     if ((unsigned)pb >= (unsigned)a.num_pages) { bad = true; pb = 0; }
     p.ha = (long long)pa * a.Hkv + kvh;
@@ -341,32 +354,51 @@ __device__ __forceinline__ void load_pair_b(const uint8_t *pages, const float *s
     r.sb = float4{__uint_as_float(sbv.x), __uint_as_float(sbv.y), __uint_as_float(sbv.z), __uint_as_float(sbv.w)};
 }
 
+/* One pair from registers already loaded: scores, softmax, PV. */
 template <int NT>
-__device__ __forceinline__ void attend_pages_lds(const AttnArgs &a, const int *tab, int tab0, int kvh, int lpa0,
+__device__ __forceinline__ void pair_from_regs(const AttnArgs &a, const PairAddr &cur, const PairRegs &kr,
+                                               PairRegs &vr, const KeyBounds<NT> &kb, const bf16x8 (&qb)[NT][4],
+                                               WaveState<NT> &st, int lane) {
+    f32x4 sa[NT], sb[NT];
+    page_scores<NT>(kr.a0, kr.a1, qb, sa);
+    page_scores<NT>(kr.b0, kr.b1, qb, sb);
+    pair_step<NT>(a, cur, sa, sb, kr.sa, kr.sb, vr, kb, st, lane);
+}
+
+/* Two register sets rotate by name (the loop is unrolled by two): a pair's K and V are issued as the pair before it
+ * starts computing, so a whole pair's loads stay in flight behind every pair's math and no copy waits on a load. */
+template <int NT>
+__device__ __forceinline__ void attend_pages_tab(const AttnArgs &a, const TabRegs &tab, int tab0, int kvh, int lpa0,
                                                  int end, const KeyBounds<NT> &kb, const bf16x8 (&qb)[NT][4],
                                                  WaveState<NT> &st, int lane) {
+    /* wave-uniform in scalar registers, so a pair's address math is scalar and borrows no vector register a load in
+     * flight still owns */
     lpa0 = __builtin_amdgcn_readfirstlane(lpa0);
     end = __builtin_amdgcn_readfirstlane(end);
+    kvh = __builtin_amdgcn_readfirstlane(kvh);
+    tab0 = __builtin_amdgcn_readfirstlane(tab0);
     if (lpa0 >= end) return;
-    PairAddr cur = pair_addr_lds(a, tab, tab0, kvh, lpa0, end, st.bad);
-    PairRegs kr, vr;
-    load_pair_b(a.k_pages, a.kv_scale, cur, true, lane, kr);
-    load_pair_b(a.v_pages, a.kv_scale + PAGE, cur, true, lane, vr);
-    for (int lpa = lpa0; lpa < end; lpa += 2) {
-        const bool more = lpa + 2 < end;
-        const PairAddr nxt = pair_addr_lds(a, tab, tab0, kvh, more ? lpa + 2 : lpa, end, st.bad);
-        f32x4 sa[NT], sb[NT];
-        page_scores<NT>(kr.a0, kr.a1, qb, sa);
-        page_scores<NT>(kr.b0, kr.b1, qb, sb);
-        const float4 ksa = kr.sa, ksb = kr.sb;
-        load_pair_b(a.k_pages, a.kv_scale, nxt, more, lane, kr);
-        pair_step<NT>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
-        load_pair_b(a.v_pages, a.kv_scale + PAGE, nxt, more, lane, vr);
-        cur = nxt;
+    PairAddr c0 = pair_addr_tab(a, tab, tab0, kvh, lpa0, end, st.bad), c1;
+    PairRegs k0, v0, k1, v1;
+    load_pair_b(a.k_pages, a.kv_scale, c0, true, lane, k0);
+    load_pair_b(a.v_pages, a.kv_scale + PAGE, c0, true, lane, v0);
+    for (int lpa = lpa0;; lpa += 4) {
+        const bool more1 = lpa + 2 < end;
+        c1 = pair_addr_tab(a, tab, tab0, kvh, more1 ? lpa + 2 : lpa, end, st.bad);
+        load_pair_b(a.k_pages, a.kv_scale, c1, more1, lane, k1);
+        load_pair_b(a.v_pages, a.kv_scale + PAGE, c1, more1, lane, v1);
+        pair_from_regs<NT>(a, c0, k0, v0, kb, qb, st, lane);
+        if (!more1) break;
+        const bool more0 = lpa + 4 < end;
+        c0 = pair_addr_tab(a, tab, tab0, kvh, more0 ? lpa + 4 : lpa + 2, end, st.bad);
+        load_pair_b(a.k_pages, a.kv_scale, c0, more0, lane, k0);
+        load_pair_b(a.v_pages, a.kv_scale + PAGE, c0, more0, lane, v0);
+        pair_from_regs<NT>(a, c1, k1, v1, kb, qb, st, lane);
+        if (!more0) break;
     }
 }
 
-constexpr int DEC_TAB = 256;   /* block-table entries a decode wave stages at a time */
+constexpr int DEC_TAB = 256;   /* block-table entries a decode wave stages at a time (TabRegs) */
 
 /* Key range [begin, p] of a sequence of L keys and its logical pages [pg0, pg0 + npages); npages = 0 for an
  * inactive sequence (L <= 0) or one the block table cannot hold (its output is NaN). */
@@ -401,7 +433,6 @@ constexpr int MAX_DECODE_BATCH = 4096;  /* sequences per decode launch (the LDS 
  */
 __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
     extern __shared__ long long sh_cum[];  /* [B + 1]: pages of the units of sequences < b */
-    __shared__ int dec_tab[WAVES][DEC_TAB];  /* each wave's staged block-table entries */
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     if (wave == 0) {  /* exclusive prefix over sequences of Hkv * pages, 64 sequences per step */
@@ -453,13 +484,13 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         kb.lo[0] = kb.full_lo = begin;
         kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
         const int32_t *bt = a.block_table + (long long)b * a.max_pages;
-        int *tab = dec_tab[wave];
         for (int c0 = first; c0 < last; c0 += DEC_TAB) {   /* stage the table entries, then stream the pages */
             const int c1 = min(c0 + DEC_TAB, last);
+            TabRegs tab;
 #pragma unroll
             for (int i = 0; i < DEC_TAB / WAVE; i++)
-                if (c0 + i * WAVE + lane < c1) tab[i * WAVE + lane] = bt[c0 + i * WAVE + lane];
-            attend_pages_lds<1>(a, tab, c0, kvh, c0, c1, kb, qb, st, lane);
+                tab.v[i] = c0 + i * WAVE + lane < c1 ? bt[c0 + i * WAVE + lane] : 0;
+            attend_pages_tab<1>(a, tab, c0, kvh, c0, c1, kb, qb, st, lane);
         }
         st.l[0] = pair_sum32(pair_sum16(st.l[0]));
         const long long w0 = worker_of(us, P, W), w1 = worker_of(ue - 1, P, W);
