@@ -10,13 +10,15 @@ value = algorithmic HBM bytes of the step / step time (GB/s). Attention bytes pe
 (n + 1) * 264 (fp8 K + V and two fp32 scales per key) + G * 128 * 2 * 2 (q in, out) + ceil((n + 1) / 16) * 4
 (block table); the append adds (Hq + 2 Hkv) * 256 read and Hq * 256 + Hkv * 264 written per token.
 
-    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4|c5] [--pages-per-worker P] [--cpu-seqs S]
+    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4|c5|ve] [--pages-per-worker P] [--cpu-seqs S]
                     [--no-e2e]
 
 A decode workload's line also carries the metric's second half, `decode_tokens_per_s`: config 5 end to end
 (below), unless --no-e2e.
 
 --workload c4 times the chunked-prefill step instead (TFLOP/s against the 2.5 PFLOP/s bf16 dense MFMA peak).
+--workload ve times the training-side value-embedding gate forward and backward (nc_ve_forward, nc_ve_backward) at
+the reference's d24 shape (GB/s of algorithmic bytes against 8 TB/s).
 --workload c5 runs the end-to-end decoder (libnanochat_decode.so through the dec_* ABI): a random-init 26-layer
 d1664 model, 128 random 2048-token prompts prefilled, then 512 greedy steps; value = decode tokens/s.
 """
@@ -158,6 +160,117 @@ def bench_prefill(args, w):
     }
 
 
+VE_SHAPE = {"rows": 65536, "heads": 6, "vocab": 65536}   # reference d24 (C = 768), 32 x 2048 tokens
+
+
+def ve_bytes(rows, heads, distinct):
+    """Algorithmic HBM bytes of the value-embedding gate: forward reads n, v, idx and each distinct table row once,
+    writes out and gate; backward reads dout, gate, ids, order and each distinct table row, writes dn and dz, and
+    reads and writes each distinct dtable row."""
+    C = heads * 128
+    fwd = rows * (2 * C + 2 * C + 4 + 2 * C + 4 * heads) + distinct * 4 * C
+    bwd = rows * (2 * C + 4 * heads + 4 + 8 + 2 * C + 2 * heads) + distinct * (4 * C + 8 * C)
+    return fwd, bwd
+
+
+def bench_ve(args):
+    """The training-side value-embedding gate (nc_ve_forward, nc_ve_backward) at the reference's d24 shape."""
+    import numpy as np
+    import torch
+
+    from nanochat_amd.native import check, hip_library, pointer, stream
+
+    dev = torch.device("cuda:0")
+    rows, H, V = VE_SHAPE["rows"], VE_SHAPE["heads"], VE_SHAPE["vocab"]
+    C = H * 128
+    gen = torch.Generator().manual_seed(0)
+    qkv = torch.randn(rows, 3 * C, generator=gen).bfloat16().to(dev)
+    n = torch.randn(rows, C, generator=gen).bfloat16().to(dev)
+    table = torch.randn(V, C, generator=gen).to(dev)
+    w = (torch.randn(H, C, generator=gen) * 0.05).to(dev)
+    idx = torch.randint(0, V, (rows,), generator=gen, dtype=torch.int32)
+    distinct = int(torch.unique(idx).numel())
+    ids, order = torch.sort(idx.to(torch.int64), stable=True)
+    idx, ids, order = idx.to(dev), ids.to(torch.int32).to(dev), order.to(dev)
+    dqkv = torch.randn(rows, 3 * C, generator=gen).bfloat16().to(dev)
+    out = torch.empty(rows, C, dtype=torch.bfloat16, device=dev)
+    gate = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    dn, dz = torch.empty_like(out), torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
+    dtable = torch.zeros_like(table)
+    lib = hip_library()
+    v, dout = qkv[:, 2 * C:], dqkv[:, 2 * C:]
+
+    def fwd():
+        check(lib.nc_ve_forward(pointer(n), pointer(v), qkv.stride(0), pointer(idx), pointer(table), V, pointer(w),
+                                pointer(out), pointer(gate), rows, H, stream()))
+
+    def bwd():
+        check(lib.nc_ve_backward(pointer(dout), dqkv.stride(0), pointer(ids), pointer(order), pointer(table), V,
+                                 pointer(w), pointer(gate), pointer(dn), pointer(dtable), pointer(dz), rows, H,
+                                 stream()))
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        for a, b in evs:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return sorted(a.elapsed_time(b) for a, b in evs)
+
+    f_ms, b_ms = timed(fwd), timed(bwd)
+    fb, bb = ve_bytes(rows, H, distinct)
+    f_med, b_med = f_ms[len(f_ms) // 2], b_ms[len(b_ms) // 2]
+    f_gbs, b_gbs = fb / (f_med * 1e-3) / 1e9, bb / (b_med * 1e-3) / 1e9
+    total = (fb + bb) / ((f_med + b_med) * 1e-3) / 1e9
+    result = {
+        "metric": "value-embedding gate forward + backward HBM GB/s", "value": round(total, 2), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(f_med + b_med, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 activations, fp32 table/gate weights, fp32 accumulation",
+        "data": "synthetic (seeded N(0,1) bf16 rows, uniform random tokens)",
+        "config": {"workload": f"ve: {rows} rows (32 x 2048 tokens), H = {H} (C = {C}), vocab {V}, "
+                               f"{distinct} distinct tokens", "rows": rows, "heads": H, "vocab": V},
+        "forward": {"ms_median": round(f_med, 5), "bytes": fb, "gbs": round(f_gbs, 1),
+                    "frac": round(f_gbs / HBM_PEAK_GBS, 4)},
+        "backward": {"ms_median": round(b_med, 5), "bytes": bb, "gbs": round(b_gbs, 1),
+                     "frac": round(b_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(total, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(total / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "ve_forward_kernel<6> + ve_backward_kernel<6>"},
+    }
+    if args.cpu_seqs > 0:
+        result["cpu_baseline"] = ve_cpu_baseline(qkv, n, table, w, idx, dqkv, rows=rows)
+    return result
+
+
+def ve_cpu_baseline(qkv, n, table, w, idx, dqkv, rows):
+    """The oracle (numpy, float64 sums) on the first `rows` rows of the same inputs: forward and backward."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import ve_gate as ov
+
+    cores = min(16, os.cpu_count() or 1)
+    H, C = w.shape[0], w.shape[1]
+    nn = n[:rows].float().cpu().numpy()
+    vv = qkv[:rows, 2 * C:].float().cpu().numpy()
+    dd = dqkv[:rows, 2 * C:].float().cpu().numpy()
+    tab, ww = table.cpu().numpy(), w.cpu().numpy()
+    ii = idx[:rows].cpu().numpy().astype(np.int64)
+    order = np.argsort(ii, kind="stable")
+    with threadpool_limits(limits=cores):
+        t0 = time.perf_counter()
+        _, g = ov.ve_forward(nn, vv, ii, tab, ww)
+        ov.ve_backward(dd, ii[order], order, tab, ww, g.astype(np.float32))
+        dt = time.perf_counter() - t0
+    fb, bb = ve_bytes(rows, H, len(np.unique(ii)))
+    return {"value": round((fb + bb) / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"oracle forward + backward (numpy) of the first {rows} of the rows, {dt:.2f} s"}
+
+
 def model_decode_bytes(w, positions):
     """HBM bytes a decode step must read: every slot's cached keys (264 B per key per head per layer, positions
     0..p), the GEMM weights and lm_head in bf16."""
@@ -296,6 +409,9 @@ def main():
         sys.exit(1)
     from nanochat_amd.workloads import MODELS, PREFILL
 
+    if args.workload == "ve":
+        print(json.dumps(bench_ve(args)), flush=True)
+        return
     if args.workload in PREFILL:
         print(json.dumps(bench_prefill(args, PREFILL[args.workload])), flush=True)
         return

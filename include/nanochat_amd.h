@@ -62,6 +62,31 @@ void qkp_backward(const void *q, const void *k, const void *gq, const void *gk, 
 /* Blocks per tensor of qkp_backward's partial gain gradients (reference qk_prologue.cu:120-125): fixed. */
 int qkp_backward_blocks(void);
 
+/*
+ * Value-embedding gate and mix of training; same symbols, arguments and meaning as the reference's
+ * model/kernels/ve_gate.cu:199-214 (called by model/ops/ve_gate.py:13-33), with the reference's fixed shape H = 6
+ * heads, C = 768. Forward: n bf16 [rows][C] (the normed stream), v bf16 rows at v_stride elements, idx int32 [rows],
+ * table fp32 [vocab][C], w fp32 [H][C] -> out bf16 [rows][C] = v + gate[head] * bf16(table[idx]),
+ * gate fp32 [rows][H] = 2 sigmoid(n w^T). Backward: dout bf16 rows at dout_stride, ids int32 [rows] sorted tokens
+ * (equal tokens must be adjacent, else the table gradient is undefined), order int64 [rows] their rows (a row
+ * outside [0, rows) is skipped), gate from the forward -> dn bf16 [rows][C], dz bf16 [rows][H] (dw = dz^T n is the
+ * caller's GEMM), and the table's gradient added into dtable fp32 [vocab][C]. Tokens are trusted (negative ones
+ * read as a zero embedding). Like the reference they return nothing; nc_last_error() reports the status.
+ */
+void ve_forward(const void *n, const void *v, long long v_stride, const void *idx, const void *table, const void *w,
+                void *out, void *gate, long long rows, void *stream);
+void ve_backward(const void *dout, long long dout_stride, const void *ids, const void *order, const void *table,
+                 const void *w, const void *gate, void *dn, void *dtable, void *dz, long long rows, void *stream);
+
+/* ve_forward / ve_backward for any head count 1 <= heads <= 16 (C = 128 heads) and a table of `vocab` rows: a token
+ * outside [0, vocab) mixes in nothing and receives no gradient. Strides are multiples of 8 elements and at least C;
+ * n, v, table, w, out, dout, dn and dtable are 16-byte aligned. rows = 0 launches nothing. */
+int nc_ve_forward(const void *n, const void *v, long long v_stride, const int32_t *idx, const float *table,
+                  long long vocab, const float *w, void *out, float *gate, long long rows, int heads, void *stream);
+int nc_ve_backward(const void *dout, long long dout_stride, const int32_t *ids, const int64_t *order,
+                   const float *table, long long vocab, const float *w, const float *gate, void *dn, float *dtable,
+                   void *dz, long long rows, int heads, void *stream);
+
 /* Status of the last void entry point's launch on this host thread (NC_OK or a hipError_t). */
 int nc_last_error(void);
 

@@ -331,6 +331,8 @@ extern "C" void qkp_forward(const void *q, const void *k, const void *gq, const 
     last_error = (int)hipGetLastError();
 }
 
+void nc::set_last_error(int status) { last_error = status; }
+
 extern "C" int nc_last_error(void) { return last_error; }
 
 extern "C" const char *nc_status_string(int status) {

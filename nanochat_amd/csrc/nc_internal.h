@@ -9,6 +9,9 @@
 
 namespace nc {
 
+/* kv_append.hip: the status nc_last_error() reports for the calling host thread (the void entry points set it). */
+void set_last_error(int status);
+
 /* kv_append.hip: the fused QK-norm/RoPE fp8 append of n sequences of one token each; ve non-NULL adds the
  * value embedding 2 sigmoid(ve_gate[head] . ve_h[b]) ve[tokens[b]] to v before it is quantized (C: ve_h's width). */
 int append_rows(const uint16_t *qkv, long long token_stride, int n, int Hq, int Hkv, const int32_t *pos,

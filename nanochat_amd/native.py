@@ -25,7 +25,7 @@ INCLUDE = PACKAGE.parent / "include"
 LIB_DIR = PACKAGE / "lib"
 LIBRARY = LIB_DIR / "libnanochat_kv.so"
 DECODE_LIBRARY = LIB_DIR / "libnanochat_decode.so"
-KERNEL_SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip"]
+KERNEL_SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip", CSRC / "ve_gate.hip"]
 DECODE_SOURCES = [CSRC / "decoder.hip", CSRC / "skinny_gemm.hip", CSRC / "stream_gemm.hip"]
 SOURCES = KERNEL_SOURCES + DECODE_SOURCES
 HEADERS = [CSRC / "nc_device.h", CSRC / "nc_internal.h", INCLUDE / "nanochat_amd.h", INCLUDE / "nanochat_decode.h"]
@@ -90,6 +90,12 @@ SIGNATURES = {
                             c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_size_t, c_void_p], c_int),
     "nc_prefill_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
                              c_int, c_int, c_int, c_float, c_void_p, c_void_p], c_int),
+    "ve_forward": ([c_void_p, c_void_p, c_longlong] + [c_void_p] * 5 + [c_longlong, c_void_p], None),
+    "ve_backward": ([c_void_p, c_longlong] + [c_void_p] * 8 + [c_longlong, c_void_p], None),
+    "nc_ve_forward": ([c_void_p, c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_void_p, c_void_p, c_void_p,
+                       c_longlong, c_int, c_void_p], c_int),
+    "nc_ve_backward": ([c_void_p, c_longlong, c_void_p, c_void_p, c_void_p, c_longlong, c_void_p, c_void_p, c_void_p,
+                        c_void_p, c_void_p, c_longlong, c_int, c_void_p], c_int),
 }
 
 

@@ -116,6 +116,33 @@ def decode_declared():
     return set(re.findall(r"\b([A-Za-z_]\w*)\s*\([^;{]*\)\s*;", text))
 
 
+def test_ve_gate_reports_errors(lib):
+    """The value-embedding entry points check every argument before a device call."""
+    # general entry points: status codes
+    assert lib.nc_ve_forward(None, None, 768, None, None, 10, None, None, None, 0, 6, None) == 0   # no rows
+    assert lib.nc_ve_forward(None, None, 768, None, None, 10, None, None, None, 4, 6, None) == -1
+    assert lib.nc_ve_forward(None, None, 768, None, None, 10, None, None, None, 4, 17, None) == -2   # heads
+    assert lib.nc_ve_forward(None, None, 768, None, None, 10, None, None, None, 4, 0, None) == -2
+    assert lib.nc_ve_forward(None, None, 700, None, None, 10, None, None, None, 4, 6, None) == -2    # v_stride < C
+    assert lib.nc_ve_forward(None, None, 772, None, None, 10, None, None, None, 4, 6, None) == -2    # not x8
+    assert lib.nc_ve_forward(None, None, 768, None, None, 0, None, None, None, 4, 6, None) == -2     # vocab
+    assert lib.nc_ve_forward(None, None, 768, None, None, 10, None, None, None, -1, 6, None) == -2
+    assert lib.nc_ve_backward(None, 768, None, None, None, 10, None, None, None, None, None, 0, 6, None) == 0
+    assert lib.nc_ve_backward(None, 768, None, None, None, 10, None, None, None, None, None, 3, 6, None) == -1
+    assert lib.nc_ve_backward(None, 100, None, None, None, 10, None, None, None, None, None, 3, 6, None) == -2
+    # misaligned operands (fake, never dereferenced addresses)
+    p, q, r = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1008), ctypes.c_void_p(0x1004)
+    assert lib.nc_ve_forward(q, p, 768, p, p, 10, p, p, p, 4, 6, None) == -2          # n not 16-byte aligned
+    assert lib.nc_ve_backward(p, 768, p, r, p, 10, p, p, p, p, p, 4, 6, None) == -2   # order not 8-byte aligned
+    # the reference-signature symbols (H = 6): nc_last_error
+    lib.ve_forward(None, None, 768, None, None, None, None, None, 5, None)
+    assert lib.nc_last_error() == -1
+    lib.ve_forward(None, None, 768, None, None, None, None, None, 0, None)
+    assert lib.nc_last_error() == 0
+    lib.ve_backward(None, 760, None, None, None, None, None, None, None, None, 5, None)
+    assert lib.nc_last_error() == -2
+
+
 def test_decode_header_covers_the_reference_abi():
     from nanochat_amd.native import DECODE_SIGNATURES
 
