@@ -87,6 +87,19 @@ int nc_ve_backward(const void *dout, long long dout_stride, const int32_t *ids, 
                    const float *table, long long vocab, const float *w, const float *gate, void *dn, float *dtable,
                    void *dz, long long rows, int heads, void *stream);
 
+/*
+ * Training attention forward: the varlen causal attention the reference runs through FlashAttention-4
+ * (model/ops/flash_attn.py:340-345, _flash_attn_fwd(q, k, v, cu_seqlens, cu_seqlens, T, T, causal=True,
+ * window_size_left=window, return_lse=True)). q, k, v: bf16 (total, heads, 128) with contiguous heads at token strides
+ * q_stride, k_stride, v_stride (elements, multiples of 8); cu_seqlens: int32 [segments + 1] (segment s is tokens
+ * cu[s] .. cu[s+1] - 1, at most max_seqlen of them). Row i of a segment attends keys j of the same segment with
+ * j <= i and i - j <= window (window < 0: no left limit), scores scaled by softmax_scale.
+ * out: bf16 (total, heads, 128) contiguous; lse: fp32 [heads][lse_stride], ln of the row's sum of exponentials.
+ */
+int nc_flash_attn_fwd(const void *q, const void *k, const void *v, long long q_stride, long long k_stride,
+                      long long v_stride, const int32_t *cu_seqlens, int segments, int max_seqlen, int heads,
+                      int window, float softmax_scale, void *out, float *lse, long long lse_stride, void *stream);
+
 /* Status of the last void entry point's launch on this host thread (NC_OK or a hipError_t). */
 int nc_last_error(void);
 

@@ -25,7 +25,7 @@ INCLUDE = PACKAGE.parent / "include"
 LIB_DIR = PACKAGE / "lib"
 LIBRARY = LIB_DIR / "libnanochat_kv.so"
 DECODE_LIBRARY = LIB_DIR / "libnanochat_decode.so"
-KERNEL_SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip", CSRC / "ve_gate.hip"]
+KERNEL_SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip", CSRC / "ve_gate.hip", CSRC / "flash_attn.hip"]
 DECODE_SOURCES = [CSRC / "decoder.hip", CSRC / "skinny_gemm.hip", CSRC / "stream_gemm.hip"]
 SOURCES = KERNEL_SOURCES + DECODE_SOURCES
 HEADERS = [CSRC / "nc_device.h", CSRC / "nc_internal.h", INCLUDE / "nanochat_amd.h", INCLUDE / "nanochat_decode.h"]
@@ -96,6 +96,8 @@ SIGNATURES = {
                        c_longlong, c_int, c_void_p], c_int),
     "nc_ve_backward": ([c_void_p, c_longlong, c_void_p, c_void_p, c_void_p, c_longlong, c_void_p, c_void_p, c_void_p,
                         c_void_p, c_void_p, c_longlong, c_int, c_void_p], c_int),
+    "nc_flash_attn_fwd": ([c_void_p] * 3 + [c_longlong] * 3 + [c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p,
+                                                                c_void_p, c_longlong, c_void_p], c_int),
 }
 
 
