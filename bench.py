@@ -10,7 +10,7 @@ value = algorithmic HBM bytes of the step / step time (GB/s). Attention bytes pe
 (n + 1) * 264 (fp8 K + V and two fp32 scales per key) + G * 128 * 2 * 2 (q in, out) + ceil((n + 1) / 16) * 4
 (block table); the append adds (Hq + 2 Hkv) * 256 read and Hq * 256 + Hkv * 264 written per token.
 
-    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4|c5|ve] [--pages-per-worker P] [--cpu-seqs S]
+    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4|c5|ve|fa] [--pages-per-worker P] [--cpu-seqs S]
                     [--no-e2e]
 
 A decode workload's line also carries the metric's second half, `decode_tokens_per_s`: config 5 end to end
@@ -19,6 +19,8 @@ A decode workload's line also carries the metric's second half, `decode_tokens_p
 --workload c4 times the chunked-prefill step instead (TFLOP/s against the 2.5 PFLOP/s bf16 dense MFMA peak).
 --workload ve times the training-side value-embedding gate forward and backward (nc_ve_forward, nc_ve_backward) at
 the reference's d24 shape (GB/s of algorithmic bytes against 8 TB/s).
+--workload fa times the training attention forward and backward (nc_flash_attn_fwd / _bwd) at the reference's d24
+training shape (32 causal segments of 2048 tokens, 6 heads; TFLOP/s against the 2.5 PFLOP/s bf16 dense peak).
 --workload c5 runs the end-to-end decoder (libnanochat_decode.so through the dec_* ABI): a random-init 26-layer
 d1664 model, 128 random 2048-token prompts prefilled, then 512 greedy steps; value = decode tokens/s.
 """
@@ -271,6 +273,65 @@ def ve_cpu_baseline(qkv, n, table, w, idx, dqkv, rows):
             "sample": f"oracle forward + backward (numpy) of the first {rows} of the rows, {dt:.2f} s"}
 
 
+FA_SHAPE = {"segments": 32, "seqlen": 2048, "heads": 6}   # reference d24 training: 32 x 2048 tokens, C = 768
+
+
+def fa_flops(segments, seqlen, heads, window=-1):
+    """Causal-useful FLOPs of one forward: 4 * 128 per (row, visible key); the backward's algorithmic count is 2.5x
+    (five products against the forward's two)."""
+    keys = sum(min(i, window) + 1 if window >= 0 else i + 1 for i in range(seqlen))
+    return 4 * 128 * keys * segments * heads
+
+
+def bench_fa(args):
+    """The training attention forward and backward (nc_flash_attn_fwd / _bwd) at the reference's d24 shape."""
+    import torch
+
+    from nanochat_amd.flash_attn import flash_attn_bwd, flash_attn_bwd_rows, flash_attn_fwd
+
+    dev = torch.device("cuda:0")
+    S, T, H = FA_SHAPE["segments"], FA_SHAPE["seqlen"], FA_SHAPE["heads"]
+    gen = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(S * T, H, 128, generator=gen).bfloat16().to(dev) for _ in range(4))
+    cu = torch.arange(0, S * T + 1, T, dtype=torch.int32, device=dev)
+    out, lse = flash_attn_fwd(q, k, v, cu, T)
+    rows = flash_attn_bwd_rows(out, do)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        for a, b in evs:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return sorted(a.elapsed_time(b) for a, b in evs)
+
+    f_ms = timed(lambda: flash_attn_fwd(q, k, v, cu, T))
+    b_ms = timed(lambda: flash_attn_bwd(q, k, v, out, do, lse, cu, T, rows=rows))
+    f_med, b_med = f_ms[len(f_ms) // 2], b_ms[len(b_ms) // 2]
+    ff = fa_flops(S, T, H)
+    f_tf, b_tf = ff / (f_med * 1e-3) / 1e12, 2.5 * ff / (b_med * 1e-3) / 1e12
+    total = 3.5 * ff / ((f_med + b_med) * 1e-3) / 1e12
+    return {
+        "metric": "training attention forward + backward TFLOP/s (causal, MFMA)", "value": round(total, 2),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(f_med + b_med, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 MFMA, fp32 softmax and accumulation", "data": "synthetic (seeded N(0,1) bf16 q, k, v, dout)",
+        "config": {"workload": f"fa: {S} segments x {T} tokens, {H} heads of 128, causal", "segments": S, "seqlen": T,
+                   "heads": H},
+        "forward": {"ms_median": round(f_med, 5), "flops": ff, "tflops": round(f_tf, 1),
+                    "frac": round(f_tf / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "backward": {"ms_median": round(b_med, 5), "flops": int(2.5 * ff), "tflops": round(b_tf, 1),
+                     "frac": round(b_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "note": "algorithmic 2.5x forward; the two-kernel backward computes 3.5x"},
+        "roofline": {"bound": "mfma", "achieved": round(total, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(total / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "flash_fwd_kernel + flash_bwd_dkv_kernel + flash_bwd_dq_kernel"},
+    }
+
+
 def model_decode_bytes(w, positions):
     """HBM bytes a decode step must read: every slot's cached keys (264 B per key per head per layer, positions
     0..p), the GEMM weights and lm_head in bf16."""
@@ -411,6 +472,9 @@ def main():
 
     if args.workload == "ve":
         print(json.dumps(bench_ve(args)), flush=True)
+        return
+    if args.workload == "fa":
+        print(json.dumps(bench_fa(args)), flush=True)
         return
     if args.workload in PREFILL:
         print(json.dumps(bench_prefill(args, PREFILL[args.workload])), flush=True)

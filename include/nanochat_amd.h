@@ -100,6 +100,23 @@ int nc_flash_attn_fwd(const void *q, const void *k, const void *v, long long q_s
                       long long v_stride, const int32_t *cu_seqlens, int segments, int max_seqlen, int heads,
                       int window, float softmax_scale, void *out, float *lse, long long lse_stride, void *stream);
 
+/*
+ * Training attention backward (the reference's _flash_attn_bwd and bwd_bf16dq, model/ops/flash_attn.py:367-391):
+ * q, k, v, dout as the forward's inputs and the output's gradient (token strides in elements); lse from
+ * nc_flash_attn_fwd; dpsum fp32 (total, heads): D = dout . out per row (the reference's `rows`; see
+ * nc_flash_attn_bwd_rows). Writes dq, dk, dv: bf16 (total, heads, 128) with contiguous heads at their token strides.
+ * No atomics: the result does not depend on scheduling.
+ */
+int nc_flash_attn_bwd(const void *q, const void *k, const void *v, const void *dout, long long q_stride,
+                      long long k_stride, long long v_stride, long long do_stride, const float *lse, long long lse_stride,
+                      const float *dpsum, const int32_t *cu_seqlens, int segments, int max_seqlen, int heads,
+                      int window, float softmax_scale, void *dq, void *dk, void *dv, long long dq_stride,
+                      long long dk_stride, long long dv_stride, void *stream);
+
+/* dpsum (total, heads) fp32 = sum over the 128 dims of dout * out (token strides in elements, even). */
+int nc_flash_attn_bwd_rows(const void *out, long long o_stride, const void *dout, long long do_stride,
+                           long long total, int heads, float *dpsum, void *stream);
+
 /* Status of the last void entry point's launch on this host thread (NC_OK or a hipError_t). */
 int nc_last_error(void);
 

@@ -70,41 +70,57 @@ __device__ __forceinline__ Rsrc rows_rsrc(const uint16_t *base, long long row0, 
     return make_rsrc(base + row0 * stride + (long long)h * HEAD_DIM, bytes);
 }
 
-/* One key block's K and V in registers: thread t holds K chunks 4(t%4) .. +3 of key t/4, and dims 8(t/16) .. +7 of
- * keys 4(t%16) .. +3 of V. Keys past the segment read zeros. */
-struct StageRegs {
-    uint4 k[4], v[4];
+/* 64 rows x 128 dims of one head in registers: thread t holds dims 8(t/16) .. +7 of rows 4(t%16) .. +3. Rows past
+ * `rows` read zeros. One load serves both LDS layouts below. */
+struct Tile64 {
+    uint4 r[4];
 };
 
-__device__ __forceinline__ void stage_load(const FlashFwd &a, long long key0, int nkeys, int h, StageRegs &r, int t) {
-    const Rsrc rk = rows_rsrc(a.k, key0, a.k_stride, h, nkeys), rv = rows_rsrc(a.v, key0, a.v_stride, h, nkeys);
-    const int kk = t >> 2, kc = (t & 3) * 4;
+__device__ __forceinline__ void tile_load(const uint16_t *base, long long row0, long long stride, int h, int rows,
+                                          Tile64 &x, int t) {
+    const Rsrc rs = rows_rsrc(base, row0, stride, h, rows);
+    const int r0 = (t & 15) * 4, dc = t >> 4;
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.k[i] = bload(rk, (int)((kk * a.k_stride + (kc + i) * 8) * 2));
-    const int vk = (t & 15) * 4, vd = (t >> 4) * 8;
-#pragma unroll
-    for (int i = 0; i < 4; i++) r.v[i] = bload(rv, (int)(((vk + i) * a.v_stride + vd) * 2));
+    for (int i = 0; i < 4; i++) x.r[i] = bload(rs, (int)(((r0 + i) * stride + dc * 8) * 2));
 }
 
-__device__ __forceinline__ uint32_t half_of(const uint4 &u, int j) {
-    const uint32_t w = j < 2 ? (j == 0 ? u.x : u.y) : (j == 2 ? u.z : u.w);
-    return w;
+/* row-major [64][128] (k_lds layout): the A operand of products over the dimension */
+__device__ __forceinline__ void tile_store_rows(uint16_t *lds, const Tile64 &x, int t) {
+    const int r0 = (t & 15) * 4, dc = t >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) *reinterpret_cast<uint4 *>(&lds[k_lds(r0 + i, dc)]) = x.r[i];
 }
 
-__device__ __forceinline__ void stage_store(FaStage &s, const StageRegs &r, int t) {
-    const int kk = t >> 2, kc = (t & 3) * 4;
-#pragma unroll
-    for (int i = 0; i < 4; i++) *reinterpret_cast<uint4 *>(&s.k[k_lds(kk, kc + i)]) = r.k[i];
-    /* V: r.v[i] = dims vd .. vd+7 of key vk + i; dim vd + j of the four keys -> one 8-byte unit of Vt */
+__device__ __forceinline__ uint32_t word_of(const uint4 &u, int j) {
+    return j < 2 ? (j == 0 ? u.x : u.y) : (j == 2 ? u.z : u.w);
+}
+
+/* transposed [128][64] (vt_lds layout): dim vd + j of the thread's four rows is one 8-byte unit; the A operand of
+ * products over the rows */
+__device__ __forceinline__ void tile_store_cols(uint16_t *lds, const Tile64 &x, int t) {
     const int u = t & 15, vd = (t >> 4) * 8;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const int sh = (j & 1) * 16;
         uint32_t e[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) e[i] = (half_of(r.v[i], j >> 1) >> sh) & 0xFFFFu;
-        *reinterpret_cast<uint2 *>(&s.vt[vt_lds(vd + j, u)]) = uint2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+        for (int i = 0; i < 4; i++) e[i] = (word_of(x.r[i], j >> 1) >> sh) & 0xFFFFu;
+        *reinterpret_cast<uint2 *>(&lds[vt_lds(vd + j, u)]) = uint2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
     }
+}
+
+/* The A operand of a product over 32 rows of a transposed tile, in the key order of an S^T / S output pair: lane
+ * (g, c) of dim tile d holds rows 32 s2 + 4g .. +3 and 32 s2 + 16 + 4g .. +3 of dim 16 d + c. */
+__device__ __forceinline__ bf16x8 cols_operand(const uint16_t *lds, int d, int s2, int g, int c) {
+    const uint2 lo = *reinterpret_cast<const uint2 *>(&lds[vt_lds(d * 16 + c, 8 * s2 + g)]);
+    const uint2 hi = *reinterpret_cast<const uint2 *>(&lds[vt_lds(d * 16 + c, 8 * s2 + 4 + g)]);
+    return __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
+}
+
+/* The A operand of a product over the dimension from a row-major tile: lane (g, c) holds dims 32 cc + 8 g .. +7 of
+ * row 16 rt + c. */
+__device__ __forceinline__ bf16x8 rows_operand(const uint16_t *lds, int rt, int cc, int g, int c) {
+    return *reinterpret_cast<const bf16x8 *>(&lds[k_lds(rt * 16 + c, cc * 4 + g)]);
 }
 
 struct FaState {
@@ -128,7 +144,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
     for (int kt = 0; kt < 4; kt++) {
 #pragma unroll
         for (int cc = 0; cc < 4; cc++) {
-            const bf16x8 kop = *reinterpret_cast<const bf16x8 *>(&s.k[k_lds(kt * 16 + c, cc * 4 + g)]);
+            const bf16x8 kop = rows_operand(s.k, kt, cc, g, c);
 #pragma unroll
             for (int j = 0; j < 2; j++) sc[j][kt] = mfma16x16x32(kop, qb[j][cc], sc[j][kt]);
         }
@@ -181,10 +197,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
     for (int d = 0; d < 8; d++) {
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++) {
-            const int dim = d * 16 + c;
-            const uint2 lo = *reinterpret_cast<const uint2 *>(&s.vt[vt_lds(dim, 8 * s2 + g)]);
-            const uint2 hi = *reinterpret_cast<const uint2 *>(&s.vt[vt_lds(dim, 8 * s2 + 4 + g)]);
-            const bf16x8 vop = __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
+            const bf16x8 vop = cols_operand(s.vt, d, s2, g, c);
 #pragma unroll
             for (int j = 0; j < 2; j++) st.o[j][d] = mfma16x16x32(vop, pv[j][s2], st.o[j][d]);
         }
@@ -226,9 +239,11 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(FlashFwd a) {
 
     const int klo = a.window >= 0 ? max(0, qa - a.window) : 0;
     const int kb_lo = klo / FA_BN, kb_hi = qb / FA_BN;
-    StageRegs r;
-    stage_load(a, start + kb_lo * FA_BN, min(FA_BN, seglen - kb_lo * FA_BN), h, r, t);
-    stage_store(stage[0], r, t);
+    Tile64 rk, rv;
+    tile_load(a.k, start + kb_lo * FA_BN, a.k_stride, h, min(FA_BN, seglen - kb_lo * FA_BN), rk, t);
+    tile_load(a.v, start + kb_lo * FA_BN, a.v_stride, h, min(FA_BN, seglen - kb_lo * FA_BN), rv, t);
+    tile_store_rows(stage[0].k, rk, t);
+    tile_store_cols(stage[0].vt, rv, t);
     __syncthreads();
     for (int kb = kb_lo; kb <= kb_hi; kb++) {
         const int cur = (kb - kb_lo) & 1;
@@ -243,8 +258,11 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(FlashFwd a) {
                 fa_block<true>(a, stage[cur], qb_, st, k0, q0, seglen, lane);
         }
         if (more) {
-            stage_load(a, start + (kb + 1) * FA_BN, min(FA_BN, seglen - (kb + 1) * FA_BN), h, r, t);
-            stage_store(stage[cur ^ 1], r, t);
+            const int n1 = min(FA_BN, seglen - (kb + 1) * FA_BN);
+            tile_load(a.k, start + (kb + 1) * FA_BN, a.k_stride, h, n1, rk, t);
+            tile_load(a.v, start + (kb + 1) * FA_BN, a.v_stride, h, n1, rv, t);
+            tile_store_rows(stage[cur ^ 1].k, rk, t);
+            tile_store_cols(stage[cur ^ 1].vt, rv, t);
         }
         __syncthreads();
     }
@@ -268,6 +286,254 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(FlashFwd a) {
         }
         if (g == 0) a.lse[(long long)h * a.lse_stride + tok] = (st.m[j] + __log2f(l)) * FA_LN2;
     }
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Backward (the reference's _flash_attn_bwd / bwd_bf16dq, model/ops/flash_attn.py:367-391), per segment and head:
+ *   P = exp(scale S - lse), dV = P^T dO, dP = dO V^T, dS = P (dP - D) with D_i = dO_i . O_i (the caller's row
+ *   statistics: the reference's `rows`, from the o_proj backward epilogue), dQ = scale dS K, dK = scale dS^T Q.
+ * Two kernels and no atomics: flash_bwd_dkv_kernel owns 64 keys (a wave 16) and walks the query blocks that see them;
+ * flash_bwd_dq_kernel owns 128 queries (a wave 32, as the forward) and walks their key blocks. S and dP are computed
+ * in both (seven 128-deep products per (query, key) pair instead of five), the price of writing dQ once.
+ * ------------------------------------------------------------------------------------------------------------- */
+
+struct FlashBwd {
+    const uint16_t *q, *k, *v, *dout;         /* (total, H, 128) at token strides */
+    long long q_stride, k_stride, v_stride, do_stride;
+    const float *lse;                          /* [H][lse_stride], natural log */
+    long long lse_stride;
+    const float *dpsum;                        /* (total, H): D = dO . O per row */
+    const int32_t *cu;
+    int segments, H, window;
+    float scale, scale_log2;
+    uint16_t *dq, *dk, *dv;                    /* (total, H, 128) at their token strides */
+    long long dq_stride, dk_stride, dv_stride;
+};
+
+__device__ __forceinline__ bool visible(int key, int q, int seglen, int window) {
+    return key <= q && q < seglen && (window < 0 || q - key <= window);
+}
+
+__device__ __forceinline__ void store4(uint16_t *p, const f32x4 &v, float mul) {
+    *reinterpret_cast<uint2 *>(p) = uint2{(uint32_t)f32_to_bf16(v[0] * mul) | ((uint32_t)f32_to_bf16(v[1] * mul) << 16),
+                                          (uint32_t)f32_to_bf16(v[2] * mul) | ((uint32_t)f32_to_bf16(v[3] * mul) << 16)};
+}
+
+struct DkvStage {
+    uint16_t q[FA_BN * HEAD_DIM], qt[HEAD_DIM * FA_BN], dout[FA_BN * HEAD_DIM], dot[HEAD_DIM * FA_BN];
+    float lse2[FA_BN], dd[FA_BN];              /* the block's rows: lse log2(e) (+inf past the segment), D */
+};
+
+/* dK, dV of 64 keys. S = Q K^T and dP = dO V^T with queries as rows (a lane holds one key's column), so P and dS
+ * feed dV^T += dO^T P and dK^T += Q^T dS directly as B operands, with dO^T and Q^T read from transposed LDS tiles. */
+__global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dkv_kernel(FlashBwd a) {
+    __shared__ DkvStage s;
+    const int seg = blockIdx.y, h = blockIdx.z;
+    const long long start = a.cu[seg];
+    const int seglen = a.cu[seg + 1] - a.cu[seg];
+    const int k0 = blockIdx.x * FA_BN;          /* the most query blocks first */
+    if (seglen <= 0 || k0 >= seglen) return;
+    const int t = threadIdx.x, lane = t & (WAVE - 1), wave = t >> 6, g = lane >> 4, c = lane & 15;
+    const int kw = k0 + wave * 16;              /* the wave's first key */
+    const bool active = kw < seglen;
+    const int key = kw + c;
+
+    /* the wave's K and V as B operands: lane (g, c) holds dims 32 cc + 8 g .. +7 of key c */
+    bf16x8 kb_[4], vb_[4];
+    {
+        const int n = active ? min(16, seglen - kw) : 0;
+        const Rsrc rk = rows_rsrc(a.k, start + kw, a.k_stride, h, n), rv = rows_rsrc(a.v, start + kw, a.v_stride, h, n);
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            kb_[cc] = __builtin_bit_cast(bf16x8, bload(rk, (int)((c * a.k_stride + cc * 32 + g * 8) * 2)));
+            vb_[cc] = __builtin_bit_cast(bf16x8, bload(rv, (int)((c * a.v_stride + cc * 32 + g * 8) * 2)));
+        }
+    }
+    f32x4 dk[8], dv[8];
+#pragma unroll
+    for (int d = 0; d < 8; d++) dk[d] = dv[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int qhi = a.window >= 0 ? min(seglen - 1, k0 + FA_BN - 1 + a.window) : seglen - 1;
+    for (int qbk = k0 / FA_BN; qbk <= qhi / FA_BN; qbk++) {
+        const int qs = qbk * FA_BN, nq = min(FA_BN, seglen - qs);
+        {
+            Tile64 x;
+            tile_load(a.q, start + qs, a.q_stride, h, nq, x, t);
+            tile_store_rows(s.q, x, t);
+            tile_store_cols(s.qt, x, t);
+            tile_load(a.dout, start + qs, a.do_stride, h, nq, x, t);
+            tile_store_rows(s.dout, x, t);
+            tile_store_cols(s.dot, x, t);
+            if (t < FA_BN) {
+                const bool ok = t < nq;
+                s.lse2[t] = ok ? a.lse[(long long)h * a.lse_stride + start + qs + t] * FA_LOG2E : INFINITY;
+                s.dd[t] = ok ? a.dpsum[(start + qs + t) * a.H + h] : 0.0f;
+            }
+        }
+        __syncthreads();
+        if (active) {
+            const int kw1 = kw + 15, qe = qs + FA_BN - 1;
+            const bool interior = kw1 <= qs && qe < seglen && kw1 < seglen && (a.window < 0 || qe - kw <= a.window);
+            bf16x8 pb[2], db[2];
+#pragma unroll
+            for (int qt = 0; qt < 4; qt++) {
+                f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    sc = mfma16x16x32(rows_operand(s.q, qt, cc, g, c), kb_[cc], sc);
+                    dp = mfma16x16x32(rows_operand(s.dout, qt, cc, g, c), vb_[cc], dp);
+                }
+                /* lane (g, c): key c, query rows qs + 16 qt + 4 g + i */
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = qt * 16 + 4 * g + i;
+                    float p = __builtin_amdgcn_exp2f(sc[i] * a.scale_log2 - s.lse2[r]);
+                    if (!interior && !visible(key, qs + r, seglen, a.window)) p = 0.0f;
+                    const float ds = p * (dp[i] - s.dd[r]);
+                    pb[qt >> 1][(qt & 1) * 4 + i] = (__bf16)p;
+                    db[qt >> 1][(qt & 1) * 4 + i] = (__bf16)ds;
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < 8; d++)
+#pragma unroll
+                for (int s2 = 0; s2 < 2; s2++) {
+                    dv[d] = mfma16x16x32(cols_operand(s.dot, d, s2, g, c), pb[s2], dv[d]);
+                    dk[d] = mfma16x16x32(cols_operand(s.qt, d, s2, g, c), db[s2], dk[d]);
+                }
+        }
+        __syncthreads();
+    }
+    if (!active || key >= seglen) return;
+    /* dK^T, dV^T tile d: lane (g, c) holds dims 16 d + 4 g .. +3 of key c */
+    uint16_t *pk = a.dk + (start + key) * a.dk_stride + (long long)h * HEAD_DIM + 4 * g;
+    uint16_t *pv = a.dv + (start + key) * a.dv_stride + (long long)h * HEAD_DIM + 4 * g;
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+        store4(pk + d * 16, dk[d], a.scale);
+        store4(pv + d * 16, dv[d], 1.0f);
+    }
+}
+
+struct DqStage {
+    uint16_t k[FA_BN * HEAD_DIM], v[FA_BN * HEAD_DIM], kt[HEAD_DIM * FA_BN];
+};
+
+/* dQ of 128 queries: as the forward, S^T = K Q^T and dP^T = V dO^T with queries as columns, so dS^T feeds
+ * dQ^T += K^T dS^T as the B operand with K^T read from a transposed LDS tile. */
+__global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dq_kernel(FlashBwd a) {
+    __shared__ DqStage s;
+    const int seg = blockIdx.y, h = blockIdx.z;
+    const long long start = a.cu[seg];
+    const int seglen = a.cu[seg + 1] - a.cu[seg];
+    const int tile = (int)gridDim.x - 1 - (int)blockIdx.x;
+    const int qa = tile * FA_BM;
+    if (seglen <= 0 || qa >= seglen) return;
+    const int t = threadIdx.x, lane = t & (WAVE - 1), wave = t >> 6, g = lane >> 4, c = lane & 15;
+    const int qb = min(qa + FA_BM, seglen) - 1;
+    const int q0 = qa + wave * 32;
+    const bool active = q0 < seglen;
+    const int qw1 = min(q0 + 31, seglen - 1);
+
+    /* queries and dO as B operands (lane (g, c): dims 32 cc + 8 g .. +7 of row c), each column's lse and D */
+    bf16x8 qb_[2][4], ob_[2][4];
+    float lse2[2], dd[2];
+    {
+        const int n = active ? min(32, seglen - q0) : 0;
+        const Rsrc rq = rows_rsrc(a.q, start + q0, a.q_stride, h, n), ro = rows_rsrc(a.dout, start + q0, a.do_stride, h, n);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                qb_[j][cc] = __builtin_bit_cast(bf16x8, bload(rq, (int)(((16 * j + c) * a.q_stride + cc * 32 + g * 8) * 2)));
+                ob_[j][cc] = __builtin_bit_cast(bf16x8, bload(ro, (int)(((16 * j + c) * a.do_stride + cc * 32 + g * 8) * 2)));
+            }
+            const int row = q0 + 16 * j + c;
+            const bool ok = active && row < seglen;
+            lse2[j] = ok ? a.lse[(long long)h * a.lse_stride + start + row] * FA_LOG2E : INFINITY;
+            dd[j] = ok ? a.dpsum[(start + row) * a.H + h] : 0.0f;
+        }
+    }
+    f32x4 dq[2][8];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int d = 0; d < 8; d++) dq[j][d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int klo = a.window >= 0 ? max(0, qa - a.window) : 0;
+    for (int kb = klo / FA_BN; kb <= qb / FA_BN; kb++) {
+        const int k0 = kb * FA_BN, nk = min(FA_BN, seglen - k0);
+        {
+            Tile64 x;
+            tile_load(a.k, start + k0, a.k_stride, h, nk, x, t);
+            tile_store_rows(s.k, x, t);
+            tile_store_cols(s.kt, x, t);
+            tile_load(a.v, start + k0, a.v_stride, h, nk, x, t);
+            tile_store_rows(s.v, x, t);
+        }
+        __syncthreads();
+        if (active) {
+            const int k1 = k0 + FA_BN - 1;
+            const bool interior = k1 <= q0 && k1 < seglen && (a.window < 0 || qw1 - k0 <= a.window);
+            bf16x8 db[2][2];
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                f32x4 sc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}}, dp[2] = {sc[0], sc[1]};
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    const bf16x8 kop = rows_operand(s.k, kt, cc, g, c), vop = rows_operand(s.v, kt, cc, g, c);
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        sc[j] = mfma16x16x32(kop, qb_[j][cc], sc[j]);
+                        dp[j] = mfma16x16x32(vop, ob_[j][cc], dp[j]);
+                    }
+                }
+                /* lane (g, c): query column c of tile j, keys k0 + 16 kt + 4 g + i */
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        float p = __builtin_amdgcn_exp2f(sc[j][i] * a.scale_log2 - lse2[j]);
+                        if (!interior && !visible(k0 + 16 * kt + 4 * g + i, q0 + 16 * j + c, seglen, a.window)) p = 0.0f;
+                        db[j][kt >> 1][(kt & 1) * 4 + i] = (__bf16)(p * (dp[j][i] - dd[j]));
+                    }
+            }
+#pragma unroll
+            for (int d = 0; d < 8; d++)
+#pragma unroll
+                for (int s2 = 0; s2 < 2; s2++) {
+                    const bf16x8 kop = cols_operand(s.kt, d, s2, g, c);
+#pragma unroll
+                    for (int j = 0; j < 2; j++) dq[j][d] = mfma16x16x32(kop, db[j][s2], dq[j][d]);
+                }
+        }
+        __syncthreads();
+    }
+    if (!active) return;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int row = q0 + 16 * j + c;
+        if (row >= seglen) continue;
+        uint16_t *p = a.dq + (start + row) * a.dq_stride + (long long)h * HEAD_DIM + 4 * g;
+#pragma unroll
+        for (int d = 0; d < 8; d++) store4(p + d * 16, dq[j][d], a.scale);
+    }
+}
+
+/* D[row][h] = sum_d dO . O in fp32: one wave per (row, head), two dims per lane. */
+__global__ void __launch_bounds__(256) flash_bwd_rows_kernel(const uint16_t *out, long long o_stride,
+                                                             const uint16_t *dout, long long do_stride, long long n,
+                                                             int H, float *dpsum) {
+    const long long w = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (w >= n) return;
+    const int lane = threadIdx.x & (WAVE - 1), h = (int)(w % H);
+    const long long row = w / H;
+    const uint32_t o = *reinterpret_cast<const uint32_t *>(out + row * o_stride + (long long)h * HEAD_DIM + 2 * lane);
+    const uint32_t d = *reinterpret_cast<const uint32_t *>(dout + row * do_stride + (long long)h * HEAD_DIM + 2 * lane);
+    const float v = __builtin_fmaf(__uint_as_float(o & 0xFFFF0000u), __uint_as_float(d & 0xFFFF0000u),
+                                   __uint_as_float(o << 16) * __uint_as_float(d << 16));
+    const float sum = wave_sum_butterfly(v);
+    if (lane == 0) dpsum[w] = sum;
 }
 
 }  // namespace
@@ -298,5 +564,57 @@ extern "C" int nc_flash_attn_fwd(const void *q, const void *k, const void *v, lo
     a.out = (uint16_t *)out; a.lse = lse; a.lse_stride = lse_stride;
     const dim3 grid((unsigned)((max_seqlen + FA_BM - 1) / FA_BM), (unsigned)segments, (unsigned)heads);
     hipLaunchKernelGGL(flash_fwd_kernel, grid, dim3(FA_THREADS), 0, (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+
+extern "C" int nc_flash_attn_bwd_rows(const void *out, long long o_stride, const void *dout, long long do_stride,
+                                      long long total, int heads, float *dpsum, void *stream) {
+    if (total < 0 || heads < 1 || o_stride < (long long)heads * HEAD_DIM || do_stride < (long long)heads * HEAD_DIM ||
+        o_stride % 2 || do_stride % 2)
+        return NC_ERR_SHAPE;
+    if (total == 0) return NC_OK;
+    if (!out || !dout || !dpsum) return NC_ERR_NULL;
+    if (((uintptr_t)out | (uintptr_t)dout) & 3) return NC_ERR_SHAPE;
+    const long long n = total * heads;
+    hipLaunchKernelGGL(flash_bwd_rows_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)out, o_stride, (const uint16_t *)dout, do_stride, n, heads, dpsum);
+    return (int)hipGetLastError();
+}
+
+extern "C" int nc_flash_attn_bwd(const void *q, const void *k, const void *v, const void *dout, long long q_stride,
+                                 long long k_stride, long long v_stride, long long do_stride, const float *lse,
+                                 long long lse_stride, const float *dpsum, const int32_t *cu_seqlens, int segments,
+                                 int max_seqlen, int heads, int window, float softmax_scale, void *dq, void *dk,
+                                 void *dv, long long dq_stride, long long dk_stride, long long dv_stride,
+                                 void *stream) {
+    if (segments < 0 || max_seqlen < 0 || heads < 1 || heads > 65535 || segments > 65535 || lse_stride < 0 ||
+        !(softmax_scale > 0.0f))
+        return NC_ERR_SHAPE;
+    if (segments == 0 || max_seqlen == 0) return NC_OK;
+    if (!q || !k || !v || !dout || !lse || !dpsum || !cu_seqlens || !dq || !dk || !dv) return NC_ERR_NULL;
+    const long long row = (long long)heads * HEAD_DIM;
+    const long long strides[] = {q_stride, k_stride, v_stride, do_stride, dq_stride, dk_stride, dv_stride};
+    long long widest = 0;
+    for (long long st : strides) {
+        if (st < row || st % 8) return NC_ERR_SHAPE;
+        widest = max(widest, st);
+    }
+    if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)dq | (uintptr_t)dk | (uintptr_t)dv) & 15)
+        return NC_ERR_SHAPE;
+    if ((63 * widest + HEAD_DIM) * 2 >= 0x7FFFFFFFLL) return NC_ERR_SHAPE;
+    FlashBwd a;
+    a.q = (const uint16_t *)q; a.k = (const uint16_t *)k; a.v = (const uint16_t *)v; a.dout = (const uint16_t *)dout;
+    a.q_stride = q_stride; a.k_stride = k_stride; a.v_stride = v_stride; a.do_stride = do_stride;
+    a.lse = lse; a.lse_stride = lse_stride; a.dpsum = dpsum;
+    a.cu = cu_seqlens; a.segments = segments; a.H = heads; a.window = window < 0 ? -1 : window;
+    a.scale = softmax_scale; a.scale_log2 = softmax_scale * FA_LOG2E;
+    a.dq = (uint16_t *)dq; a.dk = (uint16_t *)dk; a.dv = (uint16_t *)dv;
+    a.dq_stride = dq_stride; a.dk_stride = dk_stride; a.dv_stride = dv_stride;
+    hipLaunchKernelGGL(flash_bwd_dkv_kernel, dim3((unsigned)((max_seqlen + FA_BN - 1) / FA_BN), (unsigned)segments,
+                                                  (unsigned)heads),
+                       dim3(FA_THREADS), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(flash_bwd_dq_kernel, dim3((unsigned)((max_seqlen + FA_BM - 1) / FA_BM), (unsigned)segments,
+                                                 (unsigned)heads),
+                       dim3(FA_THREADS), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }

@@ -98,6 +98,11 @@ SIGNATURES = {
                         c_void_p, c_void_p, c_longlong, c_int, c_void_p], c_int),
     "nc_flash_attn_fwd": ([c_void_p] * 3 + [c_longlong] * 3 + [c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p,
                                                                 c_void_p, c_longlong, c_void_p], c_int),
+    "nc_flash_attn_bwd": ([c_void_p] * 4 + [c_longlong] * 4 + [c_void_p, c_longlong, c_void_p, c_void_p, c_int, c_int,
+                                                                c_int, c_int, c_float, c_void_p, c_void_p, c_void_p,
+                                                                c_longlong, c_longlong, c_longlong, c_void_p], c_int),
+    "nc_flash_attn_bwd_rows": ([c_void_p, c_longlong, c_void_p, c_longlong, c_longlong, c_int, c_void_p, c_void_p],
+                               c_int),
 }
 
 
