@@ -143,6 +143,35 @@ def test_ve_gate_reports_errors(lib):
     assert lib.nc_last_error() == -2
 
 
+def test_flash_attn_reports_errors(lib):
+    """Shape, NULL and alignment checks before any device call; nothing to do returns 0 without launching."""
+    p, q = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1008)
+    fwd = lib.nc_flash_attn_fwd
+    assert fwd(None, None, None, 384, 384, 384, None, 0, 100, 3, -1, 0.1, None, None, 0, None) == 0   # no segments
+    assert fwd(None, None, None, 384, 384, 384, None, 2, 0, 3, -1, 0.1, None, None, 0, None) == 0     # max_seqlen 0
+    assert fwd(None, None, None, 384, 384, 384, None, 2, 100, 3, -1, 0.1, None, None, 0, None) == -1
+    assert fwd(p, p, p, 384, 384, 384, p, 2, 100, 0, -1, 0.1, p, p, 0, None) == -2                   # heads
+    assert fwd(p, p, p, 383, 384, 384, p, 2, 100, 3, -1, 0.1, p, p, 0, None) == -2                   # stride < row
+    assert fwd(p, p, p, 392, 384, 388, p, 2, 100, 3, -1, 0.1, p, p, 0, None) == -2                   # not x8
+    assert fwd(q, p, p, 384, 384, 384, p, 2, 100, 3, -1, 0.1, p, p, 0, None) == -2                   # alignment
+    assert fwd(p, p, p, 384, 384, 384, p, 2, 100, 3, -1, 0.0, p, p, 0, None) == -2                   # scale
+    bwd = lib.nc_flash_attn_bwd
+    args = [p, p, p, p, 384, 384, 384, 384, p, 0, p, p, 2, 100, 3, -1, 0.1, p, p, p, 384, 384, 384, None]
+    bad = list(args)
+    bad[3] = None
+    assert bwd(*bad) == -1
+    bad = list(args)
+    bad[22] = 380
+    assert bwd(*bad) == -2
+    bad = list(args)
+    bad[19] = q
+    assert bwd(*bad) == -2
+    rows = lib.nc_flash_attn_bwd_rows
+    assert rows(None, 384, None, 384, 0, 3, None, None) == 0
+    assert rows(None, 384, None, 384, 5, 3, None, None) == -1
+    assert rows(p, 380, p, 384, 5, 3, p, None) == -2
+
+
 def test_decode_header_covers_the_reference_abi():
     from nanochat_amd.native import DECODE_SIGNATURES
 
