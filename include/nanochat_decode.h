@@ -76,6 +76,11 @@ void *dec_create_slots(const int *cfg, const uint64_t *ptrs, const float *scal, 
 void dec_debug_logits(void *handle, float *out, int rows);
 void dec_debug_cache(void *handle, int layer, int b, int at, int n, uint8_t *k, uint8_t *v, float *scales);
 
+/* Slot b's block-table row, max_length / 16 (rounded up) entries: b * pages + e is the slot's own page e,
+ * dec_batch() * pages + i page i of the prompt store, shared read-only after dec_load_prompt (pages = the row's
+ * length). */
+void dec_debug_table(void *handle, int b, int32_t *out);
+
 /* Whether a step over more than 64 slots runs as two concurrent lanes or as one (the default); whether the step's
  * body replays captured graphs or launches its kernels one by one (the default). Both synchronize. */
 void dec_debug_set_split(void *handle, int on);

@@ -428,19 +428,22 @@ __global__ void set_active_kernel(unsigned long long *active, SlotMasks m) {
 
 __global__ void take_alt_kernel(int32_t *tokens, const int32_t *alt_tokens, int b) { tokens[b] = alt_tokens[b]; }
 
-/* Copy n positions of every layer and head between two places of the same pools: (page src_page0 + (src_pos + i) / 16,
- * slot (src_pos + i) % 16) -> likewise at dst; codes keep their tile layout, both scales move. A wave per
- * (position, layer, head); lane l moves dims l and l + 64 of K and of V. */
+/* Copy n positions of every layer and head between two places of the same pools: position p of a side is slot p % 16
+ * of page tab[p / 16] (a slot's block-table row) or, with tab NULL, of page page0 + p / 16 (the prompt store); codes
+ * keep their tile layout, both scales move. A wave per (position, layer, head); lane l moves dims l and l + 64. */
 __global__ void __launch_bounds__(256) copy_positions_kernel(uint8_t *k_pages, uint8_t *v_pages, float *kv_scale,
-                                                             long long layer_pages, int H, int L, long long src_page0,
-                                                             int src_pos, long long dst_page0, int dst_pos, int n) {
+                                                             long long layer_pages, int H, int L, const int32_t *src_tab,
+                                                             long long src_page0, int src_pos, const int32_t *dst_tab,
+                                                             long long dst_page0, int dst_pos, int n) {
     const long long unit = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & (WAVE - 1);
     if (unit >= (long long)n * L * H) return;
     const int h = (int)(unit % H), l = (int)(unit / H % L), i = (int)(unit / ((long long)H * L));
     const int sp = src_pos + i, dp = dst_pos + i;
-    const long long sa = ((long long)l * layer_pages + src_page0 + sp / PAGE) * H + h;
-    const long long da = ((long long)l * layer_pages + dst_page0 + dp / PAGE) * H + h;
+    const long long spage = src_tab ? src_tab[sp / PAGE] : src_page0 + sp / PAGE;
+    const long long dpage = dst_tab ? dst_tab[dp / PAGE] : dst_page0 + dp / PAGE;
+    const long long sa = ((long long)l * layer_pages + spage) * H + h;
+    const long long da = ((long long)l * layer_pages + dpage) * H + h;
     const int ss = sp % PAGE, ds = dp % PAGE;
 #pragma unroll
     for (int half = 0; half < 2; half++) {
@@ -454,6 +457,28 @@ __global__ void __launch_bounds__(256) copy_positions_kernel(uint8_t *k_pages, u
 __global__ void identity_table_kernel(int32_t *table, long long n) {
     const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
     if (i < n) table[i] = (int32_t)i;
+}
+
+/* table[idx0 + i] = value0 + i for i < count */
+__global__ void set_table_kernel(int32_t *table, long long idx0, int count, int value0) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < count) table[idx0 + i] = value0 + i;
+}
+
+/* Whole pages src_page0 + z -> dst_page0 + z of layer y and head x: 2 KiB of K codes, 2 KiB of V codes, 128 bytes of
+ * scales. */
+__global__ void __launch_bounds__(256) copy_pages_kernel(uint8_t *k_pages, uint8_t *v_pages, float *kv_scale,
+                                                         long long layer_pages, int H, long long src_page0,
+                                                         long long dst_page0) {
+    const int h = blockIdx.x, l = blockIdx.y, t = threadIdx.x;
+    const long long sa = ((long long)l * layer_pages + src_page0 + blockIdx.z) * H + h;
+    const long long da = ((long long)l * layer_pages + dst_page0 + blockIdx.z) * H + h;
+    if (t < 128)
+        reinterpret_cast<uint4 *>(k_pages + da * PAGE_BYTES)[t] = reinterpret_cast<const uint4 *>(k_pages + sa * PAGE_BYTES)[t];
+    else
+        reinterpret_cast<uint4 *>(v_pages + da * PAGE_BYTES)[t - 128] =
+            reinterpret_cast<const uint4 *>(v_pages + sa * PAGE_BYTES)[t - 128];
+    if (t < 8) reinterpret_cast<float4 *>(kv_scale + da * 2 * PAGE)[t] = reinterpret_cast<const float4 *>(kv_scale + sa * 2 * PAGE)[t];
 }
 
 /* ---------------------------------------------------------------- the decoder */
@@ -498,7 +523,11 @@ struct Decoder {
     size_t lt_ws_bytes;
     uint8_t *k_pages, *v_pages;          /* [L][layer_pages][H][2048] */
     float *kv_scale;                     /* [L][layer_pages][H][2][16] */
-    int32_t *block_table;                /* [B][max_pages], identity */
+    int32_t *block_table;                /* [B][max_pages]: slot b's entry e is its own page b max_pages + e, or a
+                                            store page it shares read-only after dec_load_prompt */
+    std::vector<int32_t> table;          /* host copy of block_table (what the enqueued work leaves there) */
+    std::vector<int32_t> hpos;           /* host copy of pos: the position a live slot's next step writes */
+    std::vector<unsigned long long> live;  /* host copy of the live-slot mask of dec_set_active */
     int32_t *tokens, *alt_tokens, *pos, *first, *seq_lens, *num_new;  /* [B] */
     float *temperature, *top_p;
     unsigned long long *seed;
@@ -941,6 +970,10 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     d->block_table = (int32_t *)device_alloc(d, (size_t)d->slot_pages * sizeof(int32_t));
     hipLaunchKernelGGL(identity_table_kernel, dim3((unsigned)((d->slot_pages + 255) / 256)), dim3(256), 0, d->stream,
                        d->block_table, d->slot_pages);
+    d->table.resize(d->slot_pages);
+    for (long long i = 0; i < d->slot_pages; i++) d->table[i] = (int32_t)i;
+    d->hpos.assign(d->B, 0);
+    d->live.assign(MASK_WORDS, 0);
     const size_t B = d->B;
     int32_t *state = (int32_t *)device_alloc(d, B * 6 * sizeof(int32_t));
     d->tokens = state; d->alt_tokens = state + B; d->pos = state + 2 * B; d->first = state + 3 * B;
@@ -989,17 +1022,107 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     return d;
 }
 
-/* Slot b's positions [at, at + n) <-> store positions [store_at, store_at + n), every layer. */
-static void prompt_copy(Decoder *d, int b, int at, int store_at, int n, bool to_store) {
+/* ---------------------------------------------------------------- the prompt store as shared pages
+ *
+ * dec_load_prompt points a slot's block-table entries at the store's pages wherever the two ranges share their page
+ * phase ((store_at - at) % 16 == 0) and a page lies wholly inside the range: the prompt's K and V are then read in
+ * place, with no copy (the reference copies the store into the slot, decode.cu:1055-1075). Partial pages are copied
+ * as before. Nothing ever writes a shared page: before any write into a slot (a prefill row, a live slot's step at
+ * its host-tracked position, a partial copy) the entry is first pointed back at the slot's own page, with the store
+ * page's content copied there (copy on write); before dec_save_prompt writes store pages, every slot sharing them
+ * gets its own copy. */
+
+static long long home_page(const Decoder *d, int b, int e) { return (long long)b * d->max_pages + e; }
+
+/* Slot b's host entries [e0, e1) to the device table, one launch per run of consecutive pages. */
+static void upload_table(Decoder *d, int b, int e0, int e1) {
+    const int32_t *row = d->table.data() + home_page(d, b, 0);
+    for (int e = e0; e < e1;) {
+        int f = e + 1;
+        while (f < e1 && row[f] == row[f - 1] + 1) f++;
+        hipLaunchKernelGGL(set_table_kernel, dim3((unsigned)((f - e + 255) / 256)), dim3(256), 0, d->stream,
+                           d->block_table, home_page(d, b, e), f - e, row[e]);
+        e = f;
+    }
+    HIP_CHECK(hipGetLastError());
+}
+
+/* Slot b's entries [e0, e1) that share a store page point back at the slot's own page; with keep, the shared page is
+ * first copied there, so the positions the slot does not rewrite keep their values. */
+static void unshare(Decoder *d, int b, int e0, int e1, bool keep) {
+    int32_t *row = d->table.data() + home_page(d, b, 0);
+    int lo = e1, hi = e0;
+    for (int e = e0; e < e1;) {
+        if (row[e] == home_page(d, b, e)) {
+            e++;
+            continue;
+        }
+        int f = e + 1;
+        while (f < e1 && row[f] != home_page(d, b, f) && row[f] == row[f - 1] + 1) f++;
+        if (keep) {
+            hipLaunchKernelGGL(copy_pages_kernel, dim3((unsigned)d->H, (unsigned)d->L, (unsigned)(f - e)), dim3(256), 0,
+                               d->stream, d->k_pages, d->v_pages, d->kv_scale, d->layer_pages, d->H, (long long)row[e],
+                               home_page(d, b, e));
+            HIP_CHECK(hipGetLastError());
+        }
+        for (int i = e; i < f; i++) row[i] = (int32_t)home_page(d, b, i);
+        lo = e < lo ? e : lo;
+        hi = f > hi ? f : hi;
+        e = f;
+    }
+    if (lo < hi) upload_table(d, b, lo, hi);
+}
+
+/* Positions [at, at + n) of slot b (through its block table) <-> store positions [store_at, store_at + n). */
+static void copy_positions(Decoder *d, int b, int at, int store_at, int n, bool to_store) {
     if (n <= 0) return;
-    if (b < 0 || b >= d->B || at < 0 || at + n > d->max_len || store_at < 0 || store_at + n > d->store)
-        die("dec_save_prompt/dec_load_prompt", "slot or position range out of bounds", __LINE__);
-    const long long slot_page0 = (long long)b * d->max_pages, store_page0 = d->slot_pages;
+    const int32_t *tab = d->block_table + home_page(d, b, 0);
     const long long units = (long long)n * d->L * d->H;
     hipLaunchKernelGGL(copy_positions_kernel, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, d->stream, d->k_pages,
-                       d->v_pages, d->kv_scale, d->layer_pages, d->H, d->L, to_store ? slot_page0 : store_page0,
-                       to_store ? at : store_at, to_store ? store_page0 : slot_page0, to_store ? store_at : at, n);
+                       d->v_pages, d->kv_scale, d->layer_pages, d->H, d->L, to_store ? tab : nullptr, d->slot_pages,
+                       to_store ? at : store_at, to_store ? nullptr : tab, d->slot_pages, to_store ? store_at : at, n);
     HIP_CHECK(hipGetLastError());
+}
+
+static void check_prompt_range(const Decoder *d, int b, int at, int store_at, int n) {
+    if (b < 0 || b >= d->B || at < 0 || n < 0 || at + n > d->max_len || store_at < 0 || store_at + n > d->store)
+        die("dec_save_prompt/dec_load_prompt", "slot or position range out of bounds", __LINE__);
+}
+
+static void save_prompt(Decoder *d, int b, int at, int store_at, int n) {
+    check_prompt_range(d, b, at, store_at, n);
+    if (n == 0) return;
+    /* slots sharing the store pages about to change keep their own copies */
+    const int32_t p0 = (int32_t)(d->slot_pages + store_at / PAGE), p1 = (int32_t)(d->slot_pages + (store_at + n - 1) / PAGE);
+    for (int s = 0; s < d->B; s++) {
+        const int32_t *row = d->table.data() + home_page(d, s, 0);
+        for (int e = 0; e < d->max_pages; e++)
+            if (row[e] >= p0 && row[e] <= p1) unshare(d, s, e, e + 1, true);
+    }
+    copy_positions(d, b, at, store_at, n, true);
+}
+
+static void load_prompt(Decoder *d, int b, int at, int store_at, int n) {
+    check_prompt_range(d, b, at, store_at, n);
+    if (n == 0) return;
+    const int e_lo = (at + PAGE - 1) / PAGE, e_hi = (at + n) / PAGE;   /* pages wholly inside [at, at + n) */
+    if ((store_at - at) % PAGE != 0 || e_lo >= e_hi) {
+        unshare(d, b, at / PAGE, (at + n - 1) / PAGE + 1, true);
+        copy_positions(d, b, at, store_at, n, false);
+        return;
+    }
+    if (at % PAGE) {   /* the leading partial page */
+        unshare(d, b, at / PAGE, at / PAGE + 1, true);
+        copy_positions(d, b, at, store_at, e_lo * PAGE - at, false);
+    }
+    if ((at + n) % PAGE) {   /* the trailing partial page */
+        unshare(d, b, e_hi, e_hi + 1, true);
+        copy_positions(d, b, e_hi * PAGE, store_at + (e_hi * PAGE - at), at + n - e_hi * PAGE, false);
+    }
+    int32_t *row = d->table.data() + home_page(d, b, 0);
+    const long long shift = d->slot_pages + (store_at - at) / PAGE;
+    for (int e = e_lo; e < e_hi; e++) row[e] = (int32_t)(shift + e);
+    upload_table(d, b, e_lo, e_hi);
 }
 
 static void prefill(Decoder *d, int n, const int32_t *rows) {
@@ -1009,6 +1132,7 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
     for (int r = 0; r < n; r++)
         if (slot[r] < 0 || slot[r] >= d->B || pos[r] < 0 || pos[r] >= d->max_len || tok[r] < 0 || tok[r] >= d->vocab)
             die("dec_prefill", "row with a slot, position or token out of range", __LINE__);
+    for (int r = 0; r < n; r++) unshare(d, slot[r], pos[r] / PAGE, pos[r] / PAGE + 1, true);
     HIP_CHECK(hipEventSynchronize(d->staged));  /* the previous upload has been read */
     int32_t *s = d->staging;
     memcpy(s, tok, n * sizeof(int32_t));
@@ -1104,6 +1228,7 @@ extern "C" void dec_set_prompt(void *handle, int b, int32_t token, int32_t last,
     hipLaunchKernelGGL(nc::dec::set_slot_kernel, dim3(1), dim3(1), 0, d->stream, d->tokens, d->pos, d->first,
                        d->temperature, d->top_p, d->seed, b, token, last, temperature, top_p, seed);
     HIP_CHECK(hipGetLastError());
+    d->hpos[b] = last;
 }
 
 extern "C" int dec_prefill_rows(void *) { return nc::dec::PREFILL_ROWS; }
@@ -1111,11 +1236,11 @@ extern "C" int dec_prefill_rows(void *) { return nc::dec::PREFILL_ROWS; }
 extern "C" void dec_prefill(void *handle, int n, const int32_t *rows) { nc::dec::prefill((Decoder *)handle, n, rows); }
 
 extern "C" void dec_save_prompt(void *handle, int b, int at, int store_at, int n) {
-    nc::dec::prompt_copy((Decoder *)handle, b, at, store_at, n, true);
+    nc::dec::save_prompt((Decoder *)handle, b, at, store_at, n);
 }
 
 extern "C" void dec_load_prompt(void *handle, int b, int at, int store_at, int n) {
-    nc::dec::prompt_copy((Decoder *)handle, b, at, store_at, n, false);
+    nc::dec::load_prompt((Decoder *)handle, b, at, store_at, n);
 }
 
 extern "C" uint32_t *dec_masks(void *handle) { return ((Decoder *)handle)->host_allow; }
@@ -1140,6 +1265,7 @@ extern "C" void dec_set_active(void *handle, const unsigned long long *slots) {
     hipLaunchKernelGGL(set_active_kernel, dim3(1), dim3(64), 0, d->stream, d->active, m);
     HIP_CHECK(hipGetLastError());
     d->narrow = high + 1;
+    for (int w = 0; w < MASK_WORDS; w++) d->live[w] = w < words ? slots[w] : 0;
     if (lo >= 0) {
         const size_t n = d->vocab / WORD_BITS;
         HIP_CHECK(hipMemcpyAsync(d->allow + lo * n, d->host_allow + lo * n, (hi + 1 - lo) * n * sizeof(uint32_t),
@@ -1148,13 +1274,21 @@ extern "C" void dec_set_active(void *handle, const unsigned long long *slots) {
 }
 
 extern "C" void dec_launch_body(void *handle) {
-    nc::dec::enqueue_body((Decoder *)handle);
+    Decoder *d = (Decoder *)handle;
+    /* the step writes each live slot's K and V at its position: that page must be the slot's own */
+    for (int b = 0; b < d->B; b++)
+        if (((d->live[b / nc::dec::MASK_BITS] >> (b % nc::dec::MASK_BITS)) & 1ull) && d->hpos[b] < d->max_len)
+            nc::dec::unshare(d, b, d->hpos[b] / nc::PAGE, d->hpos[b] / nc::PAGE + 1, true);
+    nc::dec::enqueue_body(d);
     HIP_CHECK(hipGetLastError());
 }
 
 extern "C" void dec_launch_head(void *handle) {
-    nc::dec::enqueue_head((Decoder *)handle);
+    Decoder *d = (Decoder *)handle;
+    nc::dec::enqueue_head(d);
     HIP_CHECK(hipGetLastError());
+    for (int b = 0; b < d->B; b++)   /* choose_kernel's commit: pos += 1 for live slots */
+        if ((d->live[b / nc::dec::MASK_BITS] >> (b % nc::dec::MASK_BITS)) & 1ull) d->hpos[b]++;
 }
 
 extern "C" void dec_tokens(void *handle, int32_t *out) {
@@ -1187,14 +1321,19 @@ extern "C" void dec_debug_cache(void *handle, int layer, int b, int at, int n, u
         dec::die("dec_debug_cache", "layer, slot or position range out of bounds", __LINE__);
     if (n == 0) return;
     HIP_CHECK(hipStreamSynchronize(d->stream));
-    const long long page0 = b < 0 ? d->slot_pages : (long long)b * d->max_pages;
     const int first = at / PAGE, last = (at + n - 1) / PAGE, pages = last - first + 1, H = d->H;
     std::vector<uint8_t> kp((size_t)pages * H * PAGE_BYTES), vp(kp.size());
     std::vector<float> sp((size_t)pages * H * 2 * PAGE);
-    const size_t base = (size_t)(d->layer_pages * layer + page0 + first) * H;
-    HIP_CHECK(hipMemcpy(kp.data(), d->k_pages + base * PAGE_BYTES, kp.size(), hipMemcpyDeviceToHost));
-    HIP_CHECK(hipMemcpy(vp.data(), d->v_pages + base * PAGE_BYTES, vp.size(), hipMemcpyDeviceToHost));
-    HIP_CHECK(hipMemcpy(sp.data(), d->kv_scale + base * 2 * PAGE, sp.size() * sizeof(float), hipMemcpyDeviceToHost));
+    for (int pg = 0; pg < pages; pg++) {   /* a slot's pages through its block table, the store's in order */
+        const long long page = b < 0 ? d->slot_pages + first + pg : d->table[(size_t)b * d->max_pages + first + pg];
+        const size_t base = (size_t)(d->layer_pages * layer + page) * H, at_h = (size_t)pg * H;
+        HIP_CHECK(hipMemcpy(kp.data() + at_h * PAGE_BYTES, d->k_pages + base * PAGE_BYTES, (size_t)H * PAGE_BYTES,
+                            hipMemcpyDeviceToHost));
+        HIP_CHECK(hipMemcpy(vp.data() + at_h * PAGE_BYTES, d->v_pages + base * PAGE_BYTES, (size_t)H * PAGE_BYTES,
+                            hipMemcpyDeviceToHost));
+        HIP_CHECK(hipMemcpy(sp.data() + at_h * 2 * PAGE, d->kv_scale + base * 2 * PAGE, (size_t)H * 2 * PAGE * sizeof(float),
+                            hipMemcpyDeviceToHost));
+    }
     for (int i = 0; i < n; i++) {
         const int p = at + i, pg = p / PAGE - first, slot = p % PAGE;
         for (int h = 0; h < H; h++) {
@@ -1207,6 +1346,14 @@ extern "C" void dec_debug_cache(void *handle, int layer, int b, int at, int n, u
             scales[((size_t)i * H + h) * 2 + 1] = sp[(unit * 2 + 1) * PAGE + slot];
         }
     }
+}
+
+/* Slot b's block-table row (max_pages entries, host copy): entry e is b * max_pages + e (the slot's own page) or
+ * B * max_pages + i (page i of the prompt store, shared after dec_load_prompt). */
+extern "C" void dec_debug_table(void *handle, int b, int32_t *out) {
+    Decoder *d = (Decoder *)handle;
+    if (b < 0 || b >= d->B) nc::dec::die("dec_debug_table", "slot out of range", __LINE__);
+    memcpy(out, d->table.data() + (size_t)b * d->max_pages, (size_t)d->max_pages * sizeof(int32_t));
 }
 
 static const bool skinny_enabled = false;

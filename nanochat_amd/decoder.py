@@ -20,7 +20,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from .config import HEAD_DIM
+from .config import HEAD_DIM, PAGE_SIZE
 from .native import hip_library
 
 GLOBAL_PTRS, LAYER_PTRS = 4, 8   # dec_create's pointer layout (decode.cu:950-953)
@@ -194,6 +194,12 @@ class PagedDecoder:
         self.lib.dec_debug_cache(self.handle, layer, b, at, n, k.ctypes.data, v.ctypes.data, s.ctypes.data)
         return k, v, s
 
+    def table(self, b: int) -> np.ndarray:
+        """Test hook: slot b's block-table row (own page b * pages + e, or batch * pages + i: store page i)."""
+        out = np.empty(-(-self.max_length // PAGE_SIZE), np.int32)
+        self.lib.dec_debug_table(self.handle, b, out.ctypes.data)
+        return out
+
     # ---- requests (the reference's NativeDecoder.start / prefill / save / generate)
     def start(self, b: int, index: int, request: Request) -> Slot:
         n = len(request.input_ids) - 1
@@ -229,13 +235,15 @@ class PagedDecoder:
         self.pending = []
 
     def save(self, b: int, input_ids: list[int]) -> None:
-        """Keep slot b's prompt K and V in the store's next free positions, unless stored or full (never evicted)."""
+        """Keep slot b's prompt K and V in the store's next free positions, unless stored or full (never evicted).
+        Each prompt starts on a page boundary of the store, so dec_load_prompt shares its whole pages with the slots
+        that load it instead of copying them (the reference packs prompts back to back, decoder.py:226-232)."""
         key, n = tuple(input_ids), len(input_ids) - 1
         if key in self.stored or self.used + n > self.store:
             return
         self.lib.dec_save_prompt(self.handle, b, 0, self.used, n)
         self.stored[key] = self.used
-        self.used += n
+        self.used = -(-(self.used + n) // PAGE_SIZE) * PAGE_SIZE
 
     @torch.no_grad()
     def generate(self, requests: Iterable[Request]) -> Iterator[tuple[int, list[int]]]:

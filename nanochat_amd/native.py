@@ -125,6 +125,7 @@ DECODE_SIGNATURES = {
     "dec_destroy": ([c_void_p], None),
     "dec_debug_logits": ([c_void_p, c_void_p, c_int], None),
     "dec_debug_cache": ([c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p], None),
+    "dec_debug_table": ([c_void_p, c_int, c_void_p], None),
     "dec_debug_set_split": ([c_void_p, c_int], None),
     "dec_debug_set_graphs": ([c_void_p, c_int], None),
     "dec_debug_gemm": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,

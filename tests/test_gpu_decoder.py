@@ -127,17 +127,20 @@ def test_prompt_store_round_trip_and_reuse(device):
     try:
         for b in (0, 1):
             dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
-        dec.prefill()                                  # prefills, then saves both prompts (store positions 0, 49)
-        assert dec.stored == {tuple(ids[0]): 0, tuple(ids[1]): 49}
+        dec.prefill()                                  # prefills, then saves both prompts (store positions 0, 64)
+        assert dec.stored == {tuple(ids[0]): 0, tuple(ids[1]): 64}
         dec.start(5, 2, Request(input_ids=ids[0], max_new_tokens=4))   # loaded from the store, not prefilled
         assert not dec.pending
         n = len(ids[0]) - 1
+        pages = len(dec.table(5))
+        # the prompt's 3 whole pages are the store's (shared), the partial 4th is the slot's own copy
+        assert list(dec.table(5)[:4]) == [dec.batch * pages + e for e in range(3)] + [5 * pages + 3]
         for layer in range(len(m.layers)):
             a, s_ = dec.cache_rows(layer, 0, 0, n), dec.cache_rows(layer, -1, 0, n)
             c = dec.cache_rows(layer, 5, 0, n)
             for x, y, z in zip(a, s_, c):
                 assert np.array_equal(x, y) and np.array_equal(x, z), layer
-            t1 = dec.cache_rows(layer, -1, 49, len(ids[1]) - 1)
+            t1 = dec.cache_rows(layer, -1, 64, len(ids[1]) - 1)
             for x, y in zip(dec.cache_rows(layer, 1, 0, len(ids[1]) - 1), t1):
                 assert np.array_equal(x, y), layer
         dec.flags[0, [0, 1, 5]] = True
@@ -148,6 +151,53 @@ def test_prompt_store_round_trip_and_reuse(device):
         # fp32 sums (and downstream bf16 roundings) may differ: equal within the logit tolerance
         assert tokens[0] == tokens[5]
         assert np.abs(got[0] - got[5]).max() <= LOGIT_MAX_REL * np.abs(got[0]).max()
+    finally:
+        dec.close()
+
+
+def test_shared_store_pages_copy_on_write(device):
+    """A loaded prompt's whole pages are shared with the store; every later write into the slot or the store gives
+    the writer its own page: a prefill over a shared range, a save over shared store pages, a load at another page
+    phase (copied, not shared). Cache bytes compared through the block tables after each."""
+    m, w, max_length = build(device, "tiny")
+    ids = prompts([50, 41], m.vocab, seed=12)
+    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=400, max_slots=8)
+    L = len(m.layers)
+    try:
+        for b in (0, 1):   # each prefilled alone, so slot 3's prefill of B below runs the same GEMM shapes
+            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+            dec.prefill()                               # A = ids[0] at store 0, B = ids[1] at store 64
+        assert dec.stored == {tuple(ids[0]): 0, tuple(ids[1]): 64}
+        nA, nB = len(ids[0]) - 1, len(ids[1]) - 1
+        A = [dec.cache_rows(l, 0, 0, nA) for l in range(L)]
+        B = [dec.cache_rows(l, 1, 0, nB) for l in range(L)]
+        pages = len(dec.table(0))
+        store = dec.batch * pages
+
+        def same(got, want):
+            return all(np.array_equal(x, y) for x, y in zip(got, want))
+
+        dec.lib.dec_load_prompt(dec.handle, 3, 0, 0, nA)           # slot 3 shares A's pages 0..2
+        assert list(dec.table(3)[:3]) == [store, store + 1, store + 2]
+        dec.lib.dec_prefill(dec.handle, nB, np.ascontiguousarray(
+            np.array([ids[1][:-1], range(nB), [3] * nB], dtype=np.int32)).ctypes.data)   # B over A's shared pages
+        assert list(dec.table(3)[:3]) == [3 * pages + e for e in range(3)]
+        for l in range(L):
+            assert same(dec.cache_rows(l, 3, 0, nB), B[l]), l            # slot 3 holds B's rows
+            assert same(dec.cache_rows(l, -1, 0, nA), A[l]), l           # the store still holds A
+            assert same(dec.cache_rows(l, 3, nB, nA - nB), [x[nB:] for x in A[l]]), l   # A's rows past B kept (CoW)
+
+        dec.lib.dec_load_prompt(dec.handle, 4, 0, 0, nA)           # slot 4 shares A ...
+        dec.lib.dec_save_prompt(dec.handle, 1, 0, 0, nB)           # ... then B overwrites store positions 0..39
+        assert list(dec.table(4)[:3]) == [4 * pages + e for e in range(3)]
+        for l in range(L):
+            assert same(dec.cache_rows(l, 4, 0, nA), A[l]), l            # slot 4 kept A
+            assert same(dec.cache_rows(l, -1, 0, nB), B[l]), l
+
+        dec.lib.dec_load_prompt(dec.handle, 6, 3, 64, nB)          # another page phase: copied, nothing shared
+        assert list(dec.table(6)) == [6 * pages + e for e in range(pages)]
+        for l in range(L):
+            assert same(dec.cache_rows(l, 6, 3, nB), B[l]), l
     finally:
         dec.close()
 
