@@ -6,10 +6,11 @@
  * The step (attend_pair) streams two 16-token pages of one KV head straight from HBM into registers:
  * each lane issues four 16-byte loads per page pair per operand, every load instruction covering 1 KiB
  * contiguously, because the page tiling (nc_device.h) is the MFMA operand layout. Scores are
- * S^T = K Q^T by four v_mfma_f32_16x16x32_bf16 per page (fp8 codes converted exactly to bf16; the
- * per-token K scale multiplies the fp32 dot product), the online softmax runs in the log2 domain on the
- * MFMA result layout, and O^T += V^T P^T by eight MFMAs per pair with the V scale folded into P before
- * its bf16 rounding. Query columns (lane & 15) are query heads in decode and (token, head) rows in
+ * S^T = K Q^T by two v_mfma_scale_f32_16x16x128_f8f6f4 per page and tile, the cache's e4m3 K codes as they are
+ * against the query split into two e4m3 parts whose sum is the (power-of-two scaled) bf16 query exactly; the
+ * per-token K scale multiplies the fp32 dot product. The online softmax runs in the log2 domain on the MFMA
+ * result layout, and O^T += V^T P^T by eight v_mfma_f32_16x16x32_bf16 per pair (V codes converted exactly to
+ * bf16) with the V scale folded into P before its bf16 rounding. Query columns (lane & 15) are query heads in decode and (token, head) rows in
  * prefill; the lane's four row groups (lane >> 4) hold keys 4g..4g+3 of each page.
  *
  * Reference semantics: model/kernels/decode.cu:567-675 (k_attn: keys [max(p - window, 0), p], scale
@@ -55,6 +56,7 @@ struct WaveState {
     f32x4 o[NT][8];  /* O^T tile d: dims 16d + 4g + i of column c, scaled by 2^-m */
     float m[NT];     /* column c's reference max (log2 domain, equal in the four groups); exponentials use it */
     float l[NT];     /* sum of exp2(s - m) over the keys this lane's group holds */
+    float sl2;       /* score multiplier: sm_scale log2(e) 2^-e for queries staged as 2^e q (QOp) */
     bool bad;        /* a block-table entry fell outside the page pool */
 };
 
@@ -70,33 +72,78 @@ __device__ __forceinline__ void state_init(WaveState<NT> &st) {
     st.bad = false;
 }
 
-/* The query operand of column c (B operand of the score MFMAs): lane (g, c) holds dims g*32 + cc*8 .. +7 of
- * its row for MFMA cc; a NULL row gives zeros. */
-__device__ __forceinline__ void load_q(const uint16_t *row, int g, bf16x8 (&qb)[4]) {
-#pragma unroll
-    for (int cc = 0; cc < 4; cc++) {
-        if (row) {
-            const uint4 u = *reinterpret_cast<const uint4 *>(row + g * 32 + cc * 8);
-            qb[cc] = __builtin_bit_cast(bf16x8, u);
-        } else {
-            qb[cc] = __builtin_bit_cast(bf16x8, uint4{0u, 0u, 0u, 0u});
-        }
-    }
+/* The query operand of column c (B operand of the fp8 score MFMA v_mfma_scale_f32_16x16x128_f8f6f4, unit scales):
+ * lane (g, c) holds dims 32 g .. 32 g + 31 of its row as bytes 0..31, the same (lane, byte) -> k mapping as the K
+ * page's A operand (lane (g, key) holds that key's dims 32 g .. + 31). The row times 2^e (e uniform in the wave, so
+ * the wave's largest |q| lands in [128, 256)) is split into two e4m3 parts, hi = e4m3(x), lo = e4m3(x - hi): a bf16
+ * value has 8 significant bits and each part 4, so hi + lo = x exactly unless |x| < 2^-2 (then lo may lose bits
+ * below 2^-10, at most 2^-18 of the wave's largest element). The score MFMAs then read the cache's K codes as they
+ * are, with no conversion. */
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+struct QOp {
+    i32x8 hi, lo;
+};
+
+__device__ __forceinline__ f32x4 mfma_fp8(const i32x8 &a, const i32x8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);  /* E8M0 127: scale 1 */
 }
 
-/* Scores S^T (keys 4g + i of one page, column c of tile t) = K Q^T for every tile from one page's two K loads:
- * each converted K operand feeds NT MFMAs. */
+/* Stages NT rows (NULL: zeros) as QOp; returns 2^-e. Every lane of the wave must call it (a wave-wide max). */
 template <int NT>
-__device__ __forceinline__ void page_scores(const uint4 &k0, const uint4 &k1, const bf16x8 (&qb)[NT][4],
-                                            f32x4 (&s)[NT]) {
+__device__ __forceinline__ float load_q8(const uint16_t *const (&rows)[NT], int g, QOp (&q)[NT]) {
+    uint4 raw[NT][4];
+    float amax = 0.0f;
 #pragma unroll
-    for (int t = 0; t < NT; t++) s[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const bf16x8 k[4] = {fp8x8_to_bf16(k0.x, k0.y), fp8x8_to_bf16(k0.z, k0.w), fp8x8_to_bf16(k1.x, k1.y),
-                         fp8x8_to_bf16(k1.z, k1.w)};
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-    for (int cc = 0; cc < 4; cc++)
+        for (int cc = 0; cc < 4; cc++) {
+            raw[t][cc] = rows[t] ? *reinterpret_cast<const uint4 *>(rows[t] + g * 32 + cc * 8) : uint4{0u, 0u, 0u, 0u};
+            const uint32_t w[4] = {raw[t][cc].x, raw[t][cc].y, raw[t][cc].z, raw[t][cc].w};
 #pragma unroll
-        for (int t = 0; t < NT; t++) s[t] = mfma16x16x32(k[cc], qb[t][cc], s[t]);
+            for (int i = 0; i < 4; i++)
+                amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32((uint16_t)w[i])), fabsf(bf16_to_f32((uint16_t)(w[i] >> 16)))));
+        }
+    amax = wave_max(amax);
+    const int E = amax > 0.0f ? (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127 : 0;
+    const int e = min(max(7 - E, -120), 120);
+    const float up = __uint_as_float((uint32_t)(127 + e) << 23), down = __uint_as_float((uint32_t)(127 - e) << 23);
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const uint32_t w[4] = {raw[t][cc].x, raw[t][cc].y, raw[t][cc].z, raw[t][cc].w};
+#pragma unroll
+            for (int h = 0; h < 2; h++) {   /* dwords 2 cc + h of the operand: dims 32 g + 8 cc + 4 h .. + 3 */
+                float x[4];
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    x[2 * i] = bf16_to_f32((uint16_t)w[2 * h + i]) * up;
+                    x[2 * i + 1] = bf16_to_f32((uint16_t)(w[2 * h + i] >> 16)) * up;
+                }
+                int hi = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+                hi = __builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], hi, true);
+                const float r[4] = {x[0] - __builtin_amdgcn_cvt_f32_fp8(hi, 0), x[1] - __builtin_amdgcn_cvt_f32_fp8(hi, 1),
+                                    x[2] - __builtin_amdgcn_cvt_f32_fp8(hi, 2), x[3] - __builtin_amdgcn_cvt_f32_fp8(hi, 3)};
+                int lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+                lo = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], lo, true);
+                q[t].hi[2 * cc + h] = hi;
+                q[t].lo[2 * cc + h] = lo;
+            }
+        }
+    return down;
+}
+
+/* Scores S^T (keys 4g + i of one page, column c of tile t) = K Q^T for every tile from one page's two K loads
+ * (dims 32 g .. + 15, then + 16 .. + 31): two fp8 MFMAs a tile, hi then lo. */
+template <int NT>
+__device__ __forceinline__ void page_scores(const uint4 &k0, const uint4 &k1, const QOp (&qb)[NT], f32x4 (&s)[NT]) {
+    const i32x8 k = {(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z, (int)k1.w};
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        s[t] = mfma_fp8(k, qb[t].hi, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        s[t] = mfma_fp8(k, qb[t].lo, s[t]);
+    }
 }
 
 __device__ __forceinline__ uint32_t dword(const uint4 &u, int i) {
@@ -170,9 +217,11 @@ struct KeyBounds {
     int full_lo, full_hi, written_hi;
 };
 
-/* Softmax update and PV of one pair from its scores: per tile, the lazy rescale moves the reference max only
- * when a column's max grows past it by RESCALE_LOG2 (p <= 2^8 otherwise), decided for the whole wave at once;
- * each converted V operand feeds NT MFMAs. */
+/* Softmax update and PV of one pair from its scores. The lazy rescale moves a column's reference max only when the
+ * column's max grows past it by RESCALE_LOG2 (p <= 2^8 otherwise); the decision is taken once per pair for the whole
+ * wave and every tile (when any column of any tile needs it, each tile moves to its new max), so the pair's
+ * exponentials and PV MFMAs form one straight block with no branch between the tiles. Each converted V operand feeds
+ * NT MFMAs. */
 template <int NT, bool MASKED>
 __device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p, const f32x4 (&sa)[NT],
                                             const f32x4 (&sb)[NT], const float4 &ksa, const float4 &ksb, PairRegs &v,
@@ -186,43 +235,52 @@ __device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p
         v.a0 = and4(v.a0, ma); v.a1 = and4(v.a1, ma);
         v.b0 = and4(v.b0, mb); v.b1 = and4(v.b1, mb);
     }
-    const float ks[8] = {ksa.x * a.scale_log2, ksa.y * a.scale_log2, ksa.z * a.scale_log2, ksa.w * a.scale_log2,
-                         ksb.x * a.scale_log2, ksb.y * a.scale_log2, ksb.z * a.scale_log2, ksb.w * a.scale_log2};
+    const float ks[8] = {ksa.x * st.sl2, ksa.y * st.sl2, ksa.z * st.sl2, ksa.w * st.sl2,
+                         ksb.x * st.sl2, ksb.y * st.sl2, ksb.z * st.sl2, ksb.w * st.sl2};
     const float vs[8] = {v.sa.x, v.sa.y, v.sa.z, v.sa.w, v.sb.x, v.sb.y, v.sb.z, v.sb.w};
-    bf16x8 pv[NT];
+    float s[NT][8], mnew[NT];
+    bool ok[NT][8];
+    bool grow = false;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        float s[8];
-        bool ok[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const float acc = i < 4 ? sa[t][i] : sb[t][i - 4];
             if (MASKED) {
                 const int key = (i < 4 ? key_a : key_b) + (i & 3);
-                ok[i] = (i < 4 || p.has_b) && key >= kb.lo[t] && key <= kb.hi[t];
-                s[i] = ok[i] ? acc * ks[i] : -INFINITY;
+                ok[t][i] = (i < 4 || p.has_b) && key >= kb.lo[t] && key <= kb.hi[t];
+                s[t][i] = ok[t][i] ? acc * ks[i] : -INFINITY;
             } else {
-                ok[i] = true;
-                s[i] = acc * ks[i];
+                ok[t][i] = true;
+                s[t][i] = acc * ks[i];
             }
         }
-        float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+        float mt = fmaxf(fmaxf(fmaxf(s[t][0], s[t][1]), fmaxf(s[t][2], s[t][3])),
+                         fmaxf(fmaxf(s[t][4], s[t][5]), fmaxf(s[t][6], s[t][7])));
         mt = pair_max32(pair_max16(mt));   /* the column's max over the four row groups */
-        const float mnew = fmaxf(st.m[t], mt);
-        if (__any(mnew > st.m[t] + RESCALE_LOG2)) {
-            const float alpha = mnew == st.m[t] ? 1.0f : __builtin_amdgcn_exp2f(st.m[t] - mnew);
+        mnew[t] = fmaxf(st.m[t], mt);
+        grow = grow || mnew[t] > st.m[t] + RESCALE_LOG2;
+    }
+    if (__any(grow)) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float alpha = mnew[t] == st.m[t] ? 1.0f : __builtin_amdgcn_exp2f(st.m[t] - mnew[t]);
 #pragma unroll
             for (int d = 0; d < 8; d++) st.o[t][d] *= alpha;
             st.l[t] *= alpha;
-            st.m[t] = mnew;
+            st.m[t] = mnew[t];
         }
+    }
+    bf16x8 pv[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
         const float mbase = st.m[t] == -INFINITY ? 0.0f : st.m[t];  /* no key yet: every s is -inf */
         float psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float pr = __builtin_amdgcn_exp2f(s[i] - mbase);
+            const float pr = __builtin_amdgcn_exp2f(s[t][i] - mbase);
             psum += pr;
-            pv[t][i] = (__bf16)(ok[i] ? pr * vs[i] : 0.0f);
+            pv[t][i] = (__bf16)(ok[t][i] ? pr * vs[i] : 0.0f);
         }
         st.l[t] += psum;
     }
@@ -255,7 +313,7 @@ __device__ __forceinline__ void pair_step(const AttnArgs &a, const PairAddr &cur
  */
 template <int NT, bool PREFETCH>
 __device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *bt, int kvh, int lpa0, int step, int end,
-                                             const KeyBounds<NT> &kb, const bf16x8 (&qb)[NT][4], WaveState<NT> &st,
+                                             const KeyBounds<NT> &kb, const QOp (&qb)[NT], WaveState<NT> &st,
                                              int lane) {
     if (lpa0 >= end) return;
     if (PREFETCH) {
@@ -357,7 +415,7 @@ __device__ __forceinline__ void load_pair_b(const uint8_t *pages, const float *s
 /* One pair from registers already loaded: scores, softmax, PV. */
 template <int NT>
 __device__ __forceinline__ void pair_from_regs(const AttnArgs &a, const PairAddr &cur, const PairRegs &kr,
-                                               PairRegs &vr, const KeyBounds<NT> &kb, const bf16x8 (&qb)[NT][4],
+                                               PairRegs &vr, const KeyBounds<NT> &kb, const QOp (&qb)[NT],
                                                WaveState<NT> &st, int lane) {
     f32x4 sa[NT], sb[NT];
     page_scores<NT>(kr.a0, kr.a1, qb, sa);
@@ -369,7 +427,7 @@ __device__ __forceinline__ void pair_from_regs(const AttnArgs &a, const PairAddr
  * starts computing, so a whole pair's loads stay in flight behind every pair's math and no copy waits on a load. */
 template <int NT>
 __device__ __forceinline__ void attend_pages_tab(const AttnArgs &a, const TabRegs &tab, int tab0, int kvh, int lpa0,
-                                                 int end, const KeyBounds<NT> &kb, const bf16x8 (&qb)[NT][4],
+                                                 int end, const KeyBounds<NT> &kb, const QOp (&qb)[NT],
                                                  WaveState<NT> &st, int lane) {
     /* wave-uniform in scalar registers, so a pair's address math is scalar and borrows no vector register a load in
      * flight still owns */
@@ -476,10 +534,11 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         const int first = pg0 + (int)(s - us), last = pg0 + (int)(seg_end - us);
         const long long row0 = (long long)b * a.Hq + kvh * a.G;
 
-        bf16x8 qb[1][4];
-        load_q(c < a.G ? a.q + (row0 + c) * HEAD_DIM : nullptr, g, qb[0]);
+        QOp qb[1];
+        const uint16_t *const qrows[1] = {c < a.G ? a.q + (row0 + c) * HEAD_DIM : nullptr};
         WaveState<1> st;
         state_init(st);
+        st.sl2 = a.scale_log2 * load_q8<1>(qrows, g, qb);
         KeyBounds<1> kb;
         kb.lo[0] = kb.full_lo = begin;
         kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
@@ -536,6 +595,9 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
 __global__ void __launch_bounds__(HEAD_DIM) decode_combine_kernel(AttnArgs a) {
     const int b = blockIdx.x / a.Hq, h = blockIdx.x % a.Hq, d = threadIdx.x;
     const long long row = blockIdx.x;
+    const int u = b * a.Hkv + h / a.G, c = h % a.G;
+    /* the unit's partial range is loaded together with the sequence length (neither waits for the other) */
+    const int first = a.meta[2 * u], count = a.meta[2 * u + 1];
     const int L = a.seq_lens[b];
     if (L <= 0) {
         a.out[row * HEAD_DIM + d] = 0;
@@ -546,8 +608,6 @@ __global__ void __launch_bounds__(HEAD_DIM) decode_combine_kernel(AttnArgs a) {
         a.out[row * HEAD_DIM + d] = (uint16_t)0x7FC0;
         return;
     }
-    const int u = b * a.Hkv + h / a.G, c = h % a.G;
-    const int first = a.meta[2 * u], count = a.meta[2 * u + 1];
     if (count <= 1) return;  /* finished by its only wave */
     const float *ml = a.part_ml + ((long long)first * a.G + c) * 2;
     const float *po = a.part_o + ((long long)first * a.G + c) * HEAD_DIM + d;
@@ -612,11 +672,13 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     const int w_lo = a.window >= 0 ? max(start + t0 - a.window, 0) : 0;
     const int pg0 = w_lo / PAGE, pg1 = (start + t_last) / PAGE + 1;
 
-    bf16x8 qb[NT][4];
+    QOp qb[NT];
+    const uint16_t *qrows[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) load_q(live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr, g, qb[t]);
+    for (int t = 0; t < NT; t++) qrows[t] = live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr;
     WaveState<NT> st;
     state_init(st);
+    st.sl2 = a.scale_log2 * load_q8<NT>(qrows, g, qb);
     attend_pages<NT, true>(a, a.block_table + (long long)trow * a.max_pages, kvh, pg0, 2, pg1, kb, qb, st, lane);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -704,7 +766,7 @@ template <int NT>
 __device__ __forceinline__ void pf_compute(const AttnArgs &a, const int *tab, int pg0, int npages, int s,
                                            const PfStage &st, const PfScales &scs, int wpg0, int wpg1,
                                            const KeyBounds<NT> &kb,
-                                           const bf16x8 (&qb)[NT][4], WaveState<NT> &st_w, int lane) {
+                                           const QOp (&qb)[NT], WaveState<NT> &st_w, int lane) {
     const int la = 2 * s;
     if (la >= npages || pg0 + la + 1 < wpg0 || pg0 + la >= wpg1) return;
     const bool has_b = la + 1 < npages;
@@ -786,11 +848,13 @@ __global__ void __launch_bounds__(256, 2) prefill_lds_kernel(AttnArgs a) {
 
     const int32_t *bt = a.block_table + (long long)trow * a.max_pages + pg0;
     for (int i = threadIdx.x; i < npages; i += 256) tab[i] = bt[i];
-    bf16x8 qb[NT][4];
+    QOp qb[NT];
+    const uint16_t *qrows[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) load_q(live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr, g, qb[t]);
+    for (int t = 0; t < NT; t++) qrows[t] = live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr;
     WaveState<NT> st;
     state_init(st);
+    st.sl2 = a.scale_log2 * load_q8<NT>(qrows, g, qb);
     __syncthreads();   /* the table is in LDS (no fetch is in flight yet, so this fence drains nothing) */
 
     const int stages = (npages + 1) / 2;
