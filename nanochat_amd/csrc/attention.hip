@@ -738,58 +738,75 @@ __device__ __forceinline__ void pf_barrier() {
     asm volatile("" ::: "memory");
 }
 
-/* The fetches of stage s (logical pages pg0 + 2 s, + 1) into buffer st: wave w fetches K bytes [1024 w, + 1024) of the
- * pair (pages a, a, b, b), the same of V, and all 256 scale bytes into its own slot (4 bytes a lane: no lane is
- * masked off, so the compiler can count the fetches). Past the page range (s >= the workgroup's stages) it fetches
- * the last pair again, so every wave always issues PF_FETCHES. */
-__device__ __forceinline__ void pf_fetch(const AttnArgs &a, const int *tab, int npages, int kvh, int s, PfStage &st,
-                                         PfScales &sc, int wave, int lane) {
-    const int last = (npages - 1) / 2;
-    const int ps = min(s, last);
-    int la = 2 * ps, lb = la + 1 < npages ? la + 1 : la;
-    int pa = tab[la], pb = tab[lb];
-    pa = (unsigned)pa < (unsigned)a.num_pages ? pa : 0;
-    pb = (unsigned)pb < (unsigned)a.num_pages ? pb : 0;
-    const long long ph = (long long)(wave < 2 ? pa : pb) * a.Hkv + kvh;
+/* The pages of stage s (logical pages pg0 + 2 s, + 1; past the page range, the last pair again), each outside the
+ * page pool replaced by page 0 (such a pair is only read: the waves that use it report NaN). */
+struct PfPages {
+    int pa, pb;
+};
+
+__device__ __forceinline__ PfPages pf_pages(const AttnArgs &a, const int *tab, int npages, int s) {
+    const int ps = min(s, (npages - 1) / 2);
+    const int la = 2 * ps, lb = la + 1 < npages ? la + 1 : la;
+    PfPages p;
+    p.pa = tab[la];
+    p.pb = tab[lb];
+    p.pa = (unsigned)p.pa < (unsigned)a.num_pages ? p.pa : 0;
+    p.pb = (unsigned)p.pb < (unsigned)a.num_pages ? p.pb : 0;
+    return p;
+}
+
+/* The fetches of one stage (pages pg) into buffer st: wave w fetches K bytes [1024 w, 1024 w + 1024) of the pair
+ * (pages a, a, b, b), the same of V, and all 256 scale bytes into its own slot (4 bytes a lane: no lane is masked
+ * off, so the compiler can count the fetches); every wave always issues PF_FETCHES. */
+__device__ __forceinline__ void pf_fetch(const AttnArgs &a, PfPages pg, int kvh, PfStage &st, PfScales &sc, int wave,
+                                         int lane) {
+    const long long ph = (long long)(wave < 2 ? pg.pa : pg.pb) * a.Hkv + kvh;
     const int half = (wave & 1) * 1024;
     __builtin_amdgcn_global_load_lds((const void *)(a.k_pages + ph * PAGE_BYTES + half + lane * 16),
                                      (LdsVoid *)(st.b + wave * 1024), 16, 0, 0);
     __builtin_amdgcn_global_load_lds((const void *)(a.v_pages + ph * PAGE_BYTES + half + lane * 16),
                                      (LdsVoid *)(st.b + 2 * 2048 + wave * 1024), 16, 0, 0);
-    const long long sh = (long long)(lane < 32 ? pa : pb) * a.Hkv + kvh;
+    const long long sh = (long long)(lane < 32 ? pg.pa : pg.pb) * a.Hkv + kvh;
     __builtin_amdgcn_global_load_lds((const void *)(a.kv_scale + sh * 2 * PAGE + (lane & 31)), (LdsVoid *)sc.f[wave], 4,
                                      0, 0);
 }
 
+/* Whether a block-table entry of the pairs this wave computes (pairs la even with pg0 + la + 1 >= wpg0 and
+ * pg0 + la < wpg1) lies outside the page pool: checked once, from the staged table. */
+__device__ __forceinline__ bool pf_bad(const AttnArgs &a, const int *tab, int pg0, int npages, int wpg0, int wpg1,
+                                       int lane) {
+    const int la0 = (max(wpg0 - pg0 - 1, 0) + 1) & ~1;                  /* the first even la computed */
+    const int end = min(npages, ((min(npages, wpg1 - pg0) + 1) & ~1));  /* one past its pairs' last page */
+    bool bad = false;
+    for (int i = la0 + lane; i < end; i += WAVE) bad = bad || (unsigned)tab[i] >= (unsigned)a.num_pages;
+    return __any(bad);
+}
+
 /* One wave's step over stage s (buffer st) when the pair meets its key range. */
 template <int NT>
-__device__ __forceinline__ void pf_compute(const AttnArgs &a, const int *tab, int pg0, int npages, int s,
-                                           const PfStage &st, const PfScales &scs, int wpg0, int wpg1,
-                                           const KeyBounds<NT> &kb,
+__device__ __forceinline__ void pf_compute(const AttnArgs &a, int pg0, int npages, int s, const PfStage &st,
+                                           const PfScales &scs, int wpg0, int wpg1, const KeyBounds<NT> &kb,
                                            const QOp (&qb)[NT], WaveState<NT> &st_w, int lane) {
     const int la = 2 * s;
     if (la >= npages || pg0 + la + 1 < wpg0 || pg0 + la >= wpg1) return;
-    const bool has_b = la + 1 < npages;
-    if ((unsigned)tab[la] >= (unsigned)a.num_pages || (has_b && (unsigned)tab[la + 1] >= (unsigned)a.num_pages))
-        st_w.bad = true;
     const int g = lane >> 4;
     PairAddr cur;
     cur.lpa = pg0 + la;
-    cur.has_b = has_b;
+    cur.has_b = la + 1 < npages;
     cur.ha = cur.hb = 0;
     const uint4 *k4 = reinterpret_cast<const uint4 *>(st.b);
     const uint4 k0 = k4[lane], k1 = k4[64 + lane], k2 = k4[128 + lane], k3 = k4[192 + lane];
     const float *sc = scs.f[threadIdx.x >> 6];
     const float4 ksa = *reinterpret_cast<const float4 *>(sc + g * 4);
     const float4 ksb = *reinterpret_cast<const float4 *>(sc + 2 * PAGE + g * 4);
-    f32x4 sa[NT], sb[NT];
-    page_scores<NT>(k0, k1, qb, sa);
-    page_scores<NT>(k2, k3, qb, sb);
     const uint4 *v4 = reinterpret_cast<const uint4 *>(st.b + 2 * 2048);
     PairRegs vr;
     vr.a0 = v4[lane]; vr.a1 = v4[64 + lane]; vr.b0 = v4[128 + lane]; vr.b1 = v4[192 + lane];
     vr.sa = *reinterpret_cast<const float4 *>(sc + PAGE + g * 4);
     vr.sb = *reinterpret_cast<const float4 *>(sc + 3 * PAGE + g * 4);
+    f32x4 sa[NT], sb[NT];
+    page_scores<NT>(k0, k1, qb, sa);
+    page_scores<NT>(k2, k3, qb, sb);
     pair_step<NT>(a, cur, sa, sb, ksa, ksb, vr, kb, st_w, lane);
 }
 
@@ -858,23 +875,29 @@ __global__ void __launch_bounds__(256, 2) prefill_lds_kernel(AttnArgs a) {
     __syncthreads();   /* the table is in LDS (no fetch is in flight yet, so this fence drains nothing) */
 
     const int stages = (npages + 1) / 2;
-    pf_fetch(a, tab, npages, kvh, 0, pb0, ps0, wave, lane);
-    pf_fetch(a, tab, npages, kvh, 1, pb1, ps1, wave, lane);
-    pf_fetch(a, tab, npages, kvh, 2, pb2, ps2, wave, lane);
+    st.bad = pf_bad(a, tab, pg0, npages, wpg0, wpg1, lane);
+    pf_fetch(a, pf_pages(a, tab, npages, 0), kvh, pb0, ps0, wave, lane);
+    pf_fetch(a, pf_pages(a, tab, npages, 1), kvh, pb1, ps1, wave, lane);
+    pf_fetch(a, pf_pages(a, tab, npages, 2), kvh, pb2, ps2, wave, lane);
+    PfPages next = pf_pages(a, tab, npages, 3);   /* the pages of the next fetch, read a step ahead */
     /* step s: wait for stage s, barrier, refill the buffer read at step s - 1 with stage s + 3, compute stage s */
     for (int s = 0; s < stages; s += PF_BUFS) {
         pf_wait_stage(); pf_barrier();
-        pf_fetch(a, tab, npages, kvh, s + 3, pb3, ps3, wave, lane);
-        pf_compute<NT>(a, tab, pg0, npages, s, pb0, ps0, wpg0, wpg1, kb, qb, st, lane);
+        pf_fetch(a, next, kvh, pb3, ps3, wave, lane);
+        next = pf_pages(a, tab, npages, s + 4);
+        pf_compute<NT>(a, pg0, npages, s, pb0, ps0, wpg0, wpg1, kb, qb, st, lane);
         pf_wait_stage(); pf_barrier();
-        pf_fetch(a, tab, npages, kvh, s + 4, pb0, ps0, wave, lane);
-        pf_compute<NT>(a, tab, pg0, npages, s + 1, pb1, ps1, wpg0, wpg1, kb, qb, st, lane);
+        pf_fetch(a, next, kvh, pb0, ps0, wave, lane);
+        next = pf_pages(a, tab, npages, s + 5);
+        pf_compute<NT>(a, pg0, npages, s + 1, pb1, ps1, wpg0, wpg1, kb, qb, st, lane);
         pf_wait_stage(); pf_barrier();
-        pf_fetch(a, tab, npages, kvh, s + 5, pb1, ps1, wave, lane);
-        pf_compute<NT>(a, tab, pg0, npages, s + 2, pb2, ps2, wpg0, wpg1, kb, qb, st, lane);
+        pf_fetch(a, next, kvh, pb1, ps1, wave, lane);
+        next = pf_pages(a, tab, npages, s + 6);
+        pf_compute<NT>(a, pg0, npages, s + 2, pb2, ps2, wpg0, wpg1, kb, qb, st, lane);
         pf_wait_stage(); pf_barrier();
-        pf_fetch(a, tab, npages, kvh, s + 6, pb2, ps2, wave, lane);
-        pf_compute<NT>(a, tab, pg0, npages, s + 3, pb3, ps3, wpg0, wpg1, kb, qb, st, lane);
+        pf_fetch(a, next, kvh, pb2, ps2, wave, lane);
+        next = pf_pages(a, tab, npages, s + 7);
+        pf_compute<NT>(a, pg0, npages, s + 3, pb3, ps3, wpg0, wpg1, kb, qb, st, lane);
     }
     __builtin_amdgcn_s_waitcnt(0);   /* no fetch may land in LDS after the workgroup ends */
     pf_barrier();

@@ -100,3 +100,17 @@ def test_config4_full_size_subset(device):
     mx, mean = attn_errors(out[seqs], want)
     assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
     assert torch.isfinite(out.float()).all()
+
+
+def test_bad_page_gives_nan_for_its_sequence_only(device):
+    """A block-table entry outside the page pool: every row of that sequence that reads it is NaN, the other
+    sequence's rows are unchanged (both the LDS-staged and the register kernel check every pair they compute)."""
+    w = PrefillWorkload("bad", 2, 16, 4, 45, 20, paged=True)
+    inp = prefill_inputs(w, seed=5)
+    out, q, cache, table, start, _, _ = device_prefill(w, inp, device)
+    bad = table.clone()
+    bad[1, 1] = cache.num_pages + 5            # keys 16..31: seen by every row of sequence 1 (no window)
+    got = prefill_attention(q, cache, bad, start).float()
+    torch.cuda.synchronize()
+    assert torch.isnan(got[1]).all()
+    assert torch.equal(got[0], out[0].float())
