@@ -150,7 +150,7 @@ def bench_prefill(args, w):
     return {
         "metric": "chunked-prefill attention TFLOP/s over the fp8 cache (MFMA)", "value": round(achieved, 2),
         "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 KV, bf16 MFMA, fp32 softmax",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 KV, fp8 QK^T and bf16 PV MFMA, fp32 softmax",
         "data": "synthetic (seeded N(0,1) bf16 chunk and cache, random-permutation block table)",
         "config": {"workload": f"{w.name}: {w.description}", "batch": w.batch, "q_heads": w.q_heads,
                    "kv_heads": w.kv_heads, "cached": w.ctx, "chunk": w.chunk, "rope_theta": w.theta},
@@ -158,7 +158,7 @@ def bench_prefill(args, w):
         "tokens_per_s": round(w.batch * w.chunk / (ms_step * 1e-3), 1),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "nc_prefill_attn_fp8 (prefill_kernel)"},
+                     "kernel": "nc_prefill_attn_fp8 (prefill_lds_kernel)"},
     }
 
 
@@ -552,7 +552,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8e4m3 KV, bf16 MFMA, fp32 softmax",
+        "dtype": "fp8e4m3 KV, fp8 QK^T and bf16 PV MFMA, fp32 softmax",
         "data": "synthetic (seeded N(0,1) bf16, 1% 8-sigma outliers, random-permutation block table)",
         "config": {"workload": f"{w.name}: {w.description}", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
                    "keys_per_seq": inp["max_seq_len"], "page_size": 16, "step": "fused QK-norm/RoPE fp8 append + "
