@@ -217,11 +217,12 @@ struct KeyBounds {
     int full_lo, full_hi, written_hi;
 };
 
-/* Softmax update and PV of one pair from its scores. The lazy rescale moves a column's reference max only when the
- * column's max grows past it by RESCALE_LOG2 (p <= 2^8 otherwise); the decision is taken once per pair for the whole
- * wave and every tile (when any column of any tile needs it, each tile moves to its new max), so the pair's
- * exponentials and PV MFMAs form one straight block with no branch between the tiles. Each converted V operand feeds
- * NT MFMAs. */
+/* Softmax update and PV of one pair from its scores. The lazy rescale keeps each column's reference max m until a
+ * score passes it by RESCALE_LOG2 (so p <= 2^8). The common case costs one FMA and one exponential a score:
+ * p = exp2(acc ks - m) against the current m, and only when some p of the wave exceeds 2^8 (or m is still -inf)
+ * does the pair take the slow path, which finds every tile's column max, moves each tile to it (the decision is
+ * taken once per pair for the wave and every tile) and recomputes p. The pair's exponentials and PV MFMAs then form
+ * one straight block. Each converted V operand feeds NT MFMAs. */
 template <int NT, bool MASKED>
 __device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p, const f32x4 (&sa)[NT],
                                             const f32x4 (&sb)[NT], const float4 &ksa, const float4 &ksb, PairRegs &v,
@@ -238,49 +239,55 @@ __device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p
     const float ks[8] = {ksa.x * st.sl2, ksa.y * st.sl2, ksa.z * st.sl2, ksa.w * st.sl2,
                          ksb.x * st.sl2, ksb.y * st.sl2, ksb.z * st.sl2, ksb.w * st.sl2};
     const float vs[8] = {v.sa.x, v.sa.y, v.sa.z, v.sa.w, v.sb.x, v.sb.y, v.sb.z, v.sb.w};
-    float s[NT][8], mnew[NT];
     bool ok[NT][8];
-    bool grow = false;
+    float pr[NT][8];
+    float pmax = 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
+        const float negm = -st.m[t];   /* +inf before the first key: every live p is +inf, the slow path */
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const float acc = i < 4 ? sa[t][i] : sb[t][i - 4];
             if (MASKED) {
                 const int key = (i < 4 ? key_a : key_b) + (i & 3);
                 ok[t][i] = (i < 4 || p.has_b) && key >= kb.lo[t] && key <= kb.hi[t];
-                s[t][i] = ok[t][i] ? acc * ks[i] : -INFINITY;
             } else {
                 ok[t][i] = true;
-                s[t][i] = acc * ks[i];
             }
+            pr[t][i] = ok[t][i] ? __builtin_amdgcn_exp2f(__builtin_fmaf(acc, ks[i], negm)) : 0.0f;
+            pmax = fmaxf(pmax, pr[t][i]);
         }
-        float mt = fmaxf(fmaxf(fmaxf(s[t][0], s[t][1]), fmaxf(s[t][2], s[t][3])),
-                         fmaxf(fmaxf(s[t][4], s[t][5]), fmaxf(s[t][6], s[t][7])));
-        mt = pair_max32(pair_max16(mt));   /* the column's max over the four row groups */
-        mnew[t] = fmaxf(st.m[t], mt);
-        grow = grow || mnew[t] > st.m[t] + RESCALE_LOG2;
     }
-    if (__any(grow)) {
+    if (__any(!(pmax <= 256.0f))) {   /* a column's max passed its reference by more than 2^8 (or no reference yet) */
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            const float alpha = mnew[t] == st.m[t] ? 1.0f : __builtin_amdgcn_exp2f(st.m[t] - mnew[t]);
+            float s[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float acc = i < 4 ? sa[t][i] : sb[t][i - 4];
+                s[i] = ok[t][i] ? acc * ks[i] : -INFINITY;
+            }
+            float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+            mt = pair_max32(pair_max16(mt));   /* the column's max over the four row groups */
+            const float mnew = fmaxf(st.m[t], mt);
+            const float alpha = mnew == st.m[t] ? 1.0f : __builtin_amdgcn_exp2f(st.m[t] - mnew);
 #pragma unroll
             for (int d = 0; d < 8; d++) st.o[t][d] *= alpha;
             st.l[t] *= alpha;
-            st.m[t] = mnew[t];
+            st.m[t] = mnew;
+            const float mbase = mnew == -INFINITY ? 0.0f : mnew;  /* no key yet: every s is -inf */
+#pragma unroll
+            for (int i = 0; i < 8; i++) pr[t][i] = __builtin_amdgcn_exp2f(s[i] - mbase);
         }
     }
     bf16x8 pv[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        const float mbase = st.m[t] == -INFINITY ? 0.0f : st.m[t];  /* no key yet: every s is -inf */
         float psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float pr = __builtin_amdgcn_exp2f(s[t][i] - mbase);
-            psum += pr;
-            pv[t][i] = (__bf16)(ok[t][i] ? pr * vs[i] : 0.0f);
+            psum += pr[t][i];
+            pv[t][i] = (__bf16)(pr[t][i] * vs[i]);
         }
         st.l[t] += psum;
     }
