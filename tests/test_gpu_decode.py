@@ -140,3 +140,19 @@ def test_workspace_reuse_across_shapes(device):
             out, want, _, _ = run(w, device, seed=i, pps=pps)
             mx, mean = attn_errors(out, want)
             assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (w.name, pps, mx, mean)
+
+
+@pytest.mark.parametrize("pps", [0, 3])
+def test_growing_scores_rescale_mid_stream(device, pps):
+    """Key magnitudes growing along each sequence: the running max passes its reference by more than 2^8 again and
+    again after the first page pair, so the lazy rescale's slow path runs mid-stream (and split runs start on small
+    references that the combine must reconcile)."""
+    w = DecodeWorkload("grow", 2, 8, 2, 600, ctx_min=400, paged=True)
+    inp = decode_inputs(w, seed=9)
+    n = inp["k_cache"].shape[1]
+    ramp = torch.linspace(0.2, 6.0, n).view(1, n, 1, 1)
+    inp["k_cache"] = (inp["k_cache"].float() * ramp).bfloat16()
+    inp["q"] = (inp["q"].float() * 3.0).bfloat16()
+    out, want, _, _ = run(w, device, pps=pps, inp=inp)
+    mx, mean = attn_errors(out, want)
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)

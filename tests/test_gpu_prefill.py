@@ -114,3 +114,19 @@ def test_bad_page_gives_nan_for_its_sequence_only(device):
     torch.cuda.synchronize()
     assert torch.isnan(got[1]).all()
     assert torch.equal(got[0], out[0].float())
+
+
+def test_growing_scores_rescale_mid_stream(device):
+    """Cached keys whose magnitude grows twentyfold along the sequence: every chunk row's running max passes its
+    reference by more than 2^8 several times after the first page pair (the lazy rescale's slow path mid-stream)."""
+    w = PrefillWorkload("grow", 2, 16, 4, 200, 40, paged=True)
+    inp = prefill_inputs(w, seed=12)
+    ramp = torch.linspace(1.0, 20.0, w.ctx).view(1, w.ctx, 1, 1)
+    inp["k_cache"] = (inp["k_cache"].float() * ramp).bfloat16()
+    out, q, _, _, start, cos, sin = device_prefill(w, inp, device)
+    seqs = list(range(w.batch))
+    oq, ocache, otable = oracle_for(w, inp, seqs, cos, sin)
+    want = oracle_prefill(oq, ocache, otable, np.full(len(seqs), w.ctx))
+    check_relative(out, want, oracle_prefill(oq, magnitude_cache(ocache), otable, np.full(len(seqs), w.ctx)))
+    mx, mean = attn_errors(out, want)
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
