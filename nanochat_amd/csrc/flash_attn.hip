@@ -46,7 +46,7 @@ struct FlashFwd {
 
 struct FaStage {
     uint16_t k[FA_BN * HEAD_DIM];   /* [key][128], 16-byte chunk c of key j at chunk c ^ (j & 15) */
-    uint16_t vt[HEAD_DIM * FA_BN];  /* [dim][64], 8-byte unit u (keys 4u..4u+3) of dim d at unit u ^ (d & 15) */
+    uint16_t v[FA_BN * HEAD_DIM];   /* the same layout: read transposed by ds_read_b64_tr_b16 */
 };
 
 __device__ __forceinline__ int k_lds(int key, int chunk) { return key * HEAD_DIM + ((chunk ^ (key & 15)) << 3); }
@@ -123,6 +123,39 @@ __device__ __forceinline__ bf16x8 rows_operand(const uint16_t *lds, int rt, int 
     return *reinterpret_cast<const bf16x8 *>(&lds[k_lds(rt * 16 + c, cc * 4 + g)]);
 }
 
+typedef __attribute__((address_space(3))) void LdsVoid;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 LdsV4;
+
+/* A 64-row tile of one head straight into LDS in the k_lds layout by LDS DMA (no registers held): instruction i of a
+ * wave writes rows 4 i' .. 4 i' + 3 (i' = wave + 4 i), lane l the 16 bytes at LDS chunk l % 16 of row 4 i' + l / 16,
+ * fetched from the row's chunk (l % 16) ^ (row & 15). Rows past the descriptor's range read zeros. */
+__device__ __forceinline__ void tile_dma(const uint16_t *base, long long row0, long long stride, int h, int rows,
+                                         uint16_t *lds, int wave, int lane) {
+    const Rsrc rs = rows_rsrc(base, row0, stride, h, rows);
+#pragma unroll
+    for (int k = 0; k < FA_BN / 4 / 4; k++) {
+        const int i = wave + 4 * k, r = 4 * i + (lane >> 4), p = lane & 15;
+        const int off = (int)((r * stride + ((p ^ (r & 15)) << 3)) * 2);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LdsVoid *)(lds + i * 4 * HEAD_DIM), 16, off, 0, 0, 0);
+    }
+}
+
+/* The A operand of O^T += V^T P^T for dim tile d and k-step s2 from the row-major V tile, in the key order of the
+ * score MFMA's output pair: lane (g, c) gets keys 32 s2 + 4 g .. + 3, then 32 s2 + 16 + 4 g .. + 3, of dim
+ * 16 d + c. ds_read_b64_tr_b16 hands lane i of a 16-lane group element i % 4 of the 8 bytes lane 4 t + i / 4 points
+ * at, for t = 0..3: so lane j of group g points at dims 16 d + 4 (j % 4) .. + 3 of key base + j / 4. */
+__device__ __forceinline__ bf16x8 v_operand_tr(const uint16_t *v, int d, int s2, int g, int c) {
+    const int dim = 16 * d + 4 * (c & 3), chunk = dim >> 3, half = (dim >> 2) & 1;
+    const int r0 = 32 * s2 + 4 * g + (c >> 2), r1 = r0 + 16;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (LdsV4 *)(v + k_lds(r0, chunk) + 4 * half));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (LdsV4 *)(v + k_lds(r1, chunk) + 4 * half));
+    const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+    return __builtin_bit_cast(bf16x8, uint4{a.x, a.y, b.x, b.y});
+}
+
 struct FaState {
     f32x4 o[2][8];   /* O^T tile d of query tile j: dims 16d + 4g + i of column (lane & 15) */
     float m[2];      /* the column's reference max (log2 domain), equal in the four groups */
@@ -197,7 +230,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
     for (int d = 0; d < 8; d++) {
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++) {
-            const bf16x8 vop = cols_operand(s.vt, d, s2, g, c);
+            const bf16x8 vop = v_operand_tr(s.v, d, s2, g, c);
 #pragma unroll
             for (int j = 0; j < 2; j++) st.o[j][d] = mfma16x16x32(vop, pv[j][s2], st.o[j][d]);
         }
@@ -205,7 +238,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
 }
 
 __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(FlashFwd a) {
-    __shared__ FaStage stage[2];
+    __shared__ FaStage st0, st1;   /* distinct objects: a read of one never waits for DMA into the other */
     const int seg = blockIdx.y, h = blockIdx.z;
     const long long start = a.cu[seg];
     const int seglen = a.cu[seg + 1] - a.cu[seg];
@@ -239,31 +272,32 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(FlashFwd a) {
 
     const int klo = a.window >= 0 ? max(0, qa - a.window) : 0;
     const int kb_lo = klo / FA_BN, kb_hi = qb / FA_BN;
-    Tile64 rk, rv;
-    tile_load(a.k, start + kb_lo * FA_BN, a.k_stride, h, min(FA_BN, seglen - kb_lo * FA_BN), rk, t);
-    tile_load(a.v, start + kb_lo * FA_BN, a.v_stride, h, min(FA_BN, seglen - kb_lo * FA_BN), rv, t);
-    tile_store_rows(stage[0].k, rk, t);
-    tile_store_cols(stage[0].vt, rv, t);
+    /* block kb + 1 is fetched by LDS DMA into the other stage while block kb is computed; the barrier after the
+     * compute (its fence waits for this wave's DMA) makes the fetched block visible and frees the one just read */
+    auto fetch = [&](int kb, FaStage &stg) {
+        const int n = min(FA_BN, seglen - kb * FA_BN);
+        tile_dma(a.k, start + kb * FA_BN, a.k_stride, h, n, stg.k, wave, lane);
+        tile_dma(a.v, start + kb * FA_BN, a.v_stride, h, n, stg.v, wave, lane);
+    };
+    auto compute = [&](int kb, const FaStage &stg) {
+        if (!active) return;
+        const int k0 = kb * FA_BN, k1 = k0 + FA_BN - 1;
+        /* unmasked iff every key of the block is visible to every row of the wave */
+        const bool interior = k1 <= q0 && k1 < seglen && (a.window < 0 || qw1 - k0 <= a.window);
+        if (interior)
+            fa_block<false>(a, stg, qb_, st, k0, q0, seglen, lane);
+        else
+            fa_block<true>(a, stg, qb_, st, k0, q0, seglen, lane);
+    };
+    fetch(kb_lo, st0);
     __syncthreads();
-    for (int kb = kb_lo; kb <= kb_hi; kb++) {
-        const int cur = (kb - kb_lo) & 1;
-        const bool more = kb < kb_hi;
-        if (active) {
-            const int k0 = kb * FA_BN, k1 = k0 + FA_BN - 1;
-            /* unmasked iff every key of the block is visible to every row of the wave */
-            const bool interior = k1 <= q0 && k1 < seglen && (a.window < 0 || qw1 - k0 <= a.window);
-            if (interior)
-                fa_block<false>(a, stage[cur], qb_, st, k0, q0, seglen, lane);
-            else
-                fa_block<true>(a, stage[cur], qb_, st, k0, q0, seglen, lane);
-        }
-        if (more) {
-            const int n1 = min(FA_BN, seglen - (kb + 1) * FA_BN);
-            tile_load(a.k, start + (kb + 1) * FA_BN, a.k_stride, h, n1, rk, t);
-            tile_load(a.v, start + (kb + 1) * FA_BN, a.v_stride, h, n1, rv, t);
-            tile_store_rows(stage[cur ^ 1].k, rk, t);
-            tile_store_cols(stage[cur ^ 1].vt, rv, t);
-        }
+    for (int kb = kb_lo; kb <= kb_hi; kb += 2) {
+        if (kb + 1 <= kb_hi) fetch(kb + 1, st1);
+        compute(kb, st0);
+        __syncthreads();
+        if (kb + 1 > kb_hi) break;
+        if (kb + 2 <= kb_hi) fetch(kb + 2, st0);
+        compute(kb + 1, st1);
         __syncthreads();
     }
     if (!active) return;
