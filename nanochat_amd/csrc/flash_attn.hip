@@ -9,13 +9,14 @@
  *   lse[h][i] = ln sum_j exp(scale q_i . k_j)              fp32 (FA4's (H, total) layout)
  *
  * Mapping: a workgroup of four waves owns 128 query rows of one (segment, head), each wave two 16-row tiles. Keys
- * are visited in blocks of 64, staged in LDS for the four waves (K row-major with 16-byte chunks XOR-swizzled by the
- * key, V transposed with 8-byte units swizzled by the dimension, so the MFMA operand reads are conflict-free), in
- * two LDS stages: block b+1 is written to one while block b is read from the other. Scores are S^T = K Q^T
- * (v_mfma_f32_16x16x32_bf16, keys as rows, queries as columns), so a lane's scores all belong to one query; the
- * online softmax runs in the log2 domain with the lazy rescale of the decode kernels (the reference max moves only
- * when a column's max passes it by 2^8); P^T then feeds O^T += V^T P^T with no shuffle, its key order matched by the
- * order of the transposed V operand.
+ * are visited in blocks of 64, staged in LDS for the four waves (K and V row-major with 16-byte chunks XOR-swizzled
+ * by the key) by LDS DMA straight from HBM, in two LDS stages: block b+1 is fetched into one while block b is read
+ * from the other, with no registers held for the fetch. Scores are S^T = K Q^T (v_mfma_f32_16x16x32_bf16, keys as
+ * rows, queries as columns), so a lane's scores all belong to one query; the online softmax runs in the log2 domain
+ * with the lazy rescale of the decode kernels (the reference max moves only when a column's max passes it by 2^8);
+ * P^T then feeds O^T += V^T P^T with no shuffle: the V^T operand is read from the row-major tile by gfx950's
+ * transposing LDS read (ds_read_b64_tr_b16) in P's key order. The backward stages its Q, dO (or K, V) tiles the
+ * same way and reads their transposes the same way.
  */
 #include "nc_device.h"
 #include "nanochat_amd.h"
@@ -50,7 +51,6 @@ struct FaStage {
 };
 
 __device__ __forceinline__ int k_lds(int key, int chunk) { return key * HEAD_DIM + ((chunk ^ (key & 15)) << 3); }
-__device__ __forceinline__ int vt_lds(int d, int unit) { return d * FA_BN + ((unit ^ (d & 15)) << 2); }
 
 __device__ __forceinline__ Rsrc make_rsrc(const void *p, unsigned bytes) {
     const unsigned long long u = (unsigned long long)p;
@@ -68,53 +68,6 @@ __device__ __forceinline__ uint4 bload(Rsrc r, int off) {
 __device__ __forceinline__ Rsrc rows_rsrc(const uint16_t *base, long long row0, long long stride, int h, int rows) {
     const unsigned bytes = rows > 0 ? (unsigned)(((long long)(rows - 1) * stride + HEAD_DIM) * 2) : 0u;
     return make_rsrc(base + row0 * stride + (long long)h * HEAD_DIM, bytes);
-}
-
-/* 64 rows x 128 dims of one head in registers: thread t holds dims 8(t/16) .. +7 of rows 4(t%16) .. +3. Rows past
- * `rows` read zeros. One load serves both LDS layouts below. */
-struct Tile64 {
-    uint4 r[4];
-};
-
-__device__ __forceinline__ void tile_load(const uint16_t *base, long long row0, long long stride, int h, int rows,
-                                          Tile64 &x, int t) {
-    const Rsrc rs = rows_rsrc(base, row0, stride, h, rows);
-    const int r0 = (t & 15) * 4, dc = t >> 4;
-#pragma unroll
-    for (int i = 0; i < 4; i++) x.r[i] = bload(rs, (int)(((r0 + i) * stride + dc * 8) * 2));
-}
-
-/* row-major [64][128] (k_lds layout): the A operand of products over the dimension */
-__device__ __forceinline__ void tile_store_rows(uint16_t *lds, const Tile64 &x, int t) {
-    const int r0 = (t & 15) * 4, dc = t >> 4;
-#pragma unroll
-    for (int i = 0; i < 4; i++) *reinterpret_cast<uint4 *>(&lds[k_lds(r0 + i, dc)]) = x.r[i];
-}
-
-__device__ __forceinline__ uint32_t word_of(const uint4 &u, int j) {
-    return j < 2 ? (j == 0 ? u.x : u.y) : (j == 2 ? u.z : u.w);
-}
-
-/* transposed [128][64] (vt_lds layout): dim vd + j of the thread's four rows is one 8-byte unit; the A operand of
- * products over the rows */
-__device__ __forceinline__ void tile_store_cols(uint16_t *lds, const Tile64 &x, int t) {
-    const int u = t & 15, vd = (t >> 4) * 8;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int sh = (j & 1) * 16;
-        uint32_t e[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) e[i] = (word_of(x.r[i], j >> 1) >> sh) & 0xFFFFu;
-        *reinterpret_cast<uint2 *>(&lds[vt_lds(vd + j, u)]) = uint2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
-    }
-}
-
-/* The A operand of a product over 32 rows of a transposed tile, in the key order of an S^T / S output pair: lane
- * (g, c) of dim tile d holds rows 32 s2 + 4g .. +3 and 32 s2 + 16 + 4g .. +3 of dim 16 d + c. */
-__device__ __forceinline__ bf16x8 cols_operand(const uint16_t *lds, int d, int s2, int g, int c) {
-    const uint2 lo = *reinterpret_cast<const uint2 *>(&lds[vt_lds(d * 16 + c, 8 * s2 + g)]);
-    const uint2 hi = *reinterpret_cast<const uint2 *>(&lds[vt_lds(d * 16 + c, 8 * s2 + 4 + g)]);
-    return __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
 }
 
 /* The A operand of a product over the dimension from a row-major tile: lane (g, c) holds dims 32 cc + 8 g .. +7 of
@@ -141,11 +94,11 @@ __device__ __forceinline__ void tile_dma(const uint16_t *base, long long row0, l
     }
 }
 
-/* The A operand of O^T += V^T P^T for dim tile d and k-step s2 from the row-major V tile, in the key order of the
- * score MFMA's output pair: lane (g, c) gets keys 32 s2 + 4 g .. + 3, then 32 s2 + 16 + 4 g .. + 3, of dim
- * 16 d + c. ds_read_b64_tr_b16 hands lane i of a 16-lane group element i % 4 of the 8 bytes lane 4 t + i / 4 points
+/* The A operand of a product over 32 rows of a row-major (k_lds) tile (V^T in O^T += V^T P^T; dO^T, Q^T, K^T in the
+ * backward) for dim tile d and k-step s2, in the row order of a score MFMA's output pair: lane (g, c) gets rows
+ * 32 s2 + 4 g .. + 3, then 32 s2 + 16 + 4 g .. + 3, of dim 16 d + c. ds_read_b64_tr_b16 hands lane i of a 16-lane group element i % 4 of the 8 bytes lane 4 t + i / 4 points
  * at, for t = 0..3: so lane j of group g points at dims 16 d + 4 (j % 4) .. + 3 of key base + j / 4. */
-__device__ __forceinline__ bf16x8 v_operand_tr(const uint16_t *v, int d, int s2, int g, int c) {
+__device__ __forceinline__ bf16x8 tr_operand(const uint16_t *v, int d, int s2, int g, int c) {
     const int dim = 16 * d + 4 * (c & 3), chunk = dim >> 3, half = (dim >> 2) & 1;
     const int r0 = 32 * s2 + 4 * g + (c >> 2), r1 = r0 + 16;
     const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -230,7 +183,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
     for (int d = 0; d < 8; d++) {
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++) {
-            const bf16x8 vop = v_operand_tr(s.v, d, s2, g, c);
+            const bf16x8 vop = tr_operand(s.v, d, s2, g, c);
 #pragma unroll
             for (int j = 0; j < 2; j++) st.o[j][d] = mfma16x16x32(vop, pv[j][s2], st.o[j][d]);
         }
@@ -354,14 +307,14 @@ __device__ __forceinline__ void store4(uint16_t *p, const f32x4 &v, float mul) {
 }
 
 struct DkvStage {
-    uint16_t q[FA_BN * HEAD_DIM], qt[HEAD_DIM * FA_BN], dout[FA_BN * HEAD_DIM], dot[HEAD_DIM * FA_BN];
+    uint16_t q[FA_BN * HEAD_DIM], dout[FA_BN * HEAD_DIM];   /* k_lds layout; Q^T and dO^T read transposed */
     float lse2[FA_BN], dd[FA_BN];              /* the block's rows: lse log2(e) (+inf past the segment), D */
 };
 
 /* dK, dV of 64 keys. S = Q K^T and dP = dO V^T with queries as rows (a lane holds one key's column), so P and dS
  * feed dV^T += dO^T P and dK^T += Q^T dS directly as B operands, with dO^T and Q^T read from transposed LDS tiles. */
 __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dkv_kernel(FlashBwd a) {
-    __shared__ DkvStage s;
+    __shared__ DkvStage s0, s1;   /* distinct objects: a read of one never waits for DMA into the other */
     const int seg = blockIdx.y, h = blockIdx.z;
     const long long start = a.cu[seg];
     const int seglen = a.cu[seg + 1] - a.cu[seg];
@@ -388,54 +341,71 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dkv_kernel(FlashBwd a
     for (int d = 0; d < 8; d++) dk[d] = dv[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int qhi = a.window >= 0 ? min(seglen - 1, k0 + FA_BN - 1 + a.window) : seglen - 1;
-    for (int qbk = k0 / FA_BN; qbk <= qhi / FA_BN; qbk++) {
+    /* query block qbk + 1 (Q and dO by LDS DMA, the row statistics through registers) is fetched into the other stage
+     * while block qbk is computed; the barrier after the compute makes it visible and frees the one just read */
+    float rl = INFINITY, rd = 0.0f;
+    auto fetch = [&](int qbk, DkvStage &stg) {
         const int qs = qbk * FA_BN, nq = min(FA_BN, seglen - qs);
-        {
-            Tile64 x;
-            tile_load(a.q, start + qs, a.q_stride, h, nq, x, t);
-            tile_store_rows(s.q, x, t);
-            tile_store_cols(s.qt, x, t);
-            tile_load(a.dout, start + qs, a.do_stride, h, nq, x, t);
-            tile_store_rows(s.dout, x, t);
-            tile_store_cols(s.dot, x, t);
-            if (t < FA_BN) {
-                const bool ok = t < nq;
-                s.lse2[t] = ok ? a.lse[(long long)h * a.lse_stride + start + qs + t] * FA_LOG2E : INFINITY;
-                s.dd[t] = ok ? a.dpsum[(start + qs + t) * a.H + h] : 0.0f;
+        tile_dma(a.q, start + qs, a.q_stride, h, nq, stg.q, wave, lane);
+        tile_dma(a.dout, start + qs, a.do_stride, h, nq, stg.dout, wave, lane);
+        if (t < FA_BN) {
+            const bool ok = t < nq;
+            rl = ok ? a.lse[(long long)h * a.lse_stride + start + qs + t] * FA_LOG2E : INFINITY;
+            rd = ok ? a.dpsum[(start + qs + t) * a.H + h] : 0.0f;
+        }
+    };
+    auto put_stats = [&](DkvStage &stg) {
+        if (t < FA_BN) {
+            stg.lse2[t] = rl;
+            stg.dd[t] = rd;
+        }
+    };
+    auto compute = [&](int qbk, const DkvStage &s) {
+        if (!active) return;
+        const int qs = qbk * FA_BN;
+        const int kw1 = kw + 15, qe = qs + FA_BN - 1;
+        const bool interior = kw1 <= qs && qe < seglen && kw1 < seglen && (a.window < 0 || qe - kw <= a.window);
+        bf16x8 pb[2], db[2];
+#pragma unroll
+        for (int qt = 0; qt < 4; qt++) {
+            f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                sc = mfma16x16x32(rows_operand(s.q, qt, cc, g, c), kb_[cc], sc);
+                dp = mfma16x16x32(rows_operand(s.dout, qt, cc, g, c), vb_[cc], dp);
+            }
+            /* lane (g, c): key c, query rows qs + 16 qt + 4 g + i */
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = qt * 16 + 4 * g + i;
+                float p = __builtin_amdgcn_exp2f(sc[i] * a.scale_log2 - s.lse2[r]);
+                if (!interior && !visible(key, qs + r, seglen, a.window)) p = 0.0f;
+                const float ds = p * (dp[i] - s.dd[r]);
+                pb[qt >> 1][(qt & 1) * 4 + i] = (__bf16)p;
+                db[qt >> 1][(qt & 1) * 4 + i] = (__bf16)ds;
             }
         }
+#pragma unroll
+        for (int d = 0; d < 8; d++)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                dv[d] = mfma16x16x32(tr_operand(s.dout, d, s2, g, c), pb[s2], dv[d]);
+                dk[d] = mfma16x16x32(tr_operand(s.q, d, s2, g, c), db[s2], dk[d]);
+            }
+    };
+    const int qb_lo = k0 / FA_BN, qb_hi = qhi / FA_BN;
+    fetch(qb_lo, s0);
+    put_stats(s0);
+    __syncthreads();
+    for (int qbk = qb_lo; qbk <= qb_hi; qbk += 2) {
+        if (qbk + 1 <= qb_hi) fetch(qbk + 1, s1);
+        compute(qbk, s0);
+        if (qbk + 1 <= qb_hi) put_stats(s1);
         __syncthreads();
-        if (active) {
-            const int kw1 = kw + 15, qe = qs + FA_BN - 1;
-            const bool interior = kw1 <= qs && qe < seglen && kw1 < seglen && (a.window < 0 || qe - kw <= a.window);
-            bf16x8 pb[2], db[2];
-#pragma unroll
-            for (int qt = 0; qt < 4; qt++) {
-                f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    sc = mfma16x16x32(rows_operand(s.q, qt, cc, g, c), kb_[cc], sc);
-                    dp = mfma16x16x32(rows_operand(s.dout, qt, cc, g, c), vb_[cc], dp);
-                }
-                /* lane (g, c): key c, query rows qs + 16 qt + 4 g + i */
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int r = qt * 16 + 4 * g + i;
-                    float p = __builtin_amdgcn_exp2f(sc[i] * a.scale_log2 - s.lse2[r]);
-                    if (!interior && !visible(key, qs + r, seglen, a.window)) p = 0.0f;
-                    const float ds = p * (dp[i] - s.dd[r]);
-                    pb[qt >> 1][(qt & 1) * 4 + i] = (__bf16)p;
-                    db[qt >> 1][(qt & 1) * 4 + i] = (__bf16)ds;
-                }
-            }
-#pragma unroll
-            for (int d = 0; d < 8; d++)
-#pragma unroll
-                for (int s2 = 0; s2 < 2; s2++) {
-                    dv[d] = mfma16x16x32(cols_operand(s.dot, d, s2, g, c), pb[s2], dv[d]);
-                    dk[d] = mfma16x16x32(cols_operand(s.qt, d, s2, g, c), db[s2], dk[d]);
-                }
-        }
+        if (qbk + 1 > qb_hi) break;
+        if (qbk + 2 <= qb_hi) fetch(qbk + 2, s0);
+        compute(qbk + 1, s1);
+        if (qbk + 2 <= qb_hi) put_stats(s0);
         __syncthreads();
     }
     if (!active || key >= seglen) return;
@@ -450,13 +420,13 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dkv_kernel(FlashBwd a
 }
 
 struct DqStage {
-    uint16_t k[FA_BN * HEAD_DIM], v[FA_BN * HEAD_DIM], kt[HEAD_DIM * FA_BN];
+    uint16_t k[FA_BN * HEAD_DIM], v[FA_BN * HEAD_DIM];   /* k_lds layout; K^T read transposed */
 };
 
 /* dQ of 128 queries: as the forward, S^T = K Q^T and dP^T = V dO^T with queries as columns, so dS^T feeds
  * dQ^T += K^T dS^T as the B operand with K^T read from a transposed LDS tile. */
 __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dq_kernel(FlashBwd a) {
-    __shared__ DqStage s;
+    __shared__ DqStage s0, s1;   /* distinct objects: a read of one never waits for DMA into the other */
     const int seg = blockIdx.y, h = blockIdx.z;
     const long long start = a.cu[seg];
     const int seglen = a.cu[seg + 1] - a.cu[seg];
@@ -495,52 +465,58 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dq_kernel(FlashBwd a)
         for (int d = 0; d < 8; d++) dq[j][d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int klo = a.window >= 0 ? max(0, qa - a.window) : 0;
-    for (int kb = klo / FA_BN; kb <= qb / FA_BN; kb++) {
-        const int k0 = kb * FA_BN, nk = min(FA_BN, seglen - k0);
-        {
-            Tile64 x;
-            tile_load(a.k, start + k0, a.k_stride, h, nk, x, t);
-            tile_store_rows(s.k, x, t);
-            tile_store_cols(s.kt, x, t);
-            tile_load(a.v, start + k0, a.v_stride, h, nk, x, t);
-            tile_store_rows(s.v, x, t);
-        }
-        __syncthreads();
-        if (active) {
-            const int k1 = k0 + FA_BN - 1;
-            const bool interior = k1 <= q0 && k1 < seglen && (a.window < 0 || qw1 - k0 <= a.window);
-            bf16x8 db[2][2];
+    /* key block kb + 1 (K and V by LDS DMA) is fetched into the other stage while block kb is computed */
+    auto fetch = [&](int kb, DqStage &stg) {
+        const int nk = min(FA_BN, seglen - kb * FA_BN);
+        tile_dma(a.k, start + kb * FA_BN, a.k_stride, h, nk, stg.k, wave, lane);
+        tile_dma(a.v, start + kb * FA_BN, a.v_stride, h, nk, stg.v, wave, lane);
+    };
+    auto compute = [&](int kb, const DqStage &s) {
+        if (!active) return;
+        const int k0 = kb * FA_BN, k1 = k0 + FA_BN - 1;
+        const bool interior = k1 <= q0 && k1 < seglen && (a.window < 0 || qw1 - k0 <= a.window);
+        bf16x8 db[2][2];
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++) {
-                f32x4 sc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}}, dp[2] = {sc[0], sc[1]};
+        for (int kt = 0; kt < 4; kt++) {
+            f32x4 sc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}}, dp[2] = {sc[0], sc[1]};
 #pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    const bf16x8 kop = rows_operand(s.k, kt, cc, g, c), vop = rows_operand(s.v, kt, cc, g, c);
+            for (int cc = 0; cc < 4; cc++) {
+                const bf16x8 kop = rows_operand(s.k, kt, cc, g, c), vop = rows_operand(s.v, kt, cc, g, c);
 #pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        sc[j] = mfma16x16x32(kop, qb_[j][cc], sc[j]);
-                        dp[j] = mfma16x16x32(vop, ob_[j][cc], dp[j]);
-                    }
+                for (int j = 0; j < 2; j++) {
+                    sc[j] = mfma16x16x32(kop, qb_[j][cc], sc[j]);
+                    dp[j] = mfma16x16x32(vop, ob_[j][cc], dp[j]);
                 }
-                /* lane (g, c): query column c of tile j, keys k0 + 16 kt + 4 g + i */
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        float p = __builtin_amdgcn_exp2f(sc[j][i] * a.scale_log2 - lse2[j]);
-                        if (!interior && !visible(k0 + 16 * kt + 4 * g + i, q0 + 16 * j + c, seglen, a.window)) p = 0.0f;
-                        db[j][kt >> 1][(kt & 1) * 4 + i] = (__bf16)(p * (dp[j][i] - dd[j]));
-                    }
             }
+            /* lane (g, c): query column c of tile j, keys k0 + 16 kt + 4 g + i */
 #pragma unroll
-            for (int d = 0; d < 8; d++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int s2 = 0; s2 < 2; s2++) {
-                    const bf16x8 kop = cols_operand(s.kt, d, s2, g, c);
-#pragma unroll
-                    for (int j = 0; j < 2; j++) dq[j][d] = mfma16x16x32(kop, db[j][s2], dq[j][d]);
+                for (int i = 0; i < 4; i++) {
+                    float p = __builtin_amdgcn_exp2f(sc[j][i] * a.scale_log2 - lse2[j]);
+                    if (!interior && !visible(k0 + 16 * kt + 4 * g + i, q0 + 16 * j + c, seglen, a.window)) p = 0.0f;
+                    db[j][kt >> 1][(kt & 1) * 4 + i] = (__bf16)(p * (dp[j][i] - dd[j]));
                 }
         }
+#pragma unroll
+        for (int d = 0; d < 8; d++)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                const bf16x8 kop = tr_operand(s.k, d, s2, g, c);
+#pragma unroll
+                for (int j = 0; j < 2; j++) dq[j][d] = mfma16x16x32(kop, db[j][s2], dq[j][d]);
+            }
+    };
+    const int kb_lo = klo / FA_BN, kb_hi = qb / FA_BN;
+    fetch(kb_lo, s0);
+    __syncthreads();
+    for (int kb = kb_lo; kb <= kb_hi; kb += 2) {
+        if (kb + 1 <= kb_hi) fetch(kb + 1, s1);
+        compute(kb, s0);
+        __syncthreads();
+        if (kb + 1 > kb_hi) break;
+        if (kb + 2 <= kb_hi) fetch(kb + 2, s0);
+        compute(kb + 1, s1);
         __syncthreads();
     }
     if (!active) return;
