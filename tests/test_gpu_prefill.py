@@ -130,3 +130,35 @@ def test_growing_scores_rescale_mid_stream(device):
     check_relative(out, want, oracle_prefill(oq, magnitude_cache(ocache), otable, np.full(len(seqs), w.ctx)))
     mx, mean = attn_errors(out, want)
     assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("window", [-1, 25])
+def test_long_block_table_takes_register_kernel(device, window):
+    """A block-table row longer than the 4,096 entries a workgroup stages in LDS sends the launch to the
+    register-prefetch kernel (`prefill_kernel`): the same sequences, their table padded to 4,100 entries, meet the
+    oracle bound there and agree with the LDS-staged kernel's output; a bad entry still turns only its own
+    sequence into NaN."""
+    w = PrefillWorkload("wide", 2, 6, 3, 31, 50, paged=True)
+    inp = prefill_inputs(w, seed=31)
+    narrow = inp["block_table"]
+    wide = torch.zeros((narrow.shape[0], 4100), dtype=narrow.dtype)
+    wide[:, :narrow.shape[1]] = narrow
+    lds_out = device_prefill(w, inp, device, window)[0]
+    out, q, cache, table, start, cos, sin = device_prefill(w, dict(inp, block_table=wide), device, window)
+    assert table.shape[1] == 4100
+    seqs = list(range(w.batch))
+    oq, ocache, otable = oracle_for(w, inp, seqs, cos, sin)
+    want = oracle_prefill(oq, ocache, otable, np.full(len(seqs), w.ctx), window=window)
+    check_relative(out, want, oracle_prefill(oq, magnitude_cache(ocache), otable, np.full(len(seqs), w.ctx),
+                                             window=window))
+    mx, mean = attn_errors(out, want)
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+    mx, _ = attn_errors(out, f32(lds_out).astype(np.float64))
+    assert mx <= ATTN_MAX_ABS, mx
+
+    bad = table.clone()
+    bad[1, (w.ctx + w.chunk - 1) // PAGE] = cache.num_pages + 5   # the last page: every window sees it
+    got = prefill_attention(q, cache, bad, start, window=window).float()
+    torch.cuda.synchronize()
+    assert torch.isnan(got[1, -1]).all()
+    assert torch.equal(got[0], out[0].float())
