@@ -156,3 +156,17 @@ def test_growing_scores_rescale_mid_stream(device, pps):
     out, want, _, _ = run(w, device, pps=pps, inp=inp)
     mx, mean = attn_errors(out, want)
     assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("window", [-1, 5000])
+def test_long_run_restages_block_table(device, window):
+    """A wave stages 256 block-table entries at a time; with pages_per_worker = 1000 one wave takes each unit of
+    513-563 pages (8,200-9,000 cached tokens + the new one; about 313 inside the window) whole and restages its
+    table mid-run. The result meets the oracle bound and agrees with the default split, whose runs stay within one
+    staging."""
+    w = DecodeWorkload("longrun", 2, 8, 2, 9000, ctx_min=8200, paged=True)
+    out, want, inp, (cache, table, lens, q) = run(w, device, seed=7, window=window, pps=1000)
+    mx, mean = attn_errors(out, want)
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+    split = decode_attention(q, cache, table, lens, inp["max_seq_len"], window=window, pages_per_worker=0).float()
+    assert (out.float() - split).abs().max().item() <= 1e-2
