@@ -10,7 +10,7 @@ value = algorithmic HBM bytes of the step / step time (GB/s). Attention bytes pe
 (n + 1) * 264 (fp8 K + V and two fp32 scales per key) + G * 128 * 2 * 2 (q in, out) + ceil((n + 1) / 16) * 4
 (block table); the append adds (Hq + 2 Hkv) * 256 read and Hq * 256 + Hkv * 264 written per token.
 
-    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4|c5|ve|fa] [--pages-per-worker P] [--cpu-seqs S]
+    python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4|c5|ve|fa] [--workers W] [--cpu-seqs S]
                     [--no-e2e]
 
 A decode workload's line also carries the metric's second half, `decode_tokens_per_s`: config 5 end to end
@@ -448,7 +448,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c3u")
-    ap.add_argument("--pages-per-worker", type=int, default=0)
+    ap.add_argument("--workers", type=int, default=0, help="decode: waves taking the work items (0: all slots)")
     ap.add_argument("--cpu-seqs", type=int, default=64, help="sequences in the CPU baseline sample (0: skip)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="decode workloads: skip the config-5 end-to-end decode tokens/s part of the metric")
@@ -499,7 +499,7 @@ def main():
     seq_lens = ctx + 1
     q_out = torch.empty(B, 1, Hq, 128, dtype=torch.bfloat16, device=dev)
     out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(max(1, decode_workspace_bytes(B, Hq, Hkv, inp["max_seq_len"], -1, args.pages_per_worker)),
+    ws = torch.empty(max(1, decode_workspace_bytes(B, Hq, Hkv, inp["max_seq_len"], -1)),
                      dtype=torch.uint8, device=dev)
 
     def append():
@@ -507,7 +507,7 @@ def main():
 
     def attend():
         decode_attention(q_out.view(B, Hq, 128), cache, table, seq_lens, inp["max_seq_len"],
-                         pages_per_worker=args.pages_per_worker, out=out, workspace=ws)
+                         workers=args.workers, out=out, workspace=ws)
 
     for _ in range(args.warmup):
         append()
@@ -556,7 +556,7 @@ def main():
         "data": "synthetic (seeded N(0,1) bf16, 1% 8-sigma outliers, random-permutation block table)",
         "config": {"workload": f"{w.name}: {w.description}", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
                    "keys_per_seq": inp["max_seq_len"], "page_size": 16, "step": "fused QK-norm/RoPE fp8 append + "
-                   "split-K decode attention", "pages_per_worker": args.pages_per_worker or "auto"},
+                   "split-K decode attention", "workers": args.workers or "auto"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "decode_tokens_per_s_per_layer": round(B / (ms_step * 1e-3), 1),
         "attn_ms_mean": round(attn_mean_ms, 5),

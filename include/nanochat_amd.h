@@ -149,8 +149,8 @@ int nc_qk_norm_rope_append_fp8(const void *qkv, long long token_stride, int B, i
                                float *kv_scale, int num_pages, void *stream);
 
 /* Workspace bytes nc_decode_attn_fp8 needs for these sizes (0 for unsupported sizes): fp32 partial results and
- * per-(sequence, KV head) metadata, rewritten by every call before it is read (no initialization needed). */
-size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window, int pages_per_worker);
+ * per-(sequence, KV head) metadata, written by every call before it is read (no initialization needed). */
+size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window);
 
 /*
  * Single-token decode attention over the paged fp8 cache. Replaces the reference's k_attn
@@ -158,18 +158,19 @@ size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int wi
  * [max(p - window, 0), p] (window < 0: all), scores (q . k) * sm_scale, fp32 softmax, out bf16.
  * The current token must already be appended (nc_kv_append_fp8 / nc_qk_norm_rope_append_fp8).
  * q: bf16 [B][Hq][128]; out: bf16 [B][Hq][128]; seq_lens: int32 [B] (<= 0: inactive, output zeros; more
- * than max_pages * 16: output NaN); B <= 4096.
- * Work split: the pages of every (sequence, KV head) form one list that waves take in equal contiguous runs
- * (one run per wave the device holds at once), so ragged lengths cost no imbalance; runs that cut a
- * sequence leave partials merged by a second kernel. max_seq_len (a host bound on seq_lens) and
- * pages_per_worker (0: automatic) size that split; the workspace must hold nc_decode_workspace_bytes.
+ * than max_seq_len: output NaN); max_seq_len <= max_pages * 16; B <= 4096.
+ * Work split: a (sequence, KV head)'s keys are cut at every multiple of 1,024 positions and each piece is one
+ * work item with its own softmax state; pieces of one sequence are merged in position order by a second kernel.
+ * The split points depend on nothing but the sequence's own length, so its output bits do not depend on the
+ * other sequences of the launch, on its place in the batch or on `workers` (waves taking the items; 0: every
+ * wave slot of the device). The workspace must hold nc_decode_workspace_bytes.
  * A block-table entry outside [0, num_pages) makes that sequence's output NaN instead of reading outside
  * the pool.
  */
 int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
                        const int32_t *block_table, int max_pages, int num_pages,
                        const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window, float sm_scale,
-                       int pages_per_worker, void *out, void *workspace, size_t workspace_bytes, void *stream);
+                       int workers, void *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Chunked-prefill attention over the paged fp8 cache (MFMA). Replaces the reference's prefill rows

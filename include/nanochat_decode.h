@@ -20,7 +20,8 @@ extern "C" {
 
 /* cfg [7]: L, C, F, vocab, max_len, store (prompt-store positions), lazy (the BOS row a host may reject).
  * ptrs [4 + 8 L]: wte fp32 [vocab][C], cos, sin fp32 [>= max_len][64], lm_head bf16 [vocab][C]; per layer qkv bf16
- * [3C][C], o [C][C], fc [F][C], proj [C][F], ve table (must be 0), ve gate (must be 0), q norm, k norm fp32 [128].
+ * [3C][C], o [C][C], fc [F][C], proj [C][F], value-embedding table bf16 [vocab][C] and its gate fp32 [H][C] (both 0
+ * on layers without value embeddings), q norm, k norm fp32 [128].
  * scal [2L + 1]: per layer (resid, x0) lambdas, then the logit cap. window [L]: keys before a query per layer.
  * Reference: decode.cu:950-1023. */
 void *dec_create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream);
@@ -86,18 +87,11 @@ void dec_debug_table(void *handle, int b, int32_t *out);
 void dec_debug_set_split(void *handle, int on);
 void dec_debug_set_graphs(void *handle, int on);
 
-/* The decode step's skinny GEMM alone: out[n][r] = epilogue(sum_k x[n][k] w[r][k]), bf16 w [R][K] and x [N][K],
- * epi 0 bf16(s), 1 x = s + res: bf16 out and fp32 out_f32, 2 bf16(relu(p) p) with p = s rstd[n], 3 bf16(s + res),
- * 4 fp32 out_f32 = s; split over `slices` K-slices (0: the decoder's choice, dec_debug_gemm_slices) whose partial
- * sums go to part (fp32 [slices][N][R]) and are added in slice order. Returns 0, a hipError_t, -2 when (R, K, N)
- * does not fit (N <= 128, K % 128 == 0, R % 4 == 0), or -3 while the kernel is switched off (it is: its first GPU
- * run faulted and the cause is not yet found). Stream-ordered. */
-int dec_debug_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out, float *out_f32,
-                   const void *res, const float *rstd, int slices, float *part, void *stream);
-int dec_debug_gemm_slices(int R, int K);
-
-/* The decode step's range-checked weight-streaming GEMM (the one the decoder runs) alone, same arguments and
- * epilogues as dec_debug_gemm; part needs dec_debug_stream_gemm_part_bytes(R, N, slices) bytes (none for one slice).
+/* The range-checked weight-streaming GEMM alone: out[n][r] = epilogue(sum_k x[n][k] w[r][k]), bf16 w [R][K] and
+ * x [N][K], epi 0 bf16(s), 1 x = s + res: bf16 out and fp32 out_f32, 2 bf16(relu(p) p) with p = s rstd[n],
+ * 3 bf16(s + res), 4 fp32 out_f32 = s; split over `slices` K-slices (0: the default, dec_debug_stream_gemm_slices)
+ * whose partial sums go to part (fp32 [slices][N][R], dec_debug_stream_gemm_part_bytes(R, N, slices) bytes, none for
+ * one slice) and are added in slice order.
  * Returns 0, a hipError_t, or -2 when the shape, the slice count or an operand the epilogue needs does not fit.
  * Stream-ordered. */
 int dec_debug_stream_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out, float *out_f32,

@@ -54,26 +54,30 @@ _WORKSPACES: dict = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A decode workspace of at least nbytes for this device, kept for reuse (every call rewrites what it reads)."""
-    ws = _WORKSPACES.get(device)
+    """A decode workspace of at least nbytes for this device and its current stream, kept for reuse (every call
+    writes what it reads). Keyed by stream: calls on two streams never share partials, and a workspace that grows is
+    only released to the caching allocator, which keeps it from other streams until its stream's work is done."""
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        _WORKSPACES[device] = ws
+        _WORKSPACES[key] = ws
     return ws
 
 
-def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int, window: int = -1,
-                           pages_per_worker: int = 0) -> int:
-    return hip_library().nc_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_seq_len, window,
-                                                   pages_per_worker)
+def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int,
+                           window: int = -1) -> int:
+    return hip_library().nc_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_seq_len, window)
 
 
 def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Tensor, seq_lens: torch.Tensor,
-                     max_seq_len: int, window: int = -1, sm_scale: float | None = None, pages_per_worker: int = 0,
+                     max_seq_len: int, window: int = -1, sm_scale: float | None = None, workers: int = 0,
                      out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """q bf16 [B, Hq, 128] (the current token's, already appended) -> out bf16 [B, Hq, 128].
 
-    Sequence b attends its keys [max(p - window, 0), p], p = seq_lens[b] - 1; max_seq_len bounds seq_lens."""
+    Sequence b attends its keys [max(p - window, 0), p], p = seq_lens[b] - 1; max_seq_len bounds seq_lens (a longer
+    sequence's output is NaN). workers caps the waves taking the work items (0: every wave slot of the device); it
+    changes no output bit, and neither does anything about the other sequences of the call."""
     _require(q, "q", torch.bfloat16)
     B, Hq, D = q.shape
     if D != HEAD_DIM:
@@ -86,7 +90,7 @@ def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Te
         out = torch.empty_like(q)
     _require(out, "out", torch.bfloat16)
     lib = hip_library()
-    need = lib.nc_decode_workspace_bytes(B, Hq, cache.num_kv_heads, max_seq_len, window, pages_per_worker)
+    need = lib.nc_decode_workspace_bytes(B, Hq, cache.num_kv_heads, max_seq_len, window)
     if need == 0:
         raise ValueError(f"unsupported decode shape: B={B}, Hq={Hq}, Hkv={cache.num_kv_heads}")
     if workspace is None or workspace.numel() * workspace.element_size() < need:
@@ -94,8 +98,8 @@ def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Te
     check(lib.nc_decode_attn_fp8(
         pointer(q), pointer(cache.k_pages), pointer(cache.v_pages), pointer(cache.kv_scale),
         pointer(block_table), block_table.size(1), cache.num_pages, pointer(seq_lens), max_seq_len, B, Hq,
-        cache.num_kv_heads, window, sm_scale, pages_per_worker, pointer(out),
-        pointer(workspace), need, stream()))
+        cache.num_kv_heads, window, sm_scale, workers, pointer(out),
+        pointer(workspace), workspace.numel() * workspace.element_size(), stream()))
     return out
 
 

@@ -42,10 +42,11 @@ struct AttnArgs {
     const int32_t *run_slot;  /* run b's block-table row */
     int B, T, Hq, Hkv, G, window;
     float scale_log2;         /* sm_scale * log2(e) */
-    int workers;              /* decode: waves sharing the flattened page list */
-    float *part_o;            /* decode partials [B*Hkv + workers][G][128] */
-    float *part_ml;           /* [B*Hkv + workers][G][2]: reference max (log2 domain), sum */
-    int *meta;                /* [B*Hkv][2]: first partial slot and partial count of each (sequence, KV head) */
+    int workers;              /* decode: waves taking the launch's items */
+    int max_len;              /* decode: the longest sequence the launch accepts (its workspace bound) */
+    float *part_o;            /* decode partials [items][G][128] */
+    float *part_ml;           /* [items][G][2]: reference max (log2 domain), sum */
+    int *meta;                /* [B*Hkv][2]: first item and chunk count of each (sequence, KV head) */
     uint16_t *out;            /* [B][T][Hq][128] bf16 */
 };
 
@@ -377,18 +378,13 @@ __device__ __forceinline__ uint4 bload_nt(Rsrc r, int off) {
     return uint4{v[0], v[1], v[2], v[3]};
 }
 
-/* A wave's staged block-table entries: lane j of v[q] holds entry 64 q + j (DEC_TAB = 256 entries). Entry e is read
- * by v_readlane into a scalar register: no vector register or LDS access in the pair loop. */
+/* A wave's staged block-table entries of one chunk: lane j holds entry j (at most SPLIT_PAGES = 64 entries). Entry e
+ * is read by v_readlane into a scalar register: no vector register or LDS access in the pair loop. */
 struct TabRegs {
-    int v[4];
+    int v;
 };
 
-__device__ __forceinline__ int tab_entry(const TabRegs &t, int e) {
-    const int j = e & (WAVE - 1), q = e >> 6;
-    const int r0 = __builtin_amdgcn_readlane(t.v[0], j), r1 = __builtin_amdgcn_readlane(t.v[1], j);
-    const int r2 = __builtin_amdgcn_readlane(t.v[2], j), r3 = __builtin_amdgcn_readlane(t.v[3], j);
-    return q == 0 ? r0 : q == 1 ? r1 : q == 2 ? r2 : r3;
-}
+__device__ __forceinline__ int tab_entry(const TabRegs &t, int e) { return __builtin_amdgcn_readlane(t.v, e); }
 
 __device__ __forceinline__ PairAddr pair_addr_tab(const AttnArgs &a, const TabRegs &tab, int tab0, int kvh, int lpa,
                                                   int end, bool &bad) {
@@ -463,16 +459,25 @@ __device__ __forceinline__ void attend_pages_tab(const AttnArgs &a, const TabReg
     }
 }
 
-constexpr int DEC_TAB = 256;   /* block-table entries a decode wave stages at a time (TabRegs) */
+/* Split points of decode: a (sequence, KV head) unit's keys are cut at every multiple of SPLIT_PAGES pages (1,024
+ * positions), whatever the rest of the batch holds, so a sequence's sums (and its output bits) depend only on its own
+ * query, keys and length. */
+constexpr int SPLIT_PAGES = 64;
+static_assert(SPLIT_PAGES <= WAVE, "a chunk's block-table entries are staged one per lane (TabRegs)");
 
 /* Key range [begin, p] of a sequence of L keys and its logical pages [pg0, pg0 + npages); npages = 0 for an
- * inactive sequence (L <= 0) or one the block table cannot hold (its output is NaN). */
+ * inactive sequence (L <= 0) or one longer than max_len (the launch's bound; its output is NaN). */
 __device__ __forceinline__ int decode_pages(const AttnArgs &a, int L, int &begin, int &pg0) {
-    if (L <= 0 || L > a.max_pages * PAGE) return 0;
+    if (L <= 0 || L > a.max_len) return 0;
     const int p = L - 1;
     begin = a.window >= 0 ? max(p - a.window, 0) : 0;
     pg0 = begin / PAGE;
     return p / PAGE + 1 - pg0;
+}
+
+/* Chunks of logical pages [pg0, pg0 + np): one per multiple of SPLIT_PAGES the range touches. */
+__device__ __forceinline__ int unit_chunks(int pg0, int np) {
+    return np > 0 ? (pg0 + np - 1) / SPLIT_PAGES - pg0 / SPLIT_PAGES + 1 : 0;
 }
 
 __device__ __forceinline__ void store_bf16x4(uint16_t *dst, const float *v) {
@@ -482,30 +487,32 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *dst, const float *v) {
     *reinterpret_cast<uint2 *>(dst) = u;
 }
 
-/* The worker owning flattened page x when P pages are shared by W workers, worker w taking
- * [floor(w P / W), floor((w + 1) P / W)). */
-__device__ __forceinline__ long long worker_of(long long x, long long P, long long W) { return ((x + 1) * W - 1) / P; }
-
-constexpr int MAX_DECODE_BATCH = 4096;  /* sequences per decode launch (the LDS page prefix: 32 KiB) */
+constexpr int MAX_DECODE_BATCH = 4096;  /* sequences per decode launch (the LDS item prefix: 32 KiB) */
 
 /*
- * Balanced split-K decode. The (sequence, KV head) units in order b * Hkv + kvh, each with the pages of its key
- * range, form one flattened page list of P pages; `workers` waves (4 per work-group) take equal contiguous runs
- * of it, so every wave streams the same number of pages whatever the sequence lengths. A wave walks the units
- * its run touches: a unit entirely inside the run is finished in place (bf16 output), a unit cut by run
- * boundaries leaves one partial per touching wave (slot meta[u][0] + j for its j-th wave) and its first wave
- * records the slot range in meta[u] for decode_combine_kernel.
+ * Split-K decode over fixed chunks. The items are (sequence, KV head, chunk) in that order: sequence b contributes
+ * Hkv * unit_chunks items, item i of the launch is the i-th of that list. `workers` waves (4 per work-group) take
+ * items i = wid, wid + W, ... (the hardware holds every wave at once, so the waves that finish early leave the
+ * bandwidth to the rest). Every item starts from a fresh softmax state and streams only its chunk's pages, so what a
+ * wave computes for an item does not depend on which wave takes it or what else the launch holds. A unit of one chunk
+ * is finished in place (bf16 output); a unit of several leaves one partial per chunk in slot i (its item index) and
+ * its chunk-0 item records (first item, chunk count) in meta[u] for decode_combine_kernel, which merges them in chunk
+ * order.
  */
 __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
-    extern __shared__ long long sh_cum[];  /* [B + 1]: pages of the units of sequences < b */
+    extern __shared__ long long sh_cum[];  /* [B + 1]: items of the sequences < b */
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
-    if (wave == 0) {  /* exclusive prefix over sequences of Hkv * pages, 64 sequences per step */
+    if (wave == 0) {  /* exclusive prefix over sequences of Hkv * chunks, 64 sequences per step */
         long long run = 0;
         for (int b0 = 0; b0 < a.B; b0 += WAVE) {
-            int begin, pg0;
+            int begin = 0, pg0 = 0;
             const int b = b0 + lane;
-            long long v = b < a.B ? (long long)a.Hkv * decode_pages(a, a.seq_lens[b], begin, pg0) : 0;
+            long long v = 0;
+            if (b < a.B) {
+                const int np = decode_pages(a, a.seq_lens[b], begin, pg0);
+                v = (long long)a.Hkv * unit_chunks(pg0, np);
+            }
 #pragma unroll
             for (int o = 1; o < WAVE; o <<= 1) {
                 const long long t = __shfl_up(v, o, WAVE);
@@ -517,28 +524,25 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         if (lane == 0) sh_cum[0] = 0;
     }
     __syncthreads();
-    const long long P = sh_cum[a.B];
-    const long long W = min((long long)a.workers, P);  /* at most one wave per page: no run is empty */
+    const long long N = sh_cum[a.B];
+    const long long W = min((long long)a.workers, N);
     const long long wid = (long long)blockIdx.x * WAVES + wave;
     if (wid >= W) return;  /* the grid rounds the workers up to whole work-groups */
-    long long s = wid * P / W;
-    const long long e = (wid + 1) * P / W;
-    if (s >= e) return;
-    int lo_b = 0, hi_b = a.B - 1;  /* the sequence holding flattened page s: the last b with sh_cum[b] <= s */
-    while (lo_b < hi_b) {
-        const int mid = (lo_b + hi_b + 1) >> 1;
-        if (sh_cum[mid] <= s) lo_b = mid; else hi_b = mid - 1;
-    }
-    int b = lo_b;
-    while (s < e && b < a.B) {
+    for (long long it = wid; it < N; it += W) {
+        int lo_b = 0, hi_b = a.B - 1;  /* the sequence holding item it: the last b with sh_cum[b] <= it */
+        while (lo_b < hi_b) {
+            const int mid = (lo_b + hi_b + 1) >> 1;
+            if (sh_cum[mid] <= it) lo_b = mid; else hi_b = mid - 1;
+        }
+        const int b = lo_b;
         const int L = a.seq_lens[b];
         int begin = 0, pg0 = 0;
         const int np = decode_pages(a, L, begin, pg0);
-        if (np == 0 || sh_cum[b + 1] <= s) { b++; continue; }
-        const int kvh = (int)((s - sh_cum[b]) / np);
-        const long long us = sh_cum[b] + (long long)kvh * np, ue = us + np;  /* this unit's flattened pages */
-        const long long seg_end = min(e, ue);
-        const int first = pg0 + (int)(s - us), last = pg0 + (int)(seg_end - us);
+        const int nch = unit_chunks(pg0, np);
+        const int local = (int)(it - sh_cum[b]);
+        const int kvh = local / nch, j = local - kvh * nch;
+        const int chunk = pg0 / SPLIT_PAGES + j;
+        const int first = max(pg0, chunk * SPLIT_PAGES), last = min(pg0 + np, (chunk + 1) * SPLIT_PAGES);
         const long long row0 = (long long)b * a.Hq + kvh * a.G;
 
         QOp qb[1];
@@ -550,18 +554,12 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         kb.lo[0] = kb.full_lo = begin;
         kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
         const int32_t *bt = a.block_table + (long long)b * a.max_pages;
-        for (int c0 = first; c0 < last; c0 += DEC_TAB) {   /* stage the table entries, then stream the pages */
-            const int c1 = min(c0 + DEC_TAB, last);
-            TabRegs tab;
-#pragma unroll
-            for (int i = 0; i < DEC_TAB / WAVE; i++)
-                tab.v[i] = c0 + i * WAVE + lane < c1 ? bt[c0 + i * WAVE + lane] : 0;
-            attend_pages_tab<1>(a, tab, c0, kvh, c0, c1, kb, qb, st, lane);
-        }
+        TabRegs tab;
+        tab.v = first + lane < last ? bt[first + lane] : 0;
+        attend_pages_tab<1>(a, tab, first, kvh, first, last, kb, qb, st, lane);
         st.l[0] = pair_sum32(pair_sum16(st.l[0]));
-        const long long w0 = worker_of(us, P, W), w1 = worker_of(ue - 1, P, W);
         const int u = b * a.Hkv + kvh;
-        if (w0 == w1) {  /* the whole unit is in this run */
+        if (nch == 1) {
             if (c < a.G) {
                 uint16_t *dst = a.out + (row0 + c) * HEAD_DIM;
                 const float inv = 1.0f / st.l[0];
@@ -573,27 +571,22 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
                     store_bf16x4(dst + 16 * t + 4 * g, v);
                 }
             }
-        } else {
-            const long long slot = u + wid;  /* = meta[u][0] + (wid - w0) */
-            if (c < a.G) {
-                float *po = a.part_o + (slot * a.G + c) * HEAD_DIM;
+        } else if (c < a.G) {
+            float *po = a.part_o + (it * a.G + c) * HEAD_DIM;
 #pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    const f32x4 o = st.o[0][t];
-                    *reinterpret_cast<float4 *>(po + 16 * t + 4 * g) =
-                        float4{st.bad ? NAN : o[0], o[1], o[2], o[3]};
-                }
-                if (g == 0) {
-                    a.part_ml[(slot * a.G + c) * 2] = st.bad ? NAN : st.m[0];
-                    a.part_ml[(slot * a.G + c) * 2 + 1] = st.l[0];
-                }
+            for (int t = 0; t < 8; t++) {
+                const f32x4 o = st.o[0][t];
+                *reinterpret_cast<float4 *>(po + 16 * t + 4 * g) = float4{st.bad ? NAN : o[0], o[1], o[2], o[3]};
+            }
+            if (g == 0) {
+                a.part_ml[(it * a.G + c) * 2] = st.bad ? NAN : st.m[0];
+                a.part_ml[(it * a.G + c) * 2 + 1] = st.l[0];
             }
         }
-        if (wid == w0 && lane == 0) {  /* the unit's first wave: where its partials are, how many */
-            a.meta[2 * u] = (int)(u + w0);
-            a.meta[2 * u + 1] = (int)(w1 - w0 + 1);
+        if (j == 0 && lane == 0) {  /* the unit's chunk 0: where its partials are, how many */
+            a.meta[2 * u] = (int)it;
+            a.meta[2 * u + 1] = nch;
         }
-        s = seg_end;
     }
 }
 
@@ -957,11 +950,9 @@ int prefill_runs(const uint16_t *q, const uint8_t *k_pages, const uint8_t *v_pag
     return (int)hipGetLastError();
 }
 
-/* Decode workers (waves). Automatic: every wave slot the device holds at the kernel's occupancy, so one
- * balanced round covers the whole page list; at most one wave per MIN_WORKER_PAGES pages, at most
- * MAX_WORKERS. pages_per_worker > 0 asks for that many pages per wave instead. */
-constexpr int MIN_WORKER_PAGES = 16;
-constexpr int MAX_WORKERS = 4096;
+/* Decode workers (waves): by default every wave slot the device holds at the kernel's occupancy, so every item is
+ * taken in the first round whenever there are no more items than slots; workers > 0 caps them. */
+constexpr int MAX_WORKERS = 1 << 20;
 
 static long long max_unit_pages(int max_seq_len, int window) {
     long long n = (max_seq_len + PAGE - 1) / PAGE;
@@ -969,54 +960,43 @@ static long long max_unit_pages(int max_seq_len, int window) {
     return n;
 }
 
-static int worker_bound(int B, int Hkv, int max_seq_len, int window, int pages_per_worker) {
-    const long long pages = (long long)B * Hkv * max_unit_pages(max_seq_len, window);
-    long long w = (pages + MIN_WORKER_PAGES - 1) / MIN_WORKER_PAGES;
-    if (pages_per_worker > 0) w = min(w, (pages + pages_per_worker - 1) / pages_per_worker);
-    return (int)max(1LL, min(w, (long long)MAX_WORKERS));
+/* Items a launch can hold: a unit of n pages touches at most ceil(n / SPLIT_PAGES) + 1 chunks. */
+static long long item_bound(int B, int Hkv, int max_seq_len, int window) {
+    const long long n = max_unit_pages(max_seq_len, window);
+    return (long long)B * Hkv * ((n + SPLIT_PAGES - 1) / SPLIT_PAGES + 1);
 }
 
 static int device_wave_slots() {
     static int slots[64] = {0};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MAX_WORKERS;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 2048;
     if (!slots[dev]) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, 256,
                                                          (MAX_DECODE_BATCH + 1) * sizeof(long long)) != hipSuccess)
-            return MAX_WORKERS;
+            return 2048;
         slots[dev] = max(1, cus * per_cu * WAVES);
     }
     return slots[dev];
 }
 
-/* Workspace layout: partial O [B*Hkv + W][G][128] fp32, partial (max, sum) [B*Hkv + W][G][2] fp32, then
- * meta [B*Hkv][2] int32, W = worker_bound(...). Every launch rewrites what it later reads. */
-static size_t workspace_bytes_for(int B, int Hq, int Hkv, int W) {
-    const size_t slots = (size_t)B * Hkv + W, G = Hq / Hkv;
-    return slots * G * (HEAD_DIM + 2) * sizeof(float) + (size_t)B * Hkv * 2 * sizeof(int);
+/* Workspace layout: partial O [items][G][128] fp32, partial (max, sum) [items][G][2] fp32, then meta [B*Hkv][2]
+ * int32, items = item_bound(...). Every launch writes what it later reads. */
+static size_t workspace_bytes_for(int B, int Hq, int Hkv, long long items) {
+    const size_t G = Hq / Hkv;
+    return (size_t)items * G * (HEAD_DIM + 2) * sizeof(float) + (size_t)B * Hkv * 2 * sizeof(int);
 }
 
-}  // namespace nc
-
-using namespace nc;
-
-extern "C" size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window, int pages_per_worker) {
-    if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || max_seq_len <= 0) return 0;
-    return workspace_bytes_for(B, Hq, Hkv, worker_bound(B, Hkv, max_seq_len, window, pages_per_worker));
+static bool decode_shape_ok(int B, int Hq, int Hkv, int max_seq_len) {
+    return B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16 && max_seq_len > 0 && B <= MAX_DECODE_BATCH;
 }
 
-extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
-                                  const int32_t *block_table, int max_pages, int num_pages,
-                                  const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window,
-                                  float sm_scale, int pages_per_worker, void *out, void *workspace,
-                                  size_t workspace_bytes, void *stream) {
-    if (!q || !k_pages || !v_pages || !kv_scale || !block_table || !seq_lens || !out || !workspace)
-        return NC_ERR_NULL;
-    if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Hq / Hkv > 16 || max_pages <= 0 || num_pages <= 0 ||
-        max_seq_len <= 0 || (long long)max_seq_len > (long long)max_pages * PAGE || B > MAX_DECODE_BATCH)
-        return NC_ERR_SHAPE;
+/* The launch itself (arguments checked by the caller); the workspace holds workspace_bytes_for(item_bound). */
+static int launch_decode(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
+                         const int32_t *block_table, int max_pages, int num_pages, const int32_t *seq_lens,
+                         int max_seq_len, int B, int Hq, int Hkv, int window, float sm_scale, int workers, void *out,
+                         void *workspace, hipStream_t stream) {
     AttnArgs a = {};
     a.q = (const uint16_t *)q;
     a.k_pages = (const uint8_t *)k_pages; a.v_pages = (const uint8_t *)v_pages;
@@ -1024,20 +1004,43 @@ extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void
     a.block_table = block_table; a.max_pages = max_pages; a.num_pages = num_pages;
     a.seq_lens = seq_lens;
     a.B = B; a.T = 1; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.window = window;
+    a.max_len = max_seq_len;
     a.scale_log2 = sm_scale * LOG2E;
-    const int bound = worker_bound(B, Hkv, max_seq_len, window, pages_per_worker);
-    a.workers = pages_per_worker > 0 ? bound : min(bound, device_wave_slots());
+    const long long items = item_bound(B, Hkv, max_seq_len, window);
+    a.workers = (int)min((long long)(workers > 0 ? min(workers, MAX_WORKERS) : device_wave_slots()), items);
     a.out = (uint16_t *)out;
-    const size_t need = workspace_bytes_for(B, Hq, Hkv, bound);
-    if (workspace_bytes < need) return NC_ERR_WORKSPACE;
-    const size_t slots = (size_t)B * Hkv + bound;
     a.part_o = (float *)workspace;
-    a.part_ml = a.part_o + slots * a.G * HEAD_DIM;
-    a.meta = (int *)(a.part_ml + slots * a.G * 2);
+    a.part_ml = a.part_o + (size_t)items * a.G * HEAD_DIM;
+    a.meta = (int *)(a.part_ml + (size_t)items * a.G * 2);
     const int grid = (a.workers + WAVES - 1) / WAVES;
-    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(256), (B + 1) * sizeof(long long), (hipStream_t)stream, a);
-    hipLaunchKernelGGL(decode_combine_kernel, dim3(B * Hq), dim3(HEAD_DIM), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(256), (B + 1) * sizeof(long long), stream, a);
+    hipLaunchKernelGGL(decode_combine_kernel, dim3(B * Hq), dim3(HEAD_DIM), 0, stream, a);
     return (int)hipGetLastError();
+}
+
+}  // namespace nc
+
+using namespace nc;
+
+extern "C" size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window) {
+    if (!decode_shape_ok(B, Hq, Hkv, max_seq_len)) return 0;
+    return workspace_bytes_for(B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window));
+}
+
+extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
+                                  const int32_t *block_table, int max_pages, int num_pages,
+                                  const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window,
+                                  float sm_scale, int workers, void *out, void *workspace,
+                                  size_t workspace_bytes, void *stream) {
+    if (!q || !k_pages || !v_pages || !kv_scale || !block_table || !seq_lens || !out || !workspace)
+        return NC_ERR_NULL;
+    if (!decode_shape_ok(B, Hq, Hkv, max_seq_len) || max_pages <= 0 || num_pages <= 0 ||
+        (long long)max_seq_len > (long long)max_pages * PAGE || workers < 0)
+        return NC_ERR_SHAPE;
+    if (workspace_bytes < workspace_bytes_for(B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)))
+        return NC_ERR_WORKSPACE;
+    return launch_decode(q, k_pages, v_pages, kv_scale, block_table, max_pages, num_pages, seq_lens, max_seq_len, B,
+                         Hq, Hkv, window, sm_scale, workers, out, workspace, (hipStream_t)stream);
 }
 
 extern "C" int nc_prefill_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,

@@ -4,26 +4,27 @@
  *
  * A step is a stream of kernels on the caller's stream, launched eagerly:
  *   body   norm_kernel(EMBED) -> per layer { norm_kernel(RESID), qkv GEMM, the fused q/k norm + RoPE + value-embedding
- *          + fp8 append (kv_append.hip), split-K decode attention (attention.hip), o GEMM (+ residual, fp32 sum kept),
- *          rstd_kernel, fc GEMM (+ ReLU^2 of the rstd-scaled sum), proj GEMM (+ residual) }
+ *          + fp8 append (kv_append.hip), split-K decode attention (attention.hip), o GEMM (fp32 sum), rstd_kernel (adds
+ *          the residual), fc GEMM + relu2_kernel, proj GEMM (+ residual) }
  *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
  *          the allowed tokens, then the commit), the tokens to pinned host memory.
- * A step's GEMMs (<= 128 slots) are stream_gemm.hip's weight-streaming MFMA kernels with the epilogues fused (split-K
- * partials reduced in slice order by a second kernel); prefill's GEMMs are hipBLASLt matmuls (bf16 operands, fp32
- * accumulation; a plan per shape and row count, the heuristic's first algorithm; rocBLAS gemm_ex when hipBLASLt offers
- * none) followed by the epilogue kernels. skinny_gemm.hip (an earlier weight-streaming GEMM) is built but switched
- * off: its first GPU test run faulted and the cause is not found. Every kernel covers the slots up to the highest
- * active one (dec_set_active) and skips inactive slots.
+ * GEMMs are hipBLASLt matmuls (bf16 operands, fp32 accumulation; one plan per shape and row count, the heuristic's
+ * first algorithm; rocBLAS gemm_ex where hipBLASLt offers none) followed by the epilogue kernels. stream_gemm.hip's
+ * range-checked weight-streaming GEMM, whose epilogues are fused, is built and tested but off (Decoder::streaming):
+ * at the step's shapes it is not faster than the library. Every kernel covers the slots up to the highest active one
+ * (dec_set_active) and skips inactive slots.
  *
  * Numerics, op by op as decode.cu: the epilogues round once (bf16(s + residual)); the MLP reads the un-normed stream
  * scaled by its rstd; every RMS norm is 1 / sqrt(mean x^2 + FLT_EPSILON), correctly rounded (the reference: rsqrtf).
  * The KV cache is fp8 e4m3fn with one absmax scale per (token, head) (the reference caches bf16); a step's own key
- * is read back from the cache like the others.
+ * is read back from the cache like the others. Decode attention splits a slot's keys at fixed multiples of 1,024
+ * positions, so its sums depend only on the slot's own context.
  *
  * Memory: one allocation per role, sized at dec_create. The KV pool of layer l is pages [0, B max_pages) for the
- * slots (slot b owns pages b max_pages + i, the identity block table) followed by the prompt store's pages (store
- * position s at page B max_pages + s / 16, slot s % 16), so saving and loading a prompt are page-to-page copies
- * inside one pool.
+ * slots (slot b owns pages b max_pages + i) followed by the prompt store's pages (store position s at page
+ * B max_pages + s / 16, slot s % 16). dec_save_prompt copies a slot's positions into the store; dec_load_prompt points
+ * the slot's block-table entries at the store's whole pages (shared read-only, copied on the slot's first write to
+ * one) and copies only partial pages.
  */
 #include <math.h>
 #include <stdio.h>
@@ -1002,7 +1003,7 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
             part_bytes = bytes > part_bytes ? bytes : part_bytes;
         }
     d->part_bytes = part_bytes;
-    d->attn_ws_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1, 0);
+    d->attn_ws_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1);
     REQUIRE(d->attn_ws_bytes > 0, "decode attention workspace");
     for (Lane &ln : d->lane) {
         ln.part = (float *)device_alloc(d, (size_t)part_bytes);
@@ -1355,22 +1356,6 @@ extern "C" void dec_debug_table(void *handle, int b, int32_t *out) {
     if (b < 0 || b >= d->B) nc::dec::die("dec_debug_table", "slot out of range", __LINE__);
     memcpy(out, d->table.data() + (size_t)b * d->max_pages, (size_t)d->max_pages * sizeof(int32_t));
 }
-
-static const bool skinny_enabled = false;
-
-extern "C" int dec_debug_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out, float *out_f32,
-                              const void *res, const float *rstd, int slices, float *part, void *stream) {
-    nc::SkinnyGemm g = {(const uint16_t *)w, (const uint16_t *)x, R, K, N, (uint16_t *)out, out_f32,
-                        (const uint16_t *)res, rstd, nullptr};
-    if (!nc::skinny_gemm_fits(R, K, N)) return -2;
-    if (!skinny_enabled) return -3;   /* switched off, see dec_create */
-    const int S = slices > 0 ? slices : nc::skinny_gemm_slices(R, K);
-    const int e = nc::skinny_gemm(g, epi, part, S, (hipStream_t)stream);
-    if (e != 0 || S == 1) return e;
-    return nc::skinny_gemm_reduce(g, epi, part, S, (hipStream_t)stream);
-}
-
-extern "C" int dec_debug_gemm_slices(int R, int K) { return nc::skinny_gemm_slices(R, K); }
 
 extern "C" void dec_debug_set_split(void *handle, int on) {
     Decoder *d = (Decoder *)handle;

@@ -345,4 +345,4 @@ extern "C" const char *nc_status_string(int status) {
     }
 }
 
-extern "C" int nc_abi_version(void) { return 2; }
+extern "C" int nc_abi_version(void) { return 3; }

@@ -27,7 +27,8 @@ int prefill_runs(const uint16_t *q, const uint8_t *k_pages, const uint8_t *v_pag
                  const int32_t *run_row0, const int32_t *run_count, const int32_t *run_slot, int runs, int max_count,
                  int Hq, int Hkv, int window, float sm_scale, uint16_t *out, hipStream_t stream);
 
-/* skinny_gemm.hip: out[n][r] = epilogue(sum_k x[n][k] w[r][k]), bf16 operands, fp32 sums, N <= SG_MAX_N slots. */
+/* The decode step's GEMM operands: out[n][r] = epilogue(sum_k x[n][k] w[r][k]), bf16 operands, fp32 sums,
+ * N <= SG_MAX_N rows. */
 constexpr int SG_MAX_N = 128;
 enum { SG_STORE, SG_RESID2, SG_RELU2, SG_RESID, SG_F32 };
 struct SkinnyGemm {
@@ -40,14 +41,6 @@ struct SkinnyGemm {
     const float *rstd;                 /* [N] (RELU2) */
     const unsigned long long *active;  /* NULL, or the slots whose outputs are stored */
 };
-bool skinny_gemm_fits(int R, int K, int N);
-/* K-slices for (R, K): enough workgroups to fill the device, at least two 128-wide chunks a slice. */
-int skinny_gemm_slices(int R, int K);
-/* S = 1: the epilogue in the GEMM. S > 1: fp32 partials to part [S][N][R] (the caller reduces them, e.g. by
- * skinny_gemm_reduce). Returns 0, a hipError_t, or -2 when the shape does not fit (the caller uses a library GEMM). */
-int skinny_gemm(const SkinnyGemm &g, int epi, float *part, int S, hipStream_t stream);
-/* The S partials summed in slice order, then the epilogue. */
-int skinny_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, int S, hipStream_t stream);
 
 /* stream_gemm.hip: the same GEMM (SkinnyGemm operands, SG_* epilogues) with every global access range-checked by
  * buffer instructions. */

@@ -26,7 +26,7 @@ LIB_DIR = PACKAGE / "lib"
 LIBRARY = LIB_DIR / "libnanochat_kv.so"
 DECODE_LIBRARY = LIB_DIR / "libnanochat_decode.so"
 KERNEL_SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip", CSRC / "ve_gate.hip", CSRC / "flash_attn.hip"]
-DECODE_SOURCES = [CSRC / "decoder.hip", CSRC / "skinny_gemm.hip", CSRC / "stream_gemm.hip"]
+DECODE_SOURCES = [CSRC / "decoder.hip", CSRC / "stream_gemm.hip"]
 SOURCES = KERNEL_SOURCES + DECODE_SOURCES
 HEADERS = [CSRC / "nc_device.h", CSRC / "nc_internal.h", INCLUDE / "nanochat_amd.h", INCLUDE / "nanochat_decode.h"]
 HEAD_DIM = 128
@@ -85,7 +85,7 @@ SIGNATURES = {
     "nc_qk_norm_rope_append_fp8": ([c_void_p, c_longlong, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
                                     c_void_p, c_int, c_void_p], c_int),
-    "nc_decode_workspace_bytes": ([c_int, c_int, c_int, c_int, c_int, c_int], c_size_t),
+    "nc_decode_workspace_bytes": ([c_int, c_int, c_int, c_int, c_int], c_size_t),
     "nc_decode_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
                             c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_size_t, c_void_p], c_int),
     "nc_prefill_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
@@ -128,9 +128,6 @@ DECODE_SIGNATURES = {
     "dec_debug_table": ([c_void_p, c_int, c_void_p], None),
     "dec_debug_set_split": ([c_void_p, c_int], None),
     "dec_debug_set_graphs": ([c_void_p, c_int], None),
-    "dec_debug_gemm": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
-                        c_int, c_void_p, c_void_p], c_int),
-    "dec_debug_gemm_slices": ([c_int, c_int], c_int),
     "dec_debug_stream_gemm": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                c_int, c_void_p, c_void_p], c_int),
     "dec_debug_stream_gemm_slices": ([c_int, c_int], c_int),

@@ -24,7 +24,7 @@ def test_header_and_binding_agree():
 def test_library_exports_every_declared_symbol(lib):
     for name in declared():
         assert hasattr(lib, name), name
-    assert lib.nc_abi_version() == 2
+    assert lib.nc_abi_version() == 3
 
 
 def test_status_strings(lib):
@@ -48,36 +48,34 @@ def test_bad_decode_shapes_rejected(lib, B, Hq, Hkv, max_seq, max_pages):
 
 
 def test_small_workspace_rejected(lib):
-    need = lib.nc_decode_workspace_bytes(64, 16, 4, 8193, -1, 0)
+    need = lib.nc_decode_workspace_bytes(64, 16, 4, 8193, -1)
     assert need > 0
     assert lib.nc_decode_attn_fp8(*([DUMMY] * 5), 513, 64 * 513, DUMMY, 8193, 64, 16, 4, -1, 0.1, 0, DUMMY, DUMMY,
                                   need - 1, None) == -3
 
 
-def expected_workspace(B, Hq, Hkv, max_seq, window, pps):
-    """The documented layout: fp32 partials (O [128] + max, sum) for B*Hkv + W slots of G heads, then int32
-    meta [B*Hkv][2]; W = one wave per 16 pages of the largest possible page list (at most 4096), or per `pps`."""
+def expected_workspace(B, Hq, Hkv, max_seq, window):
+    """The documented layout: fp32 partials (O [128] + max, sum) of G heads for every item a launch can hold, then
+    int32 meta [B*Hkv][2]; a unit of n pages (n capped by the window) touches at most ceil(n / 64) + 1 chunks of
+    1,024 positions."""
     unit_pages = -(-max_seq // 16)
     if window >= 0:
         unit_pages = min(unit_pages, window // 16 + 2)
-    pages = B * Hkv * unit_pages
-    w = -(-pages // 16)
-    if pps > 0:
-        w = min(w, -(-pages // pps))
-    w = max(1, min(w, 4096))
-    return (B * Hkv + w) * (Hq // Hkv) * 130 * 4 + B * Hkv * 2 * 4
+    items = B * Hkv * (-(-unit_pages // 64) + 1)
+    return items * (Hq // Hkv) * 130 * 4 + B * Hkv * 2 * 4
 
 
-@pytest.mark.parametrize("args", [(1, 4, 4, 16, -1, 64), (8, 16, 4, 8193, -1, 0), (8, 16, 4, 8193, 512, 0),
-                                  (64, 16, 4, 8193, -1, 0), (64, 16, 4, 8193, -1, 258), (32, 10, 10, 4097, -1, 0)])
+@pytest.mark.parametrize("args", [(1, 4, 4, 16, -1), (8, 16, 4, 8193, -1), (8, 16, 4, 8193, 512),
+                                  (64, 16, 4, 8193, -1), (64, 16, 4, 8193, 1023), (32, 10, 10, 4097, -1)])
 def test_workspace_sizes(lib, args):
     assert lib.nc_decode_workspace_bytes(*args) == expected_workspace(*args)
 
 
 def test_workspace_window_and_bad_sizes(lib):
-    assert lib.nc_decode_workspace_bytes(8, 16, 4, 8193, 512, 0) < lib.nc_decode_workspace_bytes(8, 16, 4, 8193, -1, 0)
-    assert lib.nc_decode_workspace_bytes(0, 16, 4, 8193, -1, 0) == 0
-    assert lib.nc_decode_workspace_bytes(8, 6, 4, 8193, -1, 0) == 0
+    assert lib.nc_decode_workspace_bytes(8, 16, 4, 8193, 512) < lib.nc_decode_workspace_bytes(8, 16, 4, 8193, -1)
+    assert lib.nc_decode_workspace_bytes(0, 16, 4, 8193, -1) == 0
+    assert lib.nc_decode_workspace_bytes(8, 6, 4, 8193, -1) == 0
+    assert lib.nc_decode_workspace_bytes(4097, 16, 4, 8193, -1) == 0
 
 
 def test_bad_append_shapes_rejected(lib):
