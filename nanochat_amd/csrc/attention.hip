@@ -42,7 +42,7 @@ struct AttnArgs {
     const int32_t *run_slot;  /* run b's block-table row */
     int B, T, Hq, Hkv, G, window;
     float scale_log2;         /* sm_scale * log2(e) */
-    int workers;              /* decode: waves taking the launch's items */
+    int workers;              /* decode: waves launched (whole work-groups of 4) */
     int max_len;              /* decode: the longest sequence the launch accepts (its workspace bound) */
     float *part_o;            /* decode partials [items][G][128] */
     float *part_ml;           /* [items][G][2]: reference max (log2 domain), sum */
@@ -475,9 +475,27 @@ __device__ __forceinline__ int decode_pages(const AttnArgs &a, int L, int &begin
     return p / PAGE + 1 - pg0;
 }
 
-/* Chunks of logical pages [pg0, pg0 + np): one per multiple of SPLIT_PAGES the range touches. */
-__device__ __forceinline__ int unit_chunks(int pg0, int np) {
-    return np > 0 ? (pg0 + np - 1) / SPLIT_PAGES - pg0 / SPLIT_PAGES + 1 : 0;
+/* How a unit's logical pages [pg0, pg0 + np) split: chunks c = pg0 / SPLIT_PAGES .. (pg0 + np - 1) / SPLIT_PAGES,
+ * chunk c covering [max(pg0, c S), min(pg0 + np, (c + 1) S)) (S = SPLIT_PAGES). A chunk is full when it covers S pages;
+ * only the first (when pg0 is not a multiple of S) and the last (when the end is not) can be partial. */
+struct UnitSplit {
+    int pg0, np, nch;   /* pages, chunks */
+    int lead;           /* 1: chunk 0 is partial */
+    int nfull, npart;   /* full and partial chunks */
+};
+
+__device__ __forceinline__ UnitSplit unit_split(const AttnArgs &a, int L, int &begin) {
+    UnitSplit u = {0, 0, 0, 0, 0, 0};
+    const int np = decode_pages(a, L, begin, u.pg0);
+    if (np <= 0) return u;
+    const int e = u.pg0 + np;
+    u.np = np;
+    u.nch = (e - 1) / SPLIT_PAGES - u.pg0 / SPLIT_PAGES + 1;
+    u.lead = u.pg0 % SPLIT_PAGES != 0;
+    const int trail = e % SPLIT_PAGES != 0;
+    u.npart = u.nch == 1 ? ((u.lead || trail) ? 1 : 0) : u.lead + trail;
+    u.nfull = u.nch - u.npart;
+    return u;
 }
 
 __device__ __forceinline__ void store_bf16x4(uint16_t *dst, const float *v) {
@@ -487,62 +505,90 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *dst, const float *v) {
     *reinterpret_cast<uint2 *>(dst) = u;
 }
 
-constexpr int MAX_DECODE_BATCH = 4096;  /* sequences per decode launch (the LDS item prefix: 32 KiB) */
+constexpr int MAX_DECODE_BATCH = 4096;  /* sequences per decode launch (the LDS chunk prefixes: 32 KiB) */
+
+/* The last b in [0, B) with cum[b] <= k (cum non-decreasing, cum[0] = 0 <= k). */
+__device__ __forceinline__ int find_sequence(const int *cum, int B, int k) {
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (cum[mid] <= k) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
 
 /*
- * Split-K decode over fixed chunks. The items are (sequence, KV head, chunk) in that order: sequence b contributes
- * Hkv * unit_chunks items, item i of the launch is the i-th of that list. `workers` waves (4 per work-group) take
- * items i = wid, wid + W, ... (the hardware holds every wave at once, so the waves that finish early leave the
- * bandwidth to the rest). Every item starts from a fresh softmax state and streams only its chunk's pages, so what a
- * wave computes for an item does not depend on which wave takes it or what else the launch holds. A unit of one chunk
- * is finished in place (bf16 output); a unit of several leaves one partial per chunk in slot i (its item index) and
- * its chunk-0 item records (first item, chunk count) in meta[u] for decode_combine_kernel, which merges them in chunk
- * order.
+ * Split-K decode over fixed chunks. The work items are a unit's chunks (unit = (sequence, KV head)); every item starts
+ * from a fresh softmax state and streams only its chunk's pages, so what is computed for an item does not depend on
+ * which wave takes it or on what else the launch holds. A unit of one chunk is finished in place (bf16 output); a unit
+ * of several leaves one partial per chunk, in slot cum_all[b] + kvh nch + j (the unit-order index of chunk j), and its
+ * chunk 0 records (first slot, chunk count) in meta[u] for decode_combine_kernel, which merges them in chunk order.
+ *
+ * Schedule: the full chunks (all SPLIT_PAGES long) are numbered first, then the partial ones, each in (sequence, KV
+ * head, chunk) order; item k goes to work-group k % G (G = gridDim.x) and, within it, to wave (k / G) % 4, round
+ * k / (4 G). Equal full chunks land one per work-group before any doubles up, and the short partial chunks fill in
+ * last: every compute unit streams about the same number of pages (a CU's bandwidth, not a wave's, is the limit once
+ * it holds more than one wave), and a wave that finishes early leaves the HBM bandwidth to the others.
  */
 __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
-    extern __shared__ long long sh_cum[];  /* [B + 1]: items of the sequences < b */
+    extern __shared__ int sh_cum[];  /* [2][B + 1]: full, then partial chunks of the sequences < b */
+    int *cf = sh_cum, *cp = sh_cum + a.B + 1;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
-    if (wave == 0) {  /* exclusive prefix over sequences of Hkv * chunks, 64 sequences per step */
-        long long run = 0;
+    if (wave == 0) {  /* exclusive prefixes over sequences of Hkv * (full, partial) chunks, 64 sequences per step */
+        int run_f = 0, run_p = 0;
         for (int b0 = 0; b0 < a.B; b0 += WAVE) {
-            int begin = 0, pg0 = 0;
             const int b = b0 + lane;
-            long long v = 0;
+            int vf = 0, vp = 0;
             if (b < a.B) {
-                const int np = decode_pages(a, a.seq_lens[b], begin, pg0);
-                v = (long long)a.Hkv * unit_chunks(pg0, np);
+                int begin = 0;
+                const UnitSplit u = unit_split(a, a.seq_lens[b], begin);
+                vf = a.Hkv * u.nfull;
+                vp = a.Hkv * u.npart;
             }
 #pragma unroll
             for (int o = 1; o < WAVE; o <<= 1) {
-                const long long t = __shfl_up(v, o, WAVE);
-                if (lane >= o) v += t;
+                const int tf = __shfl_up(vf, o, WAVE), tp = __shfl_up(vp, o, WAVE);
+                if (lane >= o) {
+                    vf += tf;
+                    vp += tp;
+                }
             }
-            if (b < a.B) sh_cum[b + 1] = run + v;
-            run += __shfl(v, WAVE - 1, WAVE);
+            if (b < a.B) {
+                cf[b + 1] = run_f + vf;
+                cp[b + 1] = run_p + vp;
+            }
+            run_f += __shfl(vf, WAVE - 1, WAVE);
+            run_p += __shfl(vp, WAVE - 1, WAVE);
         }
-        if (lane == 0) sh_cum[0] = 0;
+        if (lane == 0) cf[0] = cp[0] = 0;
     }
     __syncthreads();
-    const long long N = sh_cum[a.B];
-    const long long W = min((long long)a.workers, N);
-    const long long wid = (long long)blockIdx.x * WAVES + wave;
-    if (wid >= W) return;  /* the grid rounds the workers up to whole work-groups */
-    for (long long it = wid; it < N; it += W) {
-        int lo_b = 0, hi_b = a.B - 1;  /* the sequence holding item it: the last b with sh_cum[b] <= it */
-        while (lo_b < hi_b) {
-            const int mid = (lo_b + hi_b + 1) >> 1;
-            if (sh_cum[mid] <= it) lo_b = mid; else hi_b = mid - 1;
+    const int NF = cf[a.B], N = NF + cp[a.B];
+    const long long G = gridDim.x;
+    for (long long kk = blockIdx.x + G * wave; kk < N; kk += 4 * G) {
+        const int k = (int)kk;
+        int b, kvh, j, begin = 0;
+        UnitSplit us;
+        if (k < NF) {   /* full chunk: the (k - cf[b])-th of sequence b, in (KV head, chunk) order */
+            b = find_sequence(cf, a.B, k);
+            us = unit_split(a, a.seq_lens[b], begin);
+            const int local = k - cf[b];
+            kvh = local / us.nfull;
+            j = local - kvh * us.nfull + us.lead;
+        } else {        /* partial chunk: the first and / or the last of a unit */
+            const int k2 = k - NF;
+            b = find_sequence(cp, a.B, k2);
+            us = unit_split(a, a.seq_lens[b], begin);
+            const int local = k2 - cp[b];
+            kvh = local / us.npart;
+            const int jp = local - kvh * us.npart;
+            j = (us.nch == 1 || (us.lead && jp == 0)) ? 0 : us.nch - 1;
         }
-        const int b = lo_b;
+        const long long slot = (long long)cf[b] + cp[b] + (long long)kvh * us.nch + j;
         const int L = a.seq_lens[b];
-        int begin = 0, pg0 = 0;
-        const int np = decode_pages(a, L, begin, pg0);
-        const int nch = unit_chunks(pg0, np);
-        const int local = (int)(it - sh_cum[b]);
-        const int kvh = local / nch, j = local - kvh * nch;
-        const int chunk = pg0 / SPLIT_PAGES + j;
-        const int first = max(pg0, chunk * SPLIT_PAGES), last = min(pg0 + np, (chunk + 1) * SPLIT_PAGES);
+        const int chunk = us.pg0 / SPLIT_PAGES + j;
+        const int first = max(us.pg0, chunk * SPLIT_PAGES), last = min(us.pg0 + us.np, (chunk + 1) * SPLIT_PAGES);
         const long long row0 = (long long)b * a.Hq + kvh * a.G;
 
         QOp qb[1];
@@ -559,7 +605,7 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         attend_pages_tab<1>(a, tab, first, kvh, first, last, kb, qb, st, lane);
         st.l[0] = pair_sum32(pair_sum16(st.l[0]));
         const int u = b * a.Hkv + kvh;
-        if (nch == 1) {
+        if (us.nch == 1) {
             if (c < a.G) {
                 uint16_t *dst = a.out + (row0 + c) * HEAD_DIM;
                 const float inv = 1.0f / st.l[0];
@@ -572,20 +618,20 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
                 }
             }
         } else if (c < a.G) {
-            float *po = a.part_o + (it * a.G + c) * HEAD_DIM;
+            float *po = a.part_o + (slot * a.G + c) * HEAD_DIM;
 #pragma unroll
             for (int t = 0; t < 8; t++) {
                 const f32x4 o = st.o[0][t];
                 *reinterpret_cast<float4 *>(po + 16 * t + 4 * g) = float4{st.bad ? NAN : o[0], o[1], o[2], o[3]};
             }
             if (g == 0) {
-                a.part_ml[(it * a.G + c) * 2] = st.bad ? NAN : st.m[0];
-                a.part_ml[(it * a.G + c) * 2 + 1] = st.l[0];
+                a.part_ml[(slot * a.G + c) * 2] = st.bad ? NAN : st.m[0];
+                a.part_ml[(slot * a.G + c) * 2 + 1] = st.l[0];
             }
         }
         if (j == 0 && lane == 0) {  /* the unit's chunk 0: where its partials are, how many */
-            a.meta[2 * u] = (int)it;
-            a.meta[2 * u + 1] = nch;
+            a.meta[2 * u] = (int)slot;
+            a.meta[2 * u + 1] = us.nch;
         }
     }
 }
@@ -950,8 +996,8 @@ int prefill_runs(const uint16_t *q, const uint8_t *k_pages, const uint8_t *v_pag
     return (int)hipGetLastError();
 }
 
-/* Decode workers (waves): by default every wave slot the device holds at the kernel's occupancy, so every item is
- * taken in the first round whenever there are no more items than slots; workers > 0 caps them. */
+/* Decode workers (waves, launched as work-groups of 4): by default every wave slot the device holds at the kernel's
+ * occupancy, at most 4 per item the launch can hold; workers > 0 asks for that many instead. */
 constexpr int MAX_WORKERS = 1 << 20;
 
 static long long max_unit_pages(int max_seq_len, int window) {
@@ -974,7 +1020,7 @@ static int device_wave_slots() {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, 256,
-                                                         (MAX_DECODE_BATCH + 1) * sizeof(long long)) != hipSuccess)
+                                                         2 * (MAX_DECODE_BATCH + 1) * sizeof(int)) != hipSuccess)
             return 2048;
         slots[dev] = max(1, cus * per_cu * WAVES);
     }
@@ -988,8 +1034,9 @@ static size_t workspace_bytes_for(int B, int Hq, int Hkv, long long items) {
     return (size_t)items * G * (HEAD_DIM + 2) * sizeof(float) + (size_t)B * Hkv * 2 * sizeof(int);
 }
 
-static bool decode_shape_ok(int B, int Hq, int Hkv, int max_seq_len) {
-    return B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16 && max_seq_len > 0 && B <= MAX_DECODE_BATCH;
+static bool decode_shape_ok(int B, int Hq, int Hkv, int max_seq_len, int window) {
+    return B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16 && max_seq_len > 0 && B <= MAX_DECODE_BATCH &&
+           item_bound(B, Hkv, max_seq_len, window) < (1LL << 31);
 }
 
 /* The launch itself (arguments checked by the caller); the workspace holds workspace_bytes_for(item_bound). */
@@ -1007,13 +1054,13 @@ static int launch_decode(const void *q, const void *k_pages, const void *v_pages
     a.max_len = max_seq_len;
     a.scale_log2 = sm_scale * LOG2E;
     const long long items = item_bound(B, Hkv, max_seq_len, window);
-    a.workers = (int)min((long long)(workers > 0 ? min(workers, MAX_WORKERS) : device_wave_slots()), items);
+    a.workers = (int)min((long long)(workers > 0 ? min(workers, MAX_WORKERS) : device_wave_slots()), 4 * items);
     a.out = (uint16_t *)out;
     a.part_o = (float *)workspace;
     a.part_ml = a.part_o + (size_t)items * a.G * HEAD_DIM;
     a.meta = (int *)(a.part_ml + (size_t)items * a.G * 2);
     const int grid = (a.workers + WAVES - 1) / WAVES;
-    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(256), (B + 1) * sizeof(long long), stream, a);
+    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(256), 2 * (B + 1) * sizeof(int), stream, a);
     hipLaunchKernelGGL(decode_combine_kernel, dim3(B * Hq), dim3(HEAD_DIM), 0, stream, a);
     return (int)hipGetLastError();
 }
@@ -1023,7 +1070,7 @@ static int launch_decode(const void *q, const void *k_pages, const void *v_pages
 using namespace nc;
 
 extern "C" size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window) {
-    if (!decode_shape_ok(B, Hq, Hkv, max_seq_len)) return 0;
+    if (!decode_shape_ok(B, Hq, Hkv, max_seq_len, window)) return 0;
     return workspace_bytes_for(B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window));
 }
 
@@ -1034,7 +1081,7 @@ extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void
                                   size_t workspace_bytes, void *stream) {
     if (!q || !k_pages || !v_pages || !kv_scale || !block_table || !seq_lens || !out || !workspace)
         return NC_ERR_NULL;
-    if (!decode_shape_ok(B, Hq, Hkv, max_seq_len) || max_pages <= 0 || num_pages <= 0 ||
+    if (!decode_shape_ok(B, Hq, Hkv, max_seq_len, window) || max_pages <= 0 || num_pages <= 0 ||
         (long long)max_seq_len > (long long)max_pages * PAGE || workers < 0)
         return NC_ERR_SHAPE;
     if (workspace_bytes < workspace_bytes_for(B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)))

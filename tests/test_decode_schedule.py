@@ -1,8 +1,9 @@
-"""CPU replay of decode_kernel's work split (nanochat_amd/csrc/attention.hip: the per-work-group item prefix over
-sequences, items (sequence, KV head, chunk) taken round-robin by W waves, chunks cut at multiples of 64 pages,
-partial slot = item index, meta written by each unit's chunk 0) for many shapes: every (unit, page) is attended exactly
-once, by an item whose page range depends on nothing but the unit's own length; partial slots stay inside the
-workspace bound (item_bound); meta names exactly a unit's items, in chunk order."""
+"""CPU replay of decode_kernel's work split (nanochat_amd/csrc/attention.hip: chunks cut at multiples of 64 pages; the
+per-work-group prefixes over sequences of full and partial chunks; full chunks numbered first, then partial ones;
+item k to work-group k % G, wave (k / G) % 4; partial slot = the chunk's unit-order index; meta written by each unit's
+chunk 0) for many shapes: every (unit, page) is attended exactly once, by an item whose page range depends on nothing
+but the unit's own length; partial slots stay inside the workspace bound (item_bound); meta names exactly a unit's
+chunks, in order; work-groups' page loads differ by at most about one chunk."""
 import numpy as np
 import pytest
 
@@ -19,8 +20,15 @@ def unit_pages(L, window, max_len):
     return p // PAGE + 1 - begin // PAGE, begin // PAGE
 
 
-def unit_chunks(pg0, n):
-    return (pg0 + n - 1) // SPLIT - pg0 // SPLIT + 1 if n > 0 else 0
+def unit_split(pg0, n):
+    """(chunks, lead partial, full, partial) of logical pages [pg0, pg0 + n)."""
+    if n <= 0:
+        return 0, 0, 0, 0
+    e = pg0 + n
+    nch = (e - 1) // SPLIT - pg0 // SPLIT + 1
+    lead, trail = int(pg0 % SPLIT != 0), int(e % SPLIT != 0)
+    npart = int(lead or trail) if nch == 1 else lead + trail
+    return nch, lead, nch - npart, npart
 
 
 def item_bound(B, hkv, max_len, window):
@@ -34,36 +42,46 @@ def replay(seq_lens, hkv, workers, window, max_len):
     """Returns {(b, kvh, logical page): (first, last) of the item that attended it} and checks the bookkeeping."""
     B = len(seq_lens)
     units = [unit_pages(L, window, max_len) for L in seq_lens]
-    cum = np.zeros(B + 1, np.int64)
+    split = [unit_split(pg0, n) for n, pg0 in units]
+    cf, cp = np.zeros(B + 1, np.int64), np.zeros(B + 1, np.int64)
     for b in range(B):
-        cum[b + 1] = cum[b] + hkv * unit_chunks(units[b][1], units[b][0])
-    N = int(cum[B])
-    W = min(workers, N)
-    seen, partials, meta = {}, {}, {}
-    grid = -(-workers // WAVES)
-    for wid in range(grid * WAVES):
-        if wid >= W:
-            continue
-        for it in range(wid, N, W):
-            b = max(i for i in range(B) if cum[i] <= it)
-            n, pg0 = units[b]
-            nch = unit_chunks(pg0, n)
-            local = it - cum[b]
-            kvh, j = divmod(local, nch)
-            chunk = pg0 // SPLIT + j
-            first, last = max(pg0, chunk * SPLIT), min(pg0 + n, (chunk + 1) * SPLIT)
-            assert first < last
-            for lp in range(first, last):
-                key = (b, kvh, lp)
-                assert key not in seen, key
-                seen[key] = (first, last)
-            u = b * hkv + kvh
-            if nch > 1:
-                assert 0 <= it < item_bound(B, hkv, max_len, window)
-                assert it not in partials
-                partials[it] = (u, j)
-            if j == 0:
-                meta[u] = (it, nch)
+        cf[b + 1] = cf[b] + hkv * split[b][2]
+        cp[b + 1] = cp[b] + hkv * split[b][3]
+    NF, N = int(cf[B]), int(cf[B] + cp[B])
+    G = -(-min(workers, 4 * item_bound(B, hkv, max_len, window)) // WAVES)
+    seen, partials, meta, load = {}, {}, {}, np.zeros(G, np.int64)
+    for wg in range(G):
+        for wave in range(WAVES):
+            for k in range(wg + G * wave, N, 4 * G):
+                if k < NF:
+                    b = max(i for i in range(B) if cf[i] <= k)
+                    nch, lead, nfull, npart = split[b]
+                    kvh, jf = divmod(k - cf[b], nfull)
+                    j = jf + lead
+                else:
+                    k2 = k - NF
+                    b = max(i for i in range(B) if cp[i] <= k2)
+                    nch, lead, nfull, npart = split[b]
+                    kvh, jp = divmod(k2 - cp[b], npart)
+                    j = 0 if nch == 1 or (lead and jp == 0) else nch - 1
+                n, pg0 = units[b]
+                chunk = pg0 // SPLIT + j
+                first, last = max(pg0, chunk * SPLIT), min(pg0 + n, (chunk + 1) * SPLIT)
+                assert first < last
+                assert (last - first == SPLIT) == (k < NF)
+                load[wg] += last - first
+                for lp in range(first, last):
+                    key = (b, kvh, lp)
+                    assert key not in seen, key
+                    seen[key] = (first, last)
+                slot = int(cf[b] + cp[b]) + kvh * nch + j
+                u = b * hkv + kvh
+                if nch > 1:
+                    assert 0 <= slot < item_bound(B, hkv, max_len, window)
+                    assert slot not in partials
+                    partials[slot] = (u, j)
+                if j == 0:
+                    meta[u] = (slot, nch)
     for b, (n, pg0) in enumerate(units):
         for kvh in range(hkv):
             for lp in range(pg0, pg0 + n):
@@ -73,6 +91,8 @@ def replay(seq_lens, hkv, workers, window, max_len):
                 if count > 1:
                     assert [partials[first + j] for j in range(count)] == [(b * hkv + kvh, j) for j in range(count)]
     assert len(seen) == sum(hkv * n for n, _ in units)
+    if N >= G:   # every work-group has an item: loads differ by at most about one chunk of each kind
+        assert load.max() - load.min() <= 2 * SPLIT * -(-N // (4 * G)) + SPLIT
     return seen
 
 
