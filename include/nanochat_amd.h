@@ -172,6 +172,23 @@ int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, 
                        const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window, float sm_scale,
                        int workers, void *out, void *workspace, size_t workspace_bytes, void *stream);
 
+/* Bytes of the static device workspace of nc_decode_attn_fp8_noalloc (one array per GPU, held until the process
+ * ends). */
+#define NC_DECODE_SCRATCH_BYTES (16u << 20)
+
+/*
+ * No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): nc_decode_attn_fp8 with the same arguments, results and
+ * errors, but its workspace is a static device array of NC_DECODE_SCRATCH_BYTES per GPU instead of the caller's. It
+ * calls no allocating routine. A launch that needs more than that (nc_decode_workspace_bytes) returns
+ * NC_ERR_WORKSPACE. Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * host threads) race and give undefined results; calls ordered on one stream do not.
+ */
+int nc_decode_attn_fp8_noalloc(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
+                               const int32_t *block_table, int max_pages, int num_pages, const int32_t *seq_lens,
+                               int max_seq_len, int B, int Hq, int Hkv, int window, float sm_scale, int workers,
+                               void *out, void *stream);
+
 /*
  * Chunked-prefill attention over the paged fp8 cache (MFMA). Replaces the reference's prefill rows
  * (model/kernels/decode.cu:1041-1051 with enqueue_body's append-then-attend order, 859-863): row t of

@@ -18,6 +18,8 @@
  */
 #include <math.h>
 
+#include <mutex>
+
 #include "nc_device.h"
 #include "nanochat_amd.h"
 #include "nc_internal.h"
@@ -1065,6 +1067,38 @@ static int launch_decode(const void *q, const void *k_pages, const void *v_pages
     return (int)hipGetLastError();
 }
 
+/* The allocation-free entry point's workspace: one static array per GPU, NC_DECODE_SCRATCH_BYTES long, held until the
+ * process ends. In host code `scratch` names a host-side stand-in, not device memory: its device address on the current
+ * GPU is looked up once (hipGetSymbolAddress with that GPU current) and only that address is ever passed to a kernel.
+ * Nothing in it needs clearing: decode_kernel writes every partial and meta entry before decode_combine_kernel reads
+ * it. Calls that overlap on one GPU share the array and race. */
+static __device__ __align__(256) unsigned char scratch[NC_DECODE_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+
+/* The current GPU's address of `scratch` (NULL with *err set when the lookup fails). */
+static void *scratch_on_current_device(int *err) {
+    static std::mutex lock;
+    static void *ptrs[MAX_DEVICES] = {nullptr};
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> guard(lock);
+    if (!ptrs[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+            return nullptr;
+        }
+        ptrs[dev] = p;
+    }
+    return ptrs[dev];
+}
+
 }  // namespace nc
 
 using namespace nc;
@@ -1109,4 +1143,21 @@ extern "C" int nc_prefill_attn_fp8(const void *q, const void *k_pages, const voi
     a.out = (uint16_t *)out;
     launch_prefill(a, T, B, (hipStream_t)stream);
     return (int)hipGetLastError();
+}
+
+extern "C" int nc_decode_attn_fp8_noalloc(const void *q, const void *k_pages, const void *v_pages,
+                                          const float *kv_scale, const int32_t *block_table, int max_pages,
+                                          int num_pages, const int32_t *seq_lens, int max_seq_len, int B, int Hq,
+                                          int Hkv, int window, float sm_scale, int workers, void *out, void *stream) {
+    if (!q || !k_pages || !v_pages || !kv_scale || !block_table || !seq_lens || !out) return NC_ERR_NULL;
+    if (!decode_shape_ok(B, Hq, Hkv, max_seq_len, window) || max_pages <= 0 || num_pages <= 0 ||
+        (long long)max_seq_len > (long long)max_pages * PAGE || workers < 0)
+        return NC_ERR_SHAPE;
+    if (workspace_bytes_for(B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)) > (size_t)NC_DECODE_SCRATCH_BYTES)
+        return NC_ERR_WORKSPACE;
+    int err = 0;
+    void *ws = scratch_on_current_device(&err);
+    if (!ws) return err;
+    return launch_decode(q, k_pages, v_pages, kv_scale, block_table, max_pages, num_pages, seq_lens, max_seq_len, B,
+                         Hq, Hkv, window, sm_scale, workers, out, ws, (hipStream_t)stream);
 }

@@ -14,6 +14,7 @@ DUMMY = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails i
 
 def declared():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"^\s*#.*$", "", text, flags=re.M)
     return set(re.findall(r"\b([A-Za-z_]\w*)\s*\([^;{]*\)\s*;", text))
 
 
@@ -69,6 +70,19 @@ def expected_workspace(B, Hq, Hkv, max_seq, window):
                                   (64, 16, 4, 8193, -1), (64, 16, 4, 8193, 1023), (32, 10, 10, 4097, -1)])
 def test_workspace_sizes(lib, args):
     assert lib.nc_decode_workspace_bytes(*args) == expected_workspace(*args)
+
+
+def test_noalloc_rejects_what_its_scratch_cannot_hold(lib):
+    """nc_decode_attn_fp8_noalloc checks its static workspace's size before any device call."""
+    scratch = 16 << 20
+    assert lib.nc_decode_workspace_bytes(64, 16, 4, 8193, -1) <= scratch
+    big = (256, 16, 4, 32768)
+    assert lib.nc_decode_workspace_bytes(*big, -1) > scratch
+    assert lib.nc_decode_attn_fp8_noalloc(*([DUMMY] * 5), 2048, 4, DUMMY, 32768, *big[:3], -1, 0.1, 0, DUMMY,
+                                          None) == -3
+    assert lib.nc_decode_attn_fp8_noalloc(None, *([DUMMY] * 4), 1, 1, DUMMY, 16, 1, 4, 4, -1, 0.1, 0, DUMMY,
+                                          None) == -1
+    assert lib.nc_decode_attn_fp8_noalloc(*([DUMMY] * 5), 1, 4, DUMMY, 17, 1, 4, 4, -1, 0.1, 0, DUMMY, None) == -2
 
 
 def test_workspace_window_and_bad_sizes(lib):
