@@ -18,8 +18,11 @@ layer only caches K and V (decode.cu:859-863).
 
 Pinned by tests/test_oracle_model.py: with zero o/proj weights the stream is the scaled embedding and the logits
 equal lm_head applied to torch's rms_norm (float64); the MLP equals torch's relu(rms_norm(x) W_fc^T)^2 W_proj^T
-(the rstd identity W (x r) = (W x) r); attention with one cached key returns its value; a prompt prefilled in
-one call equals the same rows fed one at a time; the value-embedding gate at zero weights adds exactly ve.
+(the rstd identity W (x r) = (W x) r); attention with one cached key returns its value; `attend` equals torch's
+scaled_dot_product_attention (float64) under an explicit band mask for windows 0, 1, inside and past the context, and
+through a one-layer model a token just outside a row's window leaves the row's output bit-identical while the one at
+the window's edge changes it; a prompt prefilled in one call equals the same rows fed one at a time; the
+value-embedding gate at zero weights adds exactly ve.
 """
 from dataclasses import dataclass, field
 
@@ -76,6 +79,17 @@ def rms_scale(v, divide=True):
     C = v.shape[-1]
     mean = ss / np.float32(C) if divide else ss * np.float32(1.0 / C)
     return (np.float32(1.0) / np.sqrt((mean + FLT_EPSILON).astype(np.float32))).astype(np.float32)
+
+
+def attend(q, K, V, p, window):
+    """One row's attention (decode.cu:567-675): q (H, 128) at position p over the cached K, V (T, H, 128) at positions
+    [max(p - window, 0), p] (window < 0: from 0), scores scaled by 1/sqrt(128), softmax in float64 -> (H, 128)."""
+    begin = max(p - window, 0) if window >= 0 else 0
+    kk = K[begin:p + 1].astype(np.float64)                    # (m, H, 128)
+    vv = V[begin:p + 1].astype(np.float64)
+    s = np.einsum("hd,mhd->hm", q.astype(np.float64), kk) * HEAD_DIM ** -0.5
+    s = np.exp(s - s.max(axis=-1, keepdims=True))
+    return np.einsum("hm,mhd->hd", s / s.sum(axis=-1, keepdims=True), vv)
 
 
 def matmul_t(x, w):
@@ -155,13 +169,7 @@ class DecoderOracle:
             att = np.zeros((n, H, HEAD_DIM), np.float64)
             for r in range(n):
                 K, V = self.k[int(slots[r])][li], self.v[int(slots[r])][li]
-                p = int(positions[r])
-                begin = max(p - ly.window, 0) if ly.window >= 0 else 0
-                kk = K[begin:p + 1].astype(np.float64)                    # (m, H, 128)
-                vv = V[begin:p + 1].astype(np.float64)
-                s = np.einsum("hd,mhd->hm", q[r].astype(np.float64), kk) * HEAD_DIM ** -0.5
-                s = np.exp(s - s.max(axis=-1, keepdims=True))
-                att[r] = np.einsum("hm,mhd->hd", s / s.sum(axis=-1, keepdims=True), vv)
+                att[r] = attend(q[r], K, V, int(positions[r]), ly.window)
             att = bf16_round(att.astype(np.float32)).reshape(n, C)
             xs = (self._mm(att, ly.o) + xm.astype(np.float64)).astype(np.float32)
             xo = bf16_round(xs)

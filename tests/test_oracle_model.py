@@ -1,5 +1,6 @@
 """Pins of oracle/model.py against closed forms and torch (float64), on tiny random models."""
 import numpy as np
+import pytest
 import torch
 import torch.nn.functional as F
 
@@ -120,3 +121,51 @@ def test_zero_gate_adds_the_value_embedding():
     e = ly.ve[4].reshape(w.H, 128)
     assert np.abs(v_ve - (v_plain + e)).max() <= 2 ** -3 * np.abs(v_plain + e).max()
     assert not np.allclose(v_ve, v_plain)
+
+
+def sdpa_band(q, K, V, p, window):
+    """torch scaled_dot_product_attention (float64) of one query row at position p over keys 0..p with an explicit
+    boolean mask: key j is visible iff p - window <= j (window < 0: every key)."""
+    qt = torch.tensor(q, dtype=torch.float64).unsqueeze(1)                       # (H, 1, 128)
+    kt = torch.tensor(K[:p + 1], dtype=torch.float64).permute(1, 0, 2).contiguous()   # (H, p + 1, 128)
+    vt = torch.tensor(V[:p + 1], dtype=torch.float64).permute(1, 0, 2).contiguous()
+    j = torch.arange(p + 1)
+    mask = (j >= p - window) if window >= 0 else torch.ones(p + 1, dtype=torch.bool)
+    return F.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask.view(1, 1, -1)).squeeze(1).numpy()
+
+
+def test_attend_is_sdpa_with_a_band_mask():
+    rng = np.random.default_rng(7)
+    T, H = 90, 3
+    K = rng.standard_normal((T, H, 128)).astype(np.float32)
+    V = rng.standard_normal((T, H, 128)).astype(np.float32)
+    for p in (0, 1, 17, 63, 89):
+        q = (rng.standard_normal((H, 128)) * 2).astype(np.float32)
+        for window in (-1, 0, 1, 5, 16, p, p + 40):
+            got = om.attend(q, K, V, p, window)
+            want = sdpa_band(q, K, V, p, window)
+            assert np.abs(got - want).max() <= 1e-12, (p, window)
+    # window 0: only the row's own key, so the output is its value
+    assert np.abs(om.attend(q, K, V, 40, 0) - V[40]).max() <= 1e-12
+
+
+@pytest.mark.parametrize("window", [0, 3, 10])
+def test_window_edge_through_the_model(window):
+    """One layer, window w: row p's output does not change (bitwise) when the token at p - w - 1 changes, and does when
+    the token at p - w changes (K, V of a position depend only on its own token in layer 0)."""
+    w = tiny(L=1, window=window, T=64)
+    rng = np.random.default_rng(window)
+    p = 20
+    base = rng.integers(1, 512, p + 1)
+
+    def row_p(tokens):
+        orc = om.DecoderOracle(w, 64)
+        return orc.body(tokens, np.arange(p + 1), np.zeros(p + 1, int))[p]
+
+    ref = row_p(base)
+    outside = base.copy()
+    outside[p - window - 1] = (base[p - window - 1] + 101) % 511 + 1
+    assert np.array_equal(row_p(outside), ref)
+    edge = base.copy()
+    edge[p - window] = (base[p - window] + 101) % 511 + 1
+    assert not np.array_equal(row_p(edge), ref)

@@ -4,6 +4,7 @@ force within one bf16 ulp; plus the product's torch rotary tables against the or
 import math
 
 import numpy as np
+import pytest
 import torch
 
 from oracle.numerics import bf16_round
@@ -108,3 +109,38 @@ def test_backward_equals_torch_autograd():
     dx, dg = qk_norm_rope_backward(x, g, c, s, dy)
     assert np.abs(dx - xt.grad.numpy()).max() <= 1e-12 * max(1.0, np.abs(dx).max())
     assert np.abs(dg - gt.grad.numpy()).max() <= 1e-12 * max(1.0, np.abs(dg).max())
+
+
+@pytest.mark.parametrize("theta,column,omega", [
+    (1e4, 32, 0.01), (1e4, 16, 0.1), (1e4, 48, 0.001),
+    (1e6, 16, 10 ** -1.5), (1e6, 32, 1e-3), (1e6, 48, 10 ** -4.5), (1e6, 8, 10 ** -0.75)])
+def test_interior_columns_have_the_closed_form_frequency(theta, column, omega):
+    """Column i's angle is t theta^(-2i/128): for these (theta, i) the frequency is a power of ten written out here
+    (theta^(-1/2) = 0.01 for theta = 1e4, i = 32, ...), so an exponent of i/D or (2i+1)/D, a swapped sin/cos or a
+    wrong theta fails. The table is the fp32 rounding of the float64 cos / sin: within one fp32 ulp of math.cos / sin
+    (a different libm), and equal almost everywhere."""
+    cos, sin = rotary_tables(8193, theta)
+    t = np.arange(8193)
+    want_c = np.array([math.cos(omega * x) for x in t], np.float32)
+    want_s = np.array([math.sin(omega * x) for x in t], np.float32)
+    for got, want in ((cos[:, column], want_c), (sin[:, column], want_s)):
+        ulp = np.spacing(np.abs(want)).astype(np.float64)
+        assert np.all(np.abs(got.astype(np.float64) - want) <= ulp), (theta, column)
+        assert (got != want).mean() < 1e-3
+
+
+@pytest.mark.parametrize("theta", [1e4, 1e6])
+def test_column_frequencies_fall_by_theta_to_the_minus_one_64th(theta):
+    """The frequencies recovered from the table (atan2 of sin / cos at a position where the angle is below pi) form
+    the geometric series omega_i = theta^(-i/64): omega_0 = 1 and each column's over the previous is theta^(-1/64)."""
+    cos, sin = rotary_tables(8193, theta)
+    omegas = []
+    for i in range(64):
+        t = 1
+        while t * 2 < 8193 and np.arctan2(sin[t * 2, i], cos[t * 2, i]) > 0 and t * 2 * np.arctan2(sin[1, i], cos[1, i]) < 3.0:
+            t *= 2
+        omegas.append(np.arctan2(float(sin[t, i]), float(cos[t, i])) / t)
+    omegas = np.array(omegas)
+    assert abs(omegas[0] - 1.0) < 1e-6
+    ratio = theta ** (-1.0 / 64)
+    assert np.allclose(omegas[1:] / omegas[:-1], ratio, rtol=2e-4), (omegas[1:] / omegas[:-1])[:4]
