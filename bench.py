@@ -375,30 +375,29 @@ def bench_model(args, w, cpu_slots=16):
     """Config 5 end to end through the decoder runtime."""
     import torch
 
-    from nanochat_amd.decoder import PagedDecoder, Request
+    from nanochat_amd.decoder import DecoderRuntime
     from nanochat_amd.workloads import model_tensors, prompt_tokens
 
     dev = torch.device("cuda:0")
     model = model_tensors(w.layers, w.hidden, w.ffn, w.vocab, w.max_length, seed=0, std=w.std, theta=w.theta,
                           softcap=w.softcap, device=dev, generator_device="cuda")
     ids = prompt_tokens(w.batch, w.prompt, w.vocab, seed=0).tolist()
-    dec = PagedDecoder(model, bos_token_id=0, max_length=w.max_length, prompt_store=0, max_slots=w.batch)
+    dec = DecoderRuntime(model, bos_token_id=0, max_length=w.max_length, prompt_store=0, max_slots=w.batch)
     try:
         if dec.batch < w.batch:
             raise RuntimeError(f"only {dec.batch} slots fit, the workload needs {w.batch}")
-        # warm-up: a short prompt per slot and a few steps (rocBLAS loads its kernels on first use)
+        # warm-up: a short prompt per slot and a few steps (the GEMM libraries load their kernels on first use)
         for b in range(w.batch):
-            dec.start(b, b, Request(input_ids=ids[b][:32], max_new_tokens=1))
+            dec.place(b, ids[b][:32])
         dec.prefill()
-        dec.flags[0, :w.batch] = True
-        dec.set_active()
+        dec.activate(range(w.batch))
         for _ in range(max(1, min(args.warmup, 5))):
             dec.step()
         torch.cuda.synchronize()
         # prefill: every prompt but its last token (the first step's input), dec_prefill_rows rows a call
         t0 = time.perf_counter()
         for b in range(w.batch):
-            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=w.steps))
+            dec.place(b, ids[b])
         dec.prefill()
         dec.stream.synchronize()
         prefill_s = time.perf_counter() - t0

@@ -1,20 +1,23 @@
-"""Batched decoding by libnanochat_decode.so: the host side of the reference's NativeDecoder
-(inference/decoder.py:122-324) over the dec_* ABI (include/nanochat_decode.h), with the fp8 paged KV cache.
+"""Host driver of libnanochat_decode.so (include/nanochat_decode.h) for this repository's tests, smoke check and
+benchmark: the fp8 paged-cache decoder behind the reference's dec_* ABI (model/kernels/decode.cu:904-1131).
 
-The call sequence is the reference's: dec_create from the weights' device addresses; per request dec_load_prompt
-(a stored prompt) or a queued prefill, then dec_set_prompt; per step dec_launch_body, the masks of the constrained
-slots (dec_masks, dec_set_active), dec_launch_head, dec_tokens; a lazy BOS that the constraint rejects gives way to
-the step's alternative (dec_take_alt).
+The reference's own host class, NativeDecoder (inference/decoder.py:123-324), binds the same library unchanged through
+`hip_library("decode")`; this module is not a copy of it. It has two layers:
 
-What differs from the reference's host side: the model is a `ModelTensors` (the decoder's inputs themselves, where
-the reference takes a CausalLM and copies its tensors), and a constraint is any object with `mask()` (None, or the
-allowed tokens as uint32 words, bit t % 32 of word t // 32) and `push(token)`, optionally `ends()` deciding a lazy
-BOS; the tokenizer-bound Reemit and syntax constraints of the reference stay with their tokenizer.
+- `DecoderRuntime` holds one decoder handle and exposes the ABI with no scheduling policy: put a prompt in a slot
+  (shared from the prompt store when stored, else queued), run the queued prefill, choose the active and masked slots,
+  run a step, read the choices; plus the test hooks (logits, cache rows, block tables).
+- `serve` is a minimal scheduler over it: requests fill free slots in order, every step decodes all live slots, and a
+  request ends on its token budget, its stopping test or BOS.
+
+The model is a `ModelTensors` (the decoder's inputs themselves). A constraint is any object with `mask()` (None, or the
+allowed tokens as uint32 words, bit t % 32 of word t // 32) and `push(token)`, optionally `ends()` deciding whether a
+chosen BOS may end the request (if not, the step's best other token is taken instead).
 """
-import ctypes
 import time
 import weakref
-from collections.abc import Callable, Iterable, Iterator
+from collections import deque
+from collections.abc import Callable, Iterable, Iterator, Sequence
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -24,7 +27,7 @@ from .config import HEAD_DIM, PAGE_SIZE
 from .native import hip_library
 
 GLOBAL_PTRS, LAYER_PTRS = 4, 8   # dec_create's pointer layout (decode.cu:950-953)
-MASK_BITS = 64                   # slots per word of dec_set_active's masks
+SLOTS_PER_WORD = 64              # dec_set_active's slot masks are uint64 words
 
 
 @dataclass
@@ -93,10 +96,10 @@ class ModelTensors:
 
 @dataclass(frozen=True, kw_only=True)
 class Request:
-    """A continuation of input_ids (BOS and at least one more token) by at most max_new_tokens (>= 1) tokens, within
-    the constraint's masks, until stopping_criteria holds (reference decoder.py:28-40). temperature 0: argmax (ties
-    to the lowest id); > 0: a softmax(logits / temperature) sample drawn from (seed, generated position) alone;
-    top_p < 1: nucleus sampling."""
+    """What to decode (the fields of the reference's Request, inference/decoder.py:28-40). input_ids starts with BOS
+    and holds at least one more token; at most max_new_tokens (>= 1) tokens follow. temperature 0 picks the largest
+    logit (lowest id on ties); T > 0 samples softmax(capped logits / T) with noise drawn from (seed, generated
+    position), within the top_p nucleus when top_p < 1. stopping_criteria sees the tokens generated so far."""
     input_ids: list[int]
     max_new_tokens: int
     stopping_criteria: Callable[[list[int]], bool] = lambda out: False
@@ -106,217 +109,210 @@ class Request:
     seed: int = 0
 
 
-@dataclass
-class Slot:
-    """A request in a slot: index, request, start and first-token host times, generated tokens."""
-    index: int
-    request: Request
-    start: float
-    first: float | None = None
-    out: list[int] = field(default_factory=list)
+class DecoderRuntime:
+    """One libnanochat_decode.so decoder with up to `max_slots` slots (fewer when device memory runs short).
 
-
-class PagedDecoder:
-    """Decoding of up to `batch` slots by libnanochat_decode.so, slots sized by free device memory (at most
-    max_slots). max_length: a slot's cache positions; prompt_store: positions of the device prompt store."""
+    max_length: cache positions per slot; prompt_store: positions of the device prompt store, where every prefilled
+    prompt is kept (page-aligned, never evicted) so that a later slot given the same prompt shares its pages."""
 
     @torch.no_grad()
-    def __init__(self, model: ModelTensors, *, bos_token_id: int, max_length: int, prompt_store: int,
+    def __init__(self, model: ModelTensors, *, bos_token_id: int, max_length: int, prompt_store: int = 0,
                  max_slots: int | None = None):
         model.check()
         if max_length > model.cos.size(0):
             raise ValueError(f"max_length {max_length} exceeds the rotary table's {model.cos.size(0)} positions")
-        torch.cuda.empty_cache()
-        self.lib = lib = hip_library("decode")
-        self.model = model  # the decoder reads these tensors in place for its whole life
-        L, C = len(model.layers), model.hidden
-        self.vocab, self.max_length, self.bos = model.vocab, max_length, bos_token_id
-        ptrs = [model.wte.data_ptr(), model.cos.data_ptr(), model.sin.data_ptr(), model.lm_head.data_ptr()]
+        self.lib = hip_library("decode")
+        self.model = model   # the handle reads these tensors in place until it is destroyed
+        self.vocab, self.max_length, self.bos, self.store_size = model.vocab, max_length, bos_token_id, prompt_store
+        ptrs = [model.wte, model.cos, model.sin, model.lm_head]
         for ly in model.layers:
-            ptrs += [ly.qkv.data_ptr(), ly.o.data_ptr(), ly.fc.data_ptr(), ly.proj.data_ptr(),
-                     0 if ly.ve is None else ly.ve.data_ptr(), 0 if ly.ve_gate is None else ly.ve_gate.data_ptr(),
-                     ly.q_norm.data_ptr(), ly.k_norm.data_ptr()]
-        ptrs = np.array(ptrs, dtype=np.uint64)
-        scal = np.array([v for pair in zip(model.resid_lambdas, model.x0_lambdas) for v in pair] + [model.softcap],
-                        dtype=np.float32)
-        cfg = np.array([L, C, model.ffn, model.vocab, max_length, prompt_store, bos_token_id], dtype=np.int32)
-        window = np.array(model.windows, dtype=np.int32)
+            ptrs += [ly.qkv, ly.o, ly.fc, ly.proj, ly.ve, ly.ve_gate, ly.q_norm, ly.k_norm]
+        self._ptrs = np.array([0 if t is None else t.data_ptr() for t in ptrs], dtype=np.uint64)
+        lambdas = [x for pair in zip(model.resid_lambdas, model.x0_lambdas) for x in pair]
+        self._scal = np.array(lambdas + [model.softcap], dtype=np.float32)
+        self._cfg = np.array([len(model.layers), model.hidden, model.ffn, model.vocab, max_length, prompt_store,
+                              bos_token_id], dtype=np.int32)
+        self._window = np.array(model.windows, dtype=np.int32)
+        torch.cuda.empty_cache()
         self.stream = torch.cuda.Stream(model.wte.device)
-        torch.cuda.synchronize()  # the weights were written on the current stream; the decoder runs on its own
-        if max_slots is None:
-            self.handle = lib.dec_create(cfg.ctypes.data, ptrs.ctypes.data, scal.ctypes.data, window.ctypes.data,
-                                         self.stream.cuda_stream)
-        else:
-            self.handle = lib.dec_create_slots(cfg.ctypes.data, ptrs.ctypes.data, scal.ctypes.data,
-                                               window.ctypes.data, self.stream.cuda_stream, max_slots)
-        self._finalizer = weakref.finalize(self, lib.dec_destroy, self.handle)
-        self.batch = lib.dec_batch(self.handle)
-        self.tokens = np.zeros(2 * self.batch, dtype=np.int32)
-        self.masks = np.ctypeslib.as_array(lib.dec_masks(self.handle), shape=(self.batch, self.vocab // 32))
-        self.prefill_rows = lib.dec_prefill_rows(self.handle)
-        self.store = prompt_store
-        self.stored: dict[tuple[int, ...], int] = {}
-        self.used = 0
-        self.pending: list[tuple[int, list[int]]] = []
-        self.timings: dict[int, tuple[float, float, float]] = {}
-        word_slots = -(-self.batch // MASK_BITS) * MASK_BITS
-        self.flags = np.zeros((2, word_slots), dtype=bool)   # row 0: active slots, row 1: masked slots
+        torch.cuda.synchronize()   # the weights were written on another stream
+        args = (self._cfg.ctypes.data, self._ptrs.ctypes.data, self._scal.ctypes.data, self._window.ctypes.data,
+                self.stream.cuda_stream)
+        self.handle = (self.lib.dec_create(*args) if max_slots is None else
+                       self.lib.dec_create_slots(*args, max_slots))
+        self._release = weakref.finalize(self, self.lib.dec_destroy, self.handle)
+        self.batch = self.lib.dec_batch(self.handle)
+        self.rows_per_prefill = self.lib.dec_prefill_rows(self.handle)
+        self.masks = np.ctypeslib.as_array(self.lib.dec_masks(self.handle), shape=(self.batch, self.vocab // 32))
+        self._out = np.zeros(2 * self.batch, dtype=np.int32)    # dec_tokens: choices, then alternatives
+        self.choices, self.alternatives = self._out[:self.batch], self._out[self.batch:]
+        self.stored: dict[tuple[int, ...], int] = {}            # prompt -> its first store position
+        self.store_used = 0
+        self.queued: list[tuple[int, list[int]]] = []           # (slot, prompt) awaiting prefill
 
     def close(self) -> None:
-        """Free the decoder's device and pinned memory now (otherwise when it is collected)."""
-        self._finalizer()
+        """Destroy the decoder now (otherwise when the object is collected)."""
+        self._release()
 
-    # ---- the ABI, one call each
-    def set_active(self) -> None:
-        words = np.packbits(self.flags, axis=1, bitorder="little").view("<u8")
-        self.lib.dec_set_active(self.handle, np.ascontiguousarray(words).ctypes.data)
+    # --- prompts
+    def place(self, slot: int, prompt: Sequence[int], *, temperature: float = 0.0, top_p: float = 1.0,
+              seed: int = 0) -> bool:
+        """Slot `slot` continues `prompt` (BOS first), decoding from its last token. The positions before that come
+        from the prompt store when the same prompt is stored (returns True), else they are queued for `prefill`."""
+        prompt = [int(t) for t in prompt]
+        n = len(prompt) - 1
+        if not 0 <= slot < self.batch:
+            raise ValueError(f"slot {slot} outside [0, {self.batch})")
+        if n < 1 or n >= self.max_length:
+            raise ValueError(f"a prompt of {n + 1} tokens does not fit: BOS, at least one more, under max_length "
+                             f"{self.max_length}")
+        if min(prompt) < 0 or max(prompt) >= self.vocab:
+            raise ValueError(f"prompt token outside [0, {self.vocab})")
+        at = self.stored.get(tuple(prompt))
+        if at is not None:
+            self.lib.dec_load_prompt(self.handle, slot, 0, at, n)
+        else:
+            self.queued.append((slot, prompt))
+        self.lib.dec_set_prompt(self.handle, slot, prompt[-1], n, temperature, top_p, seed)
+        return at is not None
+
+    def prefill(self) -> int:
+        """Run every queued prompt (all but its last token) through the decoder, rows_per_prefill rows a call, then
+        keep each in the store; returns the rows run."""
+        if not self.queued:
+            return 0
+        table = np.concatenate([np.stack([np.array(p[:-1]), np.arange(len(p) - 1), np.full(len(p) - 1, slot)])
+                                for slot, p in self.queued], axis=1).astype(np.int32)
+        for lo in range(0, table.shape[1], self.rows_per_prefill):
+            part = np.ascontiguousarray(table[:, lo:lo + self.rows_per_prefill])
+            self.lib.dec_prefill(self.handle, part.shape[1], part.ctypes.data)
+        for slot, p in self.queued:
+            self._keep(slot, p)
+        self.queued = []
+        return table.shape[1]
+
+    def _keep(self, slot: int, prompt: list[int]) -> None:
+        """Copy the slot's prompt rows into the store at the next page boundary, if new and room is left."""
+        key, n = tuple(prompt), len(prompt) - 1
+        if key in self.stored or self.store_used + n > self.store_size:
+            return
+        self.lib.dec_save_prompt(self.handle, slot, 0, self.store_used, n)
+        self.stored[key] = self.store_used
+        self.store_used += -(-n // PAGE_SIZE) * PAGE_SIZE
+
+    # --- steps
+    def activate(self, slots: Iterable[int], masked: Iterable[int] = ()) -> None:
+        """The slots the next steps decode, and those whose choice is limited to their row of `masks`."""
+        words = -(-self.batch // SLOTS_PER_WORD)
+        bits = np.zeros((2, words * SLOTS_PER_WORD), dtype=bool)
+        for row, chosen in enumerate((slots, masked)):
+            for b in chosen:
+                if not 0 <= b < self.batch:
+                    raise ValueError(f"slot {b} outside [0, {self.batch})")
+                bits[row, b] = True
+        packed = np.ascontiguousarray(np.packbits(bits, axis=1, bitorder="little").view("<u8"))
+        self.lib.dec_set_active(self.handle, packed.ctypes.data)
 
     def step(self) -> np.ndarray:
-        """One step over the active slots (no constraints): the chosen tokens [B]."""
+        """One decode step of the active slots; returns the choices [batch] (alternatives in `alternatives`)."""
         self.lib.dec_launch_body(self.handle)
         self.lib.dec_launch_head(self.handle)
-        self.lib.dec_tokens(self.handle, self.tokens.ctypes.data)
-        return self.tokens[:self.batch]
+        self.lib.dec_tokens(self.handle, self._out.ctypes.data)
+        return self.choices
 
+    def take_alternative(self, slot: int) -> None:
+        """Slot's next input becomes its alternative (its best choice other than BOS) instead of its choice."""
+        self.lib.dec_take_alt(self.handle, slot)
+
+    # --- test hooks
     def logits(self, rows: int) -> np.ndarray:
-        """Test hook: the last head's fp32 logits of slots [0, rows)."""
+        """The last step's fp32 logits of slots [0, rows)."""
         out = np.empty((rows, self.vocab), dtype=np.float32)
         self.lib.dec_debug_logits(self.handle, out.ctypes.data, rows)
         return out
 
-    def cache_rows(self, layer: int, b: int, at: int, n: int):
-        """Test hook: slot b's (b = -1: the store's) cached rows at [at, at + n) of a layer: K codes, V codes
-        [n][H][128] uint8 and scales [n][H][2] fp32."""
+    def cache_rows(self, layer: int, slot: int, at: int, n: int):
+        """K codes, V codes [n][H][128] uint8 and scales [n][H][2] fp32 of positions [at, at + n) of a slot (-1: the
+        prompt store) in one layer."""
         H = self.model.hidden // HEAD_DIM
         k = np.empty((n, H, HEAD_DIM), np.uint8)
         v = np.empty_like(k)
         s = np.empty((n, H, 2), np.float32)
-        self.lib.dec_debug_cache(self.handle, layer, b, at, n, k.ctypes.data, v.ctypes.data, s.ctypes.data)
+        self.lib.dec_debug_cache(self.handle, layer, slot, at, n, k.ctypes.data, v.ctypes.data, s.ctypes.data)
         return k, v, s
 
-    def table(self, b: int) -> np.ndarray:
-        """Test hook: slot b's block-table row (own page b * pages + e, or batch * pages + i: store page i)."""
+    def table(self, slot: int) -> np.ndarray:
+        """The slot's block-table row: entry e is the slot's own page slot * pages + e, or batch * pages + i for page
+        i of the prompt store (shared)."""
         out = np.empty(-(-self.max_length // PAGE_SIZE), np.int32)
-        self.lib.dec_debug_table(self.handle, b, out.ctypes.data)
+        self.lib.dec_debug_table(self.handle, slot, out.ctypes.data)
         return out
 
-    # ---- requests (the reference's NativeDecoder.start / prefill / save / generate)
-    def start(self, b: int, index: int, request: Request) -> Slot:
-        n = len(request.input_ids) - 1
-        if n < 1:
-            raise ValueError(f"request {index}: input_ids needs BOS and at least one more token")
-        if request.max_new_tokens < 1:
-            raise ValueError(f"request {index}: max_new_tokens {request.max_new_tokens} < 1")
-        if n + request.max_new_tokens > self.max_length:
-            raise ValueError(f"request {index}: {n + 1} prompt and {request.max_new_tokens} new tokens need "
-                             f"{n + request.max_new_tokens} positions, max_length {self.max_length}")
-        if any(not 0 <= t < self.vocab for t in request.input_ids):
-            raise ValueError(f"request {index}: token outside [0, {self.vocab})")
-        at = self.stored.get(tuple(request.input_ids))
-        if at is None:
-            self.pending.append((b, request.input_ids))
-        else:
-            self.lib.dec_load_prompt(self.handle, b, 0, at, n)
-        self.lib.dec_set_prompt(self.handle, b, request.input_ids[-1], n, request.temperature, request.top_p,
-                                request.seed)
-        return Slot(index, request, start=time.perf_counter())
 
-    def prefill(self) -> None:
-        """The pending prompts but their last tokens, prefill_rows rows a call, then each kept in the store."""
-        if not self.pending:
-            return
-        rows = np.concatenate([np.array([ids[:-1], range(len(ids) - 1), [b] * (len(ids) - 1)], dtype=np.int32)
-                               for b, ids in self.pending], axis=1)
-        for i in range(0, rows.shape[1], self.prefill_rows):
-            chunk = np.ascontiguousarray(rows[:, i:i + self.prefill_rows])
-            self.lib.dec_prefill(self.handle, chunk.shape[1], chunk.ctypes.data)
-        for b, ids in self.pending:
-            self.save(b, ids)
-        self.pending = []
+@dataclass
+class _Live:
+    index: int
+    request: Request
+    started: float
+    first: float | None = None
+    out: list[int] = field(default_factory=list)
 
-    def save(self, b: int, input_ids: list[int]) -> None:
-        """Keep slot b's prompt K and V in the store's next free positions, unless stored or full (never evicted).
-        Each prompt starts on a page boundary of the store, so dec_load_prompt shares its whole pages with the slots
-        that load it instead of copying them (the reference packs prompts back to back, decoder.py:226-232)."""
-        key, n = tuple(input_ids), len(input_ids) - 1
-        if key in self.stored or self.used + n > self.store:
-            return
-        self.lib.dec_save_prompt(self.handle, b, 0, self.used, n)
-        self.stored[key] = self.used
-        self.used = -(-(self.used + n) // PAGE_SIZE) * PAGE_SIZE
 
-    @torch.no_grad()
-    def generate(self, requests: Iterable[Request]) -> Iterator[tuple[int, list[int]]]:
-        """Continuations of requests, consumed lazily; yields (request index, generated ids) in completion order.
-        Raises ValueError when a constraint allows no token. Sets timings {index: (start, first, end)}."""
-        lib, B = self.lib, self.batch
-        self.timings = {}
-        queue, slots = enumerate(requests), [None] * B
-        self.flags[:] = False
-        stopping: list[int] = []
+@torch.no_grad()
+def serve(rt: DecoderRuntime, requests: Iterable[Request],
+          timings: dict | None = None) -> Iterator[tuple[int, list[int]]]:
+    """Decode `requests` on rt's slots; yields (request index, generated tokens) as requests end.
 
-        def fill(b: int) -> None:
-            for i, request in queue:
-                slots[b] = self.start(b, i, request)
-                self.flags[0, b] = True
-                return
-            slots[b] = None
-            self.flags[0, b] = False
-
-        for b in range(B):
-            fill(b)
-        self.set_active()
-        while self.flags[0].any():
-            self.prefill()
-            active = [b for b, s in enumerate(slots) if s is not None]
-            lib.dec_launch_body(self.handle)
-            finished = sorted(b for b in stopping if slots[b].request.stopping_criteria(slots[b].out))
-            stopping = []
-            for b in active:
-                if b in finished or slots[b].request.constraint is None:
-                    continue
-                mask = slots[b].request.constraint.mask()
-                if mask is None:
-                    continue
-                self.masks[b] = mask
-                self.flags[1, b] = True
-                if not self.masks[b].any():
-                    raise ValueError(f"request {slots[b].index}: its constraint allows no token at position "
-                                     f"{len(slots[b].out)}")
-            self.set_active()
-            self.flags[1] = False
-            lib.dec_launch_head(self.handle)
-            lib.dec_tokens(self.handle, self.tokens.ctypes.data)
-            for b in active:  # a lazy BOS the constraint rejects gives way to the alternative (decoder.py:234-248)
-                c = slots[b].request.constraint
-                if b in finished or self.tokens[b] != self.bos or c is None or not hasattr(c, "ends") or c.ends():
-                    continue
-                if self.tokens[B + b] < 0:
-                    raise ValueError(f"request {slots[b].index}: its constraint allows no token at position "
-                                     f"{len(slots[b].out)}")
-                self.tokens[b] = self.tokens[B + b]
-                lib.dec_take_alt(self.handle, b)
-            now = time.perf_counter()
-            for b, s in enumerate(slots):
-                if s is None or b in finished:
-                    continue
-                token = int(self.tokens[b])
-                if token == self.bos:
-                    finished.append(b)
-                    continue
-                if not s.out:
-                    s.first = now
-                s.out.append(token)
-                if s.request.constraint is not None:
-                    s.request.constraint.push(token)
-                if len(s.out) == s.request.max_new_tokens:
-                    finished.append(b)
-                else:
-                    stopping.append(b)
-            if finished:
-                for b in finished:
-                    done = slots[b]
-                    fill(b)
-                    self.timings[done.index] = (done.start, now if done.first is None else done.first, now)
-                    yield done.index, done.out
-                self.set_active()
+    Requests take free slots in order. Each step: the new prompts are prefilled, the constrained slots' masks are
+    written, every live slot decodes one token. A request ends after max_new_tokens tokens, when its stopping test
+    holds, or on BOS (not included). A BOS its constraint does not accept (`ends()` false) is replaced by the step's
+    alternative. Raises ValueError when a constraint leaves no token. timings, when given, receives
+    {index: (start, first token, end)} in time.perf_counter() seconds."""
+    todo = deque(enumerate(requests))
+    live: dict[int, _Live] = {}
+    while todo or live:
+        for slot in range(rt.batch):
+            if slot not in live and todo:
+                index, req = todo.popleft()
+                if req.max_new_tokens < 1 or len(req.input_ids) - 1 + req.max_new_tokens > rt.max_length:
+                    raise ValueError(f"request {index}: {len(req.input_ids)} prompt tokens and {req.max_new_tokens} "
+                                     f"new ones do not fit max_length {rt.max_length}")
+                rt.place(slot, req.input_ids, temperature=req.temperature, top_p=req.top_p, seed=req.seed)
+                live[slot] = _Live(index, req, time.perf_counter())
+        rt.prefill()
+        masked = []
+        for slot, run in live.items():
+            mask = run.request.constraint.mask() if run.request.constraint is not None else None
+            if mask is None:
+                continue
+            if not np.any(mask):
+                raise ValueError(f"request {run.index}: no token allowed after {len(run.out)} tokens")
+            rt.masks[slot] = mask
+            masked.append(slot)
+        rt.activate(live, masked)
+        choices = rt.step()
+        now = time.perf_counter()
+        ended = []
+        for slot, run in live.items():
+            token = int(choices[slot])
+            c = run.request.constraint
+            if token == rt.bos and c is not None and hasattr(c, "ends") and not c.ends():
+                token = int(rt.alternatives[slot])
+                if token < 0:
+                    raise ValueError(f"request {run.index}: no token allowed after {len(run.out)} tokens")
+                rt.take_alternative(slot)
+            if token == rt.bos:
+                ended.append(slot)
+                continue
+            if run.first is None:
+                run.first = now
+            run.out.append(token)
+            if c is not None:
+                c.push(token)
+            if len(run.out) >= run.request.max_new_tokens or run.request.stopping_criteria(run.out):
+                ended.append(slot)
+        for slot in ended:
+            run = live.pop(slot)
+            if timings is not None:
+                timings[run.index] = (run.started, now if run.first is None else run.first, now)
+            yield run.index, run.out

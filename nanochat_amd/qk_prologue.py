@@ -14,7 +14,7 @@ from .native import NativeError, hip_library, pointer, stream
 
 def qk_forward(q: Tensor, k: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, cos: Tensor,
                sin: Tensor) -> tuple[Tensor, Tensor]:
-    """(normed and rotated q, k), contiguous."""
+    """New contiguous tensors holding q and k after the norm, the gain and the rotation (same shape, bf16)."""
     B, T, H = q.shape[:3]
     for name, t in (("q", q), ("k", k)):
         if not t.is_cuda or t.dtype != torch.bfloat16:
@@ -38,8 +38,9 @@ def qk_forward(q: Tensor, k: Tensor, q_norm_weight: Tensor, k_norm_weight: Tenso
 
 def qk_backward(q: Tensor, k: Tensor, q_norm_weight: Tensor, k_norm_weight: Tensor, dq_out: Tensor, dk_out: Tensor,
                 cos: Tensor, sin: Tensor, dq: Tensor, dk: Tensor) -> tuple[Tensor, Tensor]:
-    """Write q's and k's gradients into dq, dk (views shaped and strided like q, k); return the gains' gradients,
-    summed in a fixed order (bitwise reproducible). dq_out, dk_out: the forward outputs' gradients, contiguous."""
+    """Backward of qk_forward. dq_out, dk_out (contiguous) are the gradients of its two outputs; the inputs' gradients
+    are stored into dq, dk (bf16 views with q's and k's shape and strides), and the two gain gradients (fp32, HEAD_DIM)
+    are returned. The gain gradients are reduced over rows in one fixed order, so repeated calls agree bit for bit."""
     B, T, H, D = q.shape
     for name, t in (("q", q), ("k", k), ("dq", dq), ("dk", dk)):
         if not t.is_cuda or t.dtype != torch.bfloat16:

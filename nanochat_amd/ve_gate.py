@@ -1,7 +1,11 @@
-"""Value-embedding gate and mix of training (csrc/ve_gate.hip): v + 2 sigmoid(n W^T) per head x bf16(table[input_ids]);
-gate logits in fp32, the mix rounded once. The backward adds the table's gradient into table.grad (a leaf requiring
-grad). Same functions, arguments and results as the reference's model/ops/ve_gate.py:13-33, for any head count
-1 <= H <= 16 (the reference kernel is built for H = 6)."""
+"""Training-side value embeddings on MI355X (csrc/ve_gate.hip), drop-in for the reference's model/ops/ve_gate.py:13-33
+(same function names, arguments and returned tensors) at any head count 1 <= H <= 16 (the reference's kernel is fixed
+at H = 6).
+
+Each token row's value heads receive its embedding-table row scaled by a per-head gate: out = v + g * bf16(table[id])
+with g = 2 * sigmoid(w_head . n) from the row's normed stream n. The gate logits are fp32 dot products and the sum is
+rounded to bf16 once. The backward returns the gradients of n and w and accumulates the table's gradient into
+table.grad, creating it as zeros when absent."""
 
 import ctypes
 
@@ -12,8 +16,9 @@ from .native import NativeError, check, hip_library, pointer, stream
 
 
 def ve_forward(n: Tensor, v: Tensor, input_ids: Tensor, table: Tensor, w: Tensor) -> tuple[Tensor, Tensor]:
-    """n (B, T, C) bf16, input_ids (B, T) int32, v (B, T, H, 128) bf16 evenly spaced rows, table (V, C) and w (H, C)
-    fp32 -> (mixed v contiguous, gate (B*T, H) fp32). A token outside [0, V) mixes in nothing."""
+    """Mix value embeddings into v. Shapes: n (B, T, C) bf16; v (B, T, H, 128) bf16 with contiguous heads and one row
+    stride; input_ids (B, T) int32; table (V, C) and w (H, C) fp32. Returns the mixed values as a new contiguous
+    tensor shaped like v, and the gates (B*T, H) fp32 the backward needs. Ids outside [0, V) add nothing."""
     if v.stride(-1) != 1 or v.stride(-2) != v.size(-1) or v.stride(0) != v.size(1) * v.stride(1):
         raise NativeError("v must be (B, T, H, 128) with contiguous heads and evenly spaced rows")
     if not (n.is_contiguous() and input_ids.is_contiguous() and table.is_contiguous() and w.is_contiguous()):
@@ -27,8 +32,9 @@ def ve_forward(n: Tensor, v: Tensor, input_ids: Tensor, table: Tensor, w: Tensor
 
 def ve_backward(dv: Tensor, n: Tensor, ids: Tensor, order: Tensor, table: Tensor, w: Tensor,
                 gate: Tensor) -> tuple[Tensor, Tensor]:
-    """dv laid out as v, ids (B*T,) int32 sorted input_ids, order int64 their rows -> (dn, dw); the table's gradient
-    added into table.grad (zeros when None)."""
+    """Gradients of ve_forward. dv is the output's gradient, laid out like v; ids (B*T,) int32 are the input ids sorted
+    (equal ids adjacent) and order (B*T,) int64 the row each came from; gate is ve_forward's. Returns (dn like n,
+    dw like w); the table's gradient is added into table.grad (allocated as zeros when it is None)."""
     if table.grad is None:
         table.grad = torch.zeros_like(table)
     if dv.stride(-1) != 1 or dv.stride(-2) != dv.size(-1) or dv.stride(0) != dv.size(1) * dv.stride(1):

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from nanochat_amd.decoder import PagedDecoder, Request
+from nanochat_amd.decoder import DecoderRuntime, Request, serve
 from nanochat_amd.workloads import model_tensors
 from oracle import model as om
 from oracle import sampling
@@ -88,7 +88,7 @@ def run_steps(dec, orc, inputs, positions, slots, steps, label, temperature=None
         bound = check_logits(got[slots], want, f"{label} step {step}")
         for i, b in enumerate(slots):
             tok, alt = sampling.choose(got[b], lazy=dec.bos)
-            assert tokens[b] == tok and dec.tokens[dec.batch + b] == alt, (label, step, b)
+            assert tokens[b] == tok and dec.alternatives[b] == alt, (label, step, b)
             # the device's choice is also (nearly) the oracle's best
             assert want[i][tok] >= want[i].max() - 2 * bound
         inputs = [int(tokens[b]) for b in slots]
@@ -101,20 +101,19 @@ def test_prefill_and_greedy_steps_match_oracle(device, shape):
     m, w, max_length = build(device, shape)
     lengths = [23, 64, 5, 81] if shape == "tiny" else [17, 40, 3]
     ids = prompts(lengths, m.vocab, seed=1)
-    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+    dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
     try:
         orc = om.DecoderOracle(w, max_length)
         slots = list(range(len(ids)))
         for b in slots:
-            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=8))
+            dec.place(b, ids[b])
         dec.prefill()
         rows = [(t, p, b) for b in slots for p, t in enumerate(ids[b][:-1])]
         orc.body(*map(list, zip(*rows)), cache_only_last=True)
         for layer in range(len(m.layers)):
             for b in slots:
                 check_cache(dec, orc, layer, b, len(ids[b]) - 1, f"{shape} layer {layer} slot {b}")
-        dec.flags[0, slots] = True
-        dec.set_active()
+        dec.activate(slots)
         run_steps(dec, orc, [i[-1] for i in ids], [len(i) - 1 for i in ids], slots, 6, shape)
     finally:
         dec.close()
@@ -123,14 +122,14 @@ def test_prefill_and_greedy_steps_match_oracle(device, shape):
 def test_prompt_store_round_trip_and_reuse(device):
     m, w, max_length = build(device, "tiny")
     ids = prompts([50, 30], m.vocab, seed=2)
-    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=200, max_slots=8)
+    dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=200, max_slots=8)
     try:
         for b in (0, 1):
-            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
-        dec.prefill()                                  # prefills, then saves both prompts (store positions 0, 64)
+            dec.place(b, ids[b])
+        dec.prefill()                                  # prefills, then stores both prompts (positions 0, 64)
         assert dec.stored == {tuple(ids[0]): 0, tuple(ids[1]): 64}
-        dec.start(5, 2, Request(input_ids=ids[0], max_new_tokens=4))   # loaded from the store, not prefilled
-        assert not dec.pending
+        dec.place(5, ids[0])   # loaded from the store, not prefilled
+        assert not dec.queued
         n = len(ids[0]) - 1
         pages = len(dec.table(5))
         # the prompt's 3 whole pages are the store's (shared), the partial 4th is the slot's own copy
@@ -143,8 +142,7 @@ def test_prompt_store_round_trip_and_reuse(device):
             t1 = dec.cache_rows(layer, -1, 64, len(ids[1]) - 1)
             for x, y in zip(dec.cache_rows(layer, 1, 0, len(ids[1]) - 1), t1):
                 assert np.array_equal(x, y), layer
-        dec.flags[0, [0, 1, 5]] = True
-        dec.set_active()
+        dec.activate([0, 1, 5])
         tokens = dec.step()
         got = dec.logits(6)
         # same cache bytes and inputs; the split-K schedule partitions the two slots' keys differently, so their
@@ -161,11 +159,11 @@ def test_shared_store_pages_copy_on_write(device):
     phase (copied, not shared). Cache bytes compared through the block tables after each."""
     m, w, max_length = build(device, "tiny")
     ids = prompts([50, 41], m.vocab, seed=12)
-    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=400, max_slots=8)
+    dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=400, max_slots=8)
     L = len(m.layers)
     try:
         for b in (0, 1):   # each prefilled alone, so slot 3's prefill of B below runs the same GEMM shapes
-            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+            dec.place(b, ids[b])
             dec.prefill()                               # A = ids[0] at store 0, B = ids[1] at store 64
         assert dec.stored == {tuple(ids[0]): 0, tuple(ids[1]): 64}
         nA, nB = len(ids[0]) - 1, len(ids[1]) - 1
@@ -205,32 +203,28 @@ def test_shared_store_pages_copy_on_write(device):
 def test_masks_and_alternative(device):
     m, w, max_length = build(device, "tiny")
     ids = prompts([12, 20, 9], m.vocab, seed=3)
-    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+    dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
     try:
         for b in range(3):
-            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+            dec.place(b, ids[b])
         dec.prefill()
         rng = np.random.default_rng(4)
         allowed = rng.random(m.vocab) < 0.05
         dec.masks[1] = np.packbits(allowed, bitorder="little").view("<u4")
         dec.masks[2] = 0
         dec.masks[2, 0] = 1                       # slot 2 may choose only BOS: its alternative is none (-1)
-        dec.flags[0, :3] = True
-        dec.flags[1, [1, 2]] = True
-        dec.set_active()
+        dec.activate(range(3), masked=[1, 2])
         tokens = dec.step()
         got = dec.logits(3)
-        B = dec.batch
         for b in range(3):
             tok, alt = sampling.choose(got[b], allow=None if b == 0 else dec.masks[b], lazy=0)
-            assert tokens[b] == tok and dec.tokens[B + b] == alt, b
+            assert tokens[b] == tok and dec.alternatives[b] == alt, b
         assert allowed[tokens[1]]
-        assert tokens[2] == 0 and dec.tokens[B + 2] == -1
+        assert tokens[2] == 0 and dec.alternatives[2] == -1
         # take the alternative of slot 1: its next input is the alternative token
-        alt1 = int(dec.tokens[B + 1])
-        dec.lib.dec_take_alt(dec.handle, 1)
-        dec.flags[1] = False
-        dec.set_active()
+        alt1 = int(dec.alternatives[1])
+        dec.take_alternative(1)
+        dec.activate(range(3))
         orc = om.DecoderOracle(w, max_length)
         rows = [(t, p, b) for b in range(3) for p, t in enumerate(ids[b][:-1])]
         orc.body(*map(list, zip(*rows)), cache_only_last=True)
@@ -249,14 +243,12 @@ def test_sampling_matches_oracle_choice(device):
     m, w, max_length = build(device, "tiny")
     ids = prompts([10, 14, 18, 22], m.vocab, seed=5)
     params = [(0.9, 1.0, 7), (0.7, 0.8, 123456789012345), (1.3, 0.5, 2 ** 63 + 5), (0.0, 0.5, 1)]
-    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+    dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
     try:
         for b, (T, p, seed) in enumerate(params):
-            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=6, temperature=T, top_p=p, seed=seed))
+            dec.place(b, ids[b], temperature=T, top_p=p, seed=seed)
         dec.prefill()
-        dec.flags[0, :4] = True
-        dec.set_active()
-        B = dec.batch
+        dec.activate(range(4))
         for step in range(5):
             tokens = dec.step()
             got = dec.logits(4)
@@ -273,12 +265,12 @@ def test_sampling_matches_oracle_choice(device):
                             assert abs(e[tokens[b]] - kept.min()) <= 1e-5 * kept.min(), (step, b)
                         else:
                             assert near_tie_ok(int(tokens[b]), tok, scores), (step, b)
-                        assert dec.tokens[B + b] == -1
+                        assert dec.alternatives[b] == -1
                     else:
                         assert near_tie_ok(int(tokens[b]), tok, scores), (step, b)
-                        assert near_tie_ok(int(dec.tokens[B + b]), alt, scores), (step, b)
+                        assert near_tie_ok(int(dec.alternatives[b]), alt, scores), (step, b)
                 else:
-                    assert tokens[b] == tok and dec.tokens[B + b] == alt
+                    assert tokens[b] == tok and dec.alternatives[b] == alt
     finally:
         dec.close()
 
@@ -286,28 +278,26 @@ def test_sampling_matches_oracle_choice(device):
 def test_inactive_slot_holds_still(device):
     m, w, max_length = build(device, "tiny")
     ids = prompts([15, 25, 35], m.vocab, seed=6)
-    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+    dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
     try:
         for b in range(3):
-            dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+            dec.place(b, ids[b])
         dec.prefill()
         orc = om.DecoderOracle(w, max_length)
         rows = [(t, p, b) for b in range(3) for p, t in enumerate(ids[b][:-1])]
         orc.body(*map(list, zip(*rows)), cache_only_last=True)
-        dec.flags[0, [0, 2]] = True                    # slot 1 idles this step
-        dec.set_active()
+        dec.activate([0, 2])                           # slot 1 idles this step
         inputs, pos = run_steps(dec, orc, [ids[0][-1], ids[2][-1]], [14, 34], [0, 2], 1, "slot 1 idle")
         _, _, s = dec.cache_rows(0, 1, len(ids[1]) - 1, 1)
         assert np.all(s == 0)                          # its next position was not written
-        dec.flags[0, 1] = True
-        dec.set_active()
+        dec.activate([0, 1, 2])
         run_steps(dec, orc, [inputs[0], ids[1][-1], inputs[1]], [pos[0], 24, pos[1]], [0, 1, 2], 2, "slot 1 back")
     finally:
         dec.close()
 
 
-def test_generate_continuous_batching(device):
-    """generate() over more requests than slots: every output token is (nearly) the oracle's greedy choice given the
+def test_serve_continuous_batching(device):
+    """serve() over more requests than slots: every output token is (nearly) the oracle's greedy choice given the
     tokens before it; stopping criteria and max_new_tokens end requests; slots are refilled."""
     m, w, max_length = build(device, "tiny")
     ids = prompts([9, 30, 12, 44, 7], m.vocab, seed=7)
@@ -315,12 +305,13 @@ def test_generate_continuous_batching(device):
     requests = [Request(input_ids=ids[i], max_new_tokens=5,
                         stopping_criteria=(lambda out, k=stop_after.get(i): k is not None and len(out) >= k))
                 for i in range(5)]
-    dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=300, max_slots=2)
+    dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=300, max_slots=2)
     try:
         assert dec.batch == 2
-        done = dict(dec.generate(requests))
+        timings = {}
+        done = dict(serve(dec, requests, timings))
         assert sorted(done) == list(range(5))
-        assert sorted(dec.timings) == list(range(5))
+        assert sorted(timings) == list(range(5)) and all(a <= b <= c for a, b, c in timings.values())
         for i, out in done.items():
             assert 1 <= len(out) <= 5
             if i == 3:
@@ -343,13 +334,12 @@ def test_steps_are_deterministic(device):
     ids = prompts([20, 33, 7], m.vocab, seed=9)
     out = []
     for _ in range(2):
-        dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
+        dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
         try:
             for b in range(3):
-                dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+                dec.place(b, ids[b])
             dec.prefill()
-            dec.flags[0, :3] = True
-            dec.set_active()
+            dec.activate(range(3))
             logits = []
             for _ in range(3):
                 dec.step()
@@ -371,15 +361,14 @@ def test_two_lane_steps_match_one_lane_and_oracle(device):
     ids = prompts(lengths, m.vocab, seed=11)
     runs = []
     for split in (0, 1, 1):
-        dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=128)
+        dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=128)
         try:
             assert dec.batch >= n
             dec.lib.dec_debug_set_split(dec.handle, split)
             for b in range(n):
-                dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=4))
+                dec.place(b, ids[b])
             dec.prefill()
-            dec.flags[0, :n] = True
-            dec.set_active()
+            dec.activate(range(n))
             steps = []
             for _ in range(2):
                 tokens = dec.step()
@@ -417,15 +406,14 @@ def test_graph_replays_match_eager_steps(device, slots):
     ids = prompts(lengths, m.vocab, seed=12)
     runs = []
     for graphs in (0, 1):
-        dec = PagedDecoder(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=128)
+        dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=128)
         try:
             dec.lib.dec_debug_set_graphs(dec.handle, graphs)
             dec.lib.dec_debug_set_split(dec.handle, 1)
             for b in range(slots):
-                dec.start(b, b, Request(input_ids=ids[b], max_new_tokens=8))
+                dec.place(b, ids[b])
             dec.prefill()
-            dec.flags[0, :slots] = True
-            dec.set_active()
+            dec.activate(range(slots))
             steps = []
             for _ in range(6):
                 tokens = dec.step()
