@@ -87,17 +87,16 @@ void dec_debug_table(void *handle, int b, int32_t *out);
 void dec_debug_set_split(void *handle, int on);
 void dec_debug_set_graphs(void *handle, int on);
 
-/* The range-checked weight-streaming GEMM alone: out[n][r] = epilogue(sum_k x[n][k] w[r][k]), bf16 w [R][K] and
- * x [N][K], epi 0 bf16(s), 1 x = s + res: bf16 out and fp32 out_f32, 2 bf16(relu(p) p) with p = s rstd[n],
- * 3 bf16(s + res), 4 fp32 out_f32 = s; split over `slices` K-slices (0: the default, dec_debug_stream_gemm_slices)
- * whose partial sums go to part (fp32 [slices][N][R], dec_debug_stream_gemm_part_bytes(R, N, slices) bytes, none for
- * one slice) and are added in slice order.
- * Returns 0, a hipError_t, or -2 when the shape, the slice count or an operand the epilogue needs does not fit.
- * Stream-ordered. */
-int dec_debug_stream_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out, float *out_f32,
-                          const void *res, const float *rstd, int slices, float *part, void *stream);
-int dec_debug_stream_gemm_slices(int R, int K);
-long long dec_debug_stream_gemm_part_bytes(int R, int N, int slices);
+/* The decode step's GEMM alone (slot_gemm.hip): out[n][r] = epilogue(sum_k x[n][k] w[r][k]), bf16 w [R][K] and
+ * x [N][K] (N <= 128), epi 0 bf16(s), 1 x = s + res: bf16 out and fp32 out_f32, 2 bf16(relu(p) p) with p = s rstd[n],
+ * 3 bf16(s + res), 4 fp32 out_f32 = s; split over `slices` K-slices (0: the decoder's choice,
+ * dec_debug_slot_gemm_slices) whose partial sums go to part (fp32 [slices][N][R], dec_debug_slot_gemm_part_bytes(R, N,
+ * slices) bytes, none for one slice) and are added in slice order. Returns 0, a hipError_t, or -2 when the shape (K a
+ * multiple of 128, R of 4), the slice count or an operand the epilogue needs does not fit. Stream-ordered. */
+int dec_debug_slot_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out, float *out_f32,
+                        const void *res, const float *rstd, int slices, float *part, void *stream);
+int dec_debug_slot_gemm_slices(int R, int K);
+long long dec_debug_slot_gemm_part_bytes(int R, int N, int slices);
 
 #ifdef __cplusplus
 }

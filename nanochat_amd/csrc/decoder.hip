@@ -4,21 +4,22 @@
  *
  * A step is a stream of kernels on the caller's stream, launched eagerly:
  *   body   norm_kernel(EMBED) -> per layer { norm_kernel(RESID), qkv GEMM, the fused q/k norm + RoPE + value-embedding
- *          + fp8 append (kv_append.hip), split-K decode attention (attention.hip), o GEMM (fp32 sum), rstd_kernel (adds
- *          the residual), fc GEMM + relu2_kernel, proj GEMM (+ residual) }
+ *          + fp8 append (kv_append.hip), split-K decode attention (attention.hip), o GEMM (+ residual: fp32 sum and its
+ *          bf16 rounding), rstd_kernel, fc GEMM (+ ReLU^2 of the rstd-scaled sum), proj GEMM (+ residual) }
  *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
  *          the allowed tokens, then the commit), the tokens to pinned host memory.
- * GEMMs are hipBLASLt matmuls (bf16 operands, fp32 accumulation; one plan per shape and row count, the heuristic's
- * first algorithm; rocBLAS gemm_ex where hipBLASLt offers none) followed by the epilogue kernels. stream_gemm.hip's
- * range-checked weight-streaming GEMM, whose epilogues are fused, is built and tested but off (Decoder::streaming):
- * at the step's shapes it is not faster than the library. Every kernel covers the slots up to the highest active one
- * (dec_set_active) and skips inactive slots.
+ * A step's GEMMs are slot_gemm.hip's weight-streaming MFMA kernel with the epilogue fused (long-K GEMMs split into
+ * K-slices whose partials a second kernel adds in order). Prefill's GEMMs (up to 8,192 rows) are hipBLASLt matmuls
+ * (bf16 operands, fp32 accumulation; one plan per shape and row count, the heuristic's first algorithm; rocBLAS gemm_ex
+ * where hipBLASLt offers none) followed by the epilogue kernels. Every kernel covers the slots up to the highest active
+ * one (dec_set_active) and skips inactive slots.
  *
  * Numerics, op by op as decode.cu: the epilogues round once (bf16(s + residual)); the MLP reads the un-normed stream
  * scaled by its rstd; every RMS norm is 1 / sqrt(mean x^2 + FLT_EPSILON), correctly rounded (the reference: rsqrtf).
  * The KV cache is fp8 e4m3fn with one absmax scale per (token, head) (the reference caches bf16); a step's own key
  * is read back from the cache like the others. Decode attention splits a slot's keys at fixed multiples of 1,024
- * positions, so its sums depend only on the slot's own context.
+ * positions and the step GEMMs sum every slot's row in one fixed order, so a step's result for a slot depends only on
+ * the slot's own inputs and cache.
  *
  * Memory: one allocation per role, sized at dec_create. The KV pool of layer l is pages [0, B max_pages) for the
  * slots (slot b owns pages b max_pages + i) followed by the prompt store's pages (store position s at page
@@ -505,7 +506,7 @@ struct Lane {
     rocblas_handle blas;
     void *lt_ws;                         /* hipBLASLt workspace (Decoder::lt_ws_bytes) */
     void *attn_ws;                       /* decode-attention partials (Decoder::attn_ws_bytes) */
-    float *part;                         /* stream_gemm's split-K partial sums (Decoder::part_bytes) */
+    float *part;                         /* slot_gemm's split-K partial sums (Decoder::part_bytes) */
 };
 
 struct Decoder {
@@ -544,8 +545,7 @@ struct Decoder {
     int32_t *host_tokens;                /* pinned [2][B] */
     uint32_t *host_allow;                /* pinned [B][vocab / 32] */
     int narrow;                          /* a step's rows: the highest active slot + 1 */
-    bool streaming;                      /* decode-step GEMMs by stream_gemm (else the library GEMM) */
-    long long part_bytes;                /* each lane's stream_gemm partials, for up to SG_MAX_N rows */
+    long long part_bytes;                /* each lane's slot_gemm partials, for SG_MAX_N slots */
     bool split;                          /* a step of more than SPLIT_SLOTS slots runs as two lanes */
     bool graphs;                         /* the body replays a captured graph per (narrow, split) */
     std::map<std::pair<int, int>, hipGraphExec_t> body_graphs;  /* nullptr: seen once, run eagerly */
@@ -729,17 +729,23 @@ static uint8_t *layer_k(Decoder *d, int l) { return d->k_pages + (size_t)l * d->
 static uint8_t *layer_v(Decoder *d, int l) { return d->v_pages + (size_t)l * d->layer_pages * d->H * PAGE_BYTES; }
 static float *layer_s(Decoder *d, int l) { return d->kv_scale + (size_t)l * d->layer_pages * d->H * 2 * PAGE; }
 
-/* A GEMM with its epilogue: the weight-streaming MFMA GEMM when the rows fit it (a decode step's <= 128 slots), else
- * the library GEMM into fp32 or bf16 and the epilogue kernels. */
-static void gemm_epi(Decoder *d, const Lane &ln, int epi, const uint16_t *w, int rows, int cols, const uint16_t *in,
-                     int n, uint16_t *out, float *out_f32, const uint16_t *res, const float *rstd,
+/* A GEMM with its epilogue. A decode step (step): slot_gemm over the slots in blocks of SG_MAX_N, each slot's sums in
+ * the same order whatever the block holds, so a slot's result does not depend on the others; its split-K partials (long
+ * K) are reduced in slice order. Prefill rows: the library GEMM into fp32 or bf16, then the epilogue kernels. */
+static void gemm_epi(Decoder *d, const Lane &ln, bool step, int epi, const uint16_t *w, int rows, int cols,
+                     const uint16_t *in, int n, uint16_t *out, float *out_f32, const uint16_t *res, const float *rstd,
                      const unsigned long long *active) {
     if (n <= 0) return;
-    if (d->streaming && stream_gemm_fits(rows, cols, n)) {
-        const int S = stream_gemm_slices(rows, cols);
-        SkinnyGemm g = {w, in, rows, cols, n, out, out_f32, res, rstd, active};
-        NC_CHECK(stream_gemm(g, epi, ln.part, d->part_bytes, S, ln.stream));
-        if (S > 1) NC_CHECK(stream_gemm_reduce(g, epi, ln.part, d->part_bytes, S, ln.stream));
+    if (step) {
+        const int S = slot_gemm_slices(rows, cols);
+        for (int b0 = 0; b0 < n; b0 += SG_MAX_N) {
+            const size_t o = (size_t)b0 * rows;
+            SkinnyGemm g = {w, in + (size_t)b0 * cols, rows, cols, n - b0 < SG_MAX_N ? n - b0 : SG_MAX_N,
+                            out ? out + o : nullptr, out_f32 ? out_f32 + o : nullptr, res ? res + o : nullptr,
+                            rstd ? rstd + b0 : nullptr, active ? active + b0 / MASK_BITS : nullptr};
+            NC_CHECK(slot_gemm(g, epi, ln.part, d->part_bytes, S, ln.stream));
+            if (S > 1) NC_CHECK(slot_gemm_reduce(g, epi, ln.part, d->part_bytes, S, ln.stream));
+        }
         return;
     }
     switch (epi) {
@@ -757,14 +763,15 @@ static void gemm_epi(Decoder *d, const Lane &ln, int epi, const uint16_t *w, int
     }
 }
 
-/* The rest of a layer after its attention: o_proj + residual, the MLP. */
-static void mlp(Decoder *d, const Lane &ln, const Layer &ly, const Acts &a, int n, const unsigned long long *active) {
+/* The rest of a layer after its attention: o_proj + residual, the MLP. In a step the o GEMM's epilogue adds the
+ * residual itself (fp32 sum and its bf16 rounding), so the rstd kernel only reads the sum. */
+static void mlp(Decoder *d, const Lane &ln, bool step, const Layer &ly, const Acts &a, int n,
+                const unsigned long long *active) {
     const int C = d->C, F = d->F;
-    const bool fused = d->streaming && stream_gemm_fits(C, C, n);
-    gemm_epi(d, ln, SG_RESID2, ly.o, C, C, a.att, n, a.xo, a.acc, a.xm, nullptr, active);
-    launch_rstd(d, ln, a.acc, fused ? nullptr : a.xm, a.xo, a.rstd, active, n);
-    gemm_epi(d, ln, SG_RELU2, ly.fc, F, C, a.xo, n, a.u, a.acc, nullptr, a.rstd, active);
-    gemm_epi(d, ln, SG_RESID, ly.proj, C, F, a.u, n, a.x, nullptr, a.xo, nullptr, active);
+    gemm_epi(d, ln, step, SG_RESID2, ly.o, C, C, a.att, n, a.xo, a.acc, a.xm, nullptr, active);
+    launch_rstd(d, ln, a.acc, step ? nullptr : a.xm, a.xo, a.rstd, active, n);
+    gemm_epi(d, ln, step, SG_RELU2, ly.fc, F, C, a.xo, n, a.u, a.acc, nullptr, a.rstd, active);
+    gemm_epi(d, ln, step, SG_RESID, ly.proj, C, F, a.u, n, a.x, nullptr, a.xo, nullptr, active);
 }
 
 /* Slots [b0, b0 + n) of a step (b0 a multiple of 64, so their active mask starts at word b0 / 64). */
@@ -798,7 +805,7 @@ static void body_pre(Decoder *d, const Lane &ln, const Part &p, int l) {
     r.mixed = a.xm;
     r.out = a.h;
     launch_norm(ln, r);
-    gemm_epi(d, ln, SG_STORE, ly.qkv, 3 * C, C, a.h, p.n, a.qkv, nullptr, nullptr, nullptr, p.active);
+    gemm_epi(d, ln, true, SG_STORE, ly.qkv, 3 * C, C, a.h, p.n, a.qkv, nullptr, nullptr, nullptr, p.active);
     NC_CHECK(append_rows(a.qkv, 3LL * C, p.n, d->H, d->H, d->pos + p.b0, d->num_new + p.b0, nullptr, ly.q_gain,
                          ly.k_gain, d->cos, d->sin, d->max_len, a.q, d->block_table + (size_t)p.b0 * d->max_pages,
                          d->max_pages, layer_k(d, l), layer_v(d, l), layer_s(d, l), (int)d->layer_pages, a.h, ly.ve,
@@ -826,7 +833,7 @@ static void record_body(Decoder *d) {
         for (int l = 0; l < d->L; l++) {
             body_pre(d, ln, p, l);
             body_attn(d, ln, p, l);
-            mlp(d, ln, d->layer[l], p.a, p.n, p.active);
+            mlp(d, ln, true, d->layer[l], p.a, p.n, p.active);
         }
         return;
     }
@@ -846,7 +853,7 @@ static void record_body(Decoder *d) {
         HIP_CHECK(hipStreamWaitEvent(ln[1].stream, done[0], 0));
         body_attn(d, ln[1], p[1], l);
         HIP_CHECK(hipEventRecord(done[1], ln[1].stream));
-        for (int h = 0; h < 2; h++) mlp(d, ln[h], d->layer[l], p[h].a, p[h].n, p[h].active);
+        for (int h = 0; h < 2; h++) mlp(d, ln[h], true, d->layer[l], p[h].a, p[h].n, p[h].active);
     }
     HIP_CHECK(hipEventRecord(d->join, ln[1].stream));
     HIP_CHECK(hipStreamWaitEvent(ln[0].stream, d->join, 0));
@@ -889,7 +896,7 @@ static void enqueue_head(Decoder *d) {
         n.in = a.x;
         n.out = a.hn;
         launch_norm(d->lane[0], n);
-        gemm_epi(d, d->lane[0], SG_F32, d->lm_head, d->vocab, d->C, a.hn, R, nullptr, d->logits, nullptr, nullptr,
+        gemm_epi(d, d->lane[0], true, SG_F32, d->lm_head, d->vocab, d->C, a.hn, R, nullptr, d->logits, nullptr, nullptr,
                  d->active);
         ChoiceArgs c = {d->logits, d->probs, d->active, d->allow, d->temperature, d->top_p, d->seed, d->first,
                         d->tokens, d->alt_tokens, d->pos, d->softcap, d->vocab, d->lazy};
@@ -906,7 +913,7 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     d->lazy = cfg[6];
     REQUIRE(d->L > 0 && d->C > 0 && d->C % HEAD_DIM == 0 && d->C <= MAX_C,
             "C must be a positive multiple of 128, at most 4096");
-    REQUIRE(d->F > 0 && d->F % 4 == 0, "F must be a positive multiple of 4");
+    REQUIRE(d->F > 0 && d->F % 128 == 0, "F must be a positive multiple of 128");
     REQUIRE(d->vocab > 0 && d->vocab % WORD_BITS == 0, "vocab must be a positive multiple of 32");
     REQUIRE(d->max_len > 0 && d->store >= 0, "max_len must be positive, store non-negative");
     REQUIRE(max_slots > 0 && max_slots <= MAX_BATCH, "slots must be in [1, 1024]");
@@ -986,9 +993,6 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     d->logits = (float *)device_alloc(d, B * d->vocab * sizeof(float));
     d->probs = (float *)device_alloc(d, B * d->vocab * sizeof(float));
     d->slot = carve_acts(d, B);
-    /* partials for the most rows a streamed GEMM takes: a step's slots and prefill's row blocks (up to SG_MAX_N rows,
-     * more than the slots when B < SG_MAX_N) both call it */
-    d->streaming = false;   /* the step GEMMs stay on the library until the streamed path beats it */
     /* measured at config 5 (128 slots, 26 layers): one lane eager 6.12 ms a step, one lane with graphs 6.2-6.3 ms,
      * two lanes with graphs 6.6 ms: attention fills every CU, so the other lane's GEMMs cannot run beside it, and
      * the host stays ahead of a 6 ms step. Both stay available (dec_debug_set_split / dec_debug_set_graphs). */
@@ -997,11 +1001,11 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     long long part_bytes = 0;
     const int C = d->C, F = d->F;
     const int shapes[5][2] = {{3 * C, C}, {C, C}, {F, C}, {C, F}, {d->vocab, C}};
-    for (const auto &rk : shapes)
-        if (d->streaming && stream_gemm_fits(rk[0], rk[1], SG_MAX_N)) {
-            const long long bytes = stream_gemm_part_bytes(rk[0], SG_MAX_N, stream_gemm_slices(rk[0], rk[1]));
-            part_bytes = bytes > part_bytes ? bytes : part_bytes;
-        }
+    for (const auto &rk : shapes) {
+        REQUIRE(slot_gemm_fits(rk[0], rk[1], SG_MAX_N), "a step GEMM shape the slot GEMM does not take");
+        const long long bytes = slot_gemm_part_bytes(rk[0], SG_MAX_N, slot_gemm_slices(rk[0], rk[1]));
+        part_bytes = bytes > part_bytes ? bytes : part_bytes;
+    }
     d->part_bytes = part_bytes;
     d->attn_ws_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1);
     REQUIRE(d->attn_ws_bytes > 0, "decode attention workspace");
@@ -1181,7 +1185,7 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
         NC_CHECK(prefill_runs(a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table, d->max_pages,
                               (int)d->layer_pages, dstart, drow0, dcount, drslot, runs, max_count, d->H, d->H, ly.window,
                               SM_SCALE, a.att, d->stream));
-        mlp(d, ln, ly, a, n, nullptr);
+        mlp(d, ln, false, ly, a, n, nullptr);
     }
 }
 
@@ -1369,21 +1373,21 @@ extern "C" void dec_debug_set_graphs(void *handle, int on) {
     d->graphs = on != 0;
 }
 
-extern "C" int dec_debug_stream_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out,
-                                     float *out_f32, const void *res, const float *rstd, int slices, float *part,
-                                     void *stream) {
+extern "C" int dec_debug_slot_gemm(int epi, const void *w, int R, int K, const void *x, int N, void *out,
+                                   float *out_f32, const void *res, const float *rstd, int slices, float *part,
+                                   void *stream) {
     nc::SkinnyGemm g = {(const uint16_t *)w, (const uint16_t *)x, R, K, N, (uint16_t *)out, out_f32,
                         (const uint16_t *)res, rstd, nullptr};
-    if (!nc::stream_gemm_fits(R, K, N)) return -2;
-    const int S = slices > 0 ? slices : nc::stream_gemm_slices(R, K);
-    const long long part_bytes = nc::stream_gemm_part_bytes(R, N, S);   /* the caller allocates this much */
-    const int e = nc::stream_gemm(g, epi, part, part_bytes, S, (hipStream_t)stream);
+    if (!nc::slot_gemm_fits(R, K, N)) return -2;
+    const int S = slices > 0 ? slices : nc::slot_gemm_slices(R, K);
+    const long long part_bytes = nc::slot_gemm_part_bytes(R, N, S);   /* the caller allocates this much */
+    const int e = nc::slot_gemm(g, epi, part, part_bytes, S, (hipStream_t)stream);
     if (e != 0 || S == 1) return e;
-    return nc::stream_gemm_reduce(g, epi, part, part_bytes, S, (hipStream_t)stream);
+    return nc::slot_gemm_reduce(g, epi, part, part_bytes, S, (hipStream_t)stream);
 }
 
-extern "C" int dec_debug_stream_gemm_slices(int R, int K) { return nc::stream_gemm_slices(R, K); }
+extern "C" int dec_debug_slot_gemm_slices(int R, int K) { return nc::slot_gemm_slices(R, K); }
 
-extern "C" long long dec_debug_stream_gemm_part_bytes(int R, int N, int slices) {
-    return nc::stream_gemm_part_bytes(R, N, slices);
+extern "C" long long dec_debug_slot_gemm_part_bytes(int R, int N, int slices) {
+    return nc::slot_gemm_part_bytes(R, N, slices);
 }

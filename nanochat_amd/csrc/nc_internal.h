@@ -42,20 +42,17 @@ struct SkinnyGemm {
     const unsigned long long *active;  /* NULL, or the slots whose outputs are stored */
 };
 
-/* stream_gemm.hip: the same GEMM (SkinnyGemm operands, SG_* epilogues) with every global access range-checked by
- * buffer instructions. */
-bool stream_gemm_fits(int R, int K, int N);
-/* K-slices for (R, K): at least stream_gemm_min_slices(K) (slices of at most four 128-wide chunks), more up to about
- * 128 workgroups of 128 rows. */
-int stream_gemm_min_slices(int K);
-int stream_gemm_slices(int R, int K);
+/* slot_gemm.hip: the decode step's GEMM with every global access range-checked by buffer instructions. */
+bool slot_gemm_fits(int R, int K, int N);
+/* K-slices for (R, K): 1, or enough that each covers at most 2048 of K (fixed per shape, never per slot count). */
+int slot_gemm_slices(int R, int K);
 /* Bytes of the partial sums of S slices (0 for S = 1). */
-long long stream_gemm_part_bytes(int R, int N, int S);
+long long slot_gemm_part_bytes(int R, int N, int S);
 /* S = 1: the epilogue in the GEMM. S > 1: fp32 partials to part [S][N][R] (part_bytes: its allocation, which must
- * hold them), summed by stream_gemm_reduce. Returns 0, a hipError_t, or -2 when the shape, S, the partial buffer or an
+ * hold them), summed by slot_gemm_reduce. Returns 0, a hipError_t, or -2 when the shape, S, the partial buffer or an
  * operand the epilogue needs does not fit. */
-int stream_gemm(const SkinnyGemm &g, int epi, float *part, long long part_bytes, int S, hipStream_t stream);
-int stream_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, long long part_bytes, int S,
-                       hipStream_t stream);
+int slot_gemm(const SkinnyGemm &g, int epi, float *part, long long part_bytes, int S, hipStream_t stream);
+int slot_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, long long part_bytes, int S,
+                     hipStream_t stream);
 
 }  // namespace nc

@@ -26,7 +26,7 @@ LIB_DIR = PACKAGE / "lib"
 LIBRARY = LIB_DIR / "libnanochat_kv.so"
 DECODE_LIBRARY = LIB_DIR / "libnanochat_decode.so"
 KERNEL_SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip", CSRC / "ve_gate.hip", CSRC / "flash_attn.hip"]
-DECODE_SOURCES = [CSRC / "decoder.hip", CSRC / "stream_gemm.hip"]
+DECODE_SOURCES = [CSRC / "decoder.hip", CSRC / "slot_gemm.hip"]
 SOURCES = KERNEL_SOURCES + DECODE_SOURCES
 HEADERS = [CSRC / "nc_device.h", CSRC / "nc_internal.h", INCLUDE / "nanochat_amd.h", INCLUDE / "nanochat_decode.h"]
 HEAD_DIM = 128
@@ -130,10 +130,10 @@ DECODE_SIGNATURES = {
     "dec_debug_table": ([c_void_p, c_int, c_void_p], None),
     "dec_debug_set_split": ([c_void_p, c_int], None),
     "dec_debug_set_graphs": ([c_void_p, c_int], None),
-    "dec_debug_stream_gemm": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
-                               c_int, c_void_p, c_void_p], c_int),
-    "dec_debug_stream_gemm_slices": ([c_int, c_int], c_int),
-    "dec_debug_stream_gemm_part_bytes": ([c_int, c_int, c_int], c_longlong),
+    "dec_debug_slot_gemm": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                             c_int, c_void_p, c_void_p], c_int),
+    "dec_debug_slot_gemm_slices": ([c_int, c_int], c_int),
+    "dec_debug_slot_gemm_part_bytes": ([c_int, c_int, c_int], c_longlong),
 }
 
 LIBRARIES = {"nanochat_kv": (LIBRARY, SIGNATURES), "decode": (DECODE_LIBRARY, DECODE_SIGNATURES)}

@@ -223,25 +223,24 @@ def test_decode_argtypes_match_the_reference_binding():
     assert DECODE_SIGNATURES["dec_masks"][1] == ctypes.POINTER(ctypes.c_uint32)
 
 
-def test_stream_gemm_declines_without_launching():
-    """Shapes, slice counts and missing operands the weight-streaming GEMM cannot take return -2 before any device
-    call; the slice choice keeps at most four 128-wide chunks (its LDS staging) and at least one a slice."""
+def test_slot_gemm_declines_without_launching():
+    """Shapes, slice counts and missing operands the step GEMM cannot take return -2 before any device call; long K is
+    cut into slices of at most 2,048 (16 chunks of 128), short K is never split."""
     from nanochat_amd.native import hip_library
 
     lib = hip_library("decode")
     F32, RELU2 = 4, 2
     args = (DUMMY, 1664, 6656, DUMMY, 128, DUMMY, DUMMY, DUMMY, DUMMY)
-    assert lib.dec_debug_stream_gemm(F32, DUMMY, 1664, 6656, DUMMY, 129, None, DUMMY, None, None, 1, None, None) == -2
-    assert lib.dec_debug_stream_gemm(F32, DUMMY, 1664, 6600, DUMMY, 128, None, DUMMY, None, None, 1, None, None) == -2
-    assert lib.dec_debug_stream_gemm(F32, DUMMY, 1662, 6656, DUMMY, 128, None, DUMMY, None, None, 1, None, None) == -2
-    assert lib.dec_debug_stream_gemm(F32, *args, 53, DUMMY, None) == -2           # more slices than chunks
-    assert lib.dec_debug_stream_gemm(F32, *args, 14, None, None) == -2            # partials need a buffer
-    assert lib.dec_debug_stream_gemm(F32, *args, 12, DUMMY, None) == -2           # a slice of more than 4 chunks
-    assert lib.dec_debug_stream_gemm(RELU2, DUMMY, 1664, 6656, DUMMY, 128, DUMMY, None, None, None, 1, None,
-                                     None) == -2                                   # ReLU^2 needs rstd
-    assert lib.dec_debug_stream_gemm(7, *args, 1, None, None) == -2               # no such epilogue
-    for R, K in ((4992, 1664), (1664, 1664), (6656, 1664), (1664, 6656), (65536, 1664), (100, 128)):
-        S = lib.dec_debug_stream_gemm_slices(R, K)
-        assert -(-(K // 128) // 4) <= S <= K // 128, (R, K, S)
-    assert lib.dec_debug_stream_gemm_part_bytes(1664, 128, 1) == 0
-    assert lib.dec_debug_stream_gemm_part_bytes(1664, 128, 4) == 4 * 128 * 1664 * 4
+    assert lib.dec_debug_slot_gemm(F32, DUMMY, 1664, 6656, DUMMY, 129, None, DUMMY, None, None, 1, None, None) == -2
+    assert lib.dec_debug_slot_gemm(F32, DUMMY, 1664, 6600, DUMMY, 128, None, DUMMY, None, None, 1, None, None) == -2
+    assert lib.dec_debug_slot_gemm(F32, DUMMY, 1662, 6656, DUMMY, 128, None, DUMMY, None, None, 1, None, None) == -2
+    assert lib.dec_debug_slot_gemm(F32, *args, 53, DUMMY, None) == -2           # more slices than chunks
+    assert lib.dec_debug_slot_gemm(F32, *args, 14, None, None) == -2            # partials need a buffer
+    assert lib.dec_debug_slot_gemm(RELU2, DUMMY, 1664, 6656, DUMMY, 128, DUMMY, None, None, None, 1, None,
+                                   None) == -2                                   # ReLU^2 needs rstd
+    assert lib.dec_debug_slot_gemm(7, *args, 1, None, None) == -2               # no such epilogue
+    for R, K, S in ((4992, 1664, 1), (1664, 1664, 1), (6656, 1664, 1), (1664, 6656, 4), (65536, 1664, 1),
+                    (100, 128, 1), (768, 2048, 1), (768, 2176, 2)):
+        assert lib.dec_debug_slot_gemm_slices(R, K) == S, (R, K)
+    assert lib.dec_debug_slot_gemm_part_bytes(1664, 128, 1) == 0
+    assert lib.dec_debug_slot_gemm_part_bytes(1664, 128, 4) == 4 * 128 * 1664 * 4
