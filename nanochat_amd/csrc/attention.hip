@@ -59,7 +59,7 @@ struct WaveState {
     f32x4 o[NT][8];  /* O^T tile d: dims 16d + 4g + i of column c, scaled by 2^-m */
     float m[NT];     /* column c's reference max (log2 domain, equal in the four groups); exponentials use it */
     float l[NT];     /* sum of exp2(s - m) over the keys this lane's group holds */
-    float sl2;       /* score multiplier: sm_scale log2(e) 2^-e for queries staged as 2^e q (QOp) */
+    float sl2;       /* score multiplier: sm_scale log2(e) */
     bool bad;        /* a block-table entry fell outside the page pool */
 };
 
@@ -75,44 +75,51 @@ __device__ __forceinline__ void state_init(WaveState<NT> &st) {
     st.bad = false;
 }
 
-/* The query operand of column c (B operand of the fp8 score MFMA v_mfma_scale_f32_16x16x128_f8f6f4, unit scales):
- * lane (g, c) holds dims 32 g .. 32 g + 31 of its row as bytes 0..31, the same (lane, byte) -> k mapping as the K
- * page's A operand (lane (g, key) holds that key's dims 32 g .. + 31). The row times 2^e (e uniform in the wave, so
- * the wave's largest |q| lands in [128, 256)) is split into two e4m3 parts, hi = e4m3(x), lo = e4m3(x - hi): a bf16
- * value has 8 significant bits and each part 4, so hi + lo = x exactly unless |x| < 2^-2 (then lo may lose bits
- * below 2^-10, at most 2^-18 of the wave's largest element). The score MFMAs then read the cache's K codes as they
- * are, with no conversion. */
+/* The query operand of column c (B operand of the fp8 score MFMA v_mfma_scale_f32_16x16x128_f8f6f4): lane (g, c) holds
+ * dims 32 g .. 32 g + 31 of its row as bytes 0..31, the same (lane, byte) -> k mapping as the K page's A operand
+ * (lane (g, key) holds that key's dims 32 g .. + 31). The row times 2^e (e chosen per column, from the column's own
+ * largest |q|, which lands in [128, 256)) is split into two e4m3 parts, hi = e4m3(x), lo = e4m3(x - hi): a bf16 value
+ * has 8 significant bits and each part 4, so hi + lo = x exactly unless |x| < 2^-2 (then lo may lose bits below 2^-10,
+ * at most 2^-18 of the column's largest element). The MFMA's E8M0 scale of the B operand, one per lane (a lane holds
+ * exactly one 32-element block of one column), is 2^-e, so the products come out unscaled and one score multiplier
+ * serves every column. The score MFMAs read the cache's K codes as they are, with no conversion. Since e depends on
+ * the column alone, so do its scores: a row's result does not depend on the rows that share its wave. */
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 struct QOp {
     i32x8 hi, lo;
+    int scale;   /* E8M0 code of 2^-e: 127 - e */
 };
 
-__device__ __forceinline__ f32x4 mfma_fp8(const i32x8 &a, const i32x8 &b, const f32x4 &c) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);  /* E8M0 127: scale 1 */
+__device__ __forceinline__ f32x4 mfma_fp8(const i32x8 &a, const i32x8 &b, int scale_b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, scale_b);   /* A: unit scale */
 }
 
-/* Stages NT rows (NULL: zeros) as QOp; returns 2^-e. Every lane of the wave must call it (a wave-wide max). */
+/* Stages NT rows (NULL: zeros) as QOp. Every lane of the wave must call it (a column's maximum combines its four row
+ * groups). */
 template <int NT>
-__device__ __forceinline__ float load_q8(const uint16_t *const (&rows)[NT], int g, QOp (&q)[NT]) {
+__device__ __forceinline__ void load_q8(const uint16_t *const (&rows)[NT], int g, QOp (&q)[NT]) {
     uint4 raw[NT][4];
-    float amax = 0.0f;
+    float amax[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++)
+    for (int t = 0; t < NT; t++) {
+        amax[t] = 0.0f;
 #pragma unroll
         for (int cc = 0; cc < 4; cc++) {
             raw[t][cc] = rows[t] ? *reinterpret_cast<const uint4 *>(rows[t] + g * 32 + cc * 8) : uint4{0u, 0u, 0u, 0u};
             const uint32_t w[4] = {raw[t][cc].x, raw[t][cc].y, raw[t][cc].z, raw[t][cc].w};
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32((uint16_t)w[i])), fabsf(bf16_to_f32((uint16_t)(w[i] >> 16)))));
+                amax[t] = fmaxf(amax[t], fmaxf(fabsf(bf16_to_f32((uint16_t)w[i])), fabsf(bf16_to_f32((uint16_t)(w[i] >> 16)))));
         }
-    amax = wave_max(amax);
-    const int E = amax > 0.0f ? (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127 : 0;
-    const int e = min(max(7 - E, -120), 120);
-    const float up = __uint_as_float((uint32_t)(127 + e) << 23), down = __uint_as_float((uint32_t)(127 - e) << 23);
+        amax[t] = pair_max32(pair_max16(amax[t]));   /* the column's four row groups */
+    }
 #pragma unroll
-    for (int t = 0; t < NT; t++)
+    for (int t = 0; t < NT; t++) {
+        const int E = amax[t] > 0.0f ? (int)((__float_as_uint(amax[t]) >> 23) & 0xFFu) - 127 : 0;
+        const int e = min(max(7 - E, -120), 120);
+        const float up = __uint_as_float((uint32_t)(127 + e) << 23);
+        q[t].scale = 127 - e;
 #pragma unroll
         for (int cc = 0; cc < 4; cc++) {
             const uint32_t w[4] = {raw[t][cc].x, raw[t][cc].y, raw[t][cc].z, raw[t][cc].w};
@@ -134,7 +141,7 @@ __device__ __forceinline__ float load_q8(const uint16_t *const (&rows)[NT], int 
                 q[t].lo[2 * cc + h] = lo;
             }
         }
-    return down;
+    }
 }
 
 /* Scores S^T (keys 4g + i of one page, column c of tile t) = K Q^T for every tile from one page's two K loads
@@ -144,8 +151,8 @@ __device__ __forceinline__ void page_scores(const uint4 &k0, const uint4 &k1, co
     const i32x8 k = {(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z, (int)k1.w};
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        s[t] = mfma_fp8(k, qb[t].hi, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-        s[t] = mfma_fp8(k, qb[t].lo, s[t]);
+        s[t] = mfma_fp8(k, qb[t].hi, qb[t].scale, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        s[t] = mfma_fp8(k, qb[t].lo, qb[t].scale, s[t]);
     }
 }
 
@@ -222,10 +229,11 @@ struct KeyBounds {
 
 /* Softmax update and PV of one pair from its scores. The lazy rescale keeps each column's reference max m until a
  * score passes it by RESCALE_LOG2 (so p <= 2^8). The common case costs one FMA and one exponential a score:
- * p = exp2(acc ks - m) against the current m, and only when some p of the wave exceeds 2^8 (or m is still -inf)
- * does the pair take the slow path, which finds every tile's column max, moves each tile to it (the decision is
- * taken once per pair for the wave and every tile) and recomputes p. The pair's exponentials and PV MFMAs then form
- * one straight block. Each converted V operand feeds NT MFMAs. */
+ * p = exp2(acc ks - m) against the current m. Only a column some of whose p exceed 2^8 (or whose m is still -inf) takes
+ * the slow path, which moves the column to its new max, rescales it and recomputes its p; the wave enters the slow
+ * block when any of its columns needs it, but every column's update depends on its own scores alone, so a query row's
+ * result does not depend on the rows that share its wave. The pair's exponentials and PV MFMAs then form one straight
+ * block. Each converted V operand feeds NT MFMAs. */
 template <int NT, bool MASKED>
 __device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p, const f32x4 (&sa)[NT],
                                             const f32x4 (&sb)[NT], const float4 &ksa, const float4 &ksb, PairRegs &v,
@@ -261,9 +269,14 @@ __device__ __forceinline__ void pair_update(const AttnArgs &a, const PairAddr &p
             pmax = fmaxf(pmax, pr[t][i]);
         }
     }
-    if (__any(!(pmax <= 256.0f))) {   /* a column's max passed its reference by more than 2^8 (or no reference yet) */
+    if (__any(!(pmax <= 256.0f))) {   /* some column's max passed its reference by more than 2^8 (or has none yet) */
 #pragma unroll
         for (int t = 0; t < NT; t++) {
+            float pc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) pc = fmaxf(pc, pr[t][i]);
+            pc = pair_max32(pair_max16(pc));   /* the column's largest p over its four row groups */
+            if (pc <= 256.0f) continue;        /* this column keeps its reference and its p (NaN-free: pc >= 0) */
             float s[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -597,7 +610,8 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         const uint16_t *const qrows[1] = {c < a.G ? a.q + (row0 + c) * HEAD_DIM : nullptr};
         WaveState<1> st;
         state_init(st);
-        st.sl2 = a.scale_log2 * load_q8<1>(qrows, g, qb);
+        load_q8<1>(qrows, g, qb);
+        st.sl2 = a.scale_log2;
         KeyBounds<1> kb;
         kb.lo[0] = kb.full_lo = begin;
         kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
@@ -718,7 +732,9 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     kb.full_lo = a.window >= 0 ? max(start + t_last - a.window, 0) : 0;       /* its last row's window start */
     kb.written_hi = start + T - 1;
     const int w_lo = a.window >= 0 ? max(start + t0 - a.window, 0) : 0;
-    const int pg0 = w_lo / PAGE, pg1 = (start + t_last) / PAGE + 1;
+    /* page pairs start at even logical pages, so a key's pair (and its place in a column's sums) depends on the key
+     * alone, not on which rows share the wave */
+    const int pg0 = (w_lo / PAGE) & ~1, pg1 = (start + t_last) / PAGE + 1;
 
     QOp qb[NT];
     const uint16_t *qrows[NT];
@@ -726,7 +742,8 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
     for (int t = 0; t < NT; t++) qrows[t] = live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr;
     WaveState<NT> st;
     state_init(st);
-    st.sl2 = a.scale_log2 * load_q8<NT>(qrows, g, qb);
+    load_q8<NT>(qrows, g, qb);
+    st.sl2 = a.scale_log2;
     attend_pages<NT, true>(a, a.block_table + (long long)trow * a.max_pages, kvh, pg0, 2, pg1, kb, qb, st, lane);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -895,7 +912,8 @@ __global__ void __launch_bounds__(256, 2) prefill_lds_kernel(AttnArgs a) {
     }
     /* the workgroup's pages [pg0, pg0 + npages) and this wave's [wpg0, wpg1) */
     const int wg_last = min(wg_t0 + WAVES * tpw, T) - 1;
-    const int pg0 = (a.window >= 0 ? max(start + wg_t0 - a.window, 0) : 0) / PAGE;
+    /* pairs start at even logical pages: a key's pair does not depend on which rows share the workgroup */
+    const int pg0 = ((a.window >= 0 ? max(start + wg_t0 - a.window, 0) : 0) / PAGE) & ~1;
     const int npages = (start + wg_last) / PAGE + 1 - pg0;
     const int t_last = on ? min(t0 + tpw, T) - 1 : t0;
     const int wpg0 = (a.window >= 0 ? max(start + t0 - a.window, 0) : 0) / PAGE;
@@ -919,7 +937,8 @@ __global__ void __launch_bounds__(256, 2) prefill_lds_kernel(AttnArgs a) {
     for (int t = 0; t < NT; t++) qrows[t] = live[t] ? a.q + qrow[t] * HEAD_DIM : nullptr;
     WaveState<NT> st;
     state_init(st);
-    st.sl2 = a.scale_log2 * load_q8<NT>(qrows, g, qb);
+    load_q8<NT>(qrows, g, qb);
+    st.sl2 = a.scale_log2;
     __syncthreads();   /* the table is in LDS (no fetch is in flight yet, so this fence drains nothing) */
 
     const int stages = (npages + 1) / 2;

@@ -52,6 +52,8 @@ constexpr int MASK_BITS = 64;              /* slots per word of a slot mask */
 constexpr int MASK_WORDS = MAX_BATCH / MASK_BITS;
 constexpr int WORD_BITS = 32;              /* tokens per word of an allowed-token mask */
 constexpr int PREFILL_ROWS = 8192;         /* rows per dec_prefill call */
+constexpr int PREFILL_BLOCK = 1024;        /* prefill GEMMs run on whole blocks of this many rows */
+static_assert(PREFILL_ROWS % PREFILL_BLOCK == 0, "prefill blocks pad into the row buffers");
 constexpr int SPLIT_SLOTS = 64;            /* a step over more slots runs as two lanes (enqueue_body) */
 constexpr int GLOBAL_PTRS = 4, LAYER_PTRS = 8;
 constexpr int CHOICE_THREADS = 1024, CHOICE_WAVES = CHOICE_THREADS / WAVE;
@@ -670,7 +672,7 @@ static void lt_release(Decoder *d) {
 /* out[n][rows] = in[n][cols] . W[rows][cols]^T: column-major rows x n = (W as cols x rows)^T (cols x n). resid
  * non-NULL: out = bf16(s + resid) by beta = 1 (one rounding of the fp32 sum). hipBLASLt's plan for the shape,
  * else rocBLAS gemm_ex. */
-static void gemm(Decoder *d, const Lane &ln, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
+static void gemm_once(Decoder *d, const Lane &ln, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
                  void *out, bool f32, const uint16_t *resid = nullptr) {
     if (n <= 0) return;
     const float alpha = 1.0f, beta = resid ? 1.0f : 0.0f;
@@ -687,6 +689,18 @@ static void gemm(Decoder *d, const Lane &ln, const uint16_t *w, int rows, int co
                                rocblas_datatype_bf16_r, cols, in, rocblas_datatype_bf16_r, cols, &beta,
                                resid ? (const void *)resid : out, ot, rows, out, ot, rows, rocblas_datatype_f32_r,
                                rocblas_gemm_algo_standard, 0, 0));
+}
+
+/* gemm over prefill rows in whole blocks of PREFILL_BLOCK (the last one padded with the rows after n, whose results
+ * nothing reads; the row buffers hold PREFILL_ROWS), so every call runs one plan per shape and a row's sums do not
+ * depend on how many rows share the call. */
+static void gemm(Decoder *d, const Lane &ln, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
+                 void *out, bool f32, const uint16_t *resid = nullptr) {
+    if (n > PREFILL_ROWS) die("gemm", "more rows than the prefill buffers hold", __LINE__);
+    const size_t osz = f32 ? 4 : 2;
+    for (int b0 = 0; b0 < n; b0 += PREFILL_BLOCK)
+        gemm_once(d, ln, w, rows, cols, in + (size_t)b0 * cols, PREFILL_BLOCK, (char *)out + (size_t)b0 * rows * osz,
+                  f32, resid ? resid + (size_t)b0 * rows : nullptr);
 }
 
 static NormArgs norm_args(Decoder *d, int kind, const Acts &a, int rows, int32_t *tokens,
