@@ -1,17 +1,18 @@
 """Decode-step benchmark of the fp8 KV path on one MI355X.
 
-A step is one pass of the hot path over one batch: the fused QK-norm + RoPE + fp8 append of the step's token
-for every sequence (nc_qk_norm_rope_append_fp8), then split-K decode attention over the paged fp8 cache
-(nc_decode_attn_fp8). Default workload: the headline "bs64 ctx8K" (B = 64, 16 query / 4 KV heads, 8192
+A step is one pass of the hot path over one batch: the QK-norm + RoPE + fp8 append of the step's token for every
+sequence, then split-K decode attention over the paged fp8 cache, both in one launch (nc_decode_step_fp8; with
+--two-launch, nc_qk_norm_rope_append_fp8 then nc_decode_attn_fp8, the same bits). Default workload: the headline "bs64 ctx8K" (B = 64, 16 query / 4 KV heads, 8192
 cached tokens + the step's, 16-token pages under a random-permutation block table, 1% outliers at 8 sigma),
 synthetic seeded data resident in HBM before the timed region.
 
 value = algorithmic HBM bytes of the step / step time (GB/s). Attention bytes per (sequence, KV head):
 (n + 1) * 264 (fp8 K + V and two fp32 scales per key) + G * 128 * 2 * 2 (q in, out) + ceil((n + 1) / 16) * 4
-(block table); the append adds (Hq + 2 Hkv) * 256 read and Hq * 256 + Hkv * 264 written per token.
+(block table); the append adds 2 Hkv * 256 read (the token's k and v rows; its q row is the attention's q read) and
+Hkv * 264 written (codes and scales) per token.
 
     python bench.py [--steps K] [--warmup W] [--workload c3u|c3|c2|c1|c4|c5|ve|fa] [--workers W] [--cpu-seqs S]
-                    [--no-e2e]
+                    [--no-e2e] [--two-launch]
 
 A decode workload's line also carries the metric's second half, `decode_tokens_per_s`: config 5 end to end
 (below), unless --no-e2e.
@@ -50,8 +51,10 @@ def attention_bytes(ctx_lens, q_heads, kv_heads):
     return total
 
 
-def append_bytes(batch, q_heads, kv_heads):
-    return batch * ((q_heads + 2 * kv_heads) * 256 + q_heads * 256 + kv_heads * 264)
+def append_bytes(batch, kv_heads):
+    """What the step's append adds to the attention's bytes: each token's k and v rows read, codes and scales
+    written."""
+    return batch * (2 * kv_heads * 256 + kv_heads * 264)
 
 
 def traffic_from_profiles(kernel, workload):
@@ -449,6 +452,8 @@ def main():
     ap.add_argument("--workload", default="c3u")
     ap.add_argument("--workers", type=int, default=0, help="decode: waves taking the work items (0: all slots)")
     ap.add_argument("--cpu-seqs", type=int, default=64, help="sequences in the CPU baseline sample (0: skip)")
+    ap.add_argument("--two-launch", action="store_true",
+                    help="decode: the step as nc_qk_norm_rope_append_fp8 + nc_decode_attn_fp8 (the same bits)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="decode workloads: skip the config-5 end-to-end decode tokens/s part of the metric")
     args = ap.parse_args()
@@ -459,7 +464,7 @@ def main():
 
     import torch
 
-    from nanochat_amd.attention import decode_attention, decode_workspace_bytes, qk_norm_rope_append
+    from nanochat_amd.attention import decode_attention, decode_step, decode_workspace_bytes, qk_norm_rope_append
     from nanochat_amd.kv_cache import PagedKVCache
     from nanochat_amd.rotary import rotary_tables
     from nanochat_amd.workloads import DECODE, decode_inputs
@@ -498,19 +503,23 @@ def main():
     seq_lens = ctx + 1
     q_out = torch.empty(B, 1, Hq, 128, dtype=torch.bfloat16, device=dev)
     out = torch.empty(B, Hq, 128, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(max(1, decode_workspace_bytes(B, Hq, Hkv, inp["max_seq_len"], -1)),
+    ws = torch.zeros(max(1, decode_workspace_bytes(B, Hq, Hkv, inp["max_seq_len"], -1)),
                      dtype=torch.uint8, device=dev)
 
-    def append():
-        qk_norm_rope_append(qkv, Hq, cache, table, ctx, gain, gain, cos, sin, q_out=q_out)
+    if args.two_launch:
+        def step():
+            qk_norm_rope_append(qkv, Hq, cache, table, ctx, gain, gain, cos, sin, q_out=q_out)
+            decode_attention(q_out.view(B, Hq, 128), cache, table, seq_lens, inp["max_seq_len"],
+                             workers=args.workers, out=out, workspace=ws)
+    else:
+        qkv_rows = qkv.view(B, -1)
 
-    def attend():
-        decode_attention(q_out.view(B, Hq, 128), cache, table, seq_lens, inp["max_seq_len"],
-                         workers=args.workers, out=out, workspace=ws)
+        def step():
+            decode_step(qkv_rows, Hq, cache, table, seq_lens, gain, gain, cos, sin, inp["max_seq_len"],
+                        workers=args.workers, out=out, workspace=ws)
 
     for _ in range(args.warmup):
-        append()
-        attend()
+        step()
     torch.cuda.synchronize()
 
     # timed region: K whole steps between two events on the launch stream
@@ -518,28 +527,26 @@ def main():
     torch.cuda.synchronize()
     start.record()
     for _ in range(args.steps):
-        append()
-        attend()
+        step()
     stop.record()
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(stop) / args.steps
 
-    # per-launch duration of the dominant entry point (split-K attention + its combine), events per launch
+    # per-launch duration of the step's kernel (one launch; two with --two-launch), events per step
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     for a, b in evs:
-        append()
         a.record()
-        attend()
+        step()
         b.record()
     torch.cuda.synchronize()
     attn_ms = sorted(a.elapsed_time(b) for a, b in evs)
     attn_mean_ms = sum(attn_ms) / len(attn_ms)
 
     attn_b = attention_bytes(inp["ctx_lens"].tolist(), Hq, Hkv)
-    step_b = attn_b + append_bytes(B, Hq, Hkv)
+    step_b = attn_b + append_bytes(B, Hkv)
     value = step_b / (ms_step * 1e-3) / 1e9
-    achieved = attn_b / (attn_mean_ms * 1e-3) / 1e9
-    traffic = traffic_from_profiles("decode_attn", args.workload)
+    achieved = step_b / (attn_mean_ms * 1e-3) / 1e9
+    traffic = traffic_from_profiles("decode_step", args.workload)
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -554,17 +561,20 @@ def main():
         "dtype": "fp8e4m3 KV, fp8 QK^T and bf16 PV MFMA, fp32 softmax",
         "data": "synthetic (seeded N(0,1) bf16, 1% 8-sigma outliers, random-permutation block table)",
         "config": {"workload": f"{w.name}: {w.description}", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
-                   "keys_per_seq": inp["max_seq_len"], "page_size": 16, "step": "fused QK-norm/RoPE fp8 append + "
-                   "split-K decode attention", "workers": args.workers or "auto"},
+                   "keys_per_seq": inp["max_seq_len"], "page_size": 16,
+                   "step": ("QK-norm/RoPE fp8 append, then split-K decode attention (two launches)" if args.two_launch
+                            else "fused decode step: QK-norm/RoPE fp8 append + split-K decode attention, one launch"),
+                   "workers": args.workers or "auto"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "decode_tokens_per_s_per_layer": round(B / (ms_step * 1e-3), 1),
-        "attn_ms_mean": round(attn_mean_ms, 5),
-        "attn_ms_p10_p50_p90": [round(attn_ms[len(attn_ms) // 10], 5), round(attn_ms[len(attn_ms) // 2], 5),
-                                round(attn_ms[9 * len(attn_ms) // 10], 5)],
+        "launch_ms_mean": round(attn_mean_ms, 5),
+        "launch_ms_p10_p50_p90": [round(attn_ms[len(attn_ms) // 10], 5), round(attn_ms[len(attn_ms) // 2], 5),
+                                  round(attn_ms[9 * len(attn_ms) // 10], 5)],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "nc_decode_attn_fp8 (decode_kernel + decode_combine_kernel)",
-                     "bytes_per_launch": attn_b},
+                     "kernel": ("qk_norm_rope append_kernel + decode_kernel<false>" if args.two_launch
+                                else "nc_decode_step_fp8 (decode_kernel<true>)"),
+                     "bytes_per_launch": step_b},
     }
     if args.cpu_seqs > 0:
         result["cpu_baseline"] = cpu_baseline(w, inp, args.cpu_seqs)

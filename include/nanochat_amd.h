@@ -148,8 +148,11 @@ int nc_qk_norm_rope_append_fp8(const void *qkv, long long token_stride, int B, i
                                const int32_t *block_table, int max_pages, void *k_pages, void *v_pages,
                                float *kv_scale, int num_pages, void *stream);
 
-/* Workspace bytes nc_decode_attn_fp8 needs for these sizes (0 for unsupported sizes): fp32 partial results and
- * per-(sequence, KV head) metadata, written by every call before it is read (no initialization needed). */
+/* Workspace bytes nc_decode_attn_fp8 and nc_decode_step_fp8 need for these sizes (0 for unsupported sizes): fp32
+ * partial results from its start and, in its last 1/256, one int32 arrival count per (sequence, KV head). The
+ * workspace must be zero-filled before its first call and passed with the same workspace_bytes to every call: the
+ * counts' place depends on that size alone, partials never go there and every call returns the counts it used to
+ * zero, so one zero fill serves any number of calls of any sizes that fit, ordered on one stream. */
 size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int window);
 
 /*
@@ -159,11 +162,12 @@ size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int wi
  * The current token must already be appended (nc_kv_append_fp8 / nc_qk_norm_rope_append_fp8).
  * q: bf16 [B][Hq][128]; out: bf16 [B][Hq][128]; seq_lens: int32 [B] (<= 0: inactive, output zeros; more
  * than max_seq_len: output NaN); max_seq_len <= max_pages * 16; B <= 4096.
- * Work split: a (sequence, KV head)'s keys are cut at every multiple of 1,024 positions and each piece is one
- * work item with its own softmax state; pieces of one sequence are merged in position order by a second kernel.
- * The split points depend on nothing but the sequence's own length, so its output bits do not depend on the
- * other sequences of the launch, on its place in the batch or on `workers` (waves taking the items; 0: every
- * wave slot of the device). The workspace must hold nc_decode_workspace_bytes.
+ * Work split: a (sequence, KV head)'s keys are cut at every multiple of 1,024 positions (a last piece under 256
+ * positions joins the one before it) and each piece is one work item with its own softmax state; the wave that finishes a unit's last piece merges its pieces in position
+ * order, in the same launch (one kernel). The split points depend on nothing but the sequence's own length, so its
+ * output bits do not depend on the other sequences of the launch, on its place in the batch or on `workers` (waves
+ * taking the items; 0: every wave slot of the device). The workspace (at least nc_decode_workspace_bytes) must be
+ * zero-filled before its first use and keep one workspace_bytes value across calls.
  * A block-table entry outside [0, num_pages) makes that sequence's output NaN instead of reading outside
  * the pool.
  */
@@ -171,6 +175,27 @@ int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, 
                        const int32_t *block_table, int max_pages, int num_pages,
                        const int32_t *seq_lens, int max_seq_len, int B, int Hq, int Hkv, int window, float sm_scale,
                        int workers, void *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * The fused decode step: nc_qk_norm_rope_append_fp8 with T = 1 followed by nc_decode_attn_fp8, in one launch, with
+ * the same results bit for bit (query rows, cache bytes and scales, attention output). Replaces the reference's
+ * k_prologue + k_attn pair of a decode step (model/kernels/decode.cu:551-675, launched at 861-863). Sequence b's
+ * token sits at position p = seq_lens[b] - 1 (seq_lens <= 0: inactive, nothing appended, output zeros); its row of
+ * qkv (bf16 [B][(Hq + 2 Hkv) 128] at token_stride elements) is normed, rotated (q_gain, k_gain, cos, sin as in
+ * nc_qk_norm_rope_append_fp8; rope_len >= max_seq_len) and, when ve is not NULL, its value row gets the value
+ * embedding of token ve_tokens[b] (ve bf16 [vocab][C], ve_gate fp32 [Hkv][C], ve_h bf16 [B][C] the layer's normed
+ * input; v += 2 sigmoid(ve_gate[kvh] . h) ve[token][kvh 128 ..]); k and v are quantized into the cache and q goes to
+ * q_out (bf16 [B][Hq][128]) unless q_out is NULL; then the query attends as in nc_decode_attn_fp8. A sequence longer
+ * than max_seq_len gets NaN and no append. The page receiving a sequence's token must not appear in another
+ * sequence's block-table row (the work item that streams that page takes the token from registers while it stores
+ * it). Workspace as for nc_decode_attn_fp8.
+ */
+int nc_decode_step_fp8(const void *qkv, long long token_stride, int B, int Hq, int Hkv, const int32_t *seq_lens,
+                       const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
+                       void *q_out, const void *ve_h, const void *ve, const float *ve_gate, const int32_t *ve_tokens,
+                       int C, const int32_t *block_table, int max_pages, void *k_pages, void *v_pages, float *kv_scale,
+                       int num_pages, int max_seq_len, int window, float sm_scale, int workers, void *out,
+                       void *workspace, size_t workspace_bytes, void *stream);
 
 /* Bytes of the static device workspace of nc_decode_attn_fp8_noalloc (one array per GPU, held until the process
  * ends). */

@@ -21,6 +21,7 @@
 #include <mutex>
 
 #include "nc_device.h"
+#include "nc_row.h"
 #include "nanochat_amd.h"
 #include "nc_internal.h"
 
@@ -48,8 +49,9 @@ struct AttnArgs {
     int max_len;              /* decode: the longest sequence the launch accepts (its workspace bound) */
     float *part_o;            /* decode partials [items][G][128] */
     float *part_ml;           /* [items][G][2]: reference max (log2 domain), sum */
-    int *meta;                /* [B*Hkv][2]: first item and chunk count of each (sequence, KV head) */
+    int *arrived;             /* [B*Hkv]: chunks of each (sequence, KV head) finished so far; zero between launches */
     uint16_t *out;            /* [B][T][Hq][128] bf16 */
+    StepArgs step;            /* the fused decode step's append (decode_kernel<true>) */
 };
 
 /* A wave's running state for NT tiles of 16 query columns; lane (g, c) = (lane >> 4, lane & 15) holds column c
@@ -95,18 +97,16 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8 &a, const i32x8 &b, int sc
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, scale_b);   /* A: unit scale */
 }
 
-/* Stages NT rows (NULL: zeros) as QOp. Every lane of the wave must call it (a column's maximum combines its four row
- * groups). */
+/* QOp of NT tiles from this lane's raw bf16 (raw[t][cc] = dims 32 g + 8 cc .. + 7 of its column in tile t). Every lane
+ * of the wave must call it (a column's maximum combines its four row groups). */
 template <int NT>
-__device__ __forceinline__ void load_q8(const uint16_t *const (&rows)[NT], int g, QOp (&q)[NT]) {
-    uint4 raw[NT][4];
+__device__ __forceinline__ void q8_from_raw(const uint4 (&raw)[NT][4], QOp (&q)[NT]) {
     float amax[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         amax[t] = 0.0f;
 #pragma unroll
         for (int cc = 0; cc < 4; cc++) {
-            raw[t][cc] = rows[t] ? *reinterpret_cast<const uint4 *>(rows[t] + g * 32 + cc * 8) : uint4{0u, 0u, 0u, 0u};
             const uint32_t w[4] = {raw[t][cc].x, raw[t][cc].y, raw[t][cc].z, raw[t][cc].w};
 #pragma unroll
             for (int i = 0; i < 4; i++)
@@ -142,6 +142,18 @@ __device__ __forceinline__ void load_q8(const uint16_t *const (&rows)[NT], int g
             }
         }
     }
+}
+
+/* Stages NT rows (NULL: zeros) as QOp; every lane of the wave must call it. */
+template <int NT>
+__device__ __forceinline__ void load_q8(const uint16_t *const (&rows)[NT], int g, QOp (&q)[NT]) {
+    uint4 raw[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++)
+            raw[t][cc] = rows[t] ? *reinterpret_cast<const uint4 *>(rows[t] + g * 32 + cc * 8) : uint4{0u, 0u, 0u, 0u};
+    q8_from_raw<NT>(raw, q);
 }
 
 /* Scores S^T (keys 4g + i of one page, column c of tile t) = K Q^T for every tile from one page's two K loads
@@ -378,6 +390,11 @@ __device__ __forceinline__ void attend_pages(const AttnArgs &a, const int32_t *b
  * wait for every load in flight). */
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
+/* s_waitcnt operands (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8), expcnt and lgkmcnt left
+ * at their maxima */
+constexpr int VMCNT0 = 0x0F70;    /* vmcnt(0) */
+constexpr int VMCNT12 = 0x0F7C;   /* vmcnt(12): all but the 12 most recent vector memory operations complete */
+
 /* A descriptor over `bytes` bytes from p, p the same in every lane (its halves are read from the first lane, so the
  * descriptor lives in scalar registers and no load needs a per-lane loop). */
 __device__ __forceinline__ Rsrc page_rsrc(const void *p, int bytes) {
@@ -393,13 +410,16 @@ __device__ __forceinline__ uint4 bload_nt(Rsrc r, int off) {
     return uint4{v[0], v[1], v[2], v[3]};
 }
 
-/* A wave's staged block-table entries of one chunk: lane j holds entry j (at most SPLIT_PAGES = 64 entries). Entry e
- * is read by v_readlane into a scalar register: no vector register or LDS access in the pair loop. */
+/* A wave's staged block-table entries of one chunk: lane j holds entries j (v) and 64 + j (v2), at most 128. Entry e
+ * (wave-uniform) is read by v_readlane into a scalar register: no vector register or LDS access in the pair loop. */
 struct TabRegs {
-    int v;
+    int v, v2;
 };
 
-__device__ __forceinline__ int tab_entry(const TabRegs &t, int e) { return __builtin_amdgcn_readlane(t.v, e); }
+__device__ __forceinline__ int tab_entry(const TabRegs &t, int e) {
+    const int lo = __builtin_amdgcn_readlane(t.v, e & (WAVE - 1)), hi = __builtin_amdgcn_readlane(t.v2, e & (WAVE - 1));
+    return e < WAVE ? lo : hi;
+}
 
 __device__ __forceinline__ PairAddr pair_addr_tab(const AttnArgs &a, const TabRegs &tab, int tab0, int kvh, int lpa,
                                                   int end, bool &bad) {
@@ -442,27 +462,29 @@ __device__ __forceinline__ void pair_from_regs(const AttnArgs &a, const PairAddr
 }
 
 /* Two register sets rotate by name (the loop is unrolled by two): a pair's K and V are issued as the pair before it
- * starts computing, so a whole pair's loads stay in flight behind every pair's math and no copy waits on a load. */
+ * starts computing, so a whole pair's loads stay in flight behind every pair's math and no copy waits on a load.
+ * The pass's first pair (c0, k0, v0: pages lpa0, lpa0 + 1) is issued by the caller, before it stages its query, so
+ * the query's latency hides behind the first loads. lpa0 < end.
+ */
 template <int NT>
 __device__ __forceinline__ void attend_pages_tab(const AttnArgs &a, const TabRegs &tab, int tab0, int kvh, int lpa0,
                                                  int end, const KeyBounds<NT> &kb, const QOp (&qb)[NT],
-                                                 WaveState<NT> &st, int lane) {
+                                                 WaveState<NT> &st, int lane, PairAddr c0, PairRegs k0, PairRegs v0,
+                                                 bool fence_stores) {
     /* wave-uniform in scalar registers, so a pair's address math is scalar and borrows no vector register a load in
      * flight still owns */
     lpa0 = __builtin_amdgcn_readfirstlane(lpa0);
     end = __builtin_amdgcn_readfirstlane(end);
     kvh = __builtin_amdgcn_readfirstlane(kvh);
     tab0 = __builtin_amdgcn_readfirstlane(tab0);
-    if (lpa0 >= end) return;
-    PairAddr c0 = pair_addr_tab(a, tab, tab0, kvh, lpa0, end, st.bad), c1;
-    PairRegs k0, v0, k1, v1;
-    load_pair_b(a.k_pages, a.kv_scale, c0, true, lane, k0);
-    load_pair_b(a.v_pages, a.kv_scale + PAGE, c0, true, lane, v0);
+    bool more1 = lpa0 + 2 < end;
+    PairAddr c1 = pair_addr_tab(a, tab, tab0, kvh, more1 ? lpa0 + 2 : lpa0, end, st.bad);
+    PairRegs k1, v1;
+    load_pair_b(a.k_pages, a.kv_scale, c1, more1, lane, k1);
+    load_pair_b(a.v_pages, a.kv_scale + PAGE, c1, more1, lane, v1);
+    /* the caller's stores (issued before this second pair's 12 loads) complete before any later page load issues */
+    if (fence_stores) __builtin_amdgcn_s_waitcnt(VMCNT12);
     for (int lpa = lpa0;; lpa += 4) {
-        const bool more1 = lpa + 2 < end;
-        c1 = pair_addr_tab(a, tab, tab0, kvh, more1 ? lpa + 2 : lpa, end, st.bad);
-        load_pair_b(a.k_pages, a.kv_scale, c1, more1, lane, k1);
-        load_pair_b(a.v_pages, a.kv_scale + PAGE, c1, more1, lane, v1);
         pair_from_regs<NT>(a, c0, k0, v0, kb, qb, st, lane);
         if (!more1) break;
         const bool more0 = lpa + 4 < end;
@@ -471,14 +493,21 @@ __device__ __forceinline__ void attend_pages_tab(const AttnArgs &a, const TabReg
         load_pair_b(a.v_pages, a.kv_scale + PAGE, c0, more0, lane, v0);
         pair_from_regs<NT>(a, c1, k1, v1, kb, qb, st, lane);
         if (!more0) break;
+        more1 = lpa + 6 < end;
+        c1 = pair_addr_tab(a, tab, tab0, kvh, more1 ? lpa + 6 : lpa + 4, end, st.bad);
+        load_pair_b(a.k_pages, a.kv_scale, c1, more1, lane, k1);
+        load_pair_b(a.v_pages, a.kv_scale + PAGE, c1, more1, lane, v1);
     }
 }
 
 /* Split points of decode: a (sequence, KV head) unit's keys are cut at every multiple of SPLIT_PAGES pages (1,024
- * positions), whatever the rest of the batch holds, so a sequence's sums (and its output bits) depend only on its own
- * query, keys and length. */
+ * positions), except that a last piece of fewer than MIN_TAIL pages joins the chunk before it (a sequence one token
+ * past a multiple of 1,024 would otherwise spend a work item, and a merge step, on one page). The cuts depend on
+ * nothing but the sequence's own length, whatever the rest of the batch holds, so a sequence's sums (and its output
+ * bits) depend only on its own query, keys and length. */
 constexpr int SPLIT_PAGES = 64;
-static_assert(SPLIT_PAGES <= WAVE, "a chunk's block-table entries are staged one per lane (TabRegs)");
+constexpr int MIN_TAIL = 16;
+static_assert(SPLIT_PAGES + MIN_TAIL - 1 <= 2 * WAVE, "a chunk's block-table entries are staged in two lanes' worth");
 
 /* Key range [begin, p] of a sequence of L keys and its logical pages [pg0, pg0 + npages); npages = 0 for an
  * inactive sequence (L <= 0) or one longer than max_len (the launch's bound; its output is NaN). */
@@ -490,12 +519,13 @@ __device__ __forceinline__ int decode_pages(const AttnArgs &a, int L, int &begin
     return p / PAGE + 1 - pg0;
 }
 
-/* How a unit's logical pages [pg0, pg0 + np) split: chunks c = pg0 / SPLIT_PAGES .. (pg0 + np - 1) / SPLIT_PAGES,
- * chunk c covering [max(pg0, c S), min(pg0 + np, (c + 1) S)) (S = SPLIT_PAGES). A chunk is full when it covers S pages;
- * only the first (when pg0 is not a multiple of S) and the last (when the end is not) can be partial. */
+/* How a unit's logical pages [pg0, e) split (S = SPLIT_PAGES, c0 = pg0 / S): chunk j covers [pg0 or (c0 + j) S,
+ * (c0 + j + 1) S or e), the first starting at pg0 and the last ending at e; the pieces are cut at the multiples of S
+ * and a last piece shorter than MIN_TAIL joins the one before it. A chunk is full when it covers at least S pages; only
+ * the first and the last can be partial. */
 struct UnitSplit {
     int pg0, np, nch;   /* pages, chunks */
-    int lead;           /* 1: chunk 0 is partial */
+    int p0;             /* 1: chunk 0 is partial */
     int nfull, npart;   /* full and partial chunks */
 };
 
@@ -503,14 +533,24 @@ __device__ __forceinline__ UnitSplit unit_split(const AttnArgs &a, int L, int &b
     UnitSplit u = {0, 0, 0, 0, 0, 0};
     const int np = decode_pages(a, L, begin, u.pg0);
     if (np <= 0) return u;
-    const int e = u.pg0 + np;
+    const int e = u.pg0 + np, c0 = u.pg0 / SPLIT_PAGES;
     u.np = np;
-    u.nch = (e - 1) / SPLIT_PAGES - u.pg0 / SPLIT_PAGES + 1;
-    u.lead = u.pg0 % SPLIT_PAGES != 0;
-    const int trail = e % SPLIT_PAGES != 0;
-    u.npart = u.nch == 1 ? ((u.lead || trail) ? 1 : 0) : u.lead + trail;
+    const int pieces = (e - 1) / SPLIT_PAGES - c0 + 1;
+    const int tail = e - max(u.pg0, ((e - 1) / SPLIT_PAGES) * SPLIT_PAGES);
+    u.nch = pieces - (pieces >= 2 && tail < MIN_TAIL);
+    const int size0 = (u.nch == 1 ? e : (c0 + 1) * SPLIT_PAGES) - u.pg0;
+    const int sizel = e - (c0 + u.nch - 1) * SPLIT_PAGES;
+    u.p0 = size0 < SPLIT_PAGES;
+    u.npart = u.p0 + (u.nch > 1 && sizel < SPLIT_PAGES);
     u.nfull = u.nch - u.npart;
     return u;
+}
+
+/* Logical pages [first, last) of chunk j. */
+__device__ __forceinline__ void chunk_pages(const UnitSplit &u, int j, int &first, int &last) {
+    const int c = u.pg0 / SPLIT_PAGES + j;
+    first = j == 0 ? u.pg0 : c * SPLIT_PAGES;
+    last = j == u.nch - 1 ? u.pg0 + u.np : (c + 1) * SPLIT_PAGES;
 }
 
 __device__ __forceinline__ void store_bf16x4(uint16_t *dst, const float *v) {
@@ -532,21 +572,244 @@ __device__ __forceinline__ int find_sequence(const int *cum, int B, int k) {
     return lo;
 }
 
+/* Rows of the sequences with nothing to attend (found by their empty chunk ranges): zeros for an inactive sequence
+ * (L <= 0), NaN for one longer than the launch's bound. Wave `id` of `waves` takes sequences id, id + waves, ... */
+__device__ __forceinline__ void decode_fill_rows(const AttnArgs &a, const int *cf, const int *cp, int id, int waves,
+                                                 int lane) {
+    for (int b = id; b < a.B; b += waves) {
+        if (cf[b + 1] != cf[b] || cp[b + 1] != cp[b]) continue;
+        const uint32_t w = a.seq_lens[b] <= 0 ? 0u : 0x7FC07FC0u;
+        uint2 *dst = reinterpret_cast<uint2 *>(a.out + (long long)b * a.Hq * HEAD_DIM);
+        for (int i = lane; i < a.Hq * HEAD_DIM / 4; i += WAVE) dst[i] = uint2{w, w};
+    }
+}
+
+/* The fused step's append work for one item of unit (b, kvh), the token at position p. Every item normalizes and
+ * rotates the unit's G query rows into q_lds (bf16, row h at h * 128). The item that streams the token (own: the
+ * unit's last chunk, the only one holding it) also normalizes and rotates k, mixes the value embedding into v,
+ * quantizes both and stores codes and scales into the cache (unless the page is outside the pool); it also writes
+ * q_out. Each row is the append kernel's arithmetic (nc_row.h), so the cache bytes and query bits equal those of the
+ * separate append. Every load of the item is issued before any of its arithmetic (one round trip); the raw query
+ * rows go through q_lds, where each lane's pair (dims l, l + 64) of a row is read and overwritten by the same lane.
+ *
+ * The pass reads the token's bytes back from the cache, so they must be stored before its page is loaded. The pass's
+ * first page pair is issued before these stores (the query's work hides behind its latency) and its second right
+ * after them; then the pass waits until all but the second pair's 12 loads have completed (vector memory operations
+ * of a wave complete in issue order, one counter for loads and stores), which the first pair's use needs anyway, so
+ * every later page load is issued after the stores have completed. A token in the first two pairs (first 4 pages)
+ * is the exception: the caller then issues the first pair without access (zero-range descriptors), waits here for
+ * the stores (`wait`) and issues it again. No other pass reads the token's page. */
+constexpr int MAX_G = 16;
+constexpr int Q_CHUNKS = MAX_G * HEAD_DIM * 2 / (16 * WAVE);   /* 16-byte loads a lane for the unit's query rows */
+
+/* What step_rows reads, fetched before the pass's first page pair is issued: vector memory operations of a wave
+ * complete in issue order, so a wait for anything issued after the page loads would wait for them too. */
+struct StepLoads {
+    uint4 raw[Q_CHUNKS];            /* the unit's raw query rows, 16 bytes a lane */
+    float cr, sr, g1, g2, kg1, kg2; /* rotation of position p and gains (dims l, l + 64) */
+    uint16_t kx1, kx2, vx1, vx2;    /* own: the token's k and v rows (dims l, l + 64) */
+};
+
+/* All through buffer (not flat) accesses: a flat access may address LDS, which would make the LDS accesses below wait
+ * for every vector memory operation in flight. */
+__device__ __forceinline__ StepLoads step_fetch(const AttnArgs &a, const StepArgs &s, int b, int kvh, int p, bool own,
+                                                int lane) {
+    StepLoads f;
+    const uint16_t *row = s.qkv + (long long)b * s.token_stride;
+    const Rsrc rq = page_rsrc(row + kvh * a.G * HEAD_DIM, a.G * HEAD_DIM * 2);
+#pragma unroll
+    for (int i = 0; i < Q_CHUNKS; i++) {   /* chunks past the G rows read zeros through the range (no access) */
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rq, (i * WAVE + lane) * 16, 0, 0);
+        f.raw[i] = uint4{v[0], v[1], v[2], v[3]};
+    }
+    const Rsrc rc = page_rsrc(s.cos + (long long)p * HALF, HALF * 4), rs = page_rsrc(s.sin + (long long)p * HALF, HALF * 4);
+    const Rsrc rqg = page_rsrc(s.q_gain, HEAD_DIM * 4), rkg = page_rsrc(s.k_gain, own ? HEAD_DIM * 4 : 0);
+    f.cr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, lane * 4, 0, 0));
+    f.sr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, lane * 4, 0, 0));
+    f.g1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rqg, lane * 4, 0, 0));
+    f.g2 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rqg, (lane + HALF) * 4, 0, 0));
+    f.kg1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rkg, lane * 4, 0, 0));
+    f.kg2 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rkg, (lane + HALF) * 4, 0, 0));
+    /* own: the token's k and v rows (zero-range descriptors otherwise: no access) */
+    const Rsrc rk = page_rsrc(row + (a.Hq + kvh) * HEAD_DIM, own ? HEAD_DIM * 2 : 0);
+    const Rsrc rv = page_rsrc(row + (a.Hq + a.Hkv + kvh) * HEAD_DIM, own ? HEAD_DIM * 2 : 0);
+    f.kx1 = __builtin_amdgcn_raw_buffer_load_b16(rk, lane * 2, 0, 0);
+    f.kx2 = __builtin_amdgcn_raw_buffer_load_b16(rk, (lane + HALF) * 2, 0, 0);
+    f.vx1 = __builtin_amdgcn_raw_buffer_load_b16(rv, lane * 2, 0, 0);
+    f.vx2 = __builtin_amdgcn_raw_buffer_load_b16(rv, (lane + HALF) * 2, 0, 0);
+    return f;
+}
+
+__device__ __forceinline__ void step_rows(const AttnArgs &a, const StepArgs &s, const StepLoads &f, int b, int kvh,
+                                          int p, bool own, int page, bool wait, uint16_t *q_lds, int lane) {
+#pragma unroll
+    for (int i = 0; i < Q_CHUNKS; i++)
+        if (i * WAVE * 8 < a.G * HEAD_DIM) *reinterpret_cast<uint4 *>(q_lds + (i * WAVE + lane) * 8) = f.raw[i];
+    /* unrolled (forward branches only): a loop here would make the compiler wait for every load in flight at its
+     * entry, the first page pair included */
+#pragma unroll
+    for (int h = 0; h < MAX_G; h++) {
+        if (h >= a.G) break;
+        float y1, y2;
+        norm_rope_pair(bf16_to_f32(q_lds[h * HEAD_DIM + lane]), bf16_to_f32(q_lds[h * HEAD_DIM + lane + HALF]), f.g1,
+                       f.g2, f.cr, f.sr, y1, y2);
+        const uint16_t q1 = f32_to_bf16(y1), q2 = f32_to_bf16(y2);
+        q_lds[h * HEAD_DIM + lane] = q1;
+        q_lds[h * HEAD_DIM + lane + HALF] = q2;
+        if (own && s.q_out) {
+            const Rsrc ro = page_rsrc(s.q_out + ((long long)b * a.Hq + kvh * a.G + h) * HEAD_DIM, HEAD_DIM * 2);
+            __builtin_amdgcn_raw_buffer_store_b16(q1, ro, lane * 2, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(q2, ro, (lane + HALF) * 2, 0, 0);
+        }
+    }
+    if (!own) return;
+    float y1, y2;
+    norm_rope_pair(bf16_to_f32(f.kx1), bf16_to_f32(f.kx2), f.kg1, f.kg2, f.cr, f.sr, y1, y2);
+    const float k1 = bf16_to_f32(f32_to_bf16(y1)), k2 = bf16_to_f32(f32_to_bf16(y2));
+    float v1 = bf16_to_f32(f.vx1), v2 = bf16_to_f32(f.vx2);
+    if (s.ve)
+        ve_mix_pair(s.ve_h + (long long)b * s.C, s.ve_gate + (long long)kvh * s.C, s.C,
+                    s.ve + (long long)s.ve_tokens[b] * s.C + kvh * HEAD_DIM, lane, v1, v2);
+    uint32_t kc1, kc2, vc1, vc2;
+    const int slot = p % PAGE;
+    const float ks = quantize_pair(k1, k2, kc1, kc2);
+    const float vs = quantize_pair(v1, v2, vc1, vc2);
+    if ((unsigned)page >= (unsigned)a.num_pages) return;   /* the pass reports the bad entry */
+    const long long at = (long long)page * a.Hkv + kvh;
+    const Rsrc rkp = page_rsrc(s.k_pages + at * PAGE_BYTES, PAGE_BYTES);
+    const Rsrc rvp = page_rsrc(s.v_pages + at * PAGE_BYTES, PAGE_BYTES);
+    const Rsrc rsc = page_rsrc(s.kv_scale + at * 2 * PAGE, 2 * PAGE * 4);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)kc1, rkp, k_page_offset(slot, lane), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)kc2, rkp, k_page_offset(slot, lane + HALF), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)vc1, rvp, v_page_offset(slot, lane), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)vc2, rvp, v_page_offset(slot, lane + HALF), 0, 0);
+    if (lane == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ks), rsc, slot * 4, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(vs), rsc, (PAGE + slot) * 4, 0, 0);
+    }
+    if (wait) __builtin_amdgcn_s_waitcnt(VMCNT0);
+}
+
+/* Partials cross work-groups (and XCDs, whose L2 caches are not coherent with each other) inside one launch. They
+ * are written and read with the sc1 cache policy, the encoding of agent-scope atomic stores and loads (coherent
+ * across the device: stores write through, loads miss stale lines), and the writer waits for its stores to complete
+ * (vmcnt 0) before it counts its chunk, so the wave that sees the last count reads every partial as written. This
+ * costs no cache-wide writeback or invalidate, which an agent-scope fence would (measured: twice the kernel time). */
+constexpr int SC1 = 16;   /* cache-policy operand of the buffer builtins: sc1 */
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void part_store(Rsrc r, int off, const float4 &v) {
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                                                 __float_as_uint(v.w)}, r, off, 0, SC1);
+}
+
+__device__ __forceinline__ f32x4 part_load(Rsrc r, int off) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, SC1);
+    return f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+}
+
+/* A partial slot's two descriptors: O [G][128] and (max, sum) [G][2]. */
+__device__ __forceinline__ void part_rsrc(const AttnArgs &a, long long slot, Rsrc &ro, Rsrc &rm) {
+    ro = page_rsrc(a.part_o + slot * a.G * HEAD_DIM, a.G * HEAD_DIM * 4);
+    rm = page_rsrc(a.part_ml + slot * a.G * 2, a.G * 2 * 4);
+}
+
+/* The log-sum-exp (base 2) merge of a unit's nch partials, in chunk order, into its bf16 rows. The unit's G x 128
+ * outputs are split into 16-byte pieces (piece p: column p / 32, dims 4 (p % 32) .. + 3); a call merges pieces
+ * piece0 .. piece0 + 64 P - 1, lane l taking piece0 + l, piece0 + l + 64, ..., so every lane works for any G. Chunks are taken NB at a time with all their loads issued
+ * together (the merge is latency-bound: it runs when the unit's last chunk ends): a batch raises the running maximum M
+ * to the batch's largest chunk maximum, rescales the running (sum, O) by exp2(M_old - M) and adds each chunk's
+ * (sum, O) times exp2(m_j - M), in chunk order. The order depends on nch alone, so the result does not depend on
+ * which wave merges. Out-of-range pieces and chunks read zeros through the descriptors' ranges and store nothing. */
+template <int P, int NB>
+__device__ __forceinline__ void merge_pieces(const AttnArgs &a, long long slot0, int nch, long long row0, int piece0,
+                                             int lane) {
+    const int pieces = a.G * (HEAD_DIM / 4);
+    float M[P], L[P];
+    f32x4 O[P];
+#pragma unroll
+    for (int k = 0; k < P; k++) {
+        M[k] = -INFINITY;
+        L[k] = 0.0f;
+        O[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    /* one descriptor pair over the unit's nch slots: chunk j's O at j G 512 bytes, its (max, sum) at j G 8 */
+    const Rsrc ro = page_rsrc(a.part_o + slot0 * a.G * HEAD_DIM, nch * a.G * HEAD_DIM * 4);
+    const Rsrc rm = page_rsrc(a.part_ml + slot0 * a.G * 2, nch * a.G * 2 * 4);
+    for (int j0 = 0; j0 < nch; j0 += NB) {
+        f32x4 oj[NB][P];
+        float2 ml[NB][P];
+#pragma unroll
+        for (int jj = 0; jj < NB; jj++) {
+#pragma unroll
+            for (int k = 0; k < P; k++) {
+                const int p = piece0 + lane + WAVE * k;
+                oj[jj][k] = part_load(ro, (j0 + jj) * a.G * HEAD_DIM * 4 + p * 16);
+                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rm, ((j0 + jj) * a.G + (p >> 5)) * 8, 0, SC1);
+                ml[jj][k] = float2{__uint_as_float(w[0]), __uint_as_float(w[1])};
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < P; k++) {
+            float mb = M[k];
+#pragma unroll
+            for (int jj = 0; jj < NB; jj++)
+                if (j0 + jj < nch) mb = fmaxf(mb, ml[jj][k].x);
+            const float alpha = M[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M[k] - mb);
+            L[k] *= alpha;
+            O[k] *= alpha;
+            M[k] = mb;
+#pragma unroll
+            for (int jj = 0; jj < NB; jj++) {
+                if (j0 + jj >= nch) continue;
+                const float w = ml[jj][k].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[jj][k].x - mb);
+                L[k] += ml[jj][k].y * w;
+                O[k] += oj[jj][k] * w;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < P; k++) {
+        const int p = piece0 + lane + WAVE * k;
+        if (p >= pieces) continue;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = O[k][i] / L[k];
+        store_bf16x4(a.out + (row0 + (p >> 5)) * HEAD_DIM + (p & 31) * 4, v);
+    }
+}
+
+/* 128 pieces (4 columns) per pass: one instantiation serves every G, in at most 4 passes. */
+__device__ __forceinline__ void merge_unit(const AttnArgs &a, long long slot0, int nch, long long row0, int lane) {
+    for (int piece0 = 0; piece0 < a.G * (HEAD_DIM / 4); piece0 += 2 * WAVE)
+        merge_pieces<2, 8>(a, slot0, nch, row0, piece0, lane);
+}
+
 /*
  * Split-K decode over fixed chunks. The work items are a unit's chunks (unit = (sequence, KV head)); every item starts
  * from a fresh softmax state and streams only its chunk's pages, so what is computed for an item does not depend on
  * which wave takes it or on what else the launch holds. A unit of one chunk is finished in place (bf16 output); a unit
- * of several leaves one partial per chunk, in slot cum_all[b] + kvh nch + j (the unit-order index of chunk j), and its
- * chunk 0 records (first slot, chunk count) in meta[u] for decode_combine_kernel, which merges them in chunk order.
+ * of several leaves one partial per chunk, in slot cf[b] + cp[b] + kvh nch + j (the unit-order index of chunk j), and
+ * counts its finished chunks in arrived[u]: the wave that finishes the last one merges the partials in chunk order
+ * (merge_unit) and returns the count to zero. Partials are stored and loaded device-coherently (sc1) and complete
+ * before they are counted, so the merging wave sees every other wave's partials whatever CU or XCD ran them; no
+ * second launch is needed.
  *
- * Schedule: the full chunks (all SPLIT_PAGES long) are numbered first, then the partial ones, each in (sequence, KV
+ * Schedule: the full chunks (at least SPLIT_PAGES long) are numbered first, then the partial ones, each in (sequence, KV
  * head, chunk) order; item k goes to work-group k % G (G = gridDim.x) and, within it, to wave (k / G) % 4, round
  * k / (4 G). Equal full chunks land one per work-group before any doubles up, and the short partial chunks fill in
  * last: every compute unit streams about the same number of pages (a CU's bandwidth, not a wave's, is the limit once
  * it holds more than one wave), and a wave that finishes early leaves the HBM bandwidth to the others.
+ *
+ * STEP (the fused decode step): the sequence's token at position L - 1 is appended in the same launch (step_rows):
+ * every item normalizes and rotates its query rows from the raw qkv row, and the item holding the token quantizes and
+ * stores its K and V before its pass reads them back.
  */
+template <bool STEP>
 __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
     extern __shared__ int sh_cum[];  /* [2][B + 1]: full, then partial chunks of the sequences < b */
+    __shared__ __align__(16) uint16_t sh_q[WAVES][STEP ? MAX_G * HEAD_DIM : 8];   /* the step's query rows */
+    __shared__ StepArgs sh_step;   /* the step's arguments, read per item (kept in registers they would spill) */
     int *cf = sh_cum, *cp = sh_cum + a.B + 1;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
@@ -577,8 +840,10 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
             run_p += __shfl(vp, WAVE - 1, WAVE);
         }
         if (lane == 0) cf[0] = cp[0] = 0;
+        if (STEP && lane == 0) sh_step = a.step;
     }
     __syncthreads();
+    decode_fill_rows(a, cf, cp, blockIdx.x * WAVES + wave, gridDim.x * WAVES, lane);
     const int NF = cf[a.B], N = NF + cp[a.B];
     const long long G = gridDim.x;
     for (long long kk = blockIdx.x + G * wave; kk < N; kk += 4 * G) {
@@ -590,7 +855,7 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
             us = unit_split(a, a.seq_lens[b], begin);
             const int local = k - cf[b];
             kvh = local / us.nfull;
-            j = local - kvh * us.nfull + us.lead;
+            j = local - kvh * us.nfull + us.p0;
         } else {        /* partial chunk: the first and / or the last of a unit */
             const int k2 = k - NF;
             b = find_sequence(cp, a.B, k2);
@@ -598,29 +863,64 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
             const int local = k2 - cp[b];
             kvh = local / us.npart;
             const int jp = local - kvh * us.npart;
-            j = (us.nch == 1 || (us.lead && jp == 0)) ? 0 : us.nch - 1;
+            j = (us.p0 && jp == 0) ? 0 : us.nch - 1;
         }
         const long long slot = (long long)cf[b] + cp[b] + (long long)kvh * us.nch + j;
         const int L = a.seq_lens[b];
-        const int chunk = us.pg0 / SPLIT_PAGES + j;
-        const int first = max(us.pg0, chunk * SPLIT_PAGES), last = min(us.pg0 + us.np, (chunk + 1) * SPLIT_PAGES);
+        int first, last;
+        chunk_pages(us, j, first, last);
         const long long row0 = (long long)b * a.Hq + kvh * a.G;
-
-        QOp qb[1];
-        const uint16_t *const qrows[1] = {c < a.G ? a.q + (row0 + c) * HEAD_DIM : nullptr};
-        WaveState<1> st;
-        state_init(st);
-        load_q8<1>(qrows, g, qb);
-        st.sl2 = a.scale_log2;
-        KeyBounds<1> kb;
-        kb.lo[0] = kb.full_lo = begin;
-        kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
         const int32_t *bt = a.block_table + (long long)b * a.max_pages;
         TabRegs tab;
         tab.v = first + lane < last ? bt[first + lane] : 0;
-        attend_pages_tab<1>(a, tab, first, kvh, first, last, kb, qb, st, lane);
+        tab.v2 = first + WAVE + lane < last ? bt[first + WAVE + lane] : 0;
+
+        WaveState<1> st;
+        state_init(st);
+        st.sl2 = a.scale_log2;
+        const bool own = j == us.nch - 1, late = STEP && own && (L - 1) / PAGE - first < 4;
+        /* the query's loads first, then the first page pair (see StepLoads) */
+        StepLoads sl;
+        StepArgs sa;
+        uint4 qraw[1][4];
+        if (STEP) {
+            asm volatile("" ::: "memory");   /* sh_step is read here, per item, not hoisted out of the loop */
+            sa = sh_step;
+            sl = step_fetch(a, sa, b, kvh, L - 1, own, lane);
+        } else {
+            const Rsrc rq = page_rsrc(a.q + row0 * HEAD_DIM, a.G * HEAD_DIM * 2);   /* columns c >= G read zeros */
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rq, (c * HEAD_DIM + g * 32 + cc * 8) * 2, 0, 0);
+                qraw[0][cc] = uint4{v[0], v[1], v[2], v[3]};
+            }
+        }
+        PairAddr c0 = pair_addr_tab(a, tab, first, kvh, first, last, st.bad);
+        PairRegs k0, v0;
+        load_pair_b(a.k_pages, a.kv_scale, c0, !late, lane, k0);
+        load_pair_b(a.v_pages, a.kv_scale + PAGE, c0, !late, lane, v0);
+        QOp qb[1];
+        if (STEP) {
+            const int p = L - 1;
+            step_rows(a, sa, sl, b, kvh, p, own, own ? tab_entry(tab, p / PAGE - first) : 0, late, sh_q[wave], lane);
+            uint4 raw[1][4];
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++)
+                raw[0][cc] = c < a.G ? *reinterpret_cast<const uint4 *>(&sh_q[wave][c * HEAD_DIM + g * 32 + cc * 8])
+                                     : uint4{0u, 0u, 0u, 0u};
+            q8_from_raw<1>(raw, qb);
+            if (late) {
+                load_pair_b(a.k_pages, a.kv_scale, c0, true, lane, k0);
+                load_pair_b(a.v_pages, a.kv_scale + PAGE, c0, true, lane, v0);
+            }
+        } else {
+            q8_from_raw<1>(qraw, qb);
+        }
+        KeyBounds<1> kb;
+        kb.lo[0] = kb.full_lo = begin;
+        kb.hi[0] = kb.full_hi = kb.written_hi = L - 1;
+        attend_pages_tab<1>(a, tab, first, kvh, first, last, kb, qb, st, lane, c0, k0, v0, STEP && own);
         st.l[0] = pair_sum32(pair_sum16(st.l[0]));
-        const int u = b * a.Hkv + kvh;
         if (us.nch == 1) {
             if (c < a.G) {
                 uint16_t *dst = a.out + (row0 + c) * HEAD_DIM;
@@ -633,60 +933,32 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
                     store_bf16x4(dst + 16 * t + 4 * g, v);
                 }
             }
-        } else if (c < a.G) {
-            float *po = a.part_o + (slot * a.G + c) * HEAD_DIM;
+            continue;
+        }
+        {
+            Rsrc ro, rm;
+            part_rsrc(a, slot, ro, rm);
+            if (c < a.G) {
 #pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const f32x4 o = st.o[0][t];
-                *reinterpret_cast<float4 *>(po + 16 * t + 4 * g) = float4{st.bad ? NAN : o[0], o[1], o[2], o[3]};
-            }
-            if (g == 0) {
-                a.part_ml[(slot * a.G + c) * 2] = st.bad ? NAN : st.m[0];
-                a.part_ml[(slot * a.G + c) * 2 + 1] = st.l[0];
+                for (int t = 0; t < 8; t++) {
+                    const f32x4 o = st.o[0][t];
+                    part_store(ro, (c * HEAD_DIM + 16 * t + 4 * g) * 4, float4{st.bad ? NAN : o[0], o[1], o[2], o[3]});
+                }
+                if (g == 0)
+                    __builtin_amdgcn_raw_buffer_store_b64(
+                        u32x2{__float_as_uint(st.bad ? NAN : st.m[0]), __float_as_uint(st.l[0])}, rm, c * 8, 0, SC1);
             }
         }
-        if (j == 0 && lane == 0) {  /* the unit's chunk 0: where its partials are, how many */
-            a.meta[2 * u] = (int)slot;
-            a.meta[2 * u + 1] = us.nch;
+        const int u = b * a.Hkv + kvh;
+        __builtin_amdgcn_s_waitcnt(VMCNT0);   /* the partial has reached the coherent level before it is counted */
+        int prior = 0;
+        if (lane == 0) prior = __hip_atomic_fetch_add(a.arrived + u, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prior = __builtin_amdgcn_readfirstlane(prior);
+        if (prior == us.nch - 1) {   /* every other chunk of the unit has published its partial */
+            merge_unit(a, slot - j, us.nch, row0, lane);
+            if (lane == 0) __hip_atomic_store(a.arrived + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-}
-
-/* Grid B*Hq, 128 threads (one per dim): zeros for inactive sequences, NaN for ones past the block table, and
- * the log-sum-exp (base 2) merge of a unit's partials when more than one wave worked on it. */
-__global__ void __launch_bounds__(HEAD_DIM) decode_combine_kernel(AttnArgs a) {
-    const int b = blockIdx.x / a.Hq, h = blockIdx.x % a.Hq, d = threadIdx.x;
-    const long long row = blockIdx.x;
-    const int u = b * a.Hkv + h / a.G, c = h % a.G;
-    /* the unit's partial range is loaded together with the sequence length (neither waits for the other) */
-    const int first = a.meta[2 * u], count = a.meta[2 * u + 1];
-    const int L = a.seq_lens[b];
-    if (L <= 0) {
-        a.out[row * HEAD_DIM + d] = 0;
-        return;
-    }
-    int begin, pg0;
-    if (decode_pages(a, L, begin, pg0) == 0) {
-        a.out[row * HEAD_DIM + d] = (uint16_t)0x7FC0;
-        return;
-    }
-    if (count <= 1) return;  /* finished by its only wave */
-    const float *ml = a.part_ml + ((long long)first * a.G + c) * 2;
-    const float *po = a.part_o + ((long long)first * a.G + c) * HEAD_DIM + d;
-    const long long step = (long long)a.G;
-    /* one pass, online: no load depends on the running state, so unrolled iterations issue together */
-    float m = -INFINITY, ls = 0.0f, o = 0.0f;
-#pragma unroll 4
-    for (int j = 0; j < count; j++) {
-        const float mj = ml[2 * step * j], lj = ml[2 * step * j + 1], oj = po[step * HEAD_DIM * j];
-        const float mn = fmaxf(m, mj);
-        const float fo = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
-        const float fn = mj == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj - mn);
-        ls = ls * fo + lj * fn;
-        o = o * fo + oj * fn;
-        m = mn;
-    }
-    a.out[row * HEAD_DIM + d] = f32_to_bf16(o / ls);
 }
 
 /* Grid (ceil(T / (4 NT tpt)), Hkv, B), 4 waves. A wave owns NT tiles of 16 columns, each tile tpt = 16 / G
@@ -1040,7 +1312,7 @@ static int device_wave_slots() {
     if (!slots[dev]) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, 256,
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<true>, 256,
                                                          2 * (MAX_DECODE_BATCH + 1) * sizeof(int)) != hipSuccess)
             return 2048;
         slots[dev] = max(1, cus * per_cu * WAVES);
@@ -1048,11 +1320,30 @@ static int device_wave_slots() {
     return slots[dev];
 }
 
-/* Workspace layout: partial O [items][G][128] fp32, partial (max, sum) [items][G][2] fp32, then meta [B*Hkv][2]
- * int32, items = item_bound(...). Every launch writes what it later reads. */
+/* Workspace layout. Partial O [items][G][128] fp32 and partial (max, sum) [items][G][2] fp32 from the start (items =
+ * item_bound(...)); the arrival counts, int32 per (sequence, KV head), in the last 1/256 of the workspace (from
+ * count_region(bytes)). Where the counts sit depends on the workspace's size alone and no call writes partials there,
+ * so a workspace zero-filled once and passed with the same size to every call keeps zero counts between calls (each
+ * launch returns the counts it used to zero) whatever the shapes of the calls. Partials are written before they are
+ * read in the same launch. */
+static size_t partial_bytes(int Hq, int Hkv, long long items) {
+    return (size_t)items * (Hq / Hkv) * (HEAD_DIM + 2) * sizeof(float);
+}
+
+static size_t count_region(size_t bytes) { return (bytes - ((bytes >> 8) & ~(size_t)3)) & ~(size_t)3; }
+
+static bool workspace_fits(size_t bytes, int B, int Hq, int Hkv, long long items) {
+    return partial_bytes(Hq, Hkv, items) <= count_region(bytes) &&
+           (size_t)B * Hkv * sizeof(int) <= bytes - count_region(bytes);
+}
+
+/* The smallest multiple of 256 bytes that fits: 256 k with k >= P / 255 (partials below the count region) and
+ * k >= 4 B Hkv (the counts), k a multiple of 4. */
 static size_t workspace_bytes_for(int B, int Hq, int Hkv, long long items) {
-    const size_t G = Hq / Hkv;
-    return (size_t)items * G * (HEAD_DIM + 2) * sizeof(float) + (size_t)B * Hkv * 2 * sizeof(int);
+    const size_t P = partial_bytes(Hq, Hkv, items);
+    size_t k = max((P + 254) / 255, (size_t)B * Hkv * sizeof(int));
+    k = (k + 3) & ~(size_t)3;
+    return 256 * k;
 }
 
 static bool decode_shape_ok(int B, int Hq, int Hkv, int max_seq_len, int window) {
@@ -1060,11 +1351,12 @@ static bool decode_shape_ok(int B, int Hq, int Hkv, int max_seq_len, int window)
            item_bound(B, Hkv, max_seq_len, window) < (1LL << 31);
 }
 
-/* The launch itself (arguments checked by the caller); the workspace holds workspace_bytes_for(item_bound). */
+/* The launch itself (arguments checked by the caller); the workspace holds workspace_bytes_for(item_bound). step:
+ * NULL for attention alone, else the fused step's append inputs (q is then unused). */
 static int launch_decode(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
                          const int32_t *block_table, int max_pages, int num_pages, const int32_t *seq_lens,
                          int max_seq_len, int B, int Hq, int Hkv, int window, float sm_scale, int workers, void *out,
-                         void *workspace, hipStream_t stream) {
+                         void *workspace, size_t workspace_bytes, const StepArgs *step, hipStream_t stream) {
     AttnArgs a = {};
     a.q = (const uint16_t *)q;
     a.k_pages = (const uint8_t *)k_pages; a.v_pages = (const uint8_t *)v_pages;
@@ -1079,18 +1371,32 @@ static int launch_decode(const void *q, const void *k_pages, const void *v_pages
     a.out = (uint16_t *)out;
     a.part_o = (float *)workspace;
     a.part_ml = a.part_o + (size_t)items * a.G * HEAD_DIM;
-    a.meta = (int *)(a.part_ml + (size_t)items * a.G * 2);
+    a.arrived = (int *)((char *)workspace + count_region(workspace_bytes));
     const int grid = (a.workers + WAVES - 1) / WAVES;
-    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(256), 2 * (B + 1) * sizeof(int), stream, a);
-    hipLaunchKernelGGL(decode_combine_kernel, dim3(B * Hq), dim3(HEAD_DIM), 0, stream, a);
+    const size_t lds = 2 * (B + 1) * sizeof(int);
+    if (step) {
+        a.step = *step;
+        hipLaunchKernelGGL(decode_kernel<true>, dim3(grid), dim3(256), lds, stream, a);
+    } else {
+        hipLaunchKernelGGL(decode_kernel<false>, dim3(grid), dim3(256), lds, stream, a);
+    }
     return (int)hipGetLastError();
+}
+
+int decode_step(const StepArgs &step, const void *k_pages, const void *v_pages, const float *kv_scale,
+                const int32_t *block_table, int max_pages, int num_pages, const int32_t *seq_lens, int max_seq_len,
+                int B, int Hq, int Hkv, int window, float sm_scale, void *out, void *workspace, size_t workspace_bytes,
+                hipStream_t stream) {
+    if (!workspace_fits(workspace_bytes, B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window))) return NC_ERR_WORKSPACE;
+    return launch_decode(nullptr, k_pages, v_pages, kv_scale, block_table, max_pages, num_pages, seq_lens, max_seq_len,
+                         B, Hq, Hkv, window, sm_scale, 0, out, workspace, workspace_bytes, &step, stream);
 }
 
 /* The allocation-free entry point's workspace: one static array per GPU, NC_DECODE_SCRATCH_BYTES long, held until the
  * process ends. In host code `scratch` names a host-side stand-in, not device memory: its device address on the current
  * GPU is looked up once (hipGetSymbolAddress with that GPU current) and only that address is ever passed to a kernel.
- * Nothing in it needs clearing: decode_kernel writes every partial and meta entry before decode_combine_kernel reads
- * it. Calls that overlap on one GPU share the array and race. */
+ * A device array without an initializer starts zero-filled, which is what the arrival counts need; every launch
+ * leaves them zero. Calls that overlap on one GPU share the array and race. */
 static __device__ __align__(256) unsigned char scratch[NC_DECODE_SCRATCH_BYTES];
 
 constexpr int MAX_DEVICES = 64;
@@ -1137,10 +1443,40 @@ extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void
     if (!decode_shape_ok(B, Hq, Hkv, max_seq_len, window) || max_pages <= 0 || num_pages <= 0 ||
         (long long)max_seq_len > (long long)max_pages * PAGE || workers < 0)
         return NC_ERR_SHAPE;
-    if (workspace_bytes < workspace_bytes_for(B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)))
+    if (!workspace_fits(workspace_bytes, B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)))
         return NC_ERR_WORKSPACE;
     return launch_decode(q, k_pages, v_pages, kv_scale, block_table, max_pages, num_pages, seq_lens, max_seq_len, B,
-                         Hq, Hkv, window, sm_scale, workers, out, workspace, (hipStream_t)stream);
+                         Hq, Hkv, window, sm_scale, workers, out, workspace, workspace_bytes, nullptr,
+                         (hipStream_t)stream);
+}
+
+extern "C" int nc_decode_step_fp8(const void *qkv, long long token_stride, int B, int Hq, int Hkv,
+                                  const int32_t *seq_lens, const float *q_gain, const float *k_gain, const float *cos,
+                                  const float *sin, int rope_len, void *q_out, const void *ve_h, const void *ve,
+                                  const float *ve_gate, const int32_t *ve_tokens, int C, const int32_t *block_table,
+                                  int max_pages, void *k_pages, void *v_pages, float *kv_scale, int num_pages,
+                                  int max_seq_len, int window, float sm_scale, int workers, void *out, void *workspace,
+                                  size_t workspace_bytes, void *stream) {
+    if (!qkv || !seq_lens || !q_gain || !k_gain || !cos || !sin || !block_table || !k_pages || !v_pages || !kv_scale ||
+        !out || !workspace || (ve && (!ve_h || !ve_gate || !ve_tokens)))
+        return NC_ERR_NULL;
+    if (!decode_shape_ok(B, Hq, Hkv, max_seq_len, window) || max_pages <= 0 || num_pages <= 0 ||
+        (long long)max_seq_len > (long long)max_pages * PAGE || workers < 0 || rope_len < max_seq_len ||
+        token_stride < (long long)(Hq + 2 * Hkv) * HEAD_DIM || (ve && C < Hkv * HEAD_DIM))
+        return NC_ERR_SHAPE;
+    if (!workspace_fits(workspace_bytes, B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)))
+        return NC_ERR_WORKSPACE;
+    StepArgs st = {};
+    st.qkv = (const uint16_t *)qkv;
+    st.token_stride = token_stride;
+    st.q_gain = q_gain; st.k_gain = k_gain; st.cos = cos; st.sin = sin;
+    st.q_out = (uint16_t *)q_out;
+    st.ve_h = (const uint16_t *)ve_h; st.ve = (const uint16_t *)ve; st.ve_gate = ve_gate; st.ve_tokens = ve_tokens;
+    st.C = C;
+    st.k_pages = (uint8_t *)k_pages; st.v_pages = (uint8_t *)v_pages; st.kv_scale = kv_scale;
+    return launch_decode(nullptr, k_pages, v_pages, kv_scale, block_table, max_pages, num_pages, seq_lens, max_seq_len,
+                         B, Hq, Hkv, window, sm_scale, workers, out, workspace, workspace_bytes, &st,
+                         (hipStream_t)stream);
 }
 
 extern "C" int nc_prefill_attn_fp8(const void *q, const void *k_pages, const void *v_pages, const float *kv_scale,
@@ -1172,11 +1508,12 @@ extern "C" int nc_decode_attn_fp8_noalloc(const void *q, const void *k_pages, co
     if (!decode_shape_ok(B, Hq, Hkv, max_seq_len, window) || max_pages <= 0 || num_pages <= 0 ||
         (long long)max_seq_len > (long long)max_pages * PAGE || workers < 0)
         return NC_ERR_SHAPE;
-    if (workspace_bytes_for(B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)) > (size_t)NC_DECODE_SCRATCH_BYTES)
+    if (!workspace_fits(NC_DECODE_SCRATCH_BYTES, B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)))
         return NC_ERR_WORKSPACE;
     int err = 0;
     void *ws = scratch_on_current_device(&err);
     if (!ws) return err;
     return launch_decode(q, k_pages, v_pages, kv_scale, block_table, max_pages, num_pages, seq_lens, max_seq_len, B,
-                         Hq, Hkv, window, sm_scale, workers, out, ws, (hipStream_t)stream);
+                         Hq, Hkv, window, sm_scale, workers, out, ws, NC_DECODE_SCRATCH_BYTES, nullptr,
+                         (hipStream_t)stream);
 }

@@ -3,9 +3,10 @@
  * inference/decoder.py:132-148) over an fp8 paged KV cache.
  *
  * A step is a stream of kernels on the caller's stream, launched eagerly:
- *   body   norm_kernel(EMBED) -> per layer { norm_kernel(RESID), qkv GEMM, the fused q/k norm + RoPE + value-embedding
- *          + fp8 append (kv_append.hip), split-K decode attention (attention.hip), o GEMM (+ residual: fp32 sum and its
- *          bf16 rounding), rstd_kernel, fc GEMM (+ ReLU^2 of the rstd-scaled sum), proj GEMM (+ residual) }
+ *   body   norm_kernel(EMBED) -> per layer { norm_kernel(RESID), qkv GEMM, the fused decode step (q/k norm + RoPE +
+ *          value embedding + fp8 append of the step's token, then split-K decode attention, one launch: attention.hip),
+ *          o GEMM (+ residual: fp32 sum and its bf16 rounding), rstd_kernel, fc GEMM (+ ReLU^2 of the rstd-scaled
+ *          sum), proj GEMM (+ residual) }
  *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
  *          the allowed tokens, then the commit), the tokens to pinned host memory.
  * A step's GEMMs are slot_gemm.hip's weight-streaming MFMA kernel with the epilogue fused (long-K GEMMs split into
@@ -18,7 +19,7 @@
  * scaled by its rstd; every RMS norm is 1 / sqrt(mean x^2 + FLT_EPSILON), correctly rounded (the reference: rsqrtf).
  * The KV cache is fp8 e4m3fn with one absmax scale per (token, head) (the reference caches bf16); a step's own key
  * is read back from the cache like the others. Decode attention splits a slot's keys at fixed multiples of 1,024
- * positions and the step GEMMs sum every slot's row in one fixed order, so a step's result for a slot depends only on
+ * positions (merged in position order in the same launch) and the step GEMMs sum every slot's row in one fixed order, so a step's result for a slot depends only on
  * the slot's own inputs and cache.
  *
  * Memory: one allocation per role, sized at dec_create. The KV pool of layer l is pages [0, B max_pages) for the
@@ -807,7 +808,7 @@ static void body_embed(Decoder *d, const Lane &ln, const Part &p) {
     launch_norm(ln, n);
 }
 
-/* Layer l up to its attention: the residual norm, qkv, the fused q/k norm + RoPE + fp8 append. */
+/* Layer l up to its attention: the residual norm and qkv. */
 static void body_pre(Decoder *d, const Lane &ln, const Part &p, int l) {
     const Layer &ly = d->layer[l];
     const Acts &a = p.a;
@@ -820,17 +821,21 @@ static void body_pre(Decoder *d, const Lane &ln, const Part &p, int l) {
     r.out = a.h;
     launch_norm(ln, r);
     gemm_epi(d, ln, true, SG_STORE, ly.qkv, 3 * C, C, a.h, p.n, a.qkv, nullptr, nullptr, nullptr, p.active);
-    NC_CHECK(append_rows(a.qkv, 3LL * C, p.n, d->H, d->H, d->pos + p.b0, d->num_new + p.b0, nullptr, ly.q_gain,
-                         ly.k_gain, d->cos, d->sin, d->max_len, a.q, d->block_table + (size_t)p.b0 * d->max_pages,
-                         d->max_pages, layer_k(d, l), layer_v(d, l), layer_s(d, l), (int)d->layer_pages, a.h, ly.ve,
-                         ly.ve_gate, d->tokens + p.b0, C, ln.stream));
 }
 
+/* Layer l's attention: the fused decode step (q/k norm + RoPE, value embedding, fp8 append of the step's k and v,
+ * split-K attention) in one launch. Active slots have seq_lens = pos + 1; the others 0 (no append, zero rows). */
 static void body_attn(Decoder *d, const Lane &ln, const Part &p, int l) {
-    NC_CHECK(nc_decode_attn_fp8(p.a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l),
-                                d->block_table + (size_t)p.b0 * d->max_pages, d->max_pages, (int)d->layer_pages,
-                                d->seq_lens + p.b0, d->max_len, p.n, d->H, d->H, d->layer[l].window, SM_SCALE, 0,
-                                p.a.att, ln.attn_ws, d->attn_ws_bytes, ln.stream));
+    const Layer &ly = d->layer[l];
+    StepArgs st = {};
+    st.qkv = p.a.qkv;
+    st.token_stride = 3LL * d->C;
+    st.q_gain = ly.q_gain; st.k_gain = ly.k_gain; st.cos = d->cos; st.sin = d->sin;
+    st.ve_h = p.a.h; st.ve = ly.ve; st.ve_gate = ly.ve_gate; st.ve_tokens = d->tokens + p.b0; st.C = d->C;
+    st.k_pages = layer_k(d, l); st.v_pages = layer_v(d, l); st.kv_scale = layer_s(d, l);
+    NC_CHECK(decode_step(st, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table + (size_t)p.b0 * d->max_pages,
+                         d->max_pages, (int)d->layer_pages, d->seq_lens + p.b0, d->max_len, p.n, d->H, d->H, ly.window,
+                         SM_SCALE, p.a.att, ln.attn_ws, d->attn_ws_bytes, ln.stream));
 }
 
 /* The step's body. Up to SPLIT_SLOTS slots, one lane. More: two lanes, slots [0, b1) on lane 0 and [b1, narrow) on

@@ -4,42 +4,24 @@
  * (the reference's qkp_forward) on the same row math.
  *
  * One wave per (token, head) row: lane l holds the rotation pair (dims l, l + 64), so the rotation is
- * lane-local and the row's sum of squares is one xor butterfly over the wave. Reference row math:
- * model/kernels/qk_row.cuh:19-51 (qk_row_sum, qk_rstd, qk_rotate); the build fixes the summation order
- * (lane partial x[l]^2 + x[l+64]^2, then offsets 32..1) and uses a correctly rounded 1/sqrt where the
- * reference has rsqrtf.
+ * lane-local and the row's sum of squares is one xor butterfly over the wave. The row math (nc_row.h) is
+ * shared with the fused decode step, which appends the step's token inside the attention kernel.
  */
 #include "nc_device.h"
+#include "nc_row.h"
 #include "nanochat_amd.h"
 #include "nc_internal.h"
 
 namespace nc {
 
-/* RMS norm (eps FLT_EPSILON), gain and -theta rotation of one row held as lane pairs (x1 = dim l,
- * x2 = dim l + 64); results before the bf16 rounding. Every operation is a single rounded fp32 op in the
- * order of the oracle's qk_norm_rope. All 64 lanes of the wave must call it together. */
-__device__ __forceinline__ void norm_rope_pair(float x1, float x2, float g1, float g2, float c, float s, float &y1,
-                                               float &y2) {
-    const float part = x1 * x1 + x2 * x2;
-    const float ss = wave_sum_butterfly(part);
-    const float v = ss / 128.0f + FLT_EPS;
-    const float r = 1.0f / __builtin_sqrtf(v);  /* correctly rounded (HIP's __fsqrt_rn is not, here) */
-    const float n1 = (x1 * r) * g1;
-    const float n2 = (x2 * r) * g2;
-    y1 = n1 * c + n2 * s;
-    y2 = n2 * c - n1 * s;
-}
-
 /* Quantize one row (lane pair x1 = dim l, x2 = dim l + 64, bf16 values) and store its codes into a page
  * at the byte offsets OFF(slot, dim); lane 0 stores the scale. */
 template <int (*OFF)(int, int)>
 __device__ __forceinline__ void quantize_store(float x1, float x2, uint8_t *page, float *scale_at, int slot, int lane) {
-    const float amax = wave_max(fmaxf(fabsf(x1), fabsf(x2)));
-    const float scale = amax > 0.0f ? amax / FP8_MAX : 1.0f;
-    const float q1 = fminf(fmaxf(x1 / scale, -FP8_MAX), FP8_MAX);
-    const float q2 = fminf(fmaxf(x2 / scale, -FP8_MAX), FP8_MAX);
-    page[OFF(slot, lane)] = (uint8_t)e4m3_encode(q1);
-    page[OFF(slot, lane + HALF)] = (uint8_t)e4m3_encode(q2);
+    uint32_t c1, c2;
+    const float scale = quantize_pair(x1, x2, c1, c2);
+    page[OFF(slot, lane)] = (uint8_t)c1;
+    page[OFF(slot, lane + HALF)] = (uint8_t)c2;
     if (lane == 0) *scale_at = scale;
 }
 
@@ -115,17 +97,8 @@ __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
     quantize_store<k_page_offset>(k1, k2, a.k_pages + at * PAGE_BYTES, a.kv_scale + at * 2 * PAGE + slot, slot, lane);
     float v1 = bf16_to_f32(vx[lane]), v2 = bf16_to_f32(vx[lane + HALF]);
     if (FUSED && a.ve) {
-        /* reference decode.cu:481-494: g = 2 sigmoid(ve_gate[head] . h) (lane-strided FMAs, then the butterfly),
-         * v = bf16(v + g ve[token]) */
-        const uint16_t *h = a.ve_h + tok * a.C;
-        const float *w = a.ve_gate + (long long)kvh * a.C;
-        float d = 0.0f;
-        for (int i = lane; i < a.C; i += WAVE) d = __builtin_fmaf(bf16_to_f32(h[i]), w[i], d);
-        d = wave_sum_butterfly(d);
-        const float g = 2.0f * (1.0f / (1.0f + expf(-d)));
-        const uint16_t *e = a.ve + (long long)a.ve_tokens[tok] * a.C + kvh * HEAD_DIM;
-        v1 = bf16_to_f32(f32_to_bf16(v1 + g * bf16_to_f32(e[lane])));
-        v2 = bf16_to_f32(f32_to_bf16(v2 + g * bf16_to_f32(e[lane + HALF])));
+        ve_mix_pair(a.ve_h + tok * a.C, a.ve_gate + (long long)kvh * a.C, a.C,
+                    a.ve + (long long)a.ve_tokens[tok] * a.C + kvh * HEAD_DIM, lane, v1, v2);
     }
     quantize_store<v_page_offset>(v1, v2, a.v_pages + at * PAGE_BYTES, a.kv_scale + (at * 2 + 1) * PAGE + slot, slot,
                                   lane);
@@ -345,4 +318,4 @@ extern "C" const char *nc_status_string(int status) {
     }
 }
 
-extern "C" int nc_abi_version(void) { return 3; }
+extern "C" int nc_abi_version(void) { return 4; }

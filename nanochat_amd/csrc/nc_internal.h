@@ -21,6 +21,29 @@ int append_rows(const uint16_t *qkv, long long token_stride, int n, int Hq, int 
                 const uint16_t *ve_h, const uint16_t *ve, const float *ve_gate, const int32_t *tokens, int C,
                 hipStream_t stream);
 
+/* The fused decode step's inputs: each sequence's token row as the qkv projection left it, and what the cache
+ * append needs (the fused append's arguments, for one token per sequence at position seq_lens[b] - 1). */
+struct StepArgs {
+    const uint16_t *qkv;        /* [B][(Hq + 2 Hkv) 128] bf16 at token_stride */
+    long long token_stride;
+    const float *q_gain, *k_gain;
+    const float *cos, *sin;     /* [rope_len][64] */
+    uint16_t *q_out;            /* NULL, or [B][Hq][128]: the normed, rotated queries */
+    const uint16_t *ve_h, *ve;  /* NULL ve: no value embeddings; else h [B][C], table [vocab][C] */
+    const float *ve_gate;       /* [Hkv][C] */
+    const int32_t *ve_tokens;   /* [B] */
+    int C;
+    uint8_t *k_pages, *v_pages; /* the cache the step appends to (the launch's pools) */
+    float *kv_scale;
+};
+
+/* attention.hip: nc_decode_step_fp8 for the decoder runtime (rope_len >= max_seq_len, workers = 0); the workspace
+ * as nc_decode_attn_fp8's (its size checked here). */
+int decode_step(const StepArgs &step, const void *k_pages, const void *v_pages, const float *kv_scale,
+                const int32_t *block_table, int max_pages, int num_pages, const int32_t *seq_lens, int max_seq_len,
+                int B, int Hq, int Hkv, int window, float sm_scale, void *out, void *workspace, size_t workspace_bytes,
+                hipStream_t stream);
+
 /* attention.hip: chunked prefill over runs of rows. */
 int prefill_runs(const uint16_t *q, const uint8_t *k_pages, const uint8_t *v_pages, const float *kv_scale,
                  const int32_t *block_table, int max_pages, int num_pages, const int32_t *start_pos,

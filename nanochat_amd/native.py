@@ -88,6 +88,10 @@ SIGNATURES = {
     "nc_decode_workspace_bytes": ([c_int, c_int, c_int, c_int, c_int], c_size_t),
     "nc_decode_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
                             c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_size_t, c_void_p], c_int),
+    "nc_decode_step_fp8": ([c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                            c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int,
+                            c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p,
+                            c_size_t, c_void_p], c_int),
     "nc_decode_attn_fp8_noalloc": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int,
                                     c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p], c_int),
     "nc_prefill_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,

@@ -25,7 +25,7 @@ def test_header_and_binding_agree():
 def test_library_exports_every_declared_symbol(lib):
     for name in declared():
         assert hasattr(lib, name), name
-    assert lib.nc_abi_version() == 3
+    assert lib.nc_abi_version() == 4
 
 
 def test_status_strings(lib):
@@ -52,18 +52,23 @@ def test_small_workspace_rejected(lib):
     need = lib.nc_decode_workspace_bytes(64, 16, 4, 8193, -1)
     assert need > 0
     assert lib.nc_decode_attn_fp8(*([DUMMY] * 5), 513, 64 * 513, DUMMY, 8193, 64, 16, 4, -1, 0.1, 0, DUMMY, DUMMY,
-                                  need - 1, None) == -3
+                                  need - 1024, None) == -3
 
 
 def expected_workspace(B, Hq, Hkv, max_seq, window):
-    """The documented layout: fp32 partials (O [128] + max, sum) of G heads for every item a launch can hold, then
-    int32 meta [B*Hkv][2]; a unit of n pages (n capped by the window) touches at most ceil(n / 64) + 1 chunks of
-    1,024 positions."""
+    """The documented layout: fp32 partials (O [128] + max, sum) of G heads for every item a launch can hold below the
+    last 1/256 of the workspace, which holds one int32 arrival count per (sequence, KV head); a unit of n pages (n
+    capped by the window) touches at most ceil(n / 64) + 1 chunks of 1,024 positions. The smallest such size that is a
+    multiple of 1,024 of the form 256 k, k a multiple of 4 with 255 k >= partials and k >= 4 B Hkv."""
     unit_pages = -(-max_seq // 16)
     if window >= 0:
         unit_pages = min(unit_pages, window // 16 + 2)
     items = B * Hkv * (-(-unit_pages // 64) + 1)
-    return items * (Hq // Hkv) * 130 * 4 + B * Hkv * 2 * 4
+    partials = items * (Hq // Hkv) * 130 * 4
+    k = max(-(-partials // 255), 4 * B * Hkv)
+    k = -(-k // 4) * 4
+    assert 255 * k >= partials and k >= 4 * B * Hkv
+    return 256 * k
 
 
 @pytest.mark.parametrize("args", [(1, 4, 4, 16, -1), (8, 16, 4, 8193, -1), (8, 16, 4, 8193, 512),
@@ -90,6 +95,30 @@ def test_workspace_window_and_bad_sizes(lib):
     assert lib.nc_decode_workspace_bytes(0, 16, 4, 8193, -1) == 0
     assert lib.nc_decode_workspace_bytes(8, 6, 4, 8193, -1) == 0
     assert lib.nc_decode_workspace_bytes(4097, 16, 4, 8193, -1) == 0
+
+
+def step_args(**over):
+    """nc_decode_step_fp8's arguments for B = 2, Hq = 16, Hkv = 4, max_seq_len 100 with dummy pointers; `over`
+    replaces any of them by name."""
+    args = dict(qkv=DUMMY, token_stride=24 * 128, B=2, Hq=16, Hkv=4, seq_lens=DUMMY, q_gain=DUMMY, k_gain=DUMMY,
+                cos=DUMMY, sin=DUMMY, rope_len=100, q_out=None, ve_h=None, ve=None, ve_gate=None, ve_tokens=None, C=0,
+                block_table=DUMMY, max_pages=7, k_pages=DUMMY, v_pages=DUMMY, kv_scale=DUMMY, num_pages=14,
+                max_seq_len=100, window=-1, sm_scale=0.1, workers=0, out=DUMMY, workspace=DUMMY,
+                workspace_bytes=1 << 30, stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(qkv=None), -1), (dict(cos=None), -1), (dict(workspace=None), -1), (dict(ve=DUMMY), -1),
+    (dict(ve=DUMMY, ve_h=DUMMY, ve_gate=DUMMY), -1),
+    (dict(rope_len=99), -2), (dict(token_stride=24 * 128 - 1), -2), (dict(Hq=6), -2), (dict(max_pages=6), -2),
+    (dict(ve=DUMMY, ve_h=DUMMY, ve_gate=DUMMY, ve_tokens=DUMMY, C=511), -2), (dict(workers=-1), -2),
+    (dict(workspace_bytes=0), -3)])
+def test_decode_step_rejects_bad_arguments(lib, over, code):
+    """nc_decode_step_fp8 checks its pointers, shapes (rope tables covering max_seq_len, the qkv row width, the value
+    embedding width) and workspace before any device call."""
+    assert lib.nc_decode_step_fp8(*step_args(**over)) == code
 
 
 def test_bad_append_shapes_rejected(lib):

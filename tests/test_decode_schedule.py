@@ -1,9 +1,12 @@
-"""CPU replay of decode_kernel's work split (nanochat_amd/csrc/attention.hip: chunks cut at multiples of 64 pages; the
+"""CPU replay of decode_kernel's work split (nanochat_amd/csrc/attention.hip: chunks cut at multiples of 64 pages, a last
+piece under 16 pages joined to the one before it (checked against a from-scratch cut of the page range); the
 per-work-group prefixes over sequences of full and partial chunks; full chunks numbered first, then partial ones;
-item k to work-group k % G, wave (k / G) % 4; partial slot = the chunk's unit-order index; meta written by each unit's
-chunk 0) for many shapes: every (unit, page) is attended exactly once, by an item whose page range depends on nothing
-but the unit's own length; partial slots stay inside the workspace bound (item_bound); meta names exactly a unit's
-chunks, in order; work-groups' page loads differ by at most about one chunk."""
+item k to work-group k % G, wave (k / G) % 4; partial slot = the chunk's unit-order index; the unit's chunks counted
+in arrived[u], the last to finish merging slots slot - j .. + nch) for many shapes: every (unit, page) is attended
+exactly once, by an item whose page range depends on nothing but the unit's own length; partial slots stay inside the
+workspace bound (item_bound); every chunk of a multi-chunk unit names the same first slot, the unit's chunks fill it in
+order and arrive exactly nch times (so one merge runs and the count returns to zero); the sequences left with no item
+are exactly those the kernel fills with zero or NaN rows; work-groups' page loads differ by at most about one chunk."""
 import numpy as np
 import pytest
 
@@ -20,15 +23,40 @@ def unit_pages(L, window, max_len):
     return p // PAGE + 1 - begin // PAGE, begin // PAGE
 
 
+MIN_TAIL = 16
+
+
+def chunk_ranges(pg0, n):
+    """Logical page ranges of a unit's chunks, from first principles: cut [pg0, pg0 + n) at every multiple of 64 pages,
+    then join a last piece shorter than 16 pages to the one before it."""
+    if n <= 0:
+        return []
+    e = pg0 + n
+    cuts = [pg0] + list(range((pg0 // SPLIT + 1) * SPLIT, e, SPLIT)) + [e]
+    pieces = [(a, b) for a, b in zip(cuts, cuts[1:])]
+    if len(pieces) >= 2 and pieces[-1][1] - pieces[-1][0] < MIN_TAIL:
+        pieces[-2:] = [(pieces[-2][0], e)]
+    return pieces
+
+
 def unit_split(pg0, n):
-    """(chunks, lead partial, full, partial) of logical pages [pg0, pg0 + n)."""
+    """(chunks, chunk 0 partial, full, partial) of logical pages [pg0, pg0 + n), as the kernel computes them."""
     if n <= 0:
         return 0, 0, 0, 0
-    e = pg0 + n
-    nch = (e - 1) // SPLIT - pg0 // SPLIT + 1
-    lead, trail = int(pg0 % SPLIT != 0), int(e % SPLIT != 0)
-    npart = int(lead or trail) if nch == 1 else lead + trail
-    return nch, lead, nch - npart, npart
+    e, c0 = pg0 + n, pg0 // SPLIT
+    pieces = (e - 1) // SPLIT - c0 + 1
+    tail = e - max(pg0, ((e - 1) // SPLIT) * SPLIT)
+    nch = pieces - int(pieces >= 2 and tail < MIN_TAIL)
+    size0 = (e if nch == 1 else (c0 + 1) * SPLIT) - pg0
+    sizel = e - (c0 + nch - 1) * SPLIT
+    p0 = int(size0 < SPLIT)
+    npart = p0 + int(nch > 1 and sizel < SPLIT)
+    return nch, p0, nch - npart, npart
+
+
+def chunk_pages(pg0, n, nch, j):
+    c = pg0 // SPLIT + j
+    return (pg0 if j == 0 else c * SPLIT), (pg0 + n if j == nch - 1 else (c + 1) * SPLIT)
 
 
 def item_bound(B, hkv, max_len, window):
@@ -49,26 +77,26 @@ def replay(seq_lens, hkv, workers, window, max_len):
         cp[b + 1] = cp[b] + hkv * split[b][3]
     NF, N = int(cf[B]), int(cf[B] + cp[B])
     G = -(-min(workers, 4 * item_bound(B, hkv, max_len, window)) // WAVES)
-    seen, partials, meta, load = {}, {}, {}, np.zeros(G, np.int64)
+    seen, partials, first_slot, arrived, load = {}, {}, {}, {}, np.zeros(G, np.int64)
     for wg in range(G):
         for wave in range(WAVES):
             for k in range(wg + G * wave, N, 4 * G):
                 if k < NF:
                     b = max(i for i in range(B) if cf[i] <= k)
-                    nch, lead, nfull, npart = split[b]
+                    nch, p0, nfull, npart = split[b]
                     kvh, jf = divmod(k - cf[b], nfull)
-                    j = jf + lead
+                    j = jf + p0
                 else:
                     k2 = k - NF
                     b = max(i for i in range(B) if cp[i] <= k2)
-                    nch, lead, nfull, npart = split[b]
+                    nch, p0, nfull, npart = split[b]
                     kvh, jp = divmod(k2 - cp[b], npart)
-                    j = 0 if nch == 1 or (lead and jp == 0) else nch - 1
+                    j = 0 if p0 and jp == 0 else nch - 1
                 n, pg0 = units[b]
-                chunk = pg0 // SPLIT + j
-                first, last = max(pg0, chunk * SPLIT), min(pg0 + n, (chunk + 1) * SPLIT)
-                assert first < last
-                assert (last - first == SPLIT) == (k < NF)
+                first, last = chunk_pages(pg0, n, nch, j)
+                assert (first, last) == chunk_ranges(pg0, n)[j]
+                assert 0 < last - first <= SPLIT + MIN_TAIL - 1
+                assert (last - first >= SPLIT) == (k < NF)
                 load[wg] += last - first
                 for lp in range(first, last):
                     key = (b, kvh, lp)
@@ -80,19 +108,24 @@ def replay(seq_lens, hkv, workers, window, max_len):
                     assert 0 <= slot < item_bound(B, hkv, max_len, window)
                     assert slot not in partials
                     partials[slot] = (u, j)
-                if j == 0:
-                    meta[u] = (slot, nch)
+                    assert first_slot.setdefault(u, slot - j) == slot - j
+                    arrived[u] = arrived.get(u, 0) + 1
     for b, (n, pg0) in enumerate(units):
+        # no item: exactly the sequences decode_fill_rows finds by their empty chunk ranges
+        assert (n == 0) == (cf[b + 1] == cf[b] and cp[b + 1] == cp[b])
+        nch = split[b][0]
         for kvh in range(hkv):
+            u = b * hkv + kvh
             for lp in range(pg0, pg0 + n):
                 assert (b, kvh, lp) in seen
-            if n:
-                first, count = meta[b * hkv + kvh]
-                if count > 1:
-                    assert [partials[first + j] for j in range(count)] == [(b * hkv + kvh, j) for j in range(count)]
+            if nch > 1:
+                assert arrived[u] == nch
+                assert [partials[first_slot[u] + j] for j in range(nch)] == [(u, j) for j in range(nch)]
+            else:
+                assert u not in arrived
     assert len(seen) == sum(hkv * n for n, _ in units)
     if N >= G:   # every work-group has an item: loads differ by at most about one chunk of each kind
-        assert load.max() - load.min() <= 2 * SPLIT * -(-N // (4 * G)) + SPLIT
+        assert load.max() - load.min() <= 2 * (SPLIT + MIN_TAIL) * -(-N // (4 * G)) + SPLIT + MIN_TAIL
     return seen
 
 
