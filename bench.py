@@ -66,34 +66,61 @@ def traffic_from_profiles(kernel, workload):
     return d.get("bytes_per_launch")
 
 
-def cpu_baseline(w, inp, seqs):
-    """The CPU oracle (float64 numpy restatement) on a bounded sample of the same workload: the first `seqs`
-    sequences' gather + dequantize + attention, timed after building their cache (not timed)."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def cpu_baseline(w, inp, step_bytes, runs=5):
+    """The CPU baseline of a decode workload: the PyTorch float32 restatement of the whole step (oracle/cpu_step.py:
+    the step token's QK-norm/RoPE, fp8 quantize and store, gather + dequantize + attention) of every sequence, at
+    every host thread, median of `runs` after one warm-up; the cache of the cached tokens is built untimed."""
+    import torch
 
-    from oracle.attention import decode_attention as oracle_decode
-    from oracle.layout import PAGE, PagedCache
+    from oracle import cpu_step as cs
 
-    cores = min(16, os.cpu_count() or 1)
-    sample = list(range(min(seqs, w.batch)))
-    lens = [int(inp["ctx_lens"][b]) + 1 for b in sample]
-    mp = (max(lens) + PAGE - 1) // PAGE
-    table = np.arange(len(sample) * mp, dtype=np.int32).reshape(len(sample), mp)
-    cache = PagedCache(table.size, w.kv_heads)
-    for i, b in enumerate(sample):
-        n = lens[i] - 1
-        cache.append(table, i, np.arange(n), inp["k_cache"][b, :n].float().numpy(), inp["v_cache"][b, :n].float().numpy())
-        cache.append(table, i, np.array([n]), inp["k_new"][b].float().numpy(), inp["v_new"][b].float().numpy())
-    q = inp["q"][sample].float().numpy()
-    with threadpool_limits(limits=cores):
-        t0 = time.perf_counter()
-        oracle_decode(q, cache, table, np.array(lens))
-        dt = time.perf_counter() - t0
-    nbytes = attention_bytes([n - 1 for n in lens], w.q_heads, w.kv_heads)
-    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"oracle decode attention (numpy, float64) of {len(sample)} of {w.batch} sequences "
-                      f"({sum(lens)} keys), {dt:.2f} s"}
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    B, Hq, Hkv = w.batch, w.q_heads, w.kv_heads
+    table = inp["block_table"]
+    ctx = inp["ctx_lens"].to(torch.int64)
+    cache = cs.PagedCpuCache(inp["num_pages"], Hkv)
+    for b in range(B):
+        n = int(ctx[b])
+        cache.store(table, b, torch.arange(n), inp["k_cache"][b, :n].float(), inp["v_cache"][b, :n].float())
+    qkv = torch.cat([inp["q"].reshape(B, 1, -1), inp["k_new"].reshape(B, 1, -1), inp["v_new"].reshape(B, 1, -1)],
+                    dim=2).float()
+    ones = torch.ones(128)
+    cos, sin = (torch.tensor(t) for t in _rotary(w.ctx + 2, 1e6))
+    dt = cs.time_median(lambda: cs.step(cache, table, qkv, ctx, Hq, Hkv, ones, ones, cos, sin), runs=runs)
+    return {"value": round(step_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu": cs.cpu_model(), "seconds_per_step": round(dt, 5),
+            "sample": f"the whole step ({B} sequences, {int(ctx.sum()) + B} keys): PyTorch float32 restatement "
+                      f"(oracle/cpu_step.py), torch.set_num_threads({threads}), median of {runs} after 1 warm-up"}
+
+
+def _rotary(n, theta):
+    from oracle.rope import rotary_tables
+
+    return rotary_tables(n, theta)
+
+
+def prefill_cpu_baseline(w, inp, flops, runs=5):
+    """The CPU baseline of chunked prefill: the PyTorch float32 restatement of the step (the chunk's QK-norm/RoPE,
+    quantize and store, then causal attention of every chunk row) at every host thread, median of `runs`."""
+    import torch
+
+    from oracle import cpu_step as cs
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    table, start = inp["block_table"], inp["start_pos"].to(torch.int64)
+    cache = cs.PagedCpuCache(inp["num_pages"], w.kv_heads)
+    for b in range(w.batch):
+        cache.store(table, b, torch.arange(w.ctx), inp["k_cache"][b].float(), inp["v_cache"][b].float())
+    cos, sin = (torch.tensor(t) for t in _rotary(w.ctx + w.chunk, w.theta))
+    qkv = inp["qkv"].float()
+    dt = cs.time_median(lambda: cs.step(cache, table, qkv, start, w.q_heads, w.kv_heads, inp["q_gain"],
+                                        inp["k_gain"], cos, sin), runs=runs)
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu": cs.cpu_model(), "seconds_per_step": round(dt, 4),
+            "sample": f"the whole step ({w.batch} x {w.chunk} rows onto {w.ctx}): PyTorch float32 restatement "
+                      f"(oracle/cpu_step.py), torch.set_num_threads({threads}), median of {runs} after 1 warm-up"}
 
 
 def prefill_flops(ctx, chunk, batch, q_heads):
@@ -150,7 +177,7 @@ def bench_prefill(args, w):
     attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
     flops = prefill_flops(w.ctx, w.chunk, w.batch, w.q_heads)
     achieved = flops / (attn_ms * 1e-3) / 1e12
-    return {
+    result = {
         "metric": "chunked-prefill attention TFLOP/s over the fp8 cache (MFMA)", "value": round(achieved, 2),
         "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3 KV, fp8 QK^T and bf16 PV MFMA, fp32 softmax",
@@ -163,6 +190,11 @@ def bench_prefill(args, w):
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
                      "kernel": "nc_prefill_attn_fp8 (prefill_lds_kernel)"},
     }
+    if args.cpu_seqs > 0:
+        cpu = prefill_cpu_baseline(w, inp, flops)
+        cpu["speedup_of_gpu_step"] = round(cpu["seconds_per_step"] / (ms_step * 1e-3), 1)
+        result["cpu_baseline"] = cpu
+    return result
 
 
 VE_SHAPE = {"rows": 65536, "heads": 6, "vocab": 65536}   # reference d24 (C = 768), 32 x 2048 tokens
@@ -353,7 +385,9 @@ def model_cpu_baseline(w, model, slots=16, steps=6, seed=0):
 
     from oracle import model as om
 
-    cores = min(16, os.cpu_count() or 1)
+    from oracle.cpu_step import cpu_model
+
+    cores = os.cpu_count() or 1
     weights = om.weights_from_tensors(model)
     n = w.prompt - 1
     orc = om.DecoderOracle(weights, n + steps)
@@ -370,8 +404,9 @@ def model_cpu_baseline(w, model, slots=16, steps=6, seed=0):
             tokens = orc.head(orc.body(tokens, [n + s] * slots, list(range(slots)))).argmax(axis=-1)
         dt = time.perf_counter() - t0
     return {"value": round(slots * steps / dt, 3), "unit": "decode tokens/s", "cores": cores, "kind": "port",
+            "cpu": cpu_model(),
             "sample": f"{steps} greedy decode steps of {slots} slots from context {n + 1} (caches pre-filled), "
-                      f"float64 numpy oracle", "seconds": round(dt, 3)}
+                      f"float64 numpy oracle (oracle/model.py) at {cores} BLAS threads", "seconds": round(dt, 3)}
 
 
 def bench_model(args, w, cpu_slots=16):
@@ -451,7 +486,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c3u")
     ap.add_argument("--workers", type=int, default=0, help="decode: waves taking the work items (0: all slots)")
-    ap.add_argument("--cpu-seqs", type=int, default=64, help="sequences in the CPU baseline sample (0: skip)")
+    ap.add_argument("--cpu-seqs", type=int, default=64,
+                    help="CPU baseline: 0 skips it; decode and prefill time the whole step, c5 this many slots (<= 16)")
     ap.add_argument("--two-launch", action="store_true",
                     help="decode: the step as nc_qk_norm_rope_append_fp8 + nc_decode_attn_fp8 (the same bits)")
     ap.add_argument("--no-e2e", action="store_true",
@@ -577,8 +613,8 @@ def main():
                      "bytes_per_launch": step_b},
     }
     if args.cpu_seqs > 0:
-        result["cpu_baseline"] = cpu_baseline(w, inp, args.cpu_seqs)
-        result["cpu_baseline"]["speedup_of_gpu"] = round(achieved / result["cpu_baseline"]["value"], 1)
+        result["cpu_baseline"] = cpu_baseline(w, inp, step_b)
+        result["cpu_baseline"]["speedup_of_gpu_step"] = round(value / result["cpu_baseline"]["value"], 1)
     if not args.no_e2e:
         # the metric's second half: end-to-end decode tokens/s of config 5 through the decoder runtime
         del cache, ws, qkv, q_out, out
