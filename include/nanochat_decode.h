@@ -71,15 +71,29 @@ void dec_destroy(void *handle);
 void *dec_create_slots(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream,
                        int max_slots);
 
+/* KV pages: every layer's pool holds `pool` pages the slots draw from on their first write of a page and return when
+ * a slot starts a new sequence (a write at position 0), when dec_set_prompt moves it to an earlier position (the pages
+ * past it), or on dec_release. dec_create / dec_create_slots size the pool for every slot at max_len; dec_create_pool
+ * takes pool_pages (>= max_len / 16) and fits as many slots (<= max_slots) as the memory left allows, so a host can
+ * run more sequences than full-length reservations would hold. A write that finds the pool empty aborts: such a host
+ * admits sequences by dec_debug_pages. */
+void *dec_create_pool(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream,
+                      int max_slots, long long pool_pages);
+
+/* Slot b's pages return to the pool (its shared store pages are unlinked); its next sequence starts at position 0. */
+void dec_release(void *handle, int b);
+
+/* out [2]: the pool's free pages, its size. */
+void dec_debug_pages(void *handle, long long *out);
+
 /* Test hooks (synchronize, then copy to host): the last head's fp32 logits of slots [0, rows), out [rows][vocab];
  * and the cached rows of slot b (b = -1: the prompt store) at positions [at, at + n) of one layer, k and v as
  * e4m3fn codes [n][H][128], scales [n][H][2] (K, V). */
 void dec_debug_logits(void *handle, float *out, int rows);
 void dec_debug_cache(void *handle, int layer, int b, int at, int n, uint8_t *k, uint8_t *v, float *scales);
 
-/* Slot b's block-table row, max_length / 16 (rounded up) entries: b * pages + e is the slot's own page e,
- * dec_batch() * pages + i page i of the prompt store, shared read-only after dec_load_prompt (pages = the row's
- * length). */
+/* Slot b's block-table row, max_length / 16 (rounded up) entries: -1 (no page yet), a pool page in [0, pool) of the
+ * slot's own, or pool + i for page i of the prompt store, shared read-only after dec_load_prompt. */
 void dec_debug_table(void *handle, int b, int32_t *out);
 
 /* Whether a step over more than 64 slots runs as two concurrent lanes or as one (the default); whether the step's

@@ -22,11 +22,16 @@
  * positions (merged in position order in the same launch) and the step GEMMs sum every slot's row in one fixed order, so a step's result for a slot depends only on
  * the slot's own inputs and cache.
  *
- * Memory: one allocation per role, sized at dec_create. The KV pool of layer l is pages [0, B max_pages) for the
- * slots (slot b owns pages b max_pages + i) followed by the prompt store's pages (store position s at page
- * B max_pages + s / 16, slot s % 16). dec_save_prompt copies a slot's positions into the store; dec_load_prompt points
- * the slot's block-table entries at the store's whole pages (shared read-only, copied on the slot's first write to
- * one) and copies only partial pages.
+ * Memory: one allocation per role, sized at dec_create. The KV pool of layer l is `pool` pages the slots draw from
+ * (the same page index in every layer) followed by the prompt store's pages (store position s at page pool + s / 16,
+ * slot s % 16). A slot's block-table entry is -1 until the slot first writes a position of that page, when a free
+ * page is taken from the pool (host free list); a slot's pages return to the pool when it starts a new sequence (a
+ * write at position 0), when dec_set_prompt moves it back to a shorter one, or on dec_release. dec_create sizes the
+ * pool for every slot at max_len (the reference's reservation, so a step never runs out); dec_create_pool takes a
+ * smaller pool, for more slots than full-length reservations allow, and then the host admits requests by the free
+ * pages (dec_debug_pages). dec_save_prompt copies a slot's positions into the store; dec_load_prompt points the
+ * slot's block-table entries at the store's whole pages (shared read-only, copied into a page of the slot's own on
+ * its first write to one) and copies only partial pages.
  */
 #include <math.h>
 #include <stdio.h>
@@ -459,15 +464,10 @@ __global__ void __launch_bounds__(256) copy_positions_kernel(uint8_t *k_pages, u
     if (lane < 2) kv_scale[(da * 2 + lane) * PAGE + ds] = kv_scale[(sa * 2 + lane) * PAGE + ss];
 }
 
-__global__ void identity_table_kernel(int32_t *table, long long n) {
+/* table[idx0 + i] = value0 + step i for i < count */
+__global__ void set_table_kernel(int32_t *table, long long idx0, long long count, int value0, int step) {
     const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) table[i] = (int32_t)i;
-}
-
-/* table[idx0 + i] = value0 + i for i < count */
-__global__ void set_table_kernel(int32_t *table, long long idx0, int count, int value0) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < count) table[idx0 + i] = value0 + i;
+    if (i < count) table[idx0 + i] = value0 + step * (int)i;
 }
 
 /* Whole pages src_page0 + z -> dst_page0 + z of layer y and head x: 2 KiB of K codes, 2 KiB of V codes, 128 bytes of
@@ -514,7 +514,8 @@ struct Lane {
 
 struct Decoder {
     int B, L, C, F, H, vocab, max_len, store, lazy, max_pages;
-    long long slot_pages, layer_pages;   /* pages of the slots; pages of a layer's pool (slots + store) */
+    long long pool, layer_pages;         /* pages the slots draw from; pages of a layer's pool (slots + store) */
+    std::vector<int32_t> free_pages;     /* the pool's free pages, a stack (taken from the back) */
     float softcap;
     const float *wte, *cos, *sin;
     const uint16_t *lm_head;
@@ -528,7 +529,7 @@ struct Decoder {
     size_t lt_ws_bytes;
     uint8_t *k_pages, *v_pages;          /* [L][layer_pages][H][2048] */
     float *kv_scale;                     /* [L][layer_pages][H][2][16] */
-    int32_t *block_table;                /* [B][max_pages]: slot b's entry e is its own page b max_pages + e, or a
+    int32_t *block_table;                /* [B][max_pages]: slot b's entry e is -1, a pool page of its own, or a
                                             store page it shares read-only after dec_load_prompt */
     std::vector<int32_t> table;          /* host copy of block_table (what the enqueued work leaves there) */
     std::vector<int32_t> hpos;           /* host copy of pos: the position a live slot's next step writes */
@@ -925,8 +926,10 @@ static void enqueue_head(Decoder *d) {
     HIP_CHECK(hipMemcpyAsync(d->host_tokens + d->B, d->alt_tokens, (size_t)d->B * 4, hipMemcpyDeviceToHost, d->stream));
 }
 
+/* pool_pages <= 0: a pool of max_pages per slot (every slot can reach max_len; slots as many as fit so);
+ * pool_pages > 0: a pool of that many pages, the slots as many (<= max_slots) as fit beside it. */
 static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream,
-                       int max_slots) {
+                       int max_slots, long long pool_pages) {
     Decoder *d = new Decoder();
     d->L = cfg[0]; d->C = cfg[1]; d->F = cfg[2]; d->vocab = cfg[3]; d->max_len = cfg[4]; d->store = cfg[5];
     d->lazy = cfg[6];
@@ -969,12 +972,14 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     if (hipblasLtCreate(&d->lt) != HIPBLAS_STATUS_SUCCESS) die("hipblasLtCreate", "failed", __LINE__);
     d->lt_ws_bytes = (size_t)32 << 20;
 
-    /* fixed blocks first (prefill rows, masks, store pages' share is per layer below), then the slots: B, the most
-     * slots (<= max_slots) whose KV pages, activations and choice buffers fit the free memory less a reserve */
+    /* fixed blocks first (prefill rows, masks, the store's pages and, with pool_pages, the pool), then the slots: B,
+     * the most slots (<= max_slots) whose activations, choice buffers and (without pool_pages) max_len worth of KV
+     * pages fit the free memory less a reserve */
     const size_t store_pages = ((size_t)d->store + PAGE - 1) / PAGE;
     const size_t page_set = (size_t)d->H * (2 * PAGE_BYTES + 2 * PAGE * sizeof(float));  /* a page of every head */
-    const size_t per_slot = (size_t)d->L * d->max_pages * page_set + acts_bytes(d, 1) + (size_t)d->vocab * 8 +
-                            (size_t)d->vocab / 8 + (size_t)d->max_pages * 4 + 64 +
+    REQUIRE(pool_pages <= 0 || pool_pages >= d->max_pages, "a pool must hold at least one max_len sequence");
+    const size_t per_slot = (pool_pages > 0 ? 0 : (size_t)d->L * d->max_pages * page_set) + acts_bytes(d, 1) +
+                            (size_t)d->vocab * 8 + (size_t)d->vocab / 8 + (size_t)d->max_pages * 4 + 64 +
                             (size_t)d->H * (HEAD_DIM + 2) * 4 + (size_t)d->H * 8;
     d->row = carve_acts(d, PREFILL_ROWS);
     d->rows = (int32_t *)device_alloc(d, 7 * PREFILL_ROWS * sizeof(int32_t));
@@ -982,23 +987,26 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     size_t free_bytes = 0, total_bytes = 0;
     HIP_CHECK(hipStreamSynchronize(d->stream));
     HIP_CHECK(hipMemGetInfo(&free_bytes, &total_bytes));
-    const size_t fixed = (size_t)d->L * store_pages * page_set + (size_t)4096 * d->H * (HEAD_DIM + 2) * 4;
+    const size_t fixed = (size_t)d->L * (store_pages + (pool_pages > 0 ? (size_t)pool_pages : 0)) * page_set +
+                         (size_t)4096 * d->H * (HEAD_DIM + 2) * 4;
     const size_t reserve = (size_t)2 << 30 > total_bytes / 64 ? (size_t)2 << 30 : total_bytes / 64;
     REQUIRE(free_bytes > fixed + reserve + per_slot, "no slot fits in free device memory");
     const size_t fit = (free_bytes - fixed - reserve) / per_slot;
     d->B = (int)(fit < (size_t)max_slots ? fit : (size_t)max_slots);
 
-    d->slot_pages = (long long)d->B * d->max_pages;
-    d->layer_pages = d->slot_pages + (long long)store_pages;
+    d->pool = pool_pages > 0 ? pool_pages : (long long)d->B * d->max_pages;
+    d->layer_pages = d->pool + (long long)store_pages;
     REQUIRE(d->layer_pages < (1LL << 31), "a layer's pool exceeds 2^31 pages");
     d->k_pages = (uint8_t *)device_alloc(d, (size_t)d->L * d->layer_pages * d->H * PAGE_BYTES);
     d->v_pages = (uint8_t *)device_alloc(d, (size_t)d->L * d->layer_pages * d->H * PAGE_BYTES);
     d->kv_scale = (float *)device_alloc(d, (size_t)d->L * d->layer_pages * d->H * 2 * PAGE * sizeof(float));
-    d->block_table = (int32_t *)device_alloc(d, (size_t)d->slot_pages * sizeof(int32_t));
-    hipLaunchKernelGGL(identity_table_kernel, dim3((unsigned)((d->slot_pages + 255) / 256)), dim3(256), 0, d->stream,
-                       d->block_table, d->slot_pages);
-    d->table.resize(d->slot_pages);
-    for (long long i = 0; i < d->slot_pages; i++) d->table[i] = (int32_t)i;
+    const long long entries = (long long)d->B * d->max_pages;
+    d->block_table = (int32_t *)device_alloc(d, (size_t)entries * sizeof(int32_t));
+    hipLaunchKernelGGL(set_table_kernel, dim3((unsigned)((entries + 255) / 256)), dim3(256), 0, d->stream,
+                       d->block_table, 0LL, entries, -1, 0);
+    d->table.assign(entries, -1);
+    d->free_pages.resize(d->pool);
+    for (long long i = 0; i < d->pool; i++) d->free_pages[i] = (int32_t)(d->pool - 1 - i);   /* page 0 on top */
     d->hpos.assign(d->B, 0);
     d->live.assign(MASK_WORDS, 0);
     const size_t B = d->B;
@@ -1046,65 +1054,90 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     return d;
 }
 
-/* ---------------------------------------------------------------- the prompt store as shared pages
+/* ---------------------------------------------------------------- pages: the pool and the prompt store
  *
- * dec_load_prompt points a slot's block-table entries at the store's pages wherever the two ranges share their page
- * phase ((store_at - at) % 16 == 0) and a page lies wholly inside the range: the prompt's K and V are then read in
- * place, with no copy (the reference copies the store into the slot, decode.cu:1055-1075). Partial pages are copied
- * as before. Nothing ever writes a shared page: before any write into a slot (a prefill row, a live slot's step at
- * its host-tracked position, a partial copy) the entry is first pointed back at the slot's own page, with the store
- * page's content copied there (copy on write); before dec_save_prompt writes store pages, every slot sharing them
- * gets its own copy. */
+ * A slot's block-table row maps its logical pages to pool pages taken on demand (own_pages) and returned when the
+ * slot's sequence is dropped (release_pages); entries of positions the slot has not written are -1 (never read: a
+ * pass reads only pages below its sequence's length). dec_load_prompt points a slot's entries at the store's pages
+ * wherever the two ranges share their page phase ((store_at - at) % 16 == 0) and a page lies wholly inside the range:
+ * the prompt's K and V are then read in place, with no copy (the reference copies the store into the slot,
+ * decode.cu:1055-1075). Partial pages are copied. Nothing ever writes a shared page: before any write into a slot (a
+ * prefill row, a live slot's step at its host-tracked position, a partial copy) the entry gets a pool page of the
+ * slot's own, with the store page's content copied there (copy on write); before dec_save_prompt writes store pages,
+ * every slot sharing them gets its own copy. Work is stream-ordered, so a page returned to the pool is reused only by
+ * work enqueued after every earlier reader. */
 
-static long long home_page(const Decoder *d, int b, int e) { return (long long)b * d->max_pages + e; }
+static bool store_page(const Decoder *d, int32_t page) { return page >= d->pool; }
 
-/* Slot b's host entries [e0, e1) to the device table, one launch per run of consecutive pages. */
+static int32_t *table_row(Decoder *d, int b) { return d->table.data() + (size_t)b * d->max_pages; }
+
+/* Slot b's host entries [e0, e1) to the device table, one launch per run of consecutive pages or of -1. */
 static void upload_table(Decoder *d, int b, int e0, int e1) {
-    const int32_t *row = d->table.data() + home_page(d, b, 0);
+    const int32_t *row = table_row(d, b);
     for (int e = e0; e < e1;) {
+        const int step = row[e] < 0 ? 0 : 1;
         int f = e + 1;
-        while (f < e1 && row[f] == row[f - 1] + 1) f++;
+        while (f < e1 && row[f] == row[f - 1] + step && (row[f] < 0) == (row[e] < 0)) f++;
         hipLaunchKernelGGL(set_table_kernel, dim3((unsigned)((f - e + 255) / 256)), dim3(256), 0, d->stream,
-                           d->block_table, home_page(d, b, e), f - e, row[e]);
+                           d->block_table, (long long)b * d->max_pages + e, (long long)(f - e), row[e], step);
         e = f;
     }
     HIP_CHECK(hipGetLastError());
 }
 
-/* Slot b's entries [e0, e1) that share a store page point back at the slot's own page; with keep, the shared page is
- * first copied there, so the positions the slot does not rewrite keep their values. */
-static void unshare(Decoder *d, int b, int e0, int e1, bool keep) {
-    int32_t *row = d->table.data() + home_page(d, b, 0);
+static int32_t take_page(Decoder *d) {
+    if (d->free_pages.empty())
+        die("KV page pool", "no free page left (admit fewer or shorter sequences, or give dec_create_pool more)",
+            __LINE__);
+    const int32_t p = d->free_pages.back();
+    d->free_pages.pop_back();
+    return p;
+}
+
+/* Slot b's entries [e0, e1) become pages of its own: -1 takes a pool page; a shared store page takes one too, and with
+ * keep the store page is first copied there, so the positions the slot does not rewrite keep their values. */
+static void own_pages(Decoder *d, int b, int e0, int e1, bool keep) {
+    int32_t *row = table_row(d, b);
     int lo = e1, hi = e0;
-    for (int e = e0; e < e1;) {
-        if (row[e] == home_page(d, b, e)) {
-            e++;
-            continue;
-        }
-        int f = e + 1;
-        while (f < e1 && row[f] != home_page(d, b, f) && row[f] == row[f - 1] + 1) f++;
-        if (keep) {
-            hipLaunchKernelGGL(copy_pages_kernel, dim3((unsigned)d->H, (unsigned)d->L, (unsigned)(f - e)), dim3(256), 0,
-                               d->stream, d->k_pages, d->v_pages, d->kv_scale, d->layer_pages, d->H, (long long)row[e],
-                               home_page(d, b, e));
+    for (int e = e0; e < e1; e++) {
+        if (row[e] >= 0 && !store_page(d, row[e])) continue;
+        const int32_t page = take_page(d);
+        if (row[e] >= 0 && keep) {
+            hipLaunchKernelGGL(copy_pages_kernel, dim3((unsigned)d->H, (unsigned)d->L, 1u), dim3(256), 0, d->stream,
+                               d->k_pages, d->v_pages, d->kv_scale, d->layer_pages, d->H, (long long)row[e],
+                               (long long)page);
             HIP_CHECK(hipGetLastError());
         }
-        for (int i = e; i < f; i++) row[i] = (int32_t)home_page(d, b, i);
+        row[e] = page;
         lo = e < lo ? e : lo;
-        hi = f > hi ? f : hi;
-        e = f;
+        hi = e + 1 > hi ? e + 1 : hi;
     }
     if (lo < hi) upload_table(d, b, lo, hi);
 }
 
-/* Positions [at, at + n) of slot b (through its block table) <-> store positions [store_at, store_at + n). */
+/* Slot b's entries from e0 on drop their pages: its own return to the pool, shared store pages are only unlinked. */
+static void release_pages(Decoder *d, int b, int e0) {
+    int32_t *row = table_row(d, b);
+    int lo = d->max_pages, hi = e0;
+    for (int e = e0 < 0 ? 0 : e0; e < d->max_pages; e++) {
+        if (row[e] < 0) continue;
+        if (!store_page(d, row[e])) d->free_pages.push_back(row[e]);
+        row[e] = -1;
+        lo = e < lo ? e : lo;
+        hi = e + 1;
+    }
+    if (lo < hi) upload_table(d, b, lo, hi);
+}
+
+/* Positions [at, at + n) of slot b (through its block table) <-> store positions [store_at, store_at + n). The slot's
+ * entries of those positions hold pages (the callers' checks). */
 static void copy_positions(Decoder *d, int b, int at, int store_at, int n, bool to_store) {
     if (n <= 0) return;
-    const int32_t *tab = d->block_table + home_page(d, b, 0);
+    const int32_t *tab = d->block_table + (size_t)b * d->max_pages;
     const long long units = (long long)n * d->L * d->H;
     hipLaunchKernelGGL(copy_positions_kernel, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, d->stream, d->k_pages,
-                       d->v_pages, d->kv_scale, d->layer_pages, d->H, d->L, to_store ? tab : nullptr, d->slot_pages,
-                       to_store ? at : store_at, to_store ? nullptr : tab, d->slot_pages, to_store ? store_at : at, n);
+                       d->v_pages, d->kv_scale, d->layer_pages, d->H, d->L, to_store ? tab : nullptr, d->pool,
+                       to_store ? at : store_at, to_store ? nullptr : tab, d->pool, to_store ? store_at : at, n);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -1116,36 +1149,44 @@ static void check_prompt_range(const Decoder *d, int b, int at, int store_at, in
 static void save_prompt(Decoder *d, int b, int at, int store_at, int n) {
     check_prompt_range(d, b, at, store_at, n);
     if (n == 0) return;
+    const int32_t *src = table_row(d, b);
+    for (int e = at / PAGE; e <= (at + n - 1) / PAGE; e++)
+        if (src[e] < 0) die("dec_save_prompt", "a position the slot has not cached", __LINE__);
     /* slots sharing the store pages about to change keep their own copies */
-    const int32_t p0 = (int32_t)(d->slot_pages + store_at / PAGE), p1 = (int32_t)(d->slot_pages + (store_at + n - 1) / PAGE);
+    const int32_t p0 = (int32_t)(d->pool + store_at / PAGE), p1 = (int32_t)(d->pool + (store_at + n - 1) / PAGE);
     for (int s = 0; s < d->B; s++) {
-        const int32_t *row = d->table.data() + home_page(d, s, 0);
+        const int32_t *row = table_row(d, s);
         for (int e = 0; e < d->max_pages; e++)
-            if (row[e] >= p0 && row[e] <= p1) unshare(d, s, e, e + 1, true);
+            if (row[e] >= p0 && row[e] <= p1) own_pages(d, s, e, e + 1, true);
     }
     copy_positions(d, b, at, store_at, n, true);
 }
 
+/* A load at position 0 starts the slot's sequence anew: its pages are released first. */
 static void load_prompt(Decoder *d, int b, int at, int store_at, int n) {
     check_prompt_range(d, b, at, store_at, n);
     if (n == 0) return;
+    if (at == 0) release_pages(d, b, 0);
     const int e_lo = (at + PAGE - 1) / PAGE, e_hi = (at + n) / PAGE;   /* pages wholly inside [at, at + n) */
     if ((store_at - at) % PAGE != 0 || e_lo >= e_hi) {
-        unshare(d, b, at / PAGE, (at + n - 1) / PAGE + 1, true);
+        own_pages(d, b, at / PAGE, (at + n - 1) / PAGE + 1, true);
         copy_positions(d, b, at, store_at, n, false);
         return;
     }
     if (at % PAGE) {   /* the leading partial page */
-        unshare(d, b, at / PAGE, at / PAGE + 1, true);
+        own_pages(d, b, at / PAGE, at / PAGE + 1, true);
         copy_positions(d, b, at, store_at, e_lo * PAGE - at, false);
     }
     if ((at + n) % PAGE) {   /* the trailing partial page */
-        unshare(d, b, e_hi, e_hi + 1, true);
+        own_pages(d, b, e_hi, e_hi + 1, true);
         copy_positions(d, b, e_hi * PAGE, store_at + (e_hi * PAGE - at), at + n - e_hi * PAGE, false);
     }
-    int32_t *row = d->table.data() + home_page(d, b, 0);
-    const long long shift = d->slot_pages + (store_at - at) / PAGE;
-    for (int e = e_lo; e < e_hi; e++) row[e] = (int32_t)(shift + e);
+    int32_t *row = table_row(d, b);
+    const long long shift = d->pool + (store_at - at) / PAGE;
+    for (int e = e_lo; e < e_hi; e++) {
+        if (row[e] >= 0 && !store_page(d, row[e])) d->free_pages.push_back(row[e]);
+        row[e] = (int32_t)(shift + e);
+    }
     upload_table(d, b, e_lo, e_hi);
 }
 
@@ -1156,7 +1197,11 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
     for (int r = 0; r < n; r++)
         if (slot[r] < 0 || slot[r] >= d->B || pos[r] < 0 || pos[r] >= d->max_len || tok[r] < 0 || tok[r] >= d->vocab)
             die("dec_prefill", "row with a slot, position or token out of range", __LINE__);
-    for (int r = 0; r < n; r++) unshare(d, slot[r], pos[r] / PAGE, pos[r] / PAGE + 1, true);
+    /* a row at position 0 starts its slot's sequence anew (its pages are released); every row's page is the slot's
+     * own before the rows are written */
+    for (int r = 0; r < n; r++)
+        if (pos[r] == 0) release_pages(d, slot[r], 0);
+    for (int r = 0; r < n; r++) own_pages(d, slot[r], pos[r] / PAGE, pos[r] / PAGE + 1, true);
     HIP_CHECK(hipEventSynchronize(d->staged));  /* the previous upload has been read */
     int32_t *s = d->staging;
     memcpy(s, tok, n * sizeof(int32_t));
@@ -1235,11 +1280,29 @@ using nc::dec::Decoder;
 
 extern "C" void *dec_create_slots(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window,
                                   void *stream, int max_slots) {
-    return nc::dec::create(cfg, ptrs, scal, window, stream, max_slots);
+    return nc::dec::create(cfg, ptrs, scal, window, stream, max_slots, 0);
+}
+
+extern "C" void *dec_create_pool(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window,
+                                 void *stream, int max_slots, long long pool_pages) {
+    if (pool_pages <= 0) nc::dec::die("dec_create_pool", "the pool needs at least one page", __LINE__);
+    return nc::dec::create(cfg, ptrs, scal, window, stream, max_slots, pool_pages);
+}
+
+extern "C" void dec_release(void *handle, int b) {
+    Decoder *d = (Decoder *)handle;
+    if (b < 0 || b >= d->B) nc::dec::die("dec_release", "slot out of range", __LINE__);
+    nc::dec::release_pages(d, b, 0);
+}
+
+extern "C" void dec_debug_pages(void *handle, long long *out) {
+    const Decoder *d = (const Decoder *)handle;
+    out[0] = (long long)d->free_pages.size();
+    out[1] = d->pool;
 }
 
 extern "C" void *dec_create(const int *cfg, const uint64_t *ptrs, const float *scal, const int *window, void *stream) {
-    return nc::dec::create(cfg, ptrs, scal, window, stream, nc::dec::MAX_BATCH);
+    return nc::dec::create(cfg, ptrs, scal, window, stream, nc::dec::MAX_BATCH, 0);
 }
 
 extern "C" int dec_batch(void *handle) { return ((Decoder *)handle)->B; }
@@ -1253,6 +1316,7 @@ extern "C" void dec_set_prompt(void *handle, int b, int32_t token, int32_t last,
                        d->temperature, d->top_p, d->seed, b, token, last, temperature, top_p, seed);
     HIP_CHECK(hipGetLastError());
     d->hpos[b] = last;
+    nc::dec::release_pages(d, b, last / nc::PAGE + 1);   /* pages past the slot's position hold an older sequence */
 }
 
 extern "C" int dec_prefill_rows(void *) { return nc::dec::PREFILL_ROWS; }
@@ -1302,7 +1366,7 @@ extern "C" void dec_launch_body(void *handle) {
     /* the step writes each live slot's K and V at its position: that page must be the slot's own */
     for (int b = 0; b < d->B; b++)
         if (((d->live[b / nc::dec::MASK_BITS] >> (b % nc::dec::MASK_BITS)) & 1ull) && d->hpos[b] < d->max_len)
-            nc::dec::unshare(d, b, d->hpos[b] / nc::PAGE, d->hpos[b] / nc::PAGE + 1, true);
+            nc::dec::own_pages(d, b, d->hpos[b] / nc::PAGE, d->hpos[b] / nc::PAGE + 1, true);
     nc::dec::enqueue_body(d);
     HIP_CHECK(hipGetLastError());
 }
@@ -1349,8 +1413,15 @@ extern "C" void dec_debug_cache(void *handle, int layer, int b, int at, int n, u
     std::vector<uint8_t> kp((size_t)pages * H * PAGE_BYTES), vp(kp.size());
     std::vector<float> sp((size_t)pages * H * 2 * PAGE);
     for (int pg = 0; pg < pages; pg++) {   /* a slot's pages through its block table, the store's in order */
-        const long long page = b < 0 ? d->slot_pages + first + pg : d->table[(size_t)b * d->max_pages + first + pg];
-        const size_t base = (size_t)(d->layer_pages * layer + page) * H, at_h = (size_t)pg * H;
+        const long long page = b < 0 ? d->pool + first + pg : d->table[(size_t)b * d->max_pages + first + pg];
+        const size_t at_h = (size_t)pg * H;
+        if (page < 0) {   /* a page the slot has not written: zeros */
+            memset(kp.data() + at_h * PAGE_BYTES, 0, (size_t)H * PAGE_BYTES);
+            memset(vp.data() + at_h * PAGE_BYTES, 0, (size_t)H * PAGE_BYTES);
+            memset(sp.data() + at_h * 2 * PAGE, 0, (size_t)H * 2 * PAGE * sizeof(float));
+            continue;
+        }
+        const size_t base = (size_t)(d->layer_pages * layer + page) * H;
         HIP_CHECK(hipMemcpy(kp.data() + at_h * PAGE_BYTES, d->k_pages + base * PAGE_BYTES, (size_t)H * PAGE_BYTES,
                             hipMemcpyDeviceToHost));
         HIP_CHECK(hipMemcpy(vp.data() + at_h * PAGE_BYTES, d->v_pages + base * PAGE_BYTES, (size_t)H * PAGE_BYTES,

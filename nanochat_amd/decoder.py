@@ -113,11 +113,13 @@ class DecoderRuntime:
     """One libnanochat_decode.so decoder with up to `max_slots` slots (fewer when device memory runs short).
 
     max_length: cache positions per slot; prompt_store: positions of the device prompt store, where every prefilled
-    prompt is kept (page-aligned, never evicted) so that a later slot given the same prompt shares its pages."""
+    prompt is kept (page-aligned, never evicted) so that a later slot given the same prompt shares its pages.
+    pool_pages: the KV page pool the slots draw from (16 positions a page); by default every slot can reach
+    max_length, a smaller pool lets more slots run sequences shorter than that (serve admits requests by it)."""
 
     @torch.no_grad()
     def __init__(self, model: ModelTensors, *, bos_token_id: int, max_length: int, prompt_store: int = 0,
-                 max_slots: int | None = None):
+                 max_slots: int | None = None, pool_pages: int | None = None):
         model.check()
         if max_length > model.cos.size(0):
             raise ValueError(f"max_length {max_length} exceeds the rotary table's {model.cos.size(0)} positions")
@@ -138,8 +140,12 @@ class DecoderRuntime:
         torch.cuda.synchronize()   # the weights were written on another stream
         args = (self._cfg.ctypes.data, self._ptrs.ctypes.data, self._scal.ctypes.data, self._window.ctypes.data,
                 self.stream.cuda_stream)
-        self.handle = (self.lib.dec_create(*args) if max_slots is None else
-                       self.lib.dec_create_slots(*args, max_slots))
+        if pool_pages is not None:
+            self.handle = self.lib.dec_create_pool(*args, 1024 if max_slots is None else max_slots, pool_pages)
+        elif max_slots is not None:
+            self.handle = self.lib.dec_create_slots(*args, max_slots)
+        else:
+            self.handle = self.lib.dec_create(*args)
         self._release = weakref.finalize(self, self.lib.dec_destroy, self.handle)
         self.batch = self.lib.dec_batch(self.handle)
         self.rows_per_prefill = self.lib.dec_prefill_rows(self.handle)
@@ -220,6 +226,16 @@ class DecoderRuntime:
         self.lib.dec_tokens(self.handle, self._out.ctypes.data)
         return self.choices
 
+    def release(self, slot: int) -> None:
+        """The slot's KV pages return to the pool (its next prompt starts a new sequence anyway)."""
+        self.lib.dec_release(self.handle, slot)
+
+    def pages(self) -> tuple[int, int]:
+        """(free pages, pool size) of the KV page pool."""
+        out = np.zeros(2, dtype=np.int64)
+        self.lib.dec_debug_pages(self.handle, out.ctypes.data)
+        return int(out[0]), int(out[1])
+
     def take_alternative(self, slot: int) -> None:
         """Slot's next input becomes its alternative (its best choice other than BOS) instead of its choice."""
         self.lib.dec_take_alt(self.handle, slot)
@@ -242,8 +258,8 @@ class DecoderRuntime:
         return k, v, s
 
     def table(self, slot: int) -> np.ndarray:
-        """The slot's block-table row: entry e is the slot's own page slot * pages + e, or batch * pages + i for page
-        i of the prompt store (shared)."""
+        """The slot's block-table row: entry e is -1 (no page yet), a pool page of the slot's own (below the pool
+        size), or pool size + i for page i of the prompt store (shared)."""
         out = np.empty(-(-self.max_length // PAGE_SIZE), np.int32)
         self.lib.dec_debug_table(self.handle, slot, out.ctypes.data)
         return out
@@ -263,22 +279,36 @@ def serve(rt: DecoderRuntime, requests: Iterable[Request],
           timings: dict | None = None) -> Iterator[tuple[int, list[int]]]:
     """Decode `requests` on rt's slots; yields (request index, generated tokens) as requests end.
 
-    Requests take free slots in order. Each step: the new prompts are prefilled, the constrained slots' masks are
-    written, every live slot decodes one token. A request ends after max_new_tokens tokens, when its stopping test
+    Requests take free slots in order, while the KV page pool can hold every admitted request at its longest (prompt
+    plus max_new_tokens positions); a slot's pages return to the pool when its request ends. Each step: the new
+    prompts are prefilled, the constrained slots' masks are written, every live slot decodes one token. A request ends after max_new_tokens tokens, when its stopping test
     holds, or on BOS (not included). A BOS its constraint does not accept (`ends()` false) is replaced by the step's
     alternative. Raises ValueError when a constraint leaves no token. timings, when given, receives
     {index: (start, first token, end)} in time.perf_counter() seconds."""
     todo = deque(enumerate(requests))
     live: dict[int, _Live] = {}
+    pool = rt.pages()[1]
+    reserved: dict[int, int] = {}   # slot -> pages its request may take at its longest
+
+    def pages_for(req: Request) -> int:
+        return -(-(len(req.input_ids) - 1 + req.max_new_tokens) // PAGE_SIZE)
+
     while todo or live:
         for slot in range(rt.batch):
             if slot not in live and todo:
-                index, req = todo.popleft()
+                index, req = todo[0]
                 if req.max_new_tokens < 1 or len(req.input_ids) - 1 + req.max_new_tokens > rt.max_length:
                     raise ValueError(f"request {index}: {len(req.input_ids)} prompt tokens and {req.max_new_tokens} "
                                      f"new ones do not fit max_length {rt.max_length}")
+                need = pages_for(req)
+                if sum(reserved.values()) + need > pool:
+                    if not live:
+                        raise ValueError(f"request {index} needs {need} KV pages, the pool holds {pool}")
+                    break
+                todo.popleft()
                 rt.place(slot, req.input_ids, temperature=req.temperature, top_p=req.top_p, seed=req.seed)
                 live[slot] = _Live(index, req, time.perf_counter())
+                reserved[slot] = need
         rt.prefill()
         masked = []
         for slot, run in live.items():
@@ -313,6 +343,8 @@ def serve(rt: DecoderRuntime, requests: Iterable[Request],
                 ended.append(slot)
         for slot in ended:
             run = live.pop(slot)
+            del reserved[slot]
+            rt.release(slot)
             if timings is not None:
                 timings[run.index] = (run.started, now if run.first is None else run.first, now)
             yield run.index, run.out

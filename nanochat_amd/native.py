@@ -116,6 +116,9 @@ SIGNATURES = {
 DECODE_SIGNATURES = {
     "dec_create": ([c_void_p] * 5, c_void_p),
     "dec_create_slots": ([c_void_p] * 5 + [c_int], c_void_p),
+    "dec_create_pool": ([c_void_p] * 5 + [c_int, c_longlong], c_void_p),
+    "dec_release": ([c_void_p, c_int], None),
+    "dec_debug_pages": ([c_void_p, c_void_p], None),
     "dec_batch": ([c_void_p], c_int),
     "dec_set_prompt": ([c_void_p, c_int, ctypes.c_int32, ctypes.c_int32, c_float, c_float, ctypes.c_ulonglong], None),
     "dec_prefill_rows": ([c_void_p], c_int),

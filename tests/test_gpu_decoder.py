@@ -131,9 +131,10 @@ def test_prompt_store_round_trip_and_reuse(device):
         dec.place(5, ids[0])   # loaded from the store, not prefilled
         assert not dec.queued
         n = len(ids[0]) - 1
-        pages = len(dec.table(5))
-        # the prompt's 3 whole pages are the store's (shared), the partial 4th is the slot's own copy
-        assert list(dec.table(5)[:4]) == [dec.batch * pages + e for e in range(3)] + [5 * pages + 3]
+        pool = dec.pages()[1]
+        # the prompt's 3 whole pages are the store's (shared), the partial 4th a pool page of the slot's own
+        row = dec.table(5)
+        assert list(row[:3]) == [pool + e for e in range(3)] and 0 <= row[3] < pool
         for layer in range(len(m.layers)):
             a, s_ = dec.cache_rows(layer, 0, 0, n), dec.cache_rows(layer, -1, 0, n)
             c = dec.cache_rows(layer, 5, 0, n)
@@ -154,49 +155,82 @@ def test_prompt_store_round_trip_and_reuse(device):
 
 def test_shared_store_pages_copy_on_write(device):
     """A loaded prompt's whole pages are shared with the store; every later write into the slot or the store gives
-    the writer its own page: a prefill over a shared range, a save over shared store pages, a load at another page
-    phase (copied, not shared). Cache bytes compared through the block tables after each."""
+    the writer a page of its own with the shared page's bytes copied first: prefill rows inside shared pages, a save
+    over shared store pages; a load at another page phase copies and shares nothing. Cache bytes compared through the
+    block tables after each."""
     m, w, max_length = build(device, "tiny")
     ids = prompts([50, 41], m.vocab, seed=12)
     dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=400, max_slots=8)
     L = len(m.layers)
     try:
-        for b in (0, 1):   # each prefilled alone, so slot 3's prefill of B below runs the same GEMM shapes
+        for b in (0, 1):
             dec.place(b, ids[b])
             dec.prefill()                               # A = ids[0] at store 0, B = ids[1] at store 64
         assert dec.stored == {tuple(ids[0]): 0, tuple(ids[1]): 64}
         nA, nB = len(ids[0]) - 1, len(ids[1]) - 1
         A = [dec.cache_rows(l, 0, 0, nA) for l in range(L)]
         B = [dec.cache_rows(l, 1, 0, nB) for l in range(L)]
-        pages = len(dec.table(0))
-        store = dec.batch * pages
+        store = dec.pages()[1]   # store page i is pool + i
 
         def same(got, want):
             return all(np.array_equal(x, y) for x, y in zip(got, want))
 
+        def own(row):
+            return all(0 <= p < store for p in row)
+
         dec.lib.dec_load_prompt(dec.handle, 3, 0, 0, nA)           # slot 3 shares A's pages 0..2
         assert list(dec.table(3)[:3]) == [store, store + 1, store + 2]
-        dec.lib.dec_prefill(dec.handle, nB, np.ascontiguousarray(
-            np.array([ids[1][:-1], range(nB), [3] * nB], dtype=np.int32)).ctypes.data)   # B over A's shared pages
-        assert list(dec.table(3)[:3]) == [3 * pages + e for e in range(3)]
+        lo = 20                                                     # rows lo..nB-1 of B's tokens over pages 1, 2
+        dec.lib.dec_prefill(dec.handle, nB - lo, np.ascontiguousarray(
+            np.array([ids[1][lo:-1], range(lo, nB), [3] * (nB - lo)], dtype=np.int32)).ctypes.data)
+        row = dec.table(3)
+        assert row[0] == store and own(row[1:3])
         for l in range(L):
-            assert same(dec.cache_rows(l, 3, 0, nB), B[l]), l            # slot 3 holds B's rows
-            assert same(dec.cache_rows(l, -1, 0, nA), A[l]), l           # the store still holds A
-            assert same(dec.cache_rows(l, 3, nB, nA - nB), [x[nB:] for x in A[l]]), l   # A's rows past B kept (CoW)
+            assert same(dec.cache_rows(l, 3, 0, lo), [x[:lo] for x in A[l]]), l              # copied before the rows
+            assert same(dec.cache_rows(l, 3, nB, nA - nB), [x[nB:] for x in A[l]]), l       # and after them
+            assert same(dec.cache_rows(l, -1, 0, nA), A[l]), l                              # the store still holds A
 
         dec.lib.dec_load_prompt(dec.handle, 4, 0, 0, nA)           # slot 4 shares A ...
         dec.lib.dec_save_prompt(dec.handle, 1, 0, 0, nB)           # ... then B overwrites store positions 0..39
-        assert list(dec.table(4)[:3]) == [4 * pages + e for e in range(3)]
+        row4 = dec.table(4)
+        assert own(row4[:3]) and not set(row4[:3]) & set(dec.table(3)[:3])
         for l in range(L):
             assert same(dec.cache_rows(l, 4, 0, nA), A[l]), l            # slot 4 kept A
             assert same(dec.cache_rows(l, -1, 0, nB), B[l]), l
 
         dec.lib.dec_load_prompt(dec.handle, 6, 3, 64, nB)          # another page phase: copied, nothing shared
-        assert list(dec.table(6)) == [6 * pages + e for e in range(pages)]
+        row6 = dec.table(6)
+        last = (3 + nB - 1) // 16
+        assert own(row6[:last + 1]) and all(p == -1 for p in row6[last + 1:])
         for l in range(L):
             assert same(dec.cache_rows(l, 6, 3, nB), B[l]), l
+        free, pool = dec.pages()
+        for b in range(dec.batch):
+            dec.release(b)
+        assert dec.pages() == (pool, pool)
     finally:
         dec.close()
+
+
+def test_page_pool_smaller_than_full_slots(device):
+    """A pool of 10 pages for 8 slots of max_length 160 (10 pages each): serve admits requests while their longest
+    extent fits the pool, returns each request's pages when it ends, and gives every request the same tokens as a
+    decoder whose slots all reserve max_length (a request's tokens do not depend on the batch)."""
+    m, w, max_length = build(device, "tiny")
+    reqs = [Request(input_ids=p, max_new_tokens=8) for p in prompts([30, 17, 25, 31, 9, 22, 28, 14, 31, 5],
+                                                                      m.vocab, seed=31)]
+    results = {}
+    for pool in (None, 10):
+        rt = DecoderRuntime(m, bos_token_id=0, max_length=max_length, max_slots=8, pool_pages=pool)
+        try:
+            assert rt.batch == 8
+            results[pool] = dict(serve(rt, reqs))
+            free, size = rt.pages()
+            assert free == size and size == (8 * 10 if pool is None else pool)
+        finally:
+            rt.close()
+    assert results[None] == results[10]
+    assert sorted(results[10]) == list(range(len(reqs)))
 
 
 def test_masks_and_alternative(device):
