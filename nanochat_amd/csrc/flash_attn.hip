@@ -475,37 +475,42 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dq_kernel(FlashBwd a)
         if (!active) return;
         const int k0 = kb * FA_BN, k1 = k0 + FA_BN - 1;
         const bool interior = k1 <= q0 && k1 < seglen && (a.window < 0 || qw1 - k0 <= a.window);
-        bf16x8 db[2][2];
+        /* k-step s2 (key tiles 2 s2, 2 s2 + 1): its dS^T half is formed, then consumed by the dQ products at once, so
+         * only one half is ever live; each dq element still adds k-step 0, then 1 */
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-            f32x4 sc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}}, dp[2] = {sc[0], sc[1]};
+        for (int s2 = 0; s2 < 2; s2++) {
+            bf16x8 db[2];
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const bf16x8 kop = rows_operand(s.k, kt, cc, g, c), vop = rows_operand(s.v, kt, cc, g, c);
+            for (int kk = 0; kk < 2; kk++) {
+                const int kt = 2 * s2 + kk;
+                f32x4 sc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}}, dp[2] = {sc[0], sc[1]};
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    sc[j] = mfma16x16x32(kop, qb_[j][cc], sc[j]);
-                    dp[j] = mfma16x16x32(vop, ob_[j][cc], dp[j]);
+                for (int cc = 0; cc < 4; cc++) {
+                    const bf16x8 kop = rows_operand(s.k, kt, cc, g, c), vop = rows_operand(s.v, kt, cc, g, c);
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        sc[j] = mfma16x16x32(kop, qb_[j][cc], sc[j]);
+                        dp[j] = mfma16x16x32(vop, ob_[j][cc], dp[j]);
+                    }
                 }
+                /* lane (g, c): query column c of tile j, keys k0 + 16 kt + 4 g + i */
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        float p = __builtin_amdgcn_exp2f(sc[j][i] * a.scale_log2 - lse2[j]);
+                        if (!interior && !visible(k0 + 16 * kt + 4 * g + i, q0 + 16 * j + c, seglen, a.window))
+                            p = 0.0f;
+                        db[j][kk * 4 + i] = (__bf16)(p * (dp[j][i] - dd[j]));
+                    }
             }
-            /* lane (g, c): query column c of tile j, keys k0 + 16 kt + 4 g + i */
 #pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float p = __builtin_amdgcn_exp2f(sc[j][i] * a.scale_log2 - lse2[j]);
-                    if (!interior && !visible(k0 + 16 * kt + 4 * g + i, q0 + 16 * j + c, seglen, a.window)) p = 0.0f;
-                    db[j][kt >> 1][(kt & 1) * 4 + i] = (__bf16)(p * (dp[j][i] - dd[j]));
-                }
-        }
-#pragma unroll
-        for (int d = 0; d < 8; d++)
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++) {
+            for (int d = 0; d < 8; d++) {
                 const bf16x8 kop = tr_operand(s.k, d, s2, g, c);
 #pragma unroll
-                for (int j = 0; j < 2; j++) dq[j][d] = mfma16x16x32(kop, db[j][s2], dq[j][d]);
+                for (int j = 0; j < 2; j++) dq[j][d] = mfma16x16x32(kop, db[j], dq[j][d]);
             }
+        }
     };
     const int kb_lo = klo / FA_BN, kb_hi = qb / FA_BN;
     fetch(kb_lo, s0);
