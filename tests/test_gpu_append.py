@@ -117,6 +117,36 @@ def test_qk_forward_matches_oracle(device):
         assert np.array_equal(bf16_bits(want), got.view(torch.int16).cpu().numpy().view(np.uint16))
 
 
+def test_golden_rope_vectors(device):
+    """The committed q/k-norm + rotation vectors (tests/golden/rope.npz): each row appended as the q head of its own
+    sequence at its position (the fused append, the product's rotary tables) and, as the k head, through the training
+    prologue at the same position, gives the committed bf16 bits."""
+    want = np.load(GOLDEN / "rope.npz")
+    x = torch.from_numpy(want["x_bf16"].view(np.int16)).view(torch.bfloat16)
+    pos = want["row_positions"]
+    n = x.shape[0]
+    gain = torch.from_numpy(want["gain"]).to(device)
+    cos, sin = rotary_tables(int(pos.max()) + 1, 1e6, device)
+    # fused append: sequence i holds row i as its q head (and as k and v) at position pos[i]
+    qkv = x.view(n, 1, 1, 128).expand(n, 1, 3, 128).reshape(n, 1, 3 * 128).contiguous().to(device)
+    mp = int(pos.max()) // 16 + 1
+    table = contiguous_block_table(n, mp, device)
+    cache = PagedKVCache(n * mp, 1, device)
+    q = qk_norm_rope_append(qkv, 1, cache, table, torch.from_numpy(pos.astype(np.int32)).to(device), gain, gain,
+                            cos, sin)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.view(torch.int16).cpu().numpy().view(np.uint16).reshape(n, 128), want["y_bf16"])
+    # training prologue: one sequence of pos.max() + 1 tokens, row i placed at token pos[i] of head 0 of k
+    T = int(pos.max()) + 1
+    for i in range(n):
+        fused = torch.zeros(1, T, 3, 1, 128, dtype=torch.bfloat16)
+        fused[0, pos[i], 1, 0] = x[i]
+        fused = fused.to(device)
+        _, ko = qk_forward(fused[:, :, 0], fused[:, :, 1], gain, gain, cos, sin)
+        torch.cuda.synchronize()
+        assert np.array_equal(ko[0, pos[i], 0].view(torch.int16).cpu().numpy().view(np.uint16), want["y_bf16"][i]), i
+
+
 def test_append_skips_out_of_range_pages(device):
     """A position past the block table, or a table entry outside the pool, writes nothing."""
     cache = PagedKVCache(2, 1, device)
