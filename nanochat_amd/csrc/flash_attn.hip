@@ -365,33 +365,37 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dkv_kernel(FlashBwd a
         const int qs = qbk * FA_BN;
         const int kw1 = kw + 15, qe = qs + FA_BN - 1;
         const bool interior = kw1 <= qs && qe < seglen && kw1 < seglen && (a.window < 0 || qe - kw <= a.window);
-        bf16x8 pb[2], db[2];
+        /* k-step s2 (query tiles 2 s2, 2 s2 + 1): its P and dS halves are formed, then consumed by the dV and dK
+         * products at once; each dv, dk element still adds k-step 0, then 1 */
 #pragma unroll
-        for (int qt = 0; qt < 4; qt++) {
-            f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s2 = 0; s2 < 2; s2++) {
+            bf16x8 pb, db;
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                sc = mfma16x16x32(rows_operand(s.q, qt, cc, g, c), kb_[cc], sc);
-                dp = mfma16x16x32(rows_operand(s.dout, qt, cc, g, c), vb_[cc], dp);
+            for (int qq = 0; qq < 2; qq++) {
+                const int qt = 2 * s2 + qq;
+                f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    sc = mfma16x16x32(rows_operand(s.q, qt, cc, g, c), kb_[cc], sc);
+                    dp = mfma16x16x32(rows_operand(s.dout, qt, cc, g, c), vb_[cc], dp);
+                }
+                /* lane (g, c): key c, query rows qs + 16 qt + 4 g + i */
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = qt * 16 + 4 * g + i;
+                    float p = __builtin_amdgcn_exp2f(sc[i] * a.scale_log2 - s.lse2[r]);
+                    if (!interior && !visible(key, qs + r, seglen, a.window)) p = 0.0f;
+                    const float ds = p * (dp[i] - s.dd[r]);
+                    pb[qq * 4 + i] = (__bf16)p;
+                    db[qq * 4 + i] = (__bf16)ds;
+                }
             }
-            /* lane (g, c): key c, query rows qs + 16 qt + 4 g + i */
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = qt * 16 + 4 * g + i;
-                float p = __builtin_amdgcn_exp2f(sc[i] * a.scale_log2 - s.lse2[r]);
-                if (!interior && !visible(key, qs + r, seglen, a.window)) p = 0.0f;
-                const float ds = p * (dp[i] - s.dd[r]);
-                pb[qt >> 1][(qt & 1) * 4 + i] = (__bf16)p;
-                db[qt >> 1][(qt & 1) * 4 + i] = (__bf16)ds;
+            for (int d = 0; d < 8; d++) {
+                dv[d] = mfma16x16x32(tr_operand(s.dout, d, s2, g, c), pb, dv[d]);
+                dk[d] = mfma16x16x32(tr_operand(s.q, d, s2, g, c), db, dk[d]);
             }
         }
-#pragma unroll
-        for (int d = 0; d < 8; d++)
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++) {
-                dv[d] = mfma16x16x32(tr_operand(s.dout, d, s2, g, c), pb[s2], dv[d]);
-                dk[d] = mfma16x16x32(tr_operand(s.q, d, s2, g, c), db[s2], dk[d]);
-            }
     };
     const int qb_lo = k0 / FA_BN, qb_hi = qhi / FA_BN;
     fetch(qb_lo, s0);
