@@ -183,7 +183,7 @@ def test_workspace_reuse_across_shapes(device):
 def test_growing_scores_rescale_mid_stream(device, workers):
     """Key magnitudes growing along each sequence: the running max passes its reference by more than 2^8 again and
     again after the first page pair, so the lazy rescale's slow path runs mid-stream (and the chunks start on small
-    references that the combine must reconcile)."""
+    references that the in-kernel merge must reconcile)."""
     w = DecodeWorkload("grow", 2, 8, 2, 600, ctx_min=400, paged=True)
     inp = decode_inputs(w, seed=9)
     n = inp["k_cache"].shape[1]
@@ -198,7 +198,7 @@ def test_growing_scores_rescale_mid_stream(device, workers):
 @pytest.mark.parametrize("window", [-1, 1023, 1024, 3000])
 def test_chunk_boundaries(device, window):
     """Lengths around the 1,024-position split points (1, 1,023, 1,024, 1,025, 2,048, 2,049 keys and up to 9,001),
-    with windows whose start falls inside a chunk: every piece and the combine's merge meet the oracle bound."""
+    with windows whose start falls inside a chunk: every piece and the in-kernel merge meet the oracle bound."""
     w = DecodeWorkload("chunks", 8, 8, 2, 9000, ctx_min=1, paged=True)
     inp = decode_inputs(w, seed=7)
     inp["ctx_lens"][:] = torch.tensor([0, 1022, 1023, 1024, 2047, 2048, 5000, 9000], dtype=torch.int32)
