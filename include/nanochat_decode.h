@@ -111,6 +111,9 @@ int dec_debug_slot_gemm(int epi, const void *w, int R, int K, const void *x, int
                         const void *res, const float *rstd, int slices, float *part, void *stream);
 int dec_debug_slot_gemm_slices(int R, int K);
 long long dec_debug_slot_gemm_part_bytes(int R, int N, int slices);
+/* The workgroup tile dec_debug_slot_gemm launches for (R, K, N, slices; slices 0 = the default): 100 RT + CT for RT
+ * 16-row weight tiles and CT 16-slot tiles a workgroup, or -2 when the shape does not fit. */
+int dec_debug_slot_gemm_tile(int R, int K, int N, int slices);
 
 #ifdef __cplusplus
 }

@@ -1481,3 +1481,10 @@ extern "C" int dec_debug_slot_gemm_slices(int R, int K) { return nc::slot_gemm_s
 extern "C" long long dec_debug_slot_gemm_part_bytes(int R, int N, int slices) {
     return nc::slot_gemm_part_bytes(R, N, slices);
 }
+
+extern "C" int dec_debug_slot_gemm_tile(int R, int K, int N, int slices) {
+    if (!nc::slot_gemm_fits(R, K, N)) return -2;
+    const int S = slices > 0 ? slices : nc::slot_gemm_slices(R, K);
+    if (S > K / 128) return -2;
+    return nc::slot_gemm_tile(R, K, N, S);
+}

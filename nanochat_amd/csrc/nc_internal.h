@@ -69,6 +69,8 @@ struct SkinnyGemm {
 bool slot_gemm_fits(int R, int K, int N);
 /* K-slices for (R, K): 1, or enough that each covers at most 2048 of K (fixed per shape, never per slot count). */
 int slot_gemm_slices(int R, int K);
+/* The workgroup tile a launch of (R, K, N, S) uses: 100 RT + CT (RT 16-row weight tiles, CT 16-slot tiles). */
+int slot_gemm_tile(int R, int K, int N, int S);
 /* Bytes of the partial sums of S slices (0 for S = 1). */
 long long slot_gemm_part_bytes(int R, int N, int S);
 /* S = 1: the epilogue in the GEMM. S > 1: fp32 partials to part [S][N][R] (part_bytes: its allocation, which must

@@ -4,25 +4,28 @@
  * every weight byte must come from HBM once, and every workgroup needs the whole activation block x (N x K bf16,
  * 426 KB at config 5), which comes from L2.
  *
- * A workgroup owns 32 weight rows and all N slots over its K range, walked in stages of 128 k. Each stage's operands
- * (x: up to 128 slot rows x 256 bytes; w: 32 rows x 256 bytes) go from memory into LDS by LDS DMA, 16 lanes per
- * 256-byte row segment: a load instruction that covers long contiguous row pieces runs at about 3x the per-CU rate of
- * one scattering 16-byte pieces over 16 rows (measured: 16 rows x 64 B ~35 GB/s a CU, 8 rows x 128 B 70-90 GB/s,
- * 1 KB contiguous ~110 GB/s). A ring of 3 stage buffers keeps the next two stages in flight, with hand-placed waits and
- * a barrier without a memory fence per stage (a fence would wait for every DMA in flight). What bounds it is the CU's
- * ingress: every workgroup takes in all of x (426 KB at config 5) besides its 106 KB of weights. The 4 waves split each stage's four 32-k steps (wave w
- * takes step w), so every LDS byte is read once; at the end the waves' sums meet in LDS and are added in wave (K)
- * order, then the epilogue is applied.
+ * A workgroup owns 16 RT weight rows and 16 CT slots (a slot group) over its K range, walked in stages of 128 k. Each
+ * stage's operands (x: 16 CT slot rows x 256 bytes; w: 16 RT rows x 256 bytes) go from memory into LDS by LDS DMA, 16
+ * lanes per 256-byte row segment: a load instruction that covers long contiguous row pieces runs at about 3x the
+ * per-CU rate of one scattering 16-byte pieces over 16 rows (measured: 16 rows x 64 B ~35 GB/s a CU, 8 rows x 128 B
+ * 70-90 GB/s, 1 KB contiguous ~110 GB/s). A ring of 3 stage buffers keeps the next two stages in flight, with
+ * hand-placed waits and a barrier without a memory fence per stage (a fence would wait for every DMA in flight). What
+ * bounds it is the CU's ingress (about 40 GB/s a CU with every CU reading): a workgroup takes in its slots' x rows
+ * besides its weights, so the host picks (RT, CT) per shape to make the bytes one CU takes in smallest, splitting the
+ * slots into groups where x would outweigh the weights (sl_choose). The 4 waves split each stage's four 32-k steps
+ * (wave w takes step w), so every LDS byte is read once; at the end the waves' sums meet in LDS and are added in wave
+ * (K) order, then the epilogue is applied.
  *
  * Every global access goes through a buffer resource whose range is the exact extent of its array: rows past R and
  * slots past N read zeros, stages past the range read at SL_PAST (zeros, no memory access), and no load is
  * conditional. Each output's sum runs over its K range in a fixed order (stages in order, within a stage the wave's
- * 32-k step; then the four waves in order), the same for every slot and whatever N is, so a slot's result depends on
- * its own x row only.
+ * 32-k step; then the four waves in order), the same for every slot, whatever N is and whatever tile shape holds it
+ * (an MFMA output element is the sum of its own row and column products alone), so a slot's result depends on its own
+ * x row only.
  *
  * Operand layout (v_mfma_f32_16x16x32_bf16): lane (g = lane / 16, i = lane % 16) of wave w holds, for stage k0,
- * A = w[row 16 t + i][k0 + 32 w + 8 g .. + 7] and B = x[slot 16 u + i][k0 + 32 w + 8 g .. + 7]; the result tile holds
- * rows 16 t + 4 g .. + 3 of slot 16 u + i. In LDS a row's 256 bytes (16 blocks of 16) keep block b at position
+ * A = w[row 16 t + i][k0 + 32 w + 8 g .. + 7] and B = x[slot n0 + 16 u + i][k0 + 32 w + 8 g .. + 7]; the result tile
+ * holds rows 16 t + 4 g .. + 3 of slot n0 + 16 u + i. In LDS a row's 256 bytes (16 blocks of 16) keep block b at position
  * b ^ (row % 16), so the 16 rows of one operand read fall in distinct banks; each DMA lane fetches the global block
  * that belongs at its LDS position.
  *
@@ -39,18 +42,13 @@ namespace nc {
 
 constexpr int SL_WAVES = 4;
 constexpr int SL_THREADS = SL_WAVES * WAVE;
-constexpr int SL_ROWS = 32;                      /* weight rows per workgroup at RT = 2 (16-row MFMA tiles) */
-constexpr int SL_WIDE_R = 8192;                  /* more rows than this: 64 rows a workgroup (RT = 4), so the x every
-                                                    workgroup takes in is shared by twice the weights */
-constexpr int SL_CT = SG_MAX_N / 16;             /* 16-slot MFMA tiles */
 constexpr int SL_KC = 128;                       /* k per stage: four 32-k MFMA steps, one per wave */
 constexpr int SL_ROWB = SL_KC * 2;               /* bytes of a stage's row */
-constexpr int SL_XBUF = SG_MAX_N * SL_ROWB;      /* a stage's x in LDS: 32 KiB */
-constexpr int SL_WBUF = 2 * SL_ROWS * SL_ROWB;   /* a stage's w in LDS: 16 KiB (at most 64 rows) */
-constexpr int SL_XLOADS = SL_XBUF / 1024 / SL_WAVES;   /* x DMA a wave a stage */
-/* w DMA a wave a stage for RT row tiles, and all of a stage's DMA: the newer stage in flight at each wait */
-template <int RT> constexpr int sl_wloads() { return RT * 16 * SL_ROWB / 1024 / SL_WAVES; }
-template <int RT> constexpr int sl_loads() { return SL_XLOADS + sl_wloads<RT>(); }
+/* a stage's LDS bytes and DMA instructions a wave issues for 16 T rows (T 16-row tiles; each instruction moves 1 KiB) */
+template <int T> constexpr int sl_buf() { return T * 16 * SL_ROWB; }
+template <int T> constexpr int sl_tile_loads() { return sl_buf<T>() / 1024 / SL_WAVES; }
+/* all of a stage's DMA a wave issues: the newer stage in flight at each wait */
+template <int RT, int CT> constexpr int sl_loads() { return sl_tile_loads<RT>() + sl_tile_loads<CT>(); }
 constexpr int SL_PAST = 0x7FFF0000;              /* a byte offset past every operand's range */
 constexpr int SL_MAX_K_SLICE = 2048;             /* longer K is split into slices of at most this (then reduced) */
 
@@ -125,12 +123,13 @@ __device__ __forceinline__ void sl_store(const SlotViews &v, int n, int at, floa
     bstore8(v.out, at * 2, u32x2{(uint32_t)o[0] | (uint32_t)o[1] << 16, (uint32_t)o[2] | (uint32_t)o[3] << 16});
 }
 
-/* s_waitcnt: every vector-memory load but the newest sl_loads<RT>() has landed (the stage issued after this one may stay in
- * flight), and this wave's LDS reads are done. Encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait),
+/* s_waitcnt: every vector-memory load but the newest sl_loads<RT, CT>() has landed (the stage issued after this one may
+ * stay in flight), and this wave's LDS reads are done. Encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait),
  * lgkmcnt [11:8]. */
-template <int RT>
+template <int RT, int CT>
 __device__ __forceinline__ void sl_wait_stage() {
-    constexpr int n = sl_loads<RT>();
+    constexpr int n = sl_loads<RT, CT>();
+    static_assert(n < 64, "vmcnt holds 6 bits");
     __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
 }
 
@@ -159,8 +158,8 @@ __device__ __forceinline__ void sl_fetch(Rsrc src, unsigned char *buf, int j, in
 }
 
 /* The wave's 32-k step of a stage: A and B read from LDS (block 4 wave + grp of the row, at its swizzled position). */
-template <int RT>
-__device__ __forceinline__ void sl_compute(const unsigned char *xb, const unsigned char *wb, f32x4 (&acc)[RT][SL_CT],
+template <int RT, int CT>
+__device__ __forceinline__ void sl_compute(const unsigned char *xb, const unsigned char *wb, f32x4 (&acc)[RT][CT],
                                            int wave, int i16, int grp) {
     const int pos = (4 * wave + grp) ^ i16;   /* rows 16 t + i16 and 16 u + i16 all have row % 16 = i16 */
     bf16x8 a[RT];
@@ -168,7 +167,7 @@ __device__ __forceinline__ void sl_compute(const unsigned char *xb, const unsign
     for (int t = 0; t < RT; t++)
         a[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(wb + (16 * t + i16) * SL_ROWB + pos * 16));
 #pragma unroll
-    for (int u = 0; u < SL_CT; u++) {
+    for (int u = 0; u < CT; u++) {
         const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(xb + (16 * u + i16) * SL_ROWB + pos * 16));
 #pragma unroll
         for (int t = 0; t < RT; t++) acc[t][u] = mfma16x16x32(a[t], b, acc[t][u]);
@@ -177,38 +176,40 @@ __device__ __forceinline__ void sl_compute(const unsigned char *xb, const unsign
 
 /* One ring position: wait for stage j, barrier (every wave's DMA of stage j has landed and every wave is done with
  * stage j - 1), refill the buffers stage j - 1 used with stage j + 2, compute stage j. */
-#define SL_STEP(j, XB, WB, NXB, NWB)                                                 \
-    do {                                                                             \
-        sl_wait_stage<RT>();                                                         \
-        sl_barrier();                                                                \
-        sl_fetch<SL_XLOADS>(v.x, NXB, (j) + 2, nc, kb0, rowb, 0, wave, lane);        \
-        sl_fetch<sl_wloads<RT>()>(v.w, NWB, (j) + 2, nc, kb0, rowb, r0, wave, lane); \
-        sl_compute<RT>(XB, WB, acc, wave, i16, grp);                                 \
+#define SL_STEP(j, XB, WB, NXB, NWB)                                                     \
+    do {                                                                                 \
+        sl_wait_stage<RT, CT>();                                                         \
+        sl_barrier();                                                                    \
+        sl_fetch<sl_tile_loads<CT>()>(v.x, NXB, (j) + 2, nc, kb0, rowb, n0, wave, lane); \
+        sl_fetch<sl_tile_loads<RT>()>(v.w, NWB, (j) + 2, nc, kb0, rowb, r0, wave, lane); \
+        sl_compute<RT, CT>(XB, WB, acc, wave, i16, grp);                                 \
     } while (0)
 
-/* EPI < 0: store partial sums (S > 1). RT 16-row tiles a workgroup. Grid (ceil(R / (16 RT)), S), 256 threads. */
-template <int EPI, int RT>
+/* EPI < 0: store partial sums (S > 1). RT 16-row tiles and CT 16-slot tiles a workgroup. Grid (ceil(R / (16 RT)), S,
+ * ceil(N / (16 CT))), 256 threads. */
+template <int EPI, int RT, int CT>
 __global__ void __launch_bounds__(SL_THREADS, 1) slot_gemm_kernel(SkinnyGemm g, float *part, long long part_bytes,
                                                                   int S) {
-    __shared__ __align__(16) unsigned char x0[SL_XBUF], x1[SL_XBUF], x2[SL_XBUF];
-    __shared__ __align__(16) unsigned char w0[SL_WBUF], w1[SL_WBUF], w2[SL_WBUF];
+    constexpr int XB = sl_buf<CT>(), WB = sl_buf<RT>();
+    __shared__ __align__(16) unsigned char x0[XB], x1[XB], x2[XB];
+    __shared__ __align__(16) unsigned char w0[WB], w1[WB], w2[WB];
     const SlotViews v = slot_views(g, part, part_bytes);
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const int i16 = lane & 15, grp = lane >> 4;
-    const int r0 = blockIdx.x * 16 * RT, s = blockIdx.y;
+    const int r0 = blockIdx.x * 16 * RT, s = blockIdx.y, n0 = blockIdx.z * 16 * CT;
     const int chunks = g.K / SL_KC;
     const int c0 = s * chunks / S, nc = (s + 1) * chunks / S - c0;   /* the slice: stages [c0, c0 + nc) */
     const int rowb = g.K * 2, kb0 = c0 * SL_ROWB;
 
-    f32x4 acc[RT][SL_CT];
+    f32x4 acc[RT][CT];
 #pragma unroll
     for (int t = 0; t < RT; t++)
 #pragma unroll
-        for (int u = 0; u < SL_CT; u++) acc[t][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    sl_fetch<SL_XLOADS>(v.x, x0, 0, nc, kb0, rowb, 0, wave, lane);
-    sl_fetch<sl_wloads<RT>()>(v.w, w0, 0, nc, kb0, rowb, r0, wave, lane);
-    sl_fetch<SL_XLOADS>(v.x, x1, 1, nc, kb0, rowb, 0, wave, lane);
-    sl_fetch<sl_wloads<RT>()>(v.w, w1, 1, nc, kb0, rowb, r0, wave, lane);
+        for (int u = 0; u < CT; u++) acc[t][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    sl_fetch<sl_tile_loads<CT>()>(v.x, x0, 0, nc, kb0, rowb, n0, wave, lane);
+    sl_fetch<sl_tile_loads<RT>()>(v.w, w0, 0, nc, kb0, rowb, r0, wave, lane);
+    sl_fetch<sl_tile_loads<CT>()>(v.x, x1, 1, nc, kb0, rowb, n0, wave, lane);
+    sl_fetch<sl_tile_loads<RT>()>(v.w, w1, 1, nc, kb0, rowb, r0, wave, lane);
     int j = 0;
     for (; j + 3 <= nc; j += 3) {
         SL_STEP(j, x0, w0, x2, w2);
@@ -219,39 +220,43 @@ __global__ void __launch_bounds__(SL_THREADS, 1) slot_gemm_kernel(SkinnyGemm g, 
     if (j + 1 < nc) SL_STEP(j + 1, x1, w1, x0, w0);
     __builtin_amdgcn_s_waitcnt(0);                    /* no DMA may land in LDS after this */
     sl_barrier();
-    /* the four waves' sums, added in wave (K) order, two row tiles at a time; wave w finishes slot tiles 2 w, 2 w + 1 */
+    /* the four waves' sums, added in wave (K) order, up to two row tiles at a time: each wave writes its sums of the
+     * round's (t, u) tiles (2 CT f32x4 a lane: waves 0, 1 into x0, waves 2, 3 into x1, which hold 4 CT), then wave w
+     * finishes tiles q = w, w + 4, ... of the round's TT CT */
 #pragma unroll
     for (int tt = 0; tt < RT; tt += 2) {
-        f32x4 *red = reinterpret_cast<f32x4 *>(wave < 2 ? x0 : x1) + (wave & 1) * 2 * SL_CT * WAVE;
+        constexpr int TT0 = RT < 2 ? RT : 2;
+        const int TT = RT - tt < TT0 ? RT - tt : TT0;
+        f32x4 *red = reinterpret_cast<f32x4 *>(wave < 2 ? x0 : x1) + (wave & 1) * 2 * CT * WAVE;
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+        for (int t = 0; t < TT0; t++)
 #pragma unroll
-            for (int u = 0; u < SL_CT; u++) red[(t * SL_CT + u) * WAVE + lane] = acc[tt + t][u];
+            for (int u = 0; u < CT; u++)
+                if (t < TT) red[(t * CT + u) * WAVE + lane] = acc[tt + t][u];
         sl_barrier();
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const int r = r0 + 16 * (tt + t) + 4 * grp;
+        for (int q0 = 0; q0 < TT0 * CT; q0 += SL_WAVES) {
+            const int q = q0 + wave;
+            if (q >= TT * CT) continue;
+            const int t = q / CT, u = q - t * CT;
+            const int r = r0 + 16 * (tt + t) + 4 * grp, n = n0 + 16 * u + i16;
+            f32x4 sum = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int uu = 0; uu < 2; uu++) {
-                const int u = 2 * wave + uu, n = 16 * u + i16;
-                f32x4 sum = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int w = 0; w < SL_WAVES; w++) {
-                    const f32x4 *rw = reinterpret_cast<const f32x4 *>(w < 2 ? x0 : x1) + (w & 1) * 2 * SL_CT * WAVE;
-                    const f32x4 p = rw[(t * SL_CT + u) * WAVE + lane];
-                    sum = w == 0 ? p : sum + p;
-                }
-                if (r >= g.R || n >= g.N || !sl_live(g.active, n)) continue;
-                float sv[4] = {sum[0], sum[1], sum[2], sum[3]};
-                if (EPI < 0)
-                    bstore16(v.part, ((s * g.N + n) * g.R + r) * 4,
-                             u32x4{__float_as_uint(sv[0]), __float_as_uint(sv[1]), __float_as_uint(sv[2]),
-                                   __float_as_uint(sv[3])});
-                else
-                    sl_store<EPI < 0 ? SG_STORE : EPI>(v, n, n * g.R + r, sv);
+            for (int w = 0; w < SL_WAVES; w++) {
+                const f32x4 *rw = reinterpret_cast<const f32x4 *>(w < 2 ? x0 : x1) + (w & 1) * 2 * CT * WAVE;
+                const f32x4 p = rw[(t * CT + u) * WAVE + lane];
+                sum = w == 0 ? p : sum + p;
             }
+            if (r >= g.R || n >= g.N || !sl_live(g.active, n)) continue;
+            float sv[4] = {sum[0], sum[1], sum[2], sum[3]};
+            if (EPI < 0)
+                bstore16(v.part, ((s * g.N + n) * g.R + r) * 4,
+                         u32x4{__float_as_uint(sv[0]), __float_as_uint(sv[1]), __float_as_uint(sv[2]),
+                               __float_as_uint(sv[3])});
+            else
+                sl_store<EPI < 0 ? SG_STORE : EPI>(v, n, n * g.R + r, sv);
         }
-        sl_barrier();   /* the reduction area is rewritten by the next pair of row tiles */
+        sl_barrier();   /* the reduction area is rewritten by the next round */
     }
 }
 
@@ -272,21 +277,49 @@ __global__ void __launch_bounds__(256) slot_gemm_reduce_kernel(SkinnyGemm g, con
     sl_store<EPI>(v, n, n * g.R + r, sv);
 }
 
+/* The tile shapes built, as (RT, CT). */
+struct SlTile {
+    int rt, ct;
+};
+constexpr SlTile SL_TILES[] = {{2, 2}, {3, 4}, {4, 4}, {4, 8}};
+constexpr int SL_CUS = 256;   /* MI355X compute units */
+
+/* The tile shape whose busiest CU takes in the fewest bytes: a workgroup takes in 16 (RT + CT) rows of 256 bytes a
+ * stage, and the busiest CU runs ceil(workgroups / 256) of them; ties go to the earlier entry. The choice never
+ * changes a result's bits (each output's sum order does not depend on the tile). */
+static SlTile sl_choose(int R, int K, int N, int S) {
+    SlTile best = SL_TILES[0];
+    long long best_cost = 0;
+    for (const SlTile &t : SL_TILES) {
+        const long long wgs = (long long)((R + 16 * t.rt - 1) / (16 * t.rt)) * S * ((N + 16 * t.ct - 1) / (16 * t.ct));
+        const long long cost = (wgs + SL_CUS - 1) / SL_CUS * (K / SL_KC / S) * (t.rt + t.ct);
+        if (&t == SL_TILES || cost < best_cost) {
+            best = t;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+template <int EPI, int RT, int CT>
+static void sl_launch_tile(const SkinnyGemm &g, float *part, long long part_bytes, int S, hipStream_t stream) {
+    const dim3 grid((g.R + 16 * RT - 1) / (16 * RT), S, (g.N + 16 * CT - 1) / (16 * CT)), block(SL_THREADS);
+    hipLaunchKernelGGL((slot_gemm_kernel<EPI, RT, CT>), grid, block, 0, stream, g, part, part_bytes, S);
+}
+
 template <int EPI>
 static void sl_launch(const SkinnyGemm &g, float *part, long long part_bytes, int S, hipStream_t stream) {
-    const dim3 block(SL_THREADS);
-    if (g.R > SL_WIDE_R)
-        hipLaunchKernelGGL((slot_gemm_kernel<EPI, 4>), dim3((g.R + 63) / 64, S), block, 0, stream, g, part, part_bytes,
-                           S);
-    else
-        hipLaunchKernelGGL((slot_gemm_kernel<EPI, 2>), dim3((g.R + 31) / 32, S), block, 0, stream, g, part, part_bytes,
-                           S);
+    const SlTile t = sl_choose(g.R, g.K, g.N, S);
+    if (t.rt == 2 && t.ct == 2) sl_launch_tile<EPI, 2, 2>(g, part, part_bytes, S, stream);
+    else if (t.rt == 3) sl_launch_tile<EPI, 3, 4>(g, part, part_bytes, S, stream);
+    else if (t.ct == 4) sl_launch_tile<EPI, 4, 4>(g, part, part_bytes, S, stream);
+    else sl_launch_tile<EPI, 4, 8>(g, part, part_bytes, S, stream);
 }
 
 bool slot_gemm_fits(int R, int K, int N) {
     /* every byte offset, including those of the rows and slots past R and N a tile covers, fits an int */
     return N >= 1 && N <= SG_MAX_N && K >= SL_KC && K % SL_KC == 0 && R >= 1 && R % 4 == 0 &&
-           (long long)(R + 2 * SL_ROWS) * K * 2 <= SL_PAST && (long long)SG_MAX_N * K * 2 <= SL_PAST &&
+           (long long)(R + 16 * 4) * K * 2 <= SL_PAST && (long long)SG_MAX_N * K * 2 <= SL_PAST &&
            (long long)N * R * 4 <= SL_PAST;
 }
 
@@ -294,6 +327,11 @@ int slot_gemm_slices(int R, int K) {
     (void)R;
     const int chunks = K / SL_KC, per = SL_MAX_K_SLICE / SL_KC;
     return chunks > per ? (chunks + per - 1) / per : 1;
+}
+
+int slot_gemm_tile(int R, int K, int N, int S) {
+    const SlTile t = sl_choose(R, K, N, S);
+    return 100 * t.rt + t.ct;
 }
 
 long long slot_gemm_part_bytes(int R, int N, int S) { return S > 1 ? (long long)S * N * R * 4 : 0; }

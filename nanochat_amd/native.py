@@ -141,6 +141,7 @@ DECODE_SIGNATURES = {
                              c_int, c_void_p, c_void_p], c_int),
     "dec_debug_slot_gemm_slices": ([c_int, c_int], c_int),
     "dec_debug_slot_gemm_part_bytes": ([c_int, c_int, c_int], c_longlong),
+    "dec_debug_slot_gemm_tile": ([c_int, c_int, c_int, c_int], c_int),
 }
 
 LIBRARIES = {"nanochat_kv": (LIBRARY, SIGNATURES), "decode": (DECODE_LIBRARY, DECODE_SIGNATURES)}

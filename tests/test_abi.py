@@ -273,3 +273,37 @@ def test_slot_gemm_declines_without_launching():
         assert lib.dec_debug_slot_gemm_slices(R, K) == S, (R, K)
     assert lib.dec_debug_slot_gemm_part_bytes(1664, 128, 1) == 0
     assert lib.dec_debug_slot_gemm_part_bytes(1664, 128, 4) == 4 * 128 * 1664 * 4
+
+
+def test_slot_gemm_tiles():
+    """The workgroup tile (RT 16-row weight tiles, CT 16-slot tiles, as 100 RT + CT) is the one whose busiest CU takes
+    in the fewest bytes, ceil(workgroups / 256) x stages x (RT + CT): at config 5's 128 slots qkv splits the slots into
+    two groups of 64 with 48 weight rows a workgroup (208 workgroups), o into four groups of 32 (208), fc and proj into
+    two of 64 with 64 rows (208), and lm_head keeps all 128 slots with 64 rows (1,024). The GPU tests' shapes cover every
+    tile built."""
+    from nanochat_amd.native import hip_library
+    from tests.test_gpu_slot_gemm import SHAPES
+
+    lib = hip_library("decode")
+    tiles = {(4992, 1664): 304, (1664, 1664): 202, (6656, 1664): 404, (1664, 6656): 404, (65536, 1664): 408}
+    for (R, K), t in tiles.items():
+        assert lib.dec_debug_slot_gemm_tile(R, K, 128, 0) == t, (R, K)
+
+    def cost(R, K, N, S, rt, ct):
+        wgs = -(-R // (16 * rt)) * S * -(-N // (16 * ct))
+        return -(-wgs // 256) * (K // 128 // S) * (rt + ct)
+
+    built = (202, 304, 404, 408)
+    seen = set()
+    for R, K, N in SHAPES:
+        for S in (1, 2, 3):
+            if S > K // 128:
+                continue
+            t = lib.dec_debug_slot_gemm_tile(R, K, N, S)
+            costs = [cost(R, K, N, S, b // 100, b % 100) for b in built]
+            assert t == built[costs.index(min(costs))], (R, K, N, S)
+            seen.add(t)
+    assert seen == set(built)
+    assert lib.dec_debug_slot_gemm_tile(1664, 6600, 128, 0) == -2     # K not a multiple of 128
+    assert lib.dec_debug_slot_gemm_tile(1664, 1664, 129, 0) == -2     # more than 128 slots
+    assert lib.dec_debug_slot_gemm_tile(1664, 256, 128, 3) == -2      # more slices than chunks

@@ -10,9 +10,10 @@ from nanochat_amd.native import hip_library, pointer, stream
 pytestmark = pytest.mark.gpu
 
 STORE, RESID2, RELU2, RESID, F32 = range(5)
-# the config-5 decode shapes (qkv, o, fc, proj, lm_head) at full and partial slot counts, and ragged small ones
+# the config-5 decode shapes (qkv, o, fc, proj, lm_head) at full and partial slot counts, and ragged small ones; across
+# their slice counts they use every workgroup tile (tests/test_abi.py checks which)
 SHAPES = [(4992, 1664, 128), (1664, 1664, 1), (6656, 1664, 37), (1664, 6656, 128), (100, 128, 16), (36, 256, 65),
-          (65536, 1664, 64), (260, 384, 17)]
+          (65536, 1664, 100), (260, 384, 17)]
 
 
 def bf16_ulp(x):
@@ -97,8 +98,11 @@ def test_deterministic_and_declines_bad_shapes(device):
 
 @pytest.mark.parametrize("R,K", [(4992, 1664), (1664, 6656)])
 def test_a_slots_result_does_not_depend_on_the_others(device, R, K):
-    """Slot rows are summed in one fixed order whatever N is: a row computed alone, among 128 others, at another
-    place and among 37 gives the same bits (the decoder's batch independence rests on this)."""
+    """Slot rows are summed in one fixed order whatever N is and whatever workgroup tile holds them: a row computed
+    alone, among 128 others, at another place and among 37 gives the same bits (the decoder's batch independence rests
+    on this; the three slot counts use different tiles)."""
+    lib = hip_library("decode")
+    assert len({lib.dec_debug_slot_gemm_tile(R, K, n, 0) for n in (1, 37, 128)}) >= 2
     gen = torch.Generator().manual_seed(R + K)
     w = (torch.randn(R, K, generator=gen) * 0.05).bfloat16().to(device)
     x = torch.randn(128, K, generator=gen).bfloat16().to(device)
