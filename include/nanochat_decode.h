@@ -114,6 +114,12 @@ long long dec_debug_slot_gemm_part_bytes(int R, int N, int slices);
 /* The workgroup tile dec_debug_slot_gemm launches for (R, K, N, slices; slices 0 = the default): 100 RT + CT for RT
  * 16-row weight tiles and CT 16-slot tiles a workgroup, or -2 when the shape does not fit. */
 int dec_debug_slot_gemm_tile(int R, int K, int N, int slices);
+/* The step's MLP rstd path, one K slice: epi 1 (RESID2) writes bf16(s + res) to out and each 16-row tile's sum of
+ * squares of s + res to ssq (fp32 [N][ceil(R / 16)]); epi 2 (RELU2) takes each slot's rstd from ssq (fp32
+ * [N][ceil(K / 16)], summed over tiles in order: 1 / sqrt(sum / K + FLT_EPSILON)) and writes bf16(relu(s r) s r).
+ * Returns 0, a hipError_t, or -2 when the shape or operands do not fit. Stream-ordered. */
+int dec_debug_slot_gemm_ssq(int epi, const void *w, int R, int K, const void *x, int N, void *out, const void *res,
+                            float *ssq, void *stream);
 
 #ifdef __cplusplus
 }

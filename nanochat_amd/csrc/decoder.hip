@@ -3,14 +3,16 @@
  * inference/decoder.py:132-148) over an fp8 paged KV cache.
  *
  * A step is a stream of kernels on the caller's stream, launched eagerly:
- *   body   norm_kernel(EMBED) -> per layer { norm_kernel(RESID), qkv GEMM, the fused decode step (q/k norm + RoPE +
- *          value embedding + fp8 append of the step's token, then split-K decode attention, one launch: attention.hip),
- *          o GEMM (+ residual: fp32 sum and its bf16 rounding), rstd_kernel, fc GEMM (+ ReLU^2 of the rstd-scaled
- *          sum), proj GEMM (+ residual) }
+ *   body   norm_kernel(EMBED), norm_kernel(RESID) of layer 0 -> per layer { qkv GEMM, the fused decode step (q/k
+ *          norm + RoPE + value embedding + fp8 append of the step's token, then split-K decode attention, one launch:
+ *          attention.hip), o GEMM (+ residual: the bf16 rounding of the fp32 sum, and each 16-row tile's sum of
+ *          squares), fc GEMM (+ ReLU^2 of the sum scaled by the rstd it takes from those tile sums), proj GEMM
+ *          (K-slice partials), proj_norm_kernel (the partials + residual, then the next layer's residual norm) }
  *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
  *          the allowed tokens, then the commit), the tokens to pinned host memory.
  * A step's GEMMs are slot_gemm.hip's weight-streaming MFMA kernel with the epilogue fused (long-K GEMMs split into
- * K-slices whose partials a second kernel adds in order). Prefill's GEMMs (up to 8,192 rows) are hipBLASLt matmuls
+ * K-slices whose partials a second kernel adds in order; a model wider than 2,048 computes the MLP's rstd in
+ * rstd_kernel). Prefill's GEMMs (up to 8,192 rows) are hipBLASLt matmuls
  * (bf16 operands, fp32 accumulation; one plan per shape and row count, the heuristic's first algorithm; rocBLAS gemm_ex
  * where hipBLASLt offers none) followed by the epilogue kernels. Every kernel covers the slots up to the highest active
  * one (dec_set_active) and skips inactive slots.
@@ -19,8 +21,8 @@
  * scaled by its rstd; every RMS norm is 1 / sqrt(mean x^2 + FLT_EPSILON), correctly rounded (the reference: rsqrtf).
  * The KV cache is fp8 e4m3fn with one absmax scale per (token, head) (the reference caches bf16); a step's own key
  * is read back from the cache like the others. Decode attention splits a slot's keys at fixed multiples of 1,024
- * positions (merged in position order in the same launch) and the step GEMMs sum every slot's row in one fixed order, so a step's result for a slot depends only on
- * the slot's own inputs and cache.
+ * positions (merged in position order in the same launch) and the step GEMMs sum every slot's row in one fixed order,
+ * so a step's result for a slot depends only on the slot's own inputs and cache.
  *
  * Memory: one allocation per role, sized at dec_create. The KV pool of layer l is `pool` pages the slots draw from
  * (the same page index in every layer) followed by the prompt store's pages (store position s at page pool + s / 16,
@@ -264,6 +266,82 @@ __global__ void __launch_bounds__(256) relu2_kernel(const float *s, const float 
     for (int i = 0; i < 4; i++) o[i] = f32_to_bf16(fmaxf(p[i], 0.0f) * p[i]);
     *reinterpret_cast<uint2 *>(u + at) = make_uint2((uint32_t)o[0] | (uint32_t)o[1] << 16,
                                                    (uint32_t)o[2] | (uint32_t)o[3] << 16);
+}
+
+/* A step's layer boundary in one pass (decode.cu:149-154 and 413-443 for the same math): the proj GEMM's S K-slice
+ * partials of one slot summed in slice order plus the residual, x = bf16(sum + xo); then, when the next layer's norm is
+ * asked for (mixed non-NULL), NORM_RESID over x: v = fma(l1, x, x0 l2), mixed = bf16(v), out = bf16(v r),
+ * r = 1 / sqrt(sum v^2 / C + FLT_EPSILON). A 256-thread block per slot; thread t holds the 8-element groups t, t + 256,
+ * ... (NG of them); the sum of squares is each thread's FMA chain in group order, the wave butterfly, then the four
+ * waves in order: fixed for a given C, whatever the other slots hold. */
+struct ProjNormArgs {
+    const float *part;        /* [S][N][C] fp32 partial sums (slot_gemm_partials) */
+    int S, N, C;
+    const uint16_t *res;      /* [N][C] bf16 residual (xo) */
+    uint16_t *x;              /* [N][C] bf16: the layer's output stream */
+    const float *x0;          /* [N][C] fp32 */
+    float l1, l2;             /* the next layer's resid and x0 lambdas */
+    uint16_t *mixed, *out;    /* NULL mixed: no norm */
+    const unsigned long long *active;
+};
+
+constexpr int PN_MAX_S = 8;   /* K-slices proj_norm_kernel adds (F <= 16,384) */
+
+template <int NG>
+__global__ void __launch_bounds__(256) proj_norm_kernel(ProjNormArgs a) {
+    __shared__ float wsum[256 / WAVE];
+    const int n = blockIdx.x, t = threadIdx.x;
+    if (a.active && !live(a.active, n)) return;
+    const long long row = (long long)n * a.C, slice = (long long)a.N * a.C;
+    float v[NG][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NG; j++) {
+        const int i = (j * 256 + t) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[j][e] = 0.0f;
+        if (i >= a.C) continue;
+        float sum[8], r[8], q[PN_MAX_S - 1][8];
+        load8(a.part + row + i, sum);
+#pragma unroll
+        for (int sl = 1; sl < PN_MAX_S; sl++)   /* every slice's loads before the first add */
+            if (sl < a.S) load8(a.part + sl * slice + row + i, q[sl - 1]);
+        load8(a.res + row + i, r);
+#pragma unroll
+        for (int sl = 1; sl < PN_MAX_S; sl++)
+            if (sl < a.S)
+#pragma unroll
+                for (int e = 0; e < 8; e++) sum[e] = sum[e] + q[sl - 1][e];
+#pragma unroll
+        for (int e = 0; e < 8; e++) sum[e] = sum[e] + r[e];
+        store8(a.x + row + i, sum);
+        if (!a.mixed) continue;
+        float x0[8];
+        load8(a.x0 + row + i, x0);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            v[j][e] = __builtin_fmaf(a.l1, bf16_to_f32(f32_to_bf16(sum[e])), x0[e] * a.l2);
+            ss = __builtin_fmaf(v[j][e], v[j][e], ss);
+        }
+        store8(a.mixed + row + i, v[j]);
+    }
+    if (!a.mixed) return;
+    ss = wave_sum_butterfly(ss);
+    if ((t & (WAVE - 1)) == 0) wsum[t / WAVE] = ss;
+    __syncthreads();
+    ss = wsum[0];
+#pragma unroll
+    for (int w = 1; w < 256 / WAVE; w++) ss = ss + wsum[w];
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)a.C + FLT_EPS);
+#pragma unroll
+    for (int j = 0; j < NG; j++) {
+        const int i = (j * 256 + t) * 8;
+        if (i >= a.C) continue;
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) y[e] = v[j][e] * r;
+        store8(a.out + row + i, y);
+    }
 }
 
 /* ---------------------------------------------------------------- the choice */
@@ -510,6 +588,7 @@ struct Lane {
     void *lt_ws;                         /* hipBLASLt workspace (Decoder::lt_ws_bytes) */
     void *attn_ws;                       /* decode-attention partials (Decoder::attn_ws_bytes) */
     float *part;                         /* slot_gemm's split-K partial sums (Decoder::part_bytes) */
+    float *ssq;                          /* [B][ceil(C / 16)]: the o GEMM's tile sums of squares for fc's rstd */
 };
 
 struct Decoder {
@@ -750,15 +829,17 @@ static float *layer_s(Decoder *d, int l) { return d->kv_scale + (size_t)l * d->l
  * K) are reduced in slice order. Prefill rows: the library GEMM into fp32 or bf16, then the epilogue kernels. */
 static void gemm_epi(Decoder *d, const Lane &ln, bool step, int epi, const uint16_t *w, int rows, int cols,
                      const uint16_t *in, int n, uint16_t *out, float *out_f32, const uint16_t *res, const float *rstd,
-                     const unsigned long long *active) {
+                     const unsigned long long *active, float *ssq = nullptr) {
     if (n <= 0) return;
     if (step) {
         const int S = slot_gemm_slices(rows, cols);
+        const int ssq_cols = ((epi == SG_RELU2 ? cols : rows) + 15) / 16;   /* a slot's tile sums */
         for (int b0 = 0; b0 < n; b0 += SG_MAX_N) {
             const size_t o = (size_t)b0 * rows;
             SkinnyGemm g = {w, in + (size_t)b0 * cols, rows, cols, n - b0 < SG_MAX_N ? n - b0 : SG_MAX_N,
                             out ? out + o : nullptr, out_f32 ? out_f32 + o : nullptr, res ? res + o : nullptr,
-                            rstd ? rstd + b0 : nullptr, active ? active + b0 / MASK_BITS : nullptr};
+                            rstd ? rstd + b0 : nullptr, active ? active + b0 / MASK_BITS : nullptr,
+                            ssq ? ssq + (size_t)b0 * ssq_cols : nullptr};
             NC_CHECK(slot_gemm(g, epi, ln.part, d->part_bytes, S, ln.stream));
             if (S > 1) NC_CHECK(slot_gemm_reduce(g, epi, ln.part, d->part_bytes, S, ln.stream));
         }
@@ -779,15 +860,42 @@ static void gemm_epi(Decoder *d, const Lane &ln, bool step, int epi, const uint1
     }
 }
 
+/* A step's proj GEMM and the next layer's residual norm (next; NULL after the last layer: x alone): the GEMM's fp32
+ * K-slice partials, then proj_norm_kernel adds them with the residual and normalizes the row. */
+static void proj_norm(Decoder *d, const Lane &ln, const Layer &ly, const Layer *next, const Acts &a, int n,
+                      const unsigned long long *active) {
+    const int C = d->C, F = d->F;
+    const int S = slot_gemm_slices(C, F);
+    for (int b0 = 0; b0 < n; b0 += SG_MAX_N) {
+        const int nn = n - b0 < SG_MAX_N ? n - b0 : SG_MAX_N;
+        const size_t o = (size_t)b0 * C;
+        SkinnyGemm g = {ly.proj, a.u + (size_t)b0 * F, C, F, nn, nullptr, nullptr, nullptr, nullptr,
+                        active ? active + b0 / MASK_BITS : nullptr, nullptr};
+        NC_CHECK(slot_gemm_partials(g, ln.part, d->part_bytes, S, ln.stream));
+        ProjNormArgs pa = {ln.part, S, nn, C, a.xo + o, a.x + o, a.x0 + o, next ? next->resid : 0.0f,
+                           next ? next->x0 : 0.0f, next ? a.xm + o : nullptr, next ? a.h + o : nullptr, g.active};
+        if (C <= 256 * 8) hipLaunchKernelGGL(proj_norm_kernel<1>, dim3(nn), dim3(256), 0, ln.stream, pa);
+        else hipLaunchKernelGGL(proj_norm_kernel<2>, dim3(nn), dim3(256), 0, ln.stream, pa);
+    }
+}
+
 /* The rest of a layer after its attention: o_proj + residual, the MLP. In a step the o GEMM's epilogue adds the
- * residual itself (fp32 sum and its bf16 rounding), so the rstd kernel only reads the sum. */
-static void mlp(Decoder *d, const Lane &ln, bool step, const Layer &ly, const Acts &a, int n,
+ * residual itself (fp32 sum and its bf16 rounding), so the rstd kernel only reads the sum, and the proj GEMM's sums
+ * go to proj_norm_kernel with the next layer's norm (next). */
+static void mlp(Decoder *d, const Lane &ln, bool step, const Layer &ly, const Layer *next, const Acts &a, int n,
                 const unsigned long long *active) {
     const int C = d->C, F = d->F;
+    if (step && slot_gemm_slices(C, C) == 1) {   /* o and fc in one K slice: rstd from the o GEMM's tile sums */
+        gemm_epi(d, ln, step, SG_RESID2, ly.o, C, C, a.att, n, a.xo, nullptr, a.xm, nullptr, active, ln.ssq);
+        gemm_epi(d, ln, step, SG_RELU2, ly.fc, F, C, a.xo, n, a.u, nullptr, nullptr, nullptr, active, ln.ssq);
+        proj_norm(d, ln, ly, next, a, n, active);
+        return;
+    }
     gemm_epi(d, ln, step, SG_RESID2, ly.o, C, C, a.att, n, a.xo, a.acc, a.xm, nullptr, active);
     launch_rstd(d, ln, a.acc, step ? nullptr : a.xm, a.xo, a.rstd, active, n);
     gemm_epi(d, ln, step, SG_RELU2, ly.fc, F, C, a.xo, n, a.u, a.acc, nullptr, a.rstd, active);
-    gemm_epi(d, ln, step, SG_RESID, ly.proj, C, F, a.u, n, a.x, nullptr, a.xo, nullptr, active);
+    if (step) proj_norm(d, ln, ly, next, a, n, active);
+    else gemm_epi(d, ln, step, SG_RESID, ly.proj, C, F, a.u, n, a.x, nullptr, a.xo, nullptr, active);
 }
 
 /* Slots [b0, b0 + n) of a step (b0 a multiple of 64, so their active mask starts at word b0 / 64). */
@@ -809,18 +917,21 @@ static void body_embed(Decoder *d, const Lane &ln, const Part &p) {
     launch_norm(ln, n);
 }
 
-/* Layer l up to its attention: the residual norm and qkv. */
+/* Layer l up to its attention: the residual norm (layer 0's here; a later layer's is the previous layer's
+ * proj_norm) and qkv. */
 static void body_pre(Decoder *d, const Lane &ln, const Part &p, int l) {
     const Layer &ly = d->layer[l];
     const Acts &a = p.a;
     const int C = d->C;
-    NormArgs r = norm_args(d, NORM_RESID, a, p.n, d->tokens + p.b0, p.active);
-    r.in = l == 0 ? nullptr : a.x;
-    r.l1 = ly.resid;
-    r.l2 = ly.x0;
-    r.mixed = a.xm;
-    r.out = a.h;
-    launch_norm(ln, r);
+    if (l == 0) {
+        NormArgs r = norm_args(d, NORM_RESID, a, p.n, d->tokens + p.b0, p.active);
+        r.in = nullptr;
+        r.l1 = ly.resid;
+        r.l2 = ly.x0;
+        r.mixed = a.xm;
+        r.out = a.h;
+        launch_norm(ln, r);
+    }
     gemm_epi(d, ln, true, SG_STORE, ly.qkv, 3 * C, C, a.h, p.n, a.qkv, nullptr, nullptr, nullptr, p.active);
 }
 
@@ -853,7 +964,7 @@ static void record_body(Decoder *d) {
         for (int l = 0; l < d->L; l++) {
             body_pre(d, ln, p, l);
             body_attn(d, ln, p, l);
-            mlp(d, ln, true, d->layer[l], p.a, p.n, p.active);
+            mlp(d, ln, true, d->layer[l], l + 1 < d->L ? &d->layer[l + 1] : nullptr, p.a, p.n, p.active);
         }
         return;
     }
@@ -873,7 +984,8 @@ static void record_body(Decoder *d) {
         HIP_CHECK(hipStreamWaitEvent(ln[1].stream, done[0], 0));
         body_attn(d, ln[1], p[1], l);
         HIP_CHECK(hipEventRecord(done[1], ln[1].stream));
-        for (int h = 0; h < 2; h++) mlp(d, ln[h], true, d->layer[l], p[h].a, p[h].n, p[h].active);
+        for (int h = 0; h < 2; h++)
+            mlp(d, ln[h], true, d->layer[l], l + 1 < d->L ? &d->layer[l + 1] : nullptr, p[h].a, p[h].n, p[h].active);
     }
     HIP_CHECK(hipEventRecord(d->join, ln[1].stream));
     HIP_CHECK(hipStreamWaitEvent(ln[0].stream, d->join, 0));
@@ -1033,11 +1145,16 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
         const long long bytes = slot_gemm_part_bytes(rk[0], SG_MAX_N, slot_gemm_slices(rk[0], rk[1]));
         part_bytes = bytes > part_bytes ? bytes : part_bytes;
     }
+    REQUIRE(slot_gemm_slices(C, F) <= PN_MAX_S, "the FFN width (proj_norm adds at most 8 K-slices)");
+    /* the step's proj GEMM always leaves its sums as partials (proj_norm), one slice or more */
+    const long long proj_bytes = (long long)slot_gemm_slices(C, F) * SG_MAX_N * C * 4;
+    part_bytes = proj_bytes > part_bytes ? proj_bytes : part_bytes;
     d->part_bytes = part_bytes;
     d->attn_ws_bytes = nc_decode_workspace_bytes(d->B, d->H, d->H, d->max_len, -1);
     REQUIRE(d->attn_ws_bytes > 0, "decode attention workspace");
     for (Lane &ln : d->lane) {
         ln.part = (float *)device_alloc(d, (size_t)part_bytes);
+        ln.ssq = (float *)device_alloc(d, (size_t)B * ((C + 15) / 16) * sizeof(float));
         ln.lt_ws = device_alloc(d, d->lt_ws_bytes);
         ln.attn_ws = device_alloc(d, d->attn_ws_bytes);
     }
@@ -1249,7 +1366,7 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
         NC_CHECK(prefill_runs(a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table, d->max_pages,
                               (int)d->layer_pages, dstart, drow0, dcount, drslot, runs, max_count, d->H, d->H, ly.window,
                               SM_SCALE, a.att, d->stream));
-        mlp(d, ln, false, ly, a, n, nullptr);
+        mlp(d, ln, false, ly, nullptr, a, n, nullptr);
     }
 }
 
@@ -1467,7 +1584,7 @@ extern "C" int dec_debug_slot_gemm(int epi, const void *w, int R, int K, const v
                                    float *out_f32, const void *res, const float *rstd, int slices, float *part,
                                    void *stream) {
     nc::SkinnyGemm g = {(const uint16_t *)w, (const uint16_t *)x, R, K, N, (uint16_t *)out, out_f32,
-                        (const uint16_t *)res, rstd, nullptr};
+                        (const uint16_t *)res, rstd, nullptr, nullptr};
     if (!nc::slot_gemm_fits(R, K, N)) return -2;
     const int S = slices > 0 ? slices : nc::slot_gemm_slices(R, K);
     const long long part_bytes = nc::slot_gemm_part_bytes(R, N, S);   /* the caller allocates this much */
@@ -1480,6 +1597,14 @@ extern "C" int dec_debug_slot_gemm_slices(int R, int K) { return nc::slot_gemm_s
 
 extern "C" long long dec_debug_slot_gemm_part_bytes(int R, int N, int slices) {
     return nc::slot_gemm_part_bytes(R, N, slices);
+}
+
+extern "C" int dec_debug_slot_gemm_ssq(int epi, const void *w, int R, int K, const void *x, int N, void *out,
+                                       const void *res, float *ssq, void *stream) {
+    if (!ssq || (epi != nc::SG_RESID2 && epi != nc::SG_RELU2)) return -2;
+    nc::SkinnyGemm g = {(const uint16_t *)w, (const uint16_t *)x, R, K, N, (uint16_t *)out, nullptr,
+                        (const uint16_t *)res, nullptr, nullptr, ssq};
+    return nc::slot_gemm(g, epi, nullptr, 0, 1, (hipStream_t)stream);
 }
 
 extern "C" int dec_debug_slot_gemm_tile(int R, int K, int N, int slices) {

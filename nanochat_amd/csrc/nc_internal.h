@@ -61,8 +61,12 @@ struct SkinnyGemm {
     uint16_t *out;                     /* [N][R] bf16 (STORE, RESID2, RELU2, RESID) */
     float *out_f32;                    /* [N][R] fp32 (RESID2: the sum before rounding; F32) */
     const uint16_t *res;               /* [N][R] bf16 residual (RESID2, RESID) */
-    const float *rstd;                 /* [N] (RELU2) */
+    const float *rstd;                 /* [N] (RELU2 without ssq) */
     const unsigned long long *active;  /* NULL, or the slots whose outputs are stored */
+    float *ssq;                        /* NULL, or [N][ceil(R / 16)] (RESID2: written) / [N][ceil(K / 16)] (RELU2:
+                                          read): each 16-row tile's sum of squares of the residual sum x; RELU2 then
+                                          takes rstd = 1 / sqrt((sum over tiles in order) / K + FLT_EPSILON) from it
+                                          (one slice only) */
 };
 
 /* slot_gemm.hip: the decode step's GEMM with every global access range-checked by buffer instructions. */
@@ -79,5 +83,8 @@ long long slot_gemm_part_bytes(int R, int N, int S);
 int slot_gemm(const SkinnyGemm &g, int epi, float *part, long long part_bytes, int S, hipStream_t stream);
 int slot_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, long long part_bytes, int S,
                      hipStream_t stream);
+/* The fp32 partial sums of S >= 1 slices to part [S][N][R] (part_bytes must hold S N R floats), for a caller that
+ * finishes the sum itself. */
+int slot_gemm_partials(const SkinnyGemm &g, float *part, long long part_bytes, int S, hipStream_t stream);
 
 }  // namespace nc

@@ -57,6 +57,21 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 typedef __attribute__((address_space(3))) void LdsPtr;
 
+/* The sum of a 16-lane row by DPP (no LDS round trip, unlike a shuffle): adjacent lanes, then pairs, then the row
+ * rotated by 4 and by 8; lane 0 of the row ends with ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)) + ... in a
+ * fixed association. */
+__device__ __forceinline__ float dpp_add(float v, int ctrl_sel) {
+    int o;
+    switch (ctrl_sel) {
+    case 0: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false); break;   /* quad [1,0,3,2] */
+    case 1: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false); break;   /* quad [2,3,0,1] */
+    case 2: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false); break;  /* row_ror:4 */
+    default: o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false); break; /* row_ror:8 */
+    }
+    return v + __int_as_float(o);
+}
+__device__ __forceinline__ float row16_sum(float v) { return dpp_add(dpp_add(dpp_add(dpp_add(v, 0), 1), 2), 3); }
+
 /* A raw buffer over `bytes` bytes from p (bytes < 2^31, checked by the host). */
 __device__ __forceinline__ Rsrc rsrc(const void *p, long long bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
@@ -69,6 +84,9 @@ __device__ __forceinline__ float bloadf(Rsrc r, int off) {
 }
 __device__ __forceinline__ void bstore16(Rsrc r, int off, u32x4 v) { __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0); }
 __device__ __forceinline__ void bstore8(Rsrc r, int off, u32x2 v) { __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0); }
+__device__ __forceinline__ void bstore4(Rsrc r, int off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+}
 
 __device__ __forceinline__ bool sl_live(const unsigned long long *mask, int n) {
     return !mask || ((mask[n >> 6] >> (n & 63)) & 1ull);
@@ -76,11 +94,13 @@ __device__ __forceinline__ bool sl_live(const unsigned long long *mask, int n) {
 
 /* The operand views of one launch. */
 struct SlotViews {
-    Rsrc w, x, out, out_f32, res, rstd, part;
+    Rsrc w, x, out, out_f32, res, rstd, part, ssq;
 };
 
-/* part_bytes: the partial-sum buffer's allocation (the caller's), so its range is the allocation itself. */
-__device__ __forceinline__ SlotViews slot_views(const SkinnyGemm &g, const float *part, long long part_bytes) {
+/* part_bytes: the partial-sum buffer's allocation (the caller's), so its range is the allocation itself; ssq_cols: the
+ * tile sums a slot has (ceil(R / 16) written by RESID2, ceil(K / 16) read by RELU2). */
+__device__ __forceinline__ SlotViews slot_views(const SkinnyGemm &g, const float *part, long long part_bytes,
+                                                int ssq_cols) {
     SlotViews v;
     v.w = rsrc(g.w, (long long)g.R * g.K * 2);
     v.x = rsrc(g.x, (long long)g.N * g.K * 2);
@@ -89,12 +109,13 @@ __device__ __forceinline__ SlotViews slot_views(const SkinnyGemm &g, const float
     v.res = rsrc(g.res, g.res ? (long long)g.N * g.R * 2 : 0);
     v.rstd = rsrc(g.rstd, g.rstd ? (long long)g.N * 4 : 0);
     v.part = rsrc(part, part ? part_bytes : 0);
+    v.ssq = rsrc(g.ssq, g.ssq ? (long long)g.N * ssq_cols * 4 : 0);
     return v;
 }
 
-/* The epilogue of four consecutive rows r .. r + 3 of slot n (sums s); at = n R + r. */
+/* The epilogue of four consecutive rows r .. r + 3 of slot n (sums s); at = n R + r; rstd: slot n's (RELU2). */
 template <int EPI>
-__device__ __forceinline__ void sl_store(const SlotViews &v, int n, int at, float s[4]) {
+__device__ __forceinline__ void sl_store(const SlotViews &v, int at, float s[4], float rstd) {
     if (EPI == SG_F32) {
         bstore16(v.out_f32, at * 4, u32x4{__float_as_uint(s[0]), __float_as_uint(s[1]), __float_as_uint(s[2]),
                                           __float_as_uint(s[3])});
@@ -110,10 +131,9 @@ __device__ __forceinline__ void sl_store(const SlotViews &v, int n, int at, floa
             bstore16(v.out_f32, at * 4, u32x4{__float_as_uint(s[0]), __float_as_uint(s[1]), __float_as_uint(s[2]),
                                               __float_as_uint(s[3])});
     } else if (EPI == SG_RELU2) {
-        const float r_ = bloadf(v.rstd, n * 4);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float p = s[i] * r_;
+            const float p = s[i] * rstd;
             s[i] = fmaxf(p, 0.0f) * p;
         }
     }
@@ -193,13 +213,31 @@ __global__ void __launch_bounds__(SL_THREADS, 1) slot_gemm_kernel(SkinnyGemm g, 
     constexpr int XB = sl_buf<CT>(), WB = sl_buf<RT>();
     __shared__ __align__(16) unsigned char x0[XB], x1[XB], x2[XB];
     __shared__ __align__(16) unsigned char w0[WB], w1[WB], w2[WB];
-    const SlotViews v = slot_views(g, part, part_bytes);
+    __shared__ float rs[EPI == SG_RELU2 ? 16 * CT : 1];   /* RELU2 from ssq: the group's slots' rstd */
+    const SlotViews v = slot_views(g, part, part_bytes, EPI == SG_RELU2 ? (g.K + 15) / 16 : (g.R + 15) / 16);
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const int i16 = lane & 15, grp = lane >> 4;
     const int r0 = blockIdx.x * 16 * RT, s = blockIdx.y, n0 = blockIdx.z * 16 * CT;
     const int chunks = g.K / SL_KC;
     const int c0 = s * chunks / S, nc = (s + 1) * chunks / S - c0;   /* the slice: stages [c0, c0 + nc) */
     const int rowb = g.K * 2, kb0 = c0 * SL_ROWB;
+
+    /* RELU2 from tile sums: each slot's rstd from its row's tile sums (at most 128: K <= 2048, checked by the host).
+     * Wave w takes slots n0 + 4 CT w + i; lane l holds tiles l and l + 64 of each. The loads go out before the first
+     * DMA (loads complete in issue order, so the stage waits then cover them and stall nothing); the sums are made
+     * after the main loop: (tile l + tile l + 64), then row16_sum within each 16 lanes and the rows' pair sums (lane
+     * 0's order is fixed), the same for every slot. */
+    constexpr int PW = EPI == SG_RELU2 ? 4 * CT : 1;
+    float ts0[PW], ts1[PW];
+    const int tiles = (g.K + 15) / 16;
+    if (EPI == SG_RELU2 && g.ssq) {
+#pragma unroll
+        for (int i = 0; i < PW; i++) {
+            const int n = n0 + PW * wave + i;   /* past N: zeros (the view's range) */
+            ts0[i] = lane < tiles ? bloadf(v.ssq, (n * tiles + lane) * 4) : 0.0f;
+            ts1[i] = lane + WAVE < tiles ? bloadf(v.ssq, (n * tiles + lane + WAVE) * 4) : 0.0f;
+        }
+    }
 
     f32x4 acc[RT][CT];
 #pragma unroll
@@ -219,6 +257,17 @@ __global__ void __launch_bounds__(SL_THREADS, 1) slot_gemm_kernel(SkinnyGemm g, 
     if (j < nc) SL_STEP(j, x0, w0, x2, w2);           /* nc - j is 1 or 2: uniform over the workgroup */
     if (j + 1 < nc) SL_STEP(j + 1, x1, w1, x0, w0);
     __builtin_amdgcn_s_waitcnt(0);                    /* no DMA may land in LDS after this */
+    if (EPI == SG_RELU2 && g.ssq) {   /* read by the epilogue after the reduction's first barrier */
+        static_assert(PW <= WAVE, "a lane per slot of the wave");
+        float mine = 0.0f;             /* lane i: slot i's sum (lane 0's), so one sqrt and divide serve every slot */
+#pragma unroll
+        for (int i = 0; i < PW; i++) {
+            const float ss = pair_sum32(pair_sum16(row16_sum(ts0[i] + ts1[i])));
+            const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 0));
+            mine = lane == i ? s0 : mine;
+        }
+        if (lane < PW) rs[PW * wave + lane] = 1.0f / __builtin_sqrtf(mine * (1.0f / (float)g.K) + FLT_EPS);
+    }
     sl_barrier();
     /* the four waves' sums, added in wave (K) order, up to two row tiles at a time: each wave writes its sums of the
      * round's (t, u) tiles (2 CT f32x4 a lane: waves 0, 1 into x0, waves 2, 3 into x1, which hold 4 CT), then wave w
@@ -247,14 +296,27 @@ __global__ void __launch_bounds__(SL_THREADS, 1) slot_gemm_kernel(SkinnyGemm g, 
                 const f32x4 p = rw[(t * CT + u) * WAVE + lane];
                 sum = w == 0 ? p : sum + p;
             }
-            if (r >= g.R || n >= g.N || !sl_live(g.active, n)) continue;
+            const bool ok = r < g.R && n < g.N && sl_live(g.active, n);
             float sv[4] = {sum[0], sum[1], sum[2], sum[3]};
+            if (EPI == SG_RESID2 && g.ssq) {   /* wave-uniform: every lane takes part in the tile's sum of squares */
+                if (ok) sl_store<SG_RESID2>(v, n * g.R + r, sv, 0.0f);   /* sv += the residual */
+                float sq = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) sq = __builtin_fmaf(sv[i], sv[i], sq);
+                sq = pair_sum32(pair_sum16(ok ? sq : 0.0f));   /* the tile's 16 rows (rows past R: 0) */
+                const int tile = blockIdx.x * RT + tt + t;     /* a workgroup's last tiles may lie past R */
+                if (grp == 0 && n < g.N && sl_live(g.active, n) && tile * 16 < g.R)
+                    bstore4(v.ssq, (n * ((g.R + 15) / 16) + tile) * 4, sq);
+                continue;
+            }
+            if (!ok) continue;
             if (EPI < 0)
                 bstore16(v.part, ((s * g.N + n) * g.R + r) * 4,
                          u32x4{__float_as_uint(sv[0]), __float_as_uint(sv[1]), __float_as_uint(sv[2]),
                                __float_as_uint(sv[3])});
             else
-                sl_store<EPI < 0 ? SG_STORE : EPI>(v, n, n * g.R + r, sv);
+                sl_store<EPI < 0 ? SG_STORE : EPI>(v, n * g.R + r, sv,
+                                                   EPI == SG_RELU2 ? (g.ssq ? rs[n - n0] : bloadf(v.rstd, n * 4)) : 0.0f);
         }
         sl_barrier();   /* the reduction area is rewritten by the next round */
     }
@@ -267,14 +329,14 @@ __global__ void __launch_bounds__(256) slot_gemm_reduce_kernel(SkinnyGemm g, con
     const int n = blockIdx.y;
     const int r = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (r >= g.R || !sl_live(g.active, n)) return;
-    const SlotViews v = slot_views(g, part, part_bytes);
+    const SlotViews v = slot_views(g, part, part_bytes, 0);
     float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int s = 0; s < S; s++) {
         const u32x4 p = bload16(v.part, ((s * g.N + n) * g.R + r) * 4);
 #pragma unroll
         for (int i = 0; i < 4; i++) sv[i] = sv[i] + __uint_as_float(p[i]);
     }
-    sl_store<EPI>(v, n, n * g.R + r, sv);
+    sl_store<EPI>(v, n * g.R + r, sv, EPI == SG_RELU2 ? bloadf(v.rstd, n * 4) : 0.0f);
 }
 
 /* The tile shapes built, as (RT, CT). */
@@ -342,15 +404,19 @@ static bool sl_part_fits(const SkinnyGemm &g, const float *part, long long part_
 }
 
 static bool sl_operands_fit(const SkinnyGemm &g, int epi) {
-    const bool need_out = epi != SG_F32, need_f32 = epi == SG_F32 || epi == SG_RESID2;
+    const bool need_out = epi != SG_F32, need_f32 = epi == SG_F32 || (epi == SG_RESID2 && !g.ssq);
     const bool need_res = epi == SG_RESID || epi == SG_RESID2;
-    return !((need_out && !g.out) || (need_f32 && !g.out_f32) || (need_res && !g.res) || (epi == SG_RELU2 && !g.rstd));
+    return !((need_out && !g.out) || (need_f32 && !g.out_f32) || (need_res && !g.res) ||
+             (epi == SG_RELU2 && !g.rstd && !g.ssq));
 }
 
 int slot_gemm(const SkinnyGemm &g, int epi, float *part, long long part_bytes, int S, hipStream_t stream) {
     if (!slot_gemm_fits(g.R, g.K, g.N) || S < 1 || S > g.K / SL_KC || epi < SG_STORE || epi > SG_F32) return -2;
     if (S > 1 && !sl_part_fits(g, part, part_bytes, S)) return -2;
     if (S == 1 && !sl_operands_fit(g, epi)) return -2;
+    /* tile sums: one slice, a RELU2 row of at most 128 tiles */
+    if (g.ssq && (S > 1 || (epi != SG_RESID2 && epi != SG_RELU2) || (epi == SG_RELU2 && (g.K + 15) / 16 > 2 * WAVE)))
+        return -2;
     if (S > 1) {
         sl_launch<-1>(g, part, part_bytes, S, stream);
         return (int)hipGetLastError();
@@ -365,9 +431,18 @@ int slot_gemm(const SkinnyGemm &g, int epi, float *part, long long part_bytes, i
     return (int)hipGetLastError();
 }
 
+int slot_gemm_partials(const SkinnyGemm &g, float *part, long long part_bytes, int S, hipStream_t stream) {
+    if (!slot_gemm_fits(g.R, g.K, g.N) || S < 1 || S > g.K / SL_KC || !part || g.ssq ||
+        (long long)S * g.N * g.R * 4 > part_bytes || part_bytes >= (1LL << 31))
+        return -2;
+    sl_launch<-1>(g, part, part_bytes, S, stream);
+    return (int)hipGetLastError();
+}
+
 int slot_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, long long part_bytes, int S,
                      hipStream_t stream) {
-    if (!slot_gemm_fits(g.R, g.K, g.N) || S < 2 || !sl_part_fits(g, part, part_bytes, S) || !sl_operands_fit(g, epi))
+    if (!slot_gemm_fits(g.R, g.K, g.N) || S < 2 || !sl_part_fits(g, part, part_bytes, S) || !sl_operands_fit(g, epi) ||
+        g.ssq)
         return -2;
     const dim3 grid((g.R / 4 + 255) / 256, g.N), block(256);
     switch (epi) {

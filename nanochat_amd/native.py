@@ -142,6 +142,8 @@ DECODE_SIGNATURES = {
     "dec_debug_slot_gemm_slices": ([c_int, c_int], c_int),
     "dec_debug_slot_gemm_part_bytes": ([c_int, c_int, c_int], c_longlong),
     "dec_debug_slot_gemm_tile": ([c_int, c_int, c_int, c_int], c_int),
+    "dec_debug_slot_gemm_ssq": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+                                 c_void_p], c_int),
 }
 
 LIBRARIES = {"nanochat_kv": (LIBRARY, SIGNATURES), "decode": (DECODE_LIBRARY, DECODE_SIGNATURES)}

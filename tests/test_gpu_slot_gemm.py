@@ -115,3 +115,60 @@ def test_a_slots_result_does_not_depend_on_the_others(device, R, K):
     assert torch.equal(moved, full[order])
     part = run(F32, w, x[40:77].contiguous())[1]
     assert torch.equal(part, full[40:77])
+
+
+@pytest.mark.parametrize("R,K,N", [(1664, 1664, 128), (6656, 1664, 37), (260, 384, 17), (1664, 1664, 1)])
+def test_mlp_rstd_from_tile_sums(device, R, K, N):
+    """The step's MLP rstd without its own kernel: the o GEMM (RESID2) writes each 16-row tile's sum of squares of its
+    residual sum x = s + res, and the fc GEMM (RELU2) takes rstd = 1 / sqrt(sum / K + FLT_EPSILON) from the tiles of
+    its K = C row. Against float64: the tile sums (fp32 accumulation bound), then fc's output from an x whose rows are
+    the o GEMM's (one GEMM run as both, R = K)."""
+    lib = hip_library("decode")
+    gen = torch.Generator().manual_seed(R + K + N)
+    w = (torch.randn(R, K, generator=gen) * 0.05).bfloat16()
+    x = torch.randn(N, K, generator=gen).bfloat16()
+    res = torch.randn(N, R, generator=gen).bfloat16()
+    tiles = -(-R // 16)
+    s = x.double() @ w.double().T
+    bound = (x.double().abs() @ w.double().abs().T) * K * 2.0 ** -24
+    xs = s + res.double()
+    out = torch.full((N, R), 7.0, dtype=torch.bfloat16, device=device)
+    ssq = torch.full((N, tiles), -1.0, dtype=torch.float32, device=device)
+    print(f"slot_gemm ssq RESID2 R={R} K={K} N={N}", flush=True)
+    assert lib.dec_debug_slot_gemm_ssq(1, pointer(w.to(device)), R, K, pointer(x.to(device)), N, pointer(out),
+                                       pointer(res.to(device)), pointer(ssq), stream()) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().double().numpy()
+    assert np.all(np.abs(got - xs.numpy()) <= bf16_ulp(xs.numpy()) + (bound + 2.0 ** -24 * xs.abs()).numpy() + 1e-30)
+    pad = torch.zeros(N, tiles * 16, dtype=torch.float64)
+    pad[:, :R] = xs
+    want = (pad.view(N, tiles, 16) ** 2).sum(-1)
+    err_x = bound + 2.0 ** -24 * xs.abs()                    # |x_device - x| per element
+    pad_e = torch.zeros_like(pad)
+    pad_e[:, :R] = err_x * (2 * xs.abs() + err_x)             # |x_d^2 - x^2|
+    tol = pad_e.view(N, tiles, 16).sum(-1) + want * 32 * 2.0 ** -24
+    assert ((ssq.cpu().double() - want).abs() <= tol).all()
+
+    # fc: K = R of the o GEMM above, rstd from those tile sums
+    if R != K:
+        return
+    w2 = (torch.randn(3 * K, K, generator=gen) * 0.05).bfloat16()
+    x2 = out.cpu()                                           # the o GEMM's bf16 output as fc's input
+    u = torch.full((N, 3 * K), 7.0, dtype=torch.bfloat16, device=device)
+    print(f"slot_gemm ssq RELU2 R={3 * K} K={K} N={N}", flush=True)
+    assert lib.dec_debug_slot_gemm_ssq(2, pointer(w2.to(device)), 3 * K, K, pointer(x2.to(device)), N, pointer(u),
+                                       None, pointer(ssq), stream()) == 0
+    torch.cuda.synchronize()
+    ss = ssq.cpu().double().sum(-1)
+    r = (1.0 / torch.sqrt(ss / K + 2.0 ** -23))[:, None]
+    s2 = x2.double() @ w2.double().T
+    b2 = (x2.double().abs() @ w2.double().abs().T) * K * 2.0 ** -24
+    p = s2 * r
+    ref = torch.relu(p) * p
+    # the device's rstd differs from r by its fp32 sum over <= 128 tiles and one sqrt / divide
+    rerr = r * (128 * 2.0 ** -24 + 2.0 ** -22)
+    perr = b2 * r + s2.abs() * rerr
+    tol2 = 2 * p.abs() * perr + perr ** 2 + 2.0 ** -22 * p * p
+    assert np.all(np.abs(u.cpu().double().numpy() - ref.numpy()) <= bf16_ulp(ref.numpy()) + tol2.numpy() + 1e-30)
+    assert lib.dec_debug_slot_gemm_ssq(2, pointer(w2.to(device)), 3 * K, K, pointer(x2.to(device)), N, pointer(u),
+                                       None, None, stream()) == -2
