@@ -143,12 +143,12 @@ __device__ __forceinline__ void sl_store(const SlotViews &v, int at, float s[4],
     bstore8(v.out, at * 2, u32x2{(uint32_t)o[0] | (uint32_t)o[1] << 16, (uint32_t)o[2] | (uint32_t)o[3] << 16});
 }
 
-/* s_waitcnt: every vector-memory load but the newest sl_loads<RT, CT>() has landed (the stage issued after this one may
- * stay in flight), and this wave's LDS reads are done. Encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait),
- * lgkmcnt [11:8]. */
-template <int RT, int CT>
+/* s_waitcnt: every vector-memory load but the newest (RING - 2) sl_loads<RT, CT>() has landed (the stages issued after
+ * this one may stay in flight), and this wave's LDS reads are done. Encoding: vmcnt [3:0] and [15:14], expcnt [6:4]
+ * (7: no wait), lgkmcnt [11:8]. */
+template <int RT, int CT, int RING>
 __device__ __forceinline__ void sl_wait_stage() {
-    constexpr int n = sl_loads<RT, CT>();
+    constexpr int n = (RING - 2) * sl_loads<RT, CT>();
     static_assert(n < 64, "vmcnt holds 6 bits");
     __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
 }
@@ -195,24 +195,25 @@ __device__ __forceinline__ void sl_compute(const unsigned char *xb, const unsign
 }
 
 /* One ring position: wait for stage j, barrier (every wave's DMA of stage j has landed and every wave is done with
- * stage j - 1), refill the buffers stage j - 1 used with stage j + 2, compute stage j. */
+ * stage j - 1), refill the buffers stage j - 1 used with stage j + RING - 1, compute stage j. */
 #define SL_STEP(j, XB, WB, NXB, NWB)                                                     \
     do {                                                                                 \
-        sl_wait_stage<RT, CT>();                                                         \
+        sl_wait_stage<RT, CT, RING>();                                                   \
         sl_barrier();                                                                    \
-        sl_fetch<sl_tile_loads<CT>()>(v.x, NXB, (j) + 2, nc, kb0, rowb, n0, wave, lane); \
-        sl_fetch<sl_tile_loads<RT>()>(v.w, NWB, (j) + 2, nc, kb0, rowb, r0, wave, lane); \
+        sl_fetch<sl_tile_loads<CT>()>(v.x, NXB, (j) + RING - 1, nc, kb0, rowb, n0, wave, lane); \
+        sl_fetch<sl_tile_loads<RT>()>(v.w, NWB, (j) + RING - 1, nc, kb0, rowb, r0, wave, lane); \
         sl_compute<RT, CT>(XB, WB, acc, wave, i16, grp);                                 \
     } while (0)
 
-/* EPI < 0: store partial sums (S > 1). RT 16-row tiles and CT 16-slot tiles a workgroup. Grid (ceil(R / (16 RT)), S,
- * ceil(N / (16 CT))), 256 threads. */
-template <int EPI, int RT, int CT>
+/* EPI < 0: store partial sums (S > 1). RT 16-row tiles and CT 16-slot tiles a workgroup, a ring of RING stage buffers
+ * (RING - 1 stages in flight). Grid (ceil(R / (16 RT)), S, ceil(N / (16 CT))), 256 threads. */
+template <int EPI, int RT, int CT, int RING>
 __global__ void __launch_bounds__(SL_THREADS, 1) slot_gemm_kernel(SkinnyGemm g, float *part, long long part_bytes,
                                                                   int S) {
     constexpr int XB = sl_buf<CT>(), WB = sl_buf<RT>();
-    __shared__ __align__(16) unsigned char x0[XB], x1[XB], x2[XB];
-    __shared__ __align__(16) unsigned char w0[WB], w1[WB], w2[WB];
+    static_assert(RING == 3 || RING == 4, "the loop below rotates three or four stage buffers");
+    __shared__ __align__(16) unsigned char x0[XB], x1[XB], x2[XB], x3[RING == 4 ? XB : 16];
+    __shared__ __align__(16) unsigned char w0[WB], w1[WB], w2[WB], w3[RING == 4 ? WB : 16];
     __shared__ float rs[EPI == SG_RELU2 ? 16 * CT : 1];   /* RELU2 from ssq: the group's slots' rstd */
     const SlotViews v = slot_views(g, part, part_bytes, EPI == SG_RELU2 ? (g.K + 15) / 16 : (g.R + 15) / 16);
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
@@ -249,13 +250,27 @@ __global__ void __launch_bounds__(SL_THREADS, 1) slot_gemm_kernel(SkinnyGemm g, 
     sl_fetch<sl_tile_loads<CT>()>(v.x, x1, 1, nc, kb0, rowb, n0, wave, lane);
     sl_fetch<sl_tile_loads<RT>()>(v.w, w1, 1, nc, kb0, rowb, r0, wave, lane);
     int j = 0;
-    for (; j + 3 <= nc; j += 3) {
-        SL_STEP(j, x0, w0, x2, w2);
-        SL_STEP(j + 1, x1, w1, x0, w0);
-        SL_STEP(j + 2, x2, w2, x1, w1);
+    if (RING == 3) {
+        for (; j + 3 <= nc; j += 3) {
+            SL_STEP(j, x0, w0, x2, w2);
+            SL_STEP(j + 1, x1, w1, x0, w0);
+            SL_STEP(j + 2, x2, w2, x1, w1);
+        }
+        if (j < nc) SL_STEP(j, x0, w0, x2, w2);           /* nc - j is 1 or 2: uniform over the workgroup */
+        if (j + 1 < nc) SL_STEP(j + 1, x1, w1, x0, w0);
+    } else {
+        sl_fetch<sl_tile_loads<CT>()>(v.x, x2, 2, nc, kb0, rowb, n0, wave, lane);
+        sl_fetch<sl_tile_loads<RT>()>(v.w, w2, 2, nc, kb0, rowb, r0, wave, lane);
+        for (; j + 4 <= nc; j += 4) {
+            SL_STEP(j, x0, w0, x3, w3);
+            SL_STEP(j + 1, x1, w1, x0, w0);
+            SL_STEP(j + 2, x2, w2, x1, w1);
+            SL_STEP(j + 3, x3, w3, x2, w2);
+        }
+        if (j < nc) SL_STEP(j, x0, w0, x3, w3);           /* nc - j is 1, 2 or 3: uniform over the workgroup */
+        if (j + 1 < nc) SL_STEP(j + 1, x1, w1, x0, w0);
+        if (j + 2 < nc) SL_STEP(j + 2, x2, w2, x1, w1);
     }
-    if (j < nc) SL_STEP(j, x0, w0, x2, w2);           /* nc - j is 1 or 2: uniform over the workgroup */
-    if (j + 1 < nc) SL_STEP(j + 1, x1, w1, x0, w0);
     __builtin_amdgcn_s_waitcnt(0);                    /* no DMA may land in LDS after this */
     if (EPI == SG_RELU2 && g.ssq) {   /* read by the epilogue after the reduction's first barrier */
         static_assert(PW <= WAVE, "a lane per slot of the wave");
@@ -363,10 +378,16 @@ static SlTile sl_choose(int R, int K, int N, int S) {
     return best;
 }
 
+/* A ring of four stages (three in flight) for the smallest tile, whose 16 KiB stages leave a CU's ingest idle behind
+ * two in flight (config-5 o GEMM: 8.38 -> 7.63 us); three for the larger ones, whose stage time is their ingest
+ * (measured with four: qkv 10.66 -> 10.92 us, fc 14.29 -> 14.42, proj 12.50 -> 12.71). */
+template <int RT, int CT> constexpr int sl_ring() { return sl_buf<RT>() + sl_buf<CT>() <= 16 * 1024 ? 4 : 3; }
+
 template <int EPI, int RT, int CT>
 static void sl_launch_tile(const SkinnyGemm &g, float *part, long long part_bytes, int S, hipStream_t stream) {
     const dim3 grid((g.R + 16 * RT - 1) / (16 * RT), S, (g.N + 16 * CT - 1) / (16 * CT)), block(SL_THREADS);
-    hipLaunchKernelGGL((slot_gemm_kernel<EPI, RT, CT>), grid, block, 0, stream, g, part, part_bytes, S);
+    hipLaunchKernelGGL((slot_gemm_kernel<EPI, RT, CT, sl_ring<RT, CT>()>), grid, block, 0, stream, g, part, part_bytes,
+                       S);
 }
 
 template <int EPI>
