@@ -16,6 +16,8 @@ pytestmark = pytest.mark.gpu
 SHAPES = {
     "tiny": dict(layers=3, hidden=256, ffn=1024, vocab=2048, max_length=160, windows=[40, 160, 160], ve_layers=(0, 2)),
     "wide": dict(layers=2, hidden=1664, ffn=6656, vocab=4096, max_length=96, windows=[96, 96], ve_layers=()),
+    # wider than 2,048: the step's o and fc GEMMs take two K-slices, so the MLP's rstd comes from rstd_kernel
+    "wider": dict(layers=2, hidden=2304, ffn=9216, vocab=4096, max_length=64, windows=[64, 20], ve_layers=(1,)),
 }
 # logits against the float64 oracle on the same inputs, relative to the largest |logit|: fp32 GEMM accumulation
 # flips bf16 roundings of intermediate activations and fp8 codes downstream (fp32 GEMMs alone move the oracle's
@@ -96,10 +98,10 @@ def run_steps(dec, orc, inputs, positions, slots, steps, label, temperature=None
     return inputs, positions
 
 
-@pytest.mark.parametrize("shape", ["tiny", "wide"])
+@pytest.mark.parametrize("shape", ["tiny", "wide", "wider"])
 def test_prefill_and_greedy_steps_match_oracle(device, shape):
     m, w, max_length = build(device, shape)
-    lengths = [23, 64, 5, 81] if shape == "tiny" else [17, 40, 3]
+    lengths = {"tiny": [23, 64, 5, 81], "wide": [17, 40, 3], "wider": [12, 30, 2]}[shape]
     ids = prompts(lengths, m.vocab, seed=1)
     dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=8)
     try:
