@@ -512,3 +512,34 @@ def test_a_requests_tokens_do_not_depend_on_the_batch(device):
                 assert np.array_equal(x, y), (label, layer)
         for i, ((lg, tg), (lr, tr)) in enumerate(zip(steps, ref[1])):
             assert tg == tr and np.array_equal(lg, lr), (label, i)
+
+
+def test_more_than_128_slots(device):
+    """A step over more slots than one slot-GEMM block holds (128): the GEMMs, the o GEMM's tile sums, fc's rstd and
+    proj_norm run per block of 128 slots. One prompt in slot 5 (first block) and slot 140 (second block), among 158
+    other active slots with other prompts, gives bit-identical logits and tokens over three steps; slot 140 is also
+    (nearly) the float64 oracle's greedy choice."""
+    m, w, max_length = build(device, "tiny")
+    dec = DecoderRuntime(m, bos_token_id=0, max_length=max_length, prompt_store=0, max_slots=160)
+    try:
+        assert dec.batch == 160
+        P = prompts([19], m.vocab, seed=31)[0]
+        others = prompts([3 + (b % 11) for b in range(160)], m.vocab, seed=32)
+        for b in range(160):
+            dec.place(b, P if b in (5, 140) else others[b])
+        dec.prefill()
+        dec.activate(range(160))
+        orc = om.DecoderOracle(w, max_length)
+        n = len(P) - 1
+        orc.body(P[:n], list(range(n)), [0] * n, cache_only_last=True)
+        tok = P[-1]
+        for step in range(3):
+            tokens = dec.step()
+            got = dec.logits(160)
+            print(f"160 slots step {step}: tokens {tokens[5]} {tokens[140]}", flush=True)
+            assert tokens[5] == tokens[140] and np.array_equal(got[5], got[140]), step
+            want = orc.head(orc.body([tok], [n + step], [0]))[0]
+            assert want[tokens[140]] >= want.max() - 2 * LOGIT_MAX_REL * np.abs(want).max(), step
+            tok = int(tokens[140])
+    finally:
+        dec.close()
