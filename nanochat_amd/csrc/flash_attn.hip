@@ -80,15 +80,17 @@ typedef __attribute__((address_space(3))) void LdsVoid;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 LdsV4;
 
-/* A 64-row tile of one head straight into LDS in the k_lds layout by LDS DMA (no registers held): instruction i of a
- * wave writes rows 4 i' .. 4 i' + 3 (i' = wave + 4 i), lane l the 16 bytes at LDS chunk l % 16 of row 4 i' + l / 16,
- * fetched from the row's chunk (l % 16) ^ (row & 15). Rows past the descriptor's range read zeros. */
+/* A 64-row tile of one head straight into LDS in the k_lds layout by LDS DMA (no registers held), shared by NW
+ * waves: instruction i of a wave writes rows 4 i' .. 4 i' + 3 (i' = wave + NW i), lane l the 16 bytes at LDS chunk
+ * l % 16 of row 4 i' + l / 16, fetched from the row's chunk (l % 16) ^ (row & 15). Rows past the descriptor's range
+ * read zeros. */
+template <int NW = 4>
 __device__ __forceinline__ void tile_dma(const uint16_t *base, long long row0, long long stride, int h, int rows,
                                          uint16_t *lds, int wave, int lane) {
     const Rsrc rs = rows_rsrc(base, row0, stride, h, rows);
 #pragma unroll
-    for (int k = 0; k < FA_BN / 4 / 4; k++) {
-        const int i = wave + 4 * k, r = 4 * i + (lane >> 4), p = lane & 15;
+    for (int k = 0; k < FA_BN / 4 / NW; k++) {
+        const int i = wave + NW * k, r = 4 * i + (lane >> 4), p = lane & 15;
         const int off = (int)((r * stride + ((p ^ (r & 15)) << 3)) * 2);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (LdsVoid *)(lds + i * 4 * HEAD_DIM), 16, off, 0, 0, 0);
     }
@@ -147,7 +149,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
                 float x = sc[j][kt][i] * a.scale_log2;
                 if (MASKED) {
                     const int key = kb0 + kt * 16 + 4 * g + i;
-                    const bool ok = key <= qi && key < seglen && (a.window < 0 || qi - key <= a.window);
+                    const bool ok = (key <= qi) & (key < seglen) & ((a.window < 0) | (qi - key <= a.window));
                     x = ok ? x : -INFINITY;
                 }
                 sv[kt * 4 + i] = x;
@@ -279,7 +281,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(FlashFwd a) {
  * Backward (the reference's _flash_attn_bwd / bwd_bf16dq, model/ops/flash_attn.py:367-391), per segment and head:
  *   P = exp(scale S - lse), dV = P^T dO, dP = dO V^T, dS = P (dP - D) with D_i = dO_i . O_i (the caller's row
  *   statistics: the reference's `rows`, from the o_proj backward epilogue), dQ = scale dS K, dK = scale dS^T Q.
- * Two kernels and no atomics: flash_bwd_dkv_kernel owns 64 keys (a wave 16) and walks the query blocks that see them;
+ * Two kernels and no atomics: flash_bwd_dkv_kernel owns 128 keys (a wave 16) and walks the query blocks that see them;
  * flash_bwd_dq_kernel owns 128 queries (a wave 32, as the forward) and walks their key blocks. S and dP are computed
  * in both (seven 128-deep products per (query, key) pair instead of five), the price of writing dQ once.
  * ------------------------------------------------------------------------------------------------------------- */
@@ -297,8 +299,9 @@ struct FlashBwd {
     long long dq_stride, dk_stride, dv_stride;
 };
 
+/* bitwise, not short-circuit: evaluated per element inside unrolled loops, a branch per term would split the wave */
 __device__ __forceinline__ bool visible(int key, int q, int seglen, int window) {
-    return key <= q && q < seglen && (window < 0 || q - key <= window);
+    return (key <= q) & (q < seglen) & ((window < 0) | (q - key <= window));
 }
 
 __device__ __forceinline__ void store4(uint16_t *p, const f32x4 &v, float mul) {
@@ -306,19 +309,24 @@ __device__ __forceinline__ void store4(uint16_t *p, const f32x4 &v, float mul) {
                                           (uint32_t)f32_to_bf16(v[2] * mul) | ((uint32_t)f32_to_bf16(v[3] * mul) << 16)};
 }
 
-struct DkvStage {
+struct alignas(16) DkvStage {
     uint16_t q[FA_BN * HEAD_DIM], dout[FA_BN * HEAD_DIM];   /* k_lds layout; Q^T and dO^T read transposed */
     float lse2[FA_BN], dd[FA_BN];              /* the block's rows: lse log2(e) (+inf past the segment), D */
 };
 
-/* dK, dV of 64 keys. S = Q K^T and dP = dO V^T with queries as rows (a lane holds one key's column), so P and dS
- * feed dV^T += dO^T P and dK^T += Q^T dS directly as B operands, with dO^T and Q^T read from transposed LDS tiles. */
-__global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dkv_kernel(FlashBwd a) {
+/* dK, dV of 128 keys: eight waves (two a SIMD) of 16 keys share each staged query block, so a CU takes in half the
+ * Q and dO bytes per product that four waves of 16 would. S = Q K^T and dP = dO V^T with queries as rows (a lane holds
+ * one key's column), so P and dS feed dV^T += dO^T P and dK^T += Q^T dS directly as B operands, with dO^T and Q^T read
+ * from transposed LDS tiles. */
+constexpr int DKV_WAVES = 8;
+constexpr int DKV_KEYS = 16 * DKV_WAVES;
+
+__global__ void __launch_bounds__(64 * DKV_WAVES, 2) flash_bwd_dkv_kernel(FlashBwd a) {
     __shared__ DkvStage s0, s1;   /* distinct objects: a read of one never waits for DMA into the other */
     const int seg = blockIdx.y, h = blockIdx.z;
     const long long start = a.cu[seg];
     const int seglen = a.cu[seg + 1] - a.cu[seg];
-    const int k0 = blockIdx.x * FA_BN;          /* the most query blocks first */
+    const int k0 = blockIdx.x * DKV_KEYS;       /* the most query blocks first */
     if (seglen <= 0 || k0 >= seglen) return;
     const int t = threadIdx.x, lane = t & (WAVE - 1), wave = t >> 6, g = lane >> 4, c = lane & 15;
     const int kw = k0 + wave * 16;              /* the wave's first key */
@@ -340,14 +348,14 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dkv_kernel(FlashBwd a
 #pragma unroll
     for (int d = 0; d < 8; d++) dk[d] = dv[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int qhi = a.window >= 0 ? min(seglen - 1, k0 + FA_BN - 1 + a.window) : seglen - 1;
+    const int qhi = a.window >= 0 ? min(seglen - 1, k0 + DKV_KEYS - 1 + a.window) : seglen - 1;
     /* query block qbk + 1 (Q and dO by LDS DMA, the row statistics through registers) is fetched into the other stage
      * while block qbk is computed; the barrier after the compute makes it visible and frees the one just read */
     float rl = INFINITY, rd = 0.0f;
     auto fetch = [&](int qbk, DkvStage &stg) {
         const int qs = qbk * FA_BN, nq = min(FA_BN, seglen - qs);
-        tile_dma(a.q, start + qs, a.q_stride, h, nq, stg.q, wave, lane);
-        tile_dma(a.dout, start + qs, a.do_stride, h, nq, stg.dout, wave, lane);
+        tile_dma<DKV_WAVES>(a.q, start + qs, a.q_stride, h, nq, stg.q, wave, lane);
+        tile_dma<DKV_WAVES>(a.dout, start + qs, a.do_stride, h, nq, stg.dout, wave, lane);
         if (t < FA_BN) {
             const bool ok = t < nq;
             rl = ok ? a.lse[(long long)h * a.lse_stride + start + qs + t] * FA_LOG2E : INFINITY;
@@ -364,38 +372,59 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dkv_kernel(FlashBwd a
         if (!active) return;
         const int qs = qbk * FA_BN;
         const int kw1 = kw + 15, qe = qs + FA_BN - 1;
+        if (kw > qe || (a.window >= 0 && qs - kw1 > a.window)) return;   /* no row of the block sees the wave's keys */
         const bool interior = kw1 <= qs && qe < seglen && kw1 < seglen && (a.window < 0 || qe - kw <= a.window);
-        /* k-step s2 (query tiles 2 s2, 2 s2 + 1): its P and dS halves are formed, then consumed by the dV and dK
-         * products at once; each dv, dk element still adds k-step 0, then 1 */
+        /* the four query tiles' S and dP first (eight independent accumulators, so the products pipeline), then
+         * P and dS, then the dV and dK products of k-step 0 (query tiles 0, 1) and 1 (tiles 2, 3): each dv, dk element
+         * adds k-step 0, then 1 */
+        f32x4 sc[4], dp[4];
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) {
-            bf16x8 pb, db;
+        for (int qt = 0; qt < 4; qt++) sc[qt] = dp[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int qq = 0; qq < 2; qq++) {
-                const int qt = 2 * s2 + qq;
-                f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f}, dp = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int cc = 0; cc < 4; cc++)
 #pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    sc = mfma16x16x32(rows_operand(s.q, qt, cc, g, c), kb_[cc], sc);
-                    dp = mfma16x16x32(rows_operand(s.dout, qt, cc, g, c), vb_[cc], dp);
-                }
+            for (int qt = 0; qt < 4; qt++) {
+                sc[qt] = mfma16x16x32(rows_operand(s.q, qt, cc, g, c), kb_[cc], sc[qt]);
+                dp[qt] = mfma16x16x32(rows_operand(s.dout, qt, cc, g, c), vb_[cc], dp[qt]);
+            }
+        /* the row statistics of the lane's 16 rows: one 16-byte LDS read per tile each, all issued together */
+        float4 l2[4], dd[4];
+#pragma unroll
+        for (int qt = 0; qt < 4; qt++) {
+            l2[qt] = *reinterpret_cast<const float4 *>(&s.lse2[qt * 16 + 4 * g]);
+            dd[qt] = *reinterpret_cast<const float4 *>(&s.dd[qt * 16 + 4 * g]);
+        }
+        bf16x8 pb[2], db[2];
+        /* P and dS of the lane's 16 (key, row) pairs; only a block on the diagonal, the window edge or the segment end
+         * tests each pair (interior is uniform over the wave: one scalar branch) */
+        auto stats = [&](bool masked) {
+#pragma unroll
+            for (int qt = 0; qt < 4; qt++) {
                 /* lane (g, c): key c, query rows qs + 16 qt + 4 g + i */
+                const float lv[4] = {l2[qt].x, l2[qt].y, l2[qt].z, l2[qt].w};
+                const float dv_[4] = {dd[qt].x, dd[qt].y, dd[qt].z, dd[qt].w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = qt * 16 + 4 * g + i;
-                    float p = __builtin_amdgcn_exp2f(sc[i] * a.scale_log2 - s.lse2[r]);
-                    if (!interior && !visible(key, qs + r, seglen, a.window)) p = 0.0f;
-                    const float ds = p * (dp[i] - s.dd[r]);
-                    pb[qq * 4 + i] = (__bf16)p;
-                    db[qq * 4 + i] = (__bf16)ds;
+                    const float e = __builtin_amdgcn_exp2f(sc[qt][i] * a.scale_log2 - lv[i]);
+                    const float p = !masked || visible(key, qs + r, seglen, a.window) ? e : 0.0f;
+                    const float ds = p * (dp[qt][i] - dv_[i]);
+                    pb[qt >> 1][(qt & 1) * 4 + i] = (__bf16)p;
+                    db[qt >> 1][(qt & 1) * 4 + i] = (__bf16)ds;
                 }
             }
+        };
+        if (interior)
+            stats(false);
+        else
+            stats(true);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
             for (int d = 0; d < 8; d++) {
-                dv[d] = mfma16x16x32(tr_operand(s.dout, d, s2, g, c), pb, dv[d]);
-                dk[d] = mfma16x16x32(tr_operand(s.q, d, s2, g, c), db, dk[d]);
+                dv[d] = mfma16x16x32(tr_operand(s.dout, d, s2, g, c), pb[s2], dv[d]);
+                dk[d] = mfma16x16x32(tr_operand(s.q, d, s2, g, c), db[s2], dk[d]);
             }
-        }
     };
     const int qb_lo = k0 / FA_BN, qb_hi = qhi / FA_BN;
     fetch(qb_lo, s0);
@@ -497,16 +526,23 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dq_kernel(FlashBwd a)
                         dp[j] = mfma16x16x32(vop, ob_[j][cc], dp[j]);
                     }
                 }
-                /* lane (g, c): query column c of tile j, keys k0 + 16 kt + 4 g + i */
+                /* lane (g, c): query column c of tile j, keys k0 + 16 kt + 4 g + i; only a block on the diagonal, the
+                 * window edge or the segment end tests each pair (interior is uniform: one scalar branch) */
+                auto pds = [&](bool masked) {
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                    for (int j = 0; j < 2; j++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        float p = __builtin_amdgcn_exp2f(sc[j][i] * a.scale_log2 - lse2[j]);
-                        if (!interior && !visible(k0 + 16 * kt + 4 * g + i, q0 + 16 * j + c, seglen, a.window))
-                            p = 0.0f;
-                        db[j][kk * 4 + i] = (__bf16)(p * (dp[j][i] - dd[j]));
-                    }
+                        for (int i = 0; i < 4; i++) {
+                            const float e = __builtin_amdgcn_exp2f(sc[j][i] * a.scale_log2 - lse2[j]);
+                            const float p =
+                                !masked || visible(k0 + 16 * kt + 4 * g + i, q0 + 16 * j + c, seglen, a.window) ? e : 0.0f;
+                            db[j][kk * 4 + i] = (__bf16)(p * (dp[j][i] - dd[j]));
+                        }
+                };
+                if (interior)
+                    pds(false);
+                else
+                    pds(true);
             }
 #pragma unroll
             for (int d = 0; d < 8; d++) {
@@ -629,9 +665,9 @@ extern "C" int nc_flash_attn_bwd(const void *q, const void *k, const void *v, co
     a.scale = softmax_scale; a.scale_log2 = softmax_scale * FA_LOG2E;
     a.dq = (uint16_t *)dq; a.dk = (uint16_t *)dk; a.dv = (uint16_t *)dv;
     a.dq_stride = dq_stride; a.dk_stride = dk_stride; a.dv_stride = dv_stride;
-    hipLaunchKernelGGL(flash_bwd_dkv_kernel, dim3((unsigned)((max_seqlen + FA_BN - 1) / FA_BN), (unsigned)segments,
-                                                  (unsigned)heads),
-                       dim3(FA_THREADS), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(flash_bwd_dkv_kernel, dim3((unsigned)((max_seqlen + DKV_KEYS - 1) / DKV_KEYS),
+                                                  (unsigned)segments, (unsigned)heads),
+                       dim3(64 * DKV_WAVES), 0, (hipStream_t)stream, a);
     hipLaunchKernelGGL(flash_bwd_dq_kernel, dim3((unsigned)((max_seqlen + FA_BM - 1) / FA_BM), (unsigned)segments,
                                                  (unsigned)heads),
                        dim3(FA_THREADS), 0, (hipStream_t)stream, a);
