@@ -380,13 +380,19 @@ __global__ void __launch_bounds__(64 * DKV_WAVES, 2) flash_bwd_dkv_kernel(FlashB
         f32x4 sc[4], dp[4];
 #pragma unroll
         for (int qt = 0; qt < 4; qt++) sc[qt] = dp[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        /* step st = (cc, qt), cc-major; its Q and dO operands are read one step ahead of the products */
+        bf16x8 qn = rows_operand(s.q, 0, 0, g, c), on = rows_operand(s.dout, 0, 0, g, c);
 #pragma unroll
-        for (int cc = 0; cc < 4; cc++)
-#pragma unroll
-            for (int qt = 0; qt < 4; qt++) {
-                sc[qt] = mfma16x16x32(rows_operand(s.q, qt, cc, g, c), kb_[cc], sc[qt]);
-                dp[qt] = mfma16x16x32(rows_operand(s.dout, qt, cc, g, c), vb_[cc], dp[qt]);
+        for (int st = 0; st < 16; st++) {
+            const int cc = st >> 2, qt = st & 3;
+            const bf16x8 qo = qn, oo = on;
+            if (st + 1 < 16) {
+                qn = rows_operand(s.q, (st + 1) & 3, (st + 1) >> 2, g, c);
+                on = rows_operand(s.dout, (st + 1) & 3, (st + 1) >> 2, g, c);
             }
+            sc[qt] = mfma16x16x32(qo, kb_[cc], sc[qt]);
+            dp[qt] = mfma16x16x32(oo, vb_[cc], dp[qt]);
+        }
         /* the row statistics of the lane's 16 rows: one 16-byte LDS read per tile each, all issued together */
         float4 l2[4], dd[4];
 #pragma unroll
