@@ -424,13 +424,19 @@ __global__ void __launch_bounds__(64 * DKV_WAVES, 2) flash_bwd_dkv_kernel(FlashB
             stats(false);
         else
             stats(true);
+        /* step st = (s2, d); its dO^T and Q^T operands are read one step ahead of the products */
+        bf16x8 vn = tr_operand(s.dout, 0, 0, g, c), kn = tr_operand(s.q, 0, 0, g, c);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-            for (int d = 0; d < 8; d++) {
-                dv[d] = mfma16x16x32(tr_operand(s.dout, d, s2, g, c), pb[s2], dv[d]);
-                dk[d] = mfma16x16x32(tr_operand(s.q, d, s2, g, c), db[s2], dk[d]);
+        for (int st = 0; st < 16; st++) {
+            const int s2 = st >> 3, d = st & 7;
+            const bf16x8 vo = vn, ko = kn;
+            if (st + 1 < 16) {
+                vn = tr_operand(s.dout, (st + 1) & 7, (st + 1) >> 3, g, c);
+                kn = tr_operand(s.q, (st + 1) & 7, (st + 1) >> 3, g, c);
             }
+            dv[d] = mfma16x16x32(vo, pb[s2], dv[d]);
+            dk[d] = mfma16x16x32(ko, db[s2], dk[d]);
+        }
     };
     const int qb_lo = k0 / FA_BN, qb_hi = qhi / FA_BN;
     fetch(qb_lo, s0);
