@@ -1144,6 +1144,10 @@ __device__ __forceinline__ void pf_compute(const AttnArgs &a, int pg0, int npage
     f32x4 sa[NT], sb[NT];
     page_scores<NT>(k0, k1, qb, sa);
     page_scores<NT>(k2, k3, qb, sb);
+    /* every LDS read of the pair (K, V, their scales: 12) is placed before its score products, so the pair waits on
+     * LDS once (measured at c4: 831 -> 842 TFLOP/s against reads placed among the products) */
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * NT, 0);
     pair_step<NT>(a, cur, sa, sb, ksa, ksb, vr, kb, st_w, lane);
 }
 
