@@ -1,15 +1,16 @@
 /*
  * The decode step's GEMMs on gfx950: out[n][r] = epilogue(sum_k x[n][k] w[r][k]) for a step's slots (n < N <= 128) and
  * many weight rows r, bf16 operands, fp32 sums. At N <= 128 a GEMM is bound by moving bytes, not by the matrix cores:
- * every weight byte must come from HBM once, and every workgroup needs the whole activation block x (N x K bf16,
- * 426 KB at config 5), which comes from L2.
+ * every weight byte must come from HBM once, and every workgroup needs the activation rows x of its slots (N x K
+ * bf16 is 426 KB at config 5), which come from L2.
  *
  * A workgroup owns 16 RT weight rows and 16 CT slots (a slot group) over its K range, walked in stages of 128 k. Each
  * stage's operands (x: 16 CT slot rows x 256 bytes; w: 16 RT rows x 256 bytes) go from memory into LDS by LDS DMA, 16
  * lanes per 256-byte row segment: a load instruction that covers long contiguous row pieces runs at about 3x the
  * per-CU rate of one scattering 16-byte pieces over 16 rows (measured: 16 rows x 64 B ~35 GB/s a CU, 8 rows x 128 B
- * 70-90 GB/s, 1 KB contiguous ~110 GB/s). A ring of 3 stage buffers keeps the next two stages in flight, with
- * hand-placed waits and a barrier without a memory fence per stage (a fence would wait for every DMA in flight). What
+ * 70-90 GB/s, 1 KB contiguous ~110 GB/s). A ring of RING stage buffers (3, or 4 for the smallest tile) keeps the next
+ * RING - 1 stages in flight, with hand-placed waits and a barrier without a memory fence per stage (a fence would wait
+ * for every DMA in flight). What
  * bounds it is the CU's ingress (about 40 GB/s a CU with every CU reading): a workgroup takes in its slots' x rows
  * besides its weights, so the host picks (RT, CT) per shape to make the bytes one CU takes in smallest, splitting the
  * slots into groups where x would outweigh the weights (sl_choose). The 4 waves split each stage's four 32-k steps
@@ -29,9 +30,11 @@
  * b ^ (row % 16), so the 16 rows of one operand read fall in distinct banks; each DMA lane fetches the global block
  * that belongs at its LDS position.
  *
- * S = 1: the workgroup applies the epilogue itself (the SG_* kinds of nc_internal.h). S > 1 (long K): each of S
- * K-slices stores fp32 partial sums to part[s][n][r], and slot_gemm_reduce adds them in slice order before the same
- * epilogue.
+ * S = 1: the workgroup applies the epilogue itself (the SG_* kinds of nc_internal.h). S > 1 (long K), or a caller that
+ * finishes the sums itself (slot_gemm_partials): each of S K-slices stores fp32 partial sums to part[s][n][r], and
+ * slot_gemm_reduce adds them in slice order before the same epilogue. With ssq (one slice), the residual epilogue also
+ * writes each 16-row tile's sum of squares of its sums, and the ReLU^2 epilogue takes each slot's rstd from them, so
+ * the MLP's rstd needs no kernel of its own.
  *
  * Reference: the slot GEMM and its epilogues, model/kernels/decode.cu:133-168, 295-359.
  */
