@@ -476,12 +476,22 @@ __global__ void __launch_bounds__(CHOICE_THREADS) choose_kernel(ChoiceArgs c) {
             best = key > best ? key : best;
         }
     } else {
-        for (int r = tid; r < c.vocab; r += CHOICE_THREADS) {
-            if (!allowed(r)) continue;
-            const float score = T > 0.0f ? capped(r) / T + gumbel(seed, gen, r) : s[r];
-            const unsigned long long key = choice_key(score, r);
-            best = key > best ? key : best;
-            if (r != c.lazy) alt = key > alt ? key : alt;
+        /* four logits a thread a step by 16-byte reads, four reads in flight (the vocab is a multiple of 32); the result
+         * is a maximum over keys unique per row, so the visiting order does not matter */
+        const float4 *s4 = reinterpret_cast<const float4 *>(s);
+#pragma unroll 4
+        for (int q = tid; q < c.vocab / 4; q += CHOICE_THREADS) {
+            const float4 v4 = s4[q];
+            const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int r = 4 * q + e;
+                if (!allowed(r)) continue;
+                const float score = T > 0.0f ? c.softcap * tanhf(v[e] / c.softcap) / T + gumbel(seed, gen, r) : v[e];
+                const unsigned long long key = choice_key(score, r);
+                best = key > best ? key : best;
+                if (r != c.lazy) alt = key > alt ? key : alt;
+            }
         }
     }
     best = block_max_key(best, kscratch);
