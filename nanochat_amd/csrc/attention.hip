@@ -506,7 +506,7 @@ __device__ __forceinline__ void attend_pages_tab(const AttnArgs &a, const TabReg
  * nothing but the sequence's own length, whatever the rest of the batch holds, so a sequence's sums (and its output
  * bits) depend only on its own query, keys and length. */
 constexpr int SPLIT_PAGES = 64;
-constexpr int MIN_TAIL = 16;
+constexpr int MIN_TAIL = 4;
 static_assert(SPLIT_PAGES + MIN_TAIL - 1 <= 2 * WAVE, "a chunk's block-table entries are staged in two lanes' worth");
 
 /* Key range [begin, p] of a sequence of L keys and its logical pages [pg0, pg0 + npages); npages = 0 for an

@@ -1,5 +1,5 @@
 """CPU replay of decode_kernel's work split (nanochat_amd/csrc/attention.hip: chunks cut at multiples of 64 pages, a last
-piece under 16 pages joined to the one before it (checked against a from-scratch cut of the page range); the
+piece under 4 pages joined to the one before it (checked against a from-scratch cut of the page range); the
 per-work-group prefixes over sequences of full and partial chunks; full chunks numbered first, then partial ones;
 item k to work-group k % G, wave (k / G) % 4; partial slot = the chunk's unit-order index; the unit's chunks counted
 in arrived[u], the last to finish merging slots slot - j .. + nch) for many shapes: every (unit, page) is attended
@@ -23,12 +23,12 @@ def unit_pages(L, window, max_len):
     return p // PAGE + 1 - begin // PAGE, begin // PAGE
 
 
-MIN_TAIL = 16
+MIN_TAIL = 4
 
 
 def chunk_ranges(pg0, n):
     """Logical page ranges of a unit's chunks, from first principles: cut [pg0, pg0 + n) at every multiple of 64 pages,
-    then join a last piece shorter than 16 pages to the one before it."""
+    then join a last piece shorter than 4 pages to the one before it."""
     if n <= 0:
         return []
     e = pg0 + n
