@@ -476,6 +476,55 @@ def bench_model(args, w, cpu_slots=16):
     return result
 
 
+def bench_ceiling(args):
+    """The read-only ceiling of a decode workload's step: its algorithmic bytes (attention and append) read as
+    2 KiB pages by nc_debug_read_pages, in page order and in a seeded random order (the block table's kind), at
+    two grid sizes; args.steps launches timed between events on the launch stream after args.warmup."""
+    import torch
+
+    from nanochat_amd import native
+    from nanochat_amd.workloads import DECODE, decode_ctx_lens
+
+    w = DECODE[args.workload]
+    ctx = decode_ctx_lens(w, torch.Generator().manual_seed(0))
+    step_bytes = attention_bytes(ctx.tolist(), w.q_heads, w.kv_heads) + append_bytes(w.batch, w.kv_heads)
+    pages = step_bytes // 2048
+    dev = torch.device("cuda:0")
+    src = torch.randint(0, 256, (pages * 2048,), dtype=torch.uint8, device=dev)
+    orders = {"page order": None,
+              "random order": torch.randperm(pages, generator=torch.Generator().manual_seed(1)).to(torch.int32).to(dev)}
+    lib = native.hip_library()
+    rows = []
+    for name, order in orders.items():
+        for grid in (1024, 2048):
+            sink = torch.empty(grid * 256, dtype=torch.int32, device=dev)
+
+            def launch():
+                rc = lib.nc_debug_read_pages(native.pointer(src), src.numel(), native.pointer(order) if order is not None
+                                             else None, pages, grid, native.pointer(sink), native.stream())
+                if rc:
+                    raise RuntimeError(f"nc_debug_read_pages: {lib.nc_status_string(rc).decode()}")
+
+            for _ in range(args.warmup):
+                launch()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(args.steps):
+                launch()
+            stop.record()
+            torch.cuda.synchronize()
+            us = start.elapsed_time(stop) * 1e3 / args.steps
+            rows.append({"order": name, "grid": grid, "us": round(us, 2),
+                         "tb_per_s": round(pages * 2048 / us / 1e6, 3)})
+    best = max(r["tb_per_s"] for r in rows if r["order"] == "random order")
+    return {"metric": "read-only HBM ceiling of the decode step's bytes", "value": best, "unit": "TB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "data": "synthetic (random bytes)", "frac_of_8tbs": round(best / 8.0, 4),
+            "config": {"workload": args.workload, "bytes": pages * 2048, "pages": pages,
+                       "kernel": "read_pages_kernel (nc_debug_read_pages)"}, "runs": rows}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -487,6 +536,8 @@ def main():
                     help="CPU baseline: 0 skips it; decode and prefill time the whole step, c5 this many slots (<= 16)")
     ap.add_argument("--two-launch", action="store_true",
                     help="decode: the step as nc_qk_norm_rope_append_fp8 + nc_decode_attn_fp8 (the same bits)")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="decode workloads: time a read-only pass over the step's bytes (the memory system's ceiling)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="decode workloads: skip the config-5 end-to-end decode tokens/s part of the metric")
     args = ap.parse_args()
@@ -515,6 +566,9 @@ def main():
         return
     if args.workload in PREFILL:
         print(json.dumps(bench_prefill(args, PREFILL[args.workload])), flush=True)
+        return
+    if args.ceiling:
+        print(json.dumps(bench_ceiling(args)), flush=True)
         return
     if args.workload in MODELS:
         print(json.dumps(bench_model(args, MODELS[args.workload], cpu_slots=min(args.cpu_seqs, 16))), flush=True)

@@ -225,6 +225,16 @@ int nc_prefill_attn_fp8(const void *q, const void *k_pages, const void *v_pages,
                         const int32_t *start_pos, int B, int T, int Hq, int Hkv, int window, float sm_scale,
                         void *out, void *stream);
 
+/*
+ * Measurement only; no counterpart in the reference. Reads n pages of 2 KiB (one (page, head) of K or V codes) from
+ * src (src_bytes, a multiple of 2,048), page order[i] as the i-th (order NULL: page i; an entry outside the buffer
+ * reads page 0), with `grid` workgroups of 256 threads, and writes one checksum word per thread to sink
+ * (grid x 256 uint32: their XOR is the XOR of every dword read). Its duration is the read-only ceiling of the decode
+ * step's page stream. Returns 0, NC_ERR_NULL or NC_ERR_SHAPE (grid outside [1, 65535]).
+ */
+int nc_debug_read_pages(const void *src, long long src_bytes, const int32_t *order, int n, int grid, uint32_t *sink,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,7 @@
  * Reference semantics: model/kernels/decode.cu:567-675 (k_attn: keys [max(p - window, 0), p], scale
  * 1/sqrt(128), fp32 softmax) and 859-863 (prefill rows appended before any attends).
  */
+#include <limits.h>
 #include <math.h>
 
 #include <mutex>
@@ -1520,4 +1521,48 @@ extern "C" int nc_decode_attn_fp8_noalloc(const void *q, const void *k_pages, co
     return launch_decode(q, k_pages, v_pages, kv_scale, block_table, max_pages, num_pages, seq_lens, max_seq_len, B,
                          Hq, Hkv, window, sm_scale, workers, out, ws, NC_DECODE_SCRATCH_BYTES, nullptr,
                          (hipStream_t)stream);
+}
+
+/*
+ * The read-only ceiling of the decode step's access pattern: a kernel that only reads 2 KiB pages (the size of one
+ * (page, head) of K or V codes) in a given order and folds them into a checksum. Each wave takes pages w, w + waves,
+ * ... two at a time, each page as two 16-byte loads a lane, non-temporal like the decode stream. It does no
+ * arithmetic beyond the XOR that keeps the loads, so its rate is what the memory system gives for that order of
+ * pages; the XOR of every sink word is the XOR of every dword read. Entry i of `order` (NULL: i) names the page read i-th; an entry outside
+ * [0, src_pages) reads page 0.
+ */
+__global__ void __launch_bounds__(256) read_pages_kernel(const u32x4 *src, int src_pages, const int32_t *order, int n,
+                                                         uint32_t *sink) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int waves = gridDim.x * WAVES, w = blockIdx.x * WAVES + (threadIdx.x >> 6);
+    uint32_t acc = 0;
+    for (int c0 = 2 * w; c0 < n; c0 += 2 * waves) {
+        u32x4 v[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int c = c0 + u;
+            const bool live = c < n;
+            int p = live ? (order ? order[c] : c) : 0;
+            p = (unsigned)p < (unsigned)src_pages ? p : 0;
+            const u32x4 *b = src + (size_t)p * (PAGE_BYTES / 16);
+            v[u][0] = live ? __builtin_nontemporal_load(b + lane) : u32x4{0u, 0u, 0u, 0u};
+            v[u][1] = live ? __builtin_nontemporal_load(b + WAVE + lane) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) acc ^= v[u][h][0] ^ v[u][h][1] ^ v[u][h][2] ^ v[u][h][3];
+    }
+    sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
+extern "C" int nc_debug_read_pages(const void *src, long long src_bytes, const int32_t *order, int n, int grid,
+                                   uint32_t *sink, void *stream) {
+    if (!src || !sink) return NC_ERR_NULL;
+    if (src_bytes < PAGE_BYTES || src_bytes % PAGE_BYTES || src_bytes / PAGE_BYTES > INT_MAX || n < 0 || grid <= 0 ||
+        grid > 65535)
+        return NC_ERR_SHAPE;
+    hipLaunchKernelGGL(read_pages_kernel, dim3(grid), dim3(WAVES * WAVE), 0, (hipStream_t)stream,
+                       (const u32x4 *)src, (int)(src_bytes / PAGE_BYTES), order, n, sink);
+    return (int)hipGetLastError();
 }

@@ -96,6 +96,7 @@ SIGNATURES = {
                                     c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p], c_int),
     "nc_prefill_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
                              c_int, c_int, c_int, c_float, c_void_p, c_void_p], c_int),
+    "nc_debug_read_pages": ([c_void_p, c_longlong, c_void_p, c_int, c_int, c_void_p, c_void_p], c_int),
     "ve_forward": ([c_void_p, c_void_p, c_longlong] + [c_void_p] * 5 + [c_longlong, c_void_p], None),
     "ve_backward": ([c_void_p, c_longlong] + [c_void_p] * 8 + [c_longlong, c_void_p], None),
     "nc_ve_forward": ([c_void_p, c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_void_p, c_void_p, c_void_p,

@@ -74,14 +74,18 @@ def _outliers(gen: torch.Generator, x: torch.Tensor, fraction: float) -> torch.T
     return torch.where(mask, 8.0 * torch.sign(x.float()), x.float()).to(torch.bfloat16)
 
 
+def decode_ctx_lens(w: DecodeWorkload, gen: torch.Generator) -> torch.Tensor:
+    """The sequences' cached lengths: U[ctx_min, ctx] from gen's next draw, or ctx for every sequence."""
+    if w.ctx_min:
+        return torch.randint(w.ctx_min, w.ctx + 1, (w.batch,), generator=gen, dtype=torch.int64).to(torch.int32)
+    return torch.full((w.batch,), w.ctx, dtype=torch.int32)
+
+
 def decode_inputs(w: DecodeWorkload, seed: int = 0) -> dict:
     """Host tensors of one decode step: the cache contents before it, the new token, the block table."""
     gen = torch.Generator().manual_seed(seed)
     B, D = w.batch, HEAD_DIM
-    if w.ctx_min:
-        ctx_lens = torch.randint(w.ctx_min, w.ctx + 1, (B,), generator=gen, dtype=torch.int64).to(torch.int32)
-    else:
-        ctx_lens = torch.full((B,), w.ctx, dtype=torch.int32)
+    ctx_lens = decode_ctx_lens(w, gen)
     q = _bf16_randn(gen, B, w.q_heads, D)
     k_cache = _bf16_randn(gen, B, w.ctx, w.kv_heads, D)
     v_cache = _bf16_randn(gen, B, w.ctx, w.kv_heads, D)

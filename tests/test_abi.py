@@ -34,6 +34,13 @@ def test_status_strings(lib):
     assert b"workspace" in lib.nc_status_string(-3)
 
 
+def test_read_pages_rejects_bad_arguments(lib):
+    assert lib.nc_debug_read_pages(None, 2048, None, 1, 1, DUMMY, None) == -1
+    assert lib.nc_debug_read_pages(DUMMY, 2048, None, 1, 1, None, None) == -1
+    for size, n, grid in ((2047, 1, 1), (3000, 1, 1), (0, 1, 1), (2048, -1, 1), (2048, 1, 0), (2048, 1, 65536)):
+        assert lib.nc_debug_read_pages(DUMMY, size, None, n, grid, DUMMY, None) == -2, (size, n, grid)
+
+
 def test_null_pointers_rejected(lib):
     assert lib.nc_kv_append_fp8(None, None, 512, 1, 1, 4, None, None, None, 1, None, None, None, 1, None) == -1
     assert lib.nc_decode_attn_fp8(None, *([DUMMY] * 4), 1, 1, DUMMY, 16, 1, 4, 4, -1, 0.1, 0, DUMMY, None, 0,
