@@ -340,6 +340,40 @@ __device__ __forceinline__ void pair_step(const AttnArgs &a, const PairAddr &cur
         pair_update<NT, true>(a, cur, sa, sb, ksa, ksb, vr, kb, st, lane);
 }
 
+/* pair_step with the scores made inside each branch from the pair's K operands (k0, k1: page a; k2, k3: page b), so
+ * the score MFMAs share a scheduling block with the exponentials: page a's products first, then page b's, one at a
+ * time between groups of page a's softmax instructions, which do not wait for them (c4: 830-843 -> 868-875 TFLOP/s
+ * against all eight products issued before the branch). */
+template <int NT, bool MASKED>
+__device__ __forceinline__ void pair_update_k(const AttnArgs &a, const PairAddr &p, const uint4 &k0, const uint4 &k1,
+                                              const uint4 &k2, const uint4 &k3, const QOp (&qb)[NT],
+                                              const float4 &ksa, const float4 &ksb, PairRegs &v,
+                                              const KeyBounds<NT> &kb, WaveState<NT> &st, int lane) {
+    f32x4 sa[NT], sb[NT];
+    page_scores<NT>(k0, k1, qb, sa);
+    page_scores<NT>(k2, k3, qb, sb);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * NT, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * NT; i++) {   /* groups of 2 to 10 VALU instructions measured the same */
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+    pair_update<NT, MASKED>(a, p, sa, sb, ksa, ksb, v, kb, st, lane);
+}
+
+template <int NT>
+__device__ __forceinline__ void pair_step_k(const AttnArgs &a, const PairAddr &cur, const uint4 &k0, const uint4 &k1,
+                                            const uint4 &k2, const uint4 &k3, const QOp (&qb)[NT], const float4 &ksa,
+                                            const float4 &ksb, PairRegs &vr, const KeyBounds<NT> &kb,
+                                            WaveState<NT> &st, int lane) {
+    const bool interior = cur.has_b && cur.lpa * PAGE >= kb.full_lo && cur.lpa * PAGE + 2 * PAGE - 1 <= kb.full_hi &&
+                          cur.lpa * PAGE + 2 * PAGE - 1 <= kb.written_hi;
+    if (interior)
+        pair_update_k<NT, false>(a, cur, k0, k1, k2, k3, qb, ksa, ksb, vr, kb, st, lane);
+    else
+        pair_update_k<NT, true>(a, cur, k0, k1, k2, k3, qb, ksa, ksb, vr, kb, st, lane);
+}
+
 /*
  * A wave's pass over the page pairs lpa0, lpa0 + step, ... below `end` (logical pages of KV head kvh through
  * block-table row bt). PREFETCH: the next pair's K loads are issued as soon as this pair's scores are computed,
@@ -1142,14 +1176,7 @@ __device__ __forceinline__ void pf_compute(const AttnArgs &a, int pg0, int npage
     vr.a0 = v4[lane]; vr.a1 = v4[64 + lane]; vr.b0 = v4[128 + lane]; vr.b1 = v4[192 + lane];
     vr.sa = *reinterpret_cast<const float4 *>(sc + PAGE + g * 4);
     vr.sb = *reinterpret_cast<const float4 *>(sc + 3 * PAGE + g * 4);
-    f32x4 sa[NT], sb[NT];
-    page_scores<NT>(k0, k1, qb, sa);
-    page_scores<NT>(k2, k3, qb, sb);
-    /* every LDS read of the pair (K, V, their scales: 12) is placed before its score products, so the pair waits on
-     * LDS once (measured at c4: 831 -> 842 TFLOP/s against reads placed among the products) */
-    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 4 * NT, 0);
-    pair_step<NT>(a, cur, sa, sb, ksa, ksb, vr, kb, st_w, lane);
+    pair_step_k<NT>(a, cur, k0, k1, k2, k3, qb, ksa, ksb, vr, kb, st_w, lane);
 }
 
 /* Grid and columns as prefill_kernel. */
