@@ -128,6 +128,9 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
     for (int j = 0; j < 2; j++)
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) sc[j][kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    /* raised priority while the scores issue: the SIMD's other wave runs its softmax between them (fa forward
+     * 464 -> 471.5 TFLOP/s; the same around the PV products, or around the backward's S / dP products, was slower) */
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kt = 0; kt < 4; kt++) {
 #pragma unroll
@@ -137,6 +140,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
             for (int j = 0; j < 2; j++) sc[j][kt] = mfma16x16x32(kop, qb[j][cc], sc[j][kt]);
         }
     }
+    __builtin_amdgcn_s_setprio(0);
     bf16x8 pv[2][2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
