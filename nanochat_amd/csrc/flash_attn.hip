@@ -131,15 +131,15 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
     /* raised priority while the scores issue: the SIMD's other wave runs its softmax between them (fa forward
      * 464 -> 471.5 TFLOP/s; the same around the PV products, or around the backward's S / dP products, was slower) */
     __builtin_amdgcn_s_setprio(1);
+    /* tile 0's scores, then tile 1's (K operands read from LDS once per tile), so tile 1's products can issue among
+     * tile 0's scale, mask and max instructions (the groups below): 471.8 -> 476.6 TFLOP/s; without the groups the
+     * compiler issued them all first and the forward fell to 343.6 */
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++) {
+    for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int cc = 0; cc < 4; cc++) {
-            const bf16x8 kop = rows_operand(s.k, kt, cc, g, c);
+        for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) sc[j][kt] = mfma16x16x32(kop, qb[j][cc], sc[j][kt]);
-        }
-    }
+            for (int cc = 0; cc < 4; cc++) sc[j][kt] = mfma16x16x32(rows_operand(s.k, kt, cc, g, c), qb[j][cc], sc[j][kt]);
     __builtin_amdgcn_s_setprio(0);
     bf16x8 pv[2][2];
 #pragma unroll
@@ -162,6 +162,14 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
 #pragma unroll
         for (int i = 1; i < 16; i++) mt = fmaxf(mt, sv[i]);
         mt = pair_max32(pair_max16(mt));
+        if (j == 0) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+        }
         const float mnew = fmaxf(st.m[j], mt);
         if (__any(mnew > st.m[j] + FA_RESCALE)) {
             const float alpha = mnew == st.m[j] ? 1.0f : __builtin_amdgcn_exp2f(st.m[j] - mnew);
