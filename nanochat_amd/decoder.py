@@ -2,7 +2,8 @@
 benchmark: the fp8 paged-cache decoder behind the reference's dec_* ABI (model/kernels/decode.cu:904-1131).
 
 The reference's own host class, NativeDecoder (inference/decoder.py:123-324), binds the same library unchanged through
-`hip_library("decode")`; this module is not a copy of it. It has two layers:
+`hip_library("decode")` with the argtypes of `nanochat_amd/native.py`; this module is not a copy of it. It has two
+layers:
 
 - `DecoderRuntime` holds one decoder handle and exposes the ABI with no scheduling policy: put a prompt in a slot
   (shared from the prompt store when stored, else queued), run the queued prefill, choose the active and masked slots,
