@@ -183,8 +183,8 @@ int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, 
  * token sits at position p = seq_lens[b] - 1 (seq_lens <= 0: inactive, nothing appended, output zeros); its row of
  * qkv (bf16 [B][(Hq + 2 Hkv) 128] at token_stride elements) is normed, rotated (q_gain, k_gain, cos, sin as in
  * nc_qk_norm_rope_append_fp8; rope_len >= max_seq_len) and, when ve is not NULL, its value row gets the value
- * embedding of token ve_tokens[b] (ve bf16 [vocab][C], ve_gate fp32 [Hkv][C], ve_h bf16 [B][C] the layer's normed
- * input; v += 2 sigmoid(ve_gate[kvh] . h) ve[token][kvh 128 ..]); k and v are quantized into the cache and q goes to
+ * embedding of token ve_tokens[b] (ve bf16 [ve_rows][C], ve_gate fp32 [Hkv][C], ve_h bf16 [B][C] the layer's normed
+ * input; v += 2 sigmoid(ve_gate[kvh] . h) ve[token][kvh 128 ..]; a token outside [0, ve_rows) mixes nothing); k and v are quantized into the cache and q goes to
  * q_out (bf16 [B][Hq][128]) unless q_out is NULL; then the query attends as in nc_decode_attn_fp8. A sequence longer
  * than max_seq_len gets NaN and no append. The page receiving a sequence's token must not appear in another
  * sequence's block-table row (the work item that streams that page takes the token from registers while it stores
@@ -193,7 +193,7 @@ int nc_decode_attn_fp8(const void *q, const void *k_pages, const void *v_pages, 
 int nc_decode_step_fp8(const void *qkv, long long token_stride, int B, int Hq, int Hkv, const int32_t *seq_lens,
                        const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
                        void *q_out, const void *ve_h, const void *ve, const float *ve_gate, const int32_t *ve_tokens,
-                       int C, const int32_t *block_table, int max_pages, void *k_pages, void *v_pages, float *kv_scale,
+                       int C, int ve_rows, const int32_t *block_table, int max_pages, void *k_pages, void *v_pages, float *kv_scale,
                        int num_pages, int max_seq_len, int window, float sm_scale, int workers, void *out,
                        void *workspace, size_t workspace_bytes, void *stream);
 

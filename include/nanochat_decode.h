@@ -121,6 +121,14 @@ int dec_debug_slot_gemm_tile(int R, int K, int N, int slices);
 int dec_debug_slot_gemm_ssq(int epi, const void *w, int R, int K, const void *x, int N, void *out, const void *res,
                             float *ssq, void *stream);
 
+/* The nucleus threshold of choose_kernel alone: for each of `rows` rows of probabilities e (fp32 [rows][vocab],
+ * device; e = exp(z / T - max z / T) in [0, 1], 0 for rows not allowed) and its top_p (fp32 [rows], device), the
+ * IEEE bit pattern of e*, the least e for which the rows with e' <= e* weigh more than (1 - top_p) of the total,
+ * with each row weighing the integer round(e 2^38). Rows with e >= e* (and weight > 0) form the nucleus. cut:
+ * uint32 [rows], device. Returns 0, a hipError_t, or -2 for a shape it does not take (vocab < 2^25).
+ * Stream-ordered. */
+int dec_debug_nucleus_cut(const float *e, int rows, int vocab, const float *top_p, uint32_t *cut, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

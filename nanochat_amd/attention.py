@@ -11,6 +11,8 @@
 
 Every function launches on the current torch stream and requires device tensors: there is no CPU path.
 """
+from collections import OrderedDict
+
 import torch
 
 from .config import HEAD_DIM
@@ -52,19 +54,26 @@ def qk_norm_rope_append(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache
     return q_out
 
 
-_WORKSPACES: dict = {}
+_WORKSPACES: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_WORKSPACE_STREAMS = 8
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A decode workspace of at least nbytes for this device and its current stream, kept for reuse. It starts
     zero-filled (its arrival counts must be zero before the first call; every call leaves them zero). Keyed by
-    stream: calls on two streams never share partials or counts, and a workspace that grows is only released to the
-    caching allocator, which keeps it from other streams until its stream's work is done."""
+    stream, so calls on two streams never share partials or counts. At most _WORKSPACE_STREAMS (device, stream)
+    entries are kept, the least recently used dropped first; a caller that cycles through more streams than that, or
+    creates streams per request, should pass a workspace of its own. A dropped or outgrown workspace goes back to the
+    caching allocator's pool of the stream it was allocated on, and that pool keeps the block until the cache is
+    emptied (torch.cuda.empty_cache). A stream whose handle is reused after the stream is destroyed picks up the old
+    entry, which is safe: its counts are zero whenever no call is in flight."""
     key = (device, torch.cuda.current_stream(device).cuda_stream)
-    ws = _WORKSPACES.get(key)
+    ws = _WORKSPACES.pop(key, None)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = ws
+    _WORKSPACES[key] = ws
+    while len(_WORKSPACES) > _WORKSPACE_STREAMS:
+        _WORKSPACES.popitem(last=False)
     return ws
 
 
@@ -87,12 +96,18 @@ def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Te
     if D != HEAD_DIM:
         raise ValueError(f"q must be [B, Hq, {HEAD_DIM}]")
     _require(seq_lens, "seq_lens", torch.int32)
+    if seq_lens.numel() < B:
+        raise ValueError(f"seq_lens holds {seq_lens.numel()} entries for {B} sequences")
     cache.check_table(block_table)
+    if block_table.size(0) < B:
+        raise ValueError(f"block_table has {block_table.size(0)} rows for {B} sequences")
     if sm_scale is None:
         sm_scale = HEAD_DIM ** -0.5
     if out is None:
         out = torch.empty_like(q)
     _require(out, "out", torch.bfloat16)
+    if out.numel() != q.numel():
+        raise ValueError(f"out must hold [{B}, {Hq}, {HEAD_DIM}]")
     lib = hip_library()
     need = lib.nc_decode_workspace_bytes(B, Hq, cache.num_kv_heads, max_seq_len, window)
     if need == 0:
@@ -116,8 +131,9 @@ def decode_step(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache, block_
     at position seq_lens[b] - 1; its q, k are normed and rotated, k and v quantized into `cache`, and q attends as in
     decode_attention -> out bf16 [B, Hq, 128]. The same bits as qk_norm_rope_append (start_pos = seq_lens - 1)
     followed by decode_attention. q_out (bf16 [B, Hq, 128]) receives the rotated queries when given. ve: None or
-    (h bf16 [B, C], table bf16 [vocab, C], gate fp32 [Hkv, C], tokens int32 [B]) for value embeddings. The page
-    receiving a sequence's token must not be in another sequence's row of block_table."""
+    (h bf16 [B, C], table bf16 [vocab, C], gate fp32 [Hkv, C], tokens int32 [B]) for value embeddings; a token
+    outside [0, vocab) mixes nothing. The page receiving a sequence's token must not be in another sequence's row of
+    block_table."""
     if qkv.dim() == 3:
         qkv = qkv.view(qkv.size(0), qkv.size(2)) if qkv.size(1) == 1 else qkv
     if qkv.dim() != 2:
@@ -133,18 +149,24 @@ def decode_step(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache, block_
     if cos.shape != sin.shape or cos.dim() != 2 or cos.size(1) != HEAD_DIM // 2:
         raise ValueError("cos, sin must be [positions, 64]")
     _require(seq_lens, "seq_lens", torch.int32)
+    if seq_lens.numel() < B:
+        raise ValueError(f"seq_lens holds {seq_lens.numel()} entries for {B} sequences")
     cache.check_table(block_table)
+    if block_table.size(0) < B:
+        raise ValueError(f"block_table has {block_table.size(0)} rows for {B} sequences")
     if sm_scale is None:
         sm_scale = HEAD_DIM ** -0.5
     if out is None:
         out = torch.empty(B, num_q_heads, HEAD_DIM, dtype=torch.bfloat16, device=qkv.device)
     _require(out, "out", torch.bfloat16)
+    if out.numel() != B * num_q_heads * HEAD_DIM:
+        raise ValueError(f"out must hold [{B}, {num_q_heads}, {HEAD_DIM}]")
     if q_out is not None:
         _require(q_out, "q_out", torch.bfloat16)
         if q_out.numel() != B * num_q_heads * HEAD_DIM:
             raise ValueError(f"q_out must hold [{B}, {num_q_heads}, {HEAD_DIM}]")
     ve_h = ve_table = ve_gate = ve_tokens = None
-    C = 0
+    C = rows = 0
     if ve is not None:
         ve_h, ve_table, ve_gate, ve_tokens = ve
         _require(ve_h, "ve h", torch.bfloat16)
@@ -152,6 +174,15 @@ def decode_step(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache, block_
         _require(ve_gate, "ve gate", torch.float32)
         _require(ve_tokens, "ve tokens", torch.int32)
         C = ve_h.size(-1)
+        rows = ve_table.size(0)
+        if ve_h.dim() != 2 or ve_h.size(0) < B:
+            raise ValueError(f"ve h must be [>= {B}, C]")
+        if ve_table.dim() != 2 or ve_table.size(1) != C:
+            raise ValueError(f"ve table must be [vocab, {C}]")
+        if tuple(ve_gate.shape) != (Hkv, C):
+            raise ValueError(f"ve gate must be [{Hkv}, {C}]")
+        if ve_tokens.numel() < B:
+            raise ValueError(f"ve tokens holds {ve_tokens.numel()} entries for {B} sequences")
     lib = hip_library()
     need = lib.nc_decode_workspace_bytes(B, num_q_heads, Hkv, max_seq_len, window)
     if need == 0:
@@ -162,7 +193,7 @@ def decode_step(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache, block_
         pointer(qkv), qkv.stride(0), B, num_q_heads, Hkv, pointer(seq_lens), pointer(q_gain), pointer(k_gain),
         pointer(cos), pointer(sin), cos.size(0), pointer(q_out) if q_out is not None else None,
         pointer(ve_h) if ve is not None else None, pointer(ve_table) if ve is not None else None,
-        pointer(ve_gate) if ve is not None else None, pointer(ve_tokens) if ve is not None else None, C,
+        pointer(ve_gate) if ve is not None else None, pointer(ve_tokens) if ve is not None else None, C, rows,
         pointer(block_table), block_table.size(1), pointer(cache.k_pages), pointer(cache.v_pages),
         pointer(cache.kv_scale), cache.num_pages, max_seq_len, window, sm_scale, workers, pointer(out),
         pointer(workspace), workspace.numel() * workspace.element_size(), stream()))

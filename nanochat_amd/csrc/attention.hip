@@ -706,9 +706,12 @@ __device__ __forceinline__ void step_rows(const AttnArgs &a, const StepArgs &s, 
     norm_rope_pair(bf16_to_f32(f.kx1), bf16_to_f32(f.kx2), f.kg1, f.kg2, f.cr, f.sr, y1, y2);
     const float k1 = bf16_to_f32(f32_to_bf16(y1)), k2 = bf16_to_f32(f32_to_bf16(y2));
     float v1 = bf16_to_f32(f.vx1), v2 = bf16_to_f32(f.vx2);
-    if (s.ve)
-        ve_mix_pair(s.ve_h + (long long)b * s.C, s.ve_gate + (long long)kvh * s.C, s.C,
-                    s.ve + (long long)s.ve_tokens[b] * s.C + kvh * HEAD_DIM, lane, v1, v2);
+    if (s.ve) {
+        const int token = s.ve_tokens[b];
+        if ((unsigned)token < (unsigned)s.ve_rows)
+            ve_mix_pair(s.ve_h + (long long)b * s.C, s.ve_gate + (long long)kvh * s.C, s.C,
+                        s.ve + (long long)token * s.C + kvh * HEAD_DIM, lane, v1, v2);
+    }
     uint32_t kc1, kc2, vc1, vc2;
     const int slot = p % PAGE;
     const float ks = quantize_pair(k1, k2, kc1, kc2);
@@ -1489,7 +1492,8 @@ extern "C" int nc_decode_attn_fp8(const void *q, const void *k_pages, const void
 extern "C" int nc_decode_step_fp8(const void *qkv, long long token_stride, int B, int Hq, int Hkv,
                                   const int32_t *seq_lens, const float *q_gain, const float *k_gain, const float *cos,
                                   const float *sin, int rope_len, void *q_out, const void *ve_h, const void *ve,
-                                  const float *ve_gate, const int32_t *ve_tokens, int C, const int32_t *block_table,
+                                  const float *ve_gate, const int32_t *ve_tokens, int C, int ve_rows,
+                                  const int32_t *block_table,
                                   int max_pages, void *k_pages, void *v_pages, float *kv_scale, int num_pages,
                                   int max_seq_len, int window, float sm_scale, int workers, void *out, void *workspace,
                                   size_t workspace_bytes, void *stream) {
@@ -1498,7 +1502,7 @@ extern "C" int nc_decode_step_fp8(const void *qkv, long long token_stride, int B
         return NC_ERR_NULL;
     if (!decode_shape_ok(B, Hq, Hkv, max_seq_len, window) || max_pages <= 0 || num_pages <= 0 ||
         (long long)max_seq_len > (long long)max_pages * PAGE || workers < 0 || rope_len < max_seq_len ||
-        token_stride < (long long)(Hq + 2 * Hkv) * HEAD_DIM || (ve && C < Hkv * HEAD_DIM))
+        token_stride < (long long)(Hq + 2 * Hkv) * HEAD_DIM || (ve && (C < Hkv * HEAD_DIM || ve_rows <= 0)))
         return NC_ERR_SHAPE;
     if (!workspace_fits(workspace_bytes, B, Hq, Hkv, item_bound(B, Hkv, max_seq_len, window)))
         return NC_ERR_WORKSPACE;
@@ -1509,6 +1513,7 @@ extern "C" int nc_decode_step_fp8(const void *qkv, long long token_stride, int B
     st.q_out = (uint16_t *)q_out;
     st.ve_h = (const uint16_t *)ve_h; st.ve = (const uint16_t *)ve; st.ve_gate = ve_gate; st.ve_tokens = ve_tokens;
     st.C = C;
+    st.ve_rows = ve_rows;
     st.k_pages = (uint8_t *)k_pages; st.v_pages = (uint8_t *)v_pages; st.kv_scale = kv_scale;
     return launch_decode(nullptr, k_pages, v_pages, kv_scale, block_table, max_pages, num_pages, seq_lens, max_seq_len,
                          B, Hq, Hkv, window, sm_scale, workers, out, workspace, workspace_bytes, &st,

@@ -393,17 +393,7 @@ struct ChoiceArgs {
     int vocab, lazy;
 };
 
-/* Fixed-order block reductions: the wave butterfly, then the waves in order; every thread gets the result. */
-__device__ float block_sum(float v, float *scratch) {
-    v = wave_sum_butterfly(v);
-    __syncthreads();
-    if ((threadIdx.x & (WAVE - 1)) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float s = 0.0f;
-    for (int w = 0; w < CHOICE_WAVES; w++) s = s + scratch[w];
-    return s;
-}
-
+/* Block reductions: the wave butterfly, then the waves in order; every thread gets the result. */
 __device__ float block_max(float v, float *scratch) {
     v = wave_max(v);
     __syncthreads();
@@ -428,15 +418,111 @@ __device__ unsigned long long block_max_key(unsigned long long v, unsigned long 
     return m;
 }
 
+/* ---------------------------------------------------------------- the nucleus threshold
+ *
+ * The nucleus (arXiv 1904.09751 §3.1, the rule of transformers' TopPLogitsWarper) keeps the rows whose probability
+ * is at least e*, the least probability for which the rows at or below it hold more than (1 - top_p) of the mass.
+ * The probabilities are e = exp(z / T - max z / T) in [0, 1], unnormalized. Masses are fixed point: a row weighs the
+ * integer round(e 2^NUCLEUS_FRAC_BITS), so every sum below is exact and the same whatever order the adds run in (a
+ * vocabulary under 2^25 rows keeps the total under 2^64). A row lighter than 2^-(NUCLEUS_FRAC_BITS + 1) of the largest
+ * weighs 0 and is never kept.
+ *
+ * For e >= 0 the order of the values is the order of their IEEE bit patterns, so e*'s pattern is found digit by digit
+ * from the top, 8 bits a round, as a weighted radix select. A round sums the weights of the rows that share the digits
+ * chosen so far into 256 bins by their next digit (a private histogram per wave, so the integer LDS adds of different
+ * waves never meet), merges the waves' bins, prefix-sums them, and picks the one bin in which the running mass, from
+ * the weight of every row below the current range, first passes the drop. Four rounds fix all 32 bits. */
+constexpr int NUCLEUS_FRAC_BITS = 38;
+constexpr int NUCLEUS_BINS = 256;
+
+struct NucleusShared {
+    unsigned long long hist[CHOICE_WAVES][NUCLEUS_BINS];
+    unsigned long long part[NUCLEUS_BINS / WAVE];   /* each bin-holding wave's bin total */
+    unsigned long long base;                        /* weight below the chosen bin */
+    uint32_t digit;
+};
+
+__device__ __forceinline__ unsigned long long nucleus_weight(float e) {
+    return (unsigned long long)((double)e * (double)(1ull << NUCLEUS_FRAC_BITS) + 0.5);
+}
+
+__device__ unsigned long long wave_inclusive_scan(unsigned long long v) {
+    const int lane = threadIdx.x & (WAVE - 1);
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const unsigned long long up = __shfl_up(v, d, WAVE);
+        if (lane >= d) v += up;
+    }
+    return v;
+}
+
+/* e*'s bit pattern for one slot's probabilities e[0 .. vocab), each row read by the thread that wrote it
+ * (rows tid, tid + CHOICE_THREADS, ...). Uniform over the block; every thread returns the same value. */
+__device__ uint32_t nucleus_cut(const float *e, int vocab, float top_p, NucleusShared &sh) {
+    const int tid = threadIdx.x, wave = tid / WAVE;
+    uint32_t chosen = 0;               /* the digits fixed so far, in place */
+    unsigned long long below = 0;      /* weight of every row whose pattern is under the current range */
+    unsigned long long drop = 0;       /* the mass that may be dropped, fixed in the first round */
+    for (int shift = 32 - 8; shift >= 0; shift -= 8) {
+        for (int i = tid; i < CHOICE_WAVES * NUCLEUS_BINS; i += CHOICE_THREADS) (&sh.hist[0][0])[i] = 0ull;
+        __syncthreads();
+        const unsigned long long range = (unsigned long long)chosen >> (shift + 8);
+        for (int r = tid; r < vocab; r += CHOICE_THREADS) {
+            const uint32_t bits = __float_as_uint(e[r]);
+            if (((unsigned long long)bits >> (shift + 8)) != range) continue;
+            const unsigned long long w = nucleus_weight(e[r]);
+            if (w != 0ull) atomicAdd(&sh.hist[wave][(bits >> shift) & (NUCLEUS_BINS - 1)], w);
+        }
+        __syncthreads();
+        /* threads 0..255 hold a bin each: its total over the waves, then the running sums */
+        unsigned long long bin = 0ull, upto = 0ull;
+        if (tid < NUCLEUS_BINS) {
+            for (int w = 0; w < CHOICE_WAVES; w++) bin += sh.hist[w][tid];
+            upto = wave_inclusive_scan(bin);
+            if ((tid & (WAVE - 1)) == WAVE - 1) sh.part[wave] = upto;
+        }
+        if (tid == 0) { sh.digit = NUCLEUS_BINS - 1; sh.base = below; }   /* kept only if nothing passes */
+        __syncthreads();
+        unsigned long long earlier = 0ull, range_total = 0ull;
+        for (int w = 0; w < NUCLEUS_BINS / WAVE; w++) {
+            if (w < wave) earlier += sh.part[w];
+            range_total += sh.part[w];
+        }
+        if (shift == 32 - 8 && range_total != 0ull) {
+            /* the first round's range is every row, so range_total is the whole mass. At most all but one unit of
+             * it may go, so the largest row always stays (top_p <= 0 keeps exactly the rows at the maximum). With no
+             * mass at all (no allowed row) nothing passes, and no row is kept. */
+            const double keep_out = (1.0 - (double)top_p) * (double)range_total;
+            drop = keep_out >= (double)(range_total - 1ull) ? range_total - 1ull : (unsigned long long)keep_out;
+        }
+        upto += earlier;
+        if (tid < NUCLEUS_BINS && below + upto - bin <= drop && below + upto > drop) {
+            sh.digit = (uint32_t)tid;
+            sh.base = below + upto - bin;
+        }
+        __syncthreads();
+        chosen |= sh.digit << shift;
+        below = sh.base;
+    }
+    return chosen;
+}
+
+/* The cut alone, one block per row of e (a test hook: dec_debug_nucleus_cut). */
+__global__ void __launch_bounds__(CHOICE_THREADS) nucleus_cut_kernel(const float *e, int vocab, const float *top_p,
+                                                                     uint32_t *cut) {
+    __shared__ NucleusShared sh;
+    const uint32_t u = nucleus_cut(e + (long long)blockIdx.x * vocab, vocab, top_p[blockIdx.x], sh);
+    if (threadIdx.x == 0) cut[blockIdx.x] = u;
+}
+
 /* A block per slot: its token among the allowed rows of its logits, then the commit (decode.cu:170-229, 361-411,
  * 677-688). Temperature 0: the largest logit. T > 0: the largest z / T + gumbel, z = c tanh(s / c) (Gumbel-max
- * sampling of softmax(z / T)). T > 0 and top_p < 1: the nucleus of transformers' TopPLogitsWarper (keep
- * e >= e*, the least e with C(e) > (1 - top_p) sum e, C(x) the sum of e <= x, e = exp(z / T - max z / T), found by
- * bisection on e's bits), then Gumbel-max within it. The alternative is the best key but the lazy row's (none for a
- * nucleus slot). */
+ * sampling of softmax(z / T)). T > 0 and top_p < 1: Gumbel-max within the nucleus that nucleus_cut fixes. The
+ * alternative is the best key but the lazy row's (none for a nucleus slot). */
 __global__ void __launch_bounds__(CHOICE_THREADS) choose_kernel(ChoiceArgs c) {
     __shared__ float fscratch[CHOICE_WAVES];
     __shared__ unsigned long long kscratch[CHOICE_WAVES];
+    __shared__ NucleusShared nucleus;
     const int b = blockIdx.x, tid = threadIdx.x;
     if (!live(c.active, b)) return;
     const float *s = c.logits + (long long)b * c.vocab;
@@ -449,29 +535,17 @@ __global__ void __launch_bounds__(CHOICE_THREADS) choose_kernel(ChoiceArgs c) {
     auto capped = [&](int r) { return c.softcap * tanhf(s[r] / c.softcap); };
     unsigned long long best = 0, alt = 0;
     if (T > 0.0f && top_p < 1.0f) {
-        float *e = c.probs + (long long)b * c.vocab;  /* a thread reads back only the rows it wrote */
-        float m = -INFINITY;
+        /* the slot's probabilities go to its row of c.probs; every pass over them visits a thread's own rows */
+        float *prob = c.probs + (long long)b * c.vocab;
+        float zmax = -INFINITY;
         for (int r = tid; r < c.vocab; r += CHOICE_THREADS)
-            if (allowed(r)) m = fmaxf(m, capped(r) / T);
-        m = block_max(m, fscratch);
-        float sum = 0.0f;
+            if (allowed(r)) zmax = fmaxf(zmax, capped(r) / T);
+        zmax = block_max(zmax, fscratch);
+        for (int r = tid; r < c.vocab; r += CHOICE_THREADS) prob[r] = allowed(r) ? expf(capped(r) / T - zmax) : 0.0f;
+        const uint32_t cut = nucleus_cut(prob, c.vocab, top_p, nucleus);
         for (int r = tid; r < c.vocab; r += CHOICE_THREADS) {
-            e[r] = allowed(r) ? expf(capped(r) / T - m) : 0.0f;
-            sum = sum + e[r];
-        }
-        const float drop = (1.0f - top_p) * block_sum(sum, fscratch);
-        uint32_t lo = 0u, hi = __float_as_uint(1.0f);
-        while (lo < hi) {
-            const uint32_t mid = lo + (hi - lo) / 2;
-            const float x = __uint_as_float(mid);
-            float below = 0.0f;
-            for (int r = tid; r < c.vocab; r += CHOICE_THREADS)
-                if (e[r] <= x) below = below + e[r];
-            if (block_sum(below, fscratch) > drop) hi = mid; else lo = mid + 1;
-        }
-        const float least = __uint_as_float(lo);
-        for (int r = tid; r < c.vocab; r += CHOICE_THREADS) {
-            if (e[r] < least || e[r] == 0.0f) continue;
+            const float pr = prob[r];
+            if (pr == 0.0f || __float_as_uint(pr) < cut) continue;
             const unsigned long long key = choice_key(capped(r) / T + gumbel(seed, gen, r), r);
             best = key > best ? key : best;
         }
@@ -954,6 +1028,7 @@ static void body_attn(Decoder *d, const Lane &ln, const Part &p, int l) {
     st.token_stride = 3LL * d->C;
     st.q_gain = ly.q_gain; st.k_gain = ly.k_gain; st.cos = d->cos; st.sin = d->sin;
     st.ve_h = p.a.h; st.ve = ly.ve; st.ve_gate = ly.ve_gate; st.ve_tokens = d->tokens + p.b0; st.C = d->C;
+    st.ve_rows = d->vocab;
     st.k_pages = layer_k(d, l); st.v_pages = layer_v(d, l); st.kv_scale = layer_s(d, l);
     NC_CHECK(decode_step(st, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table + (size_t)p.b0 * d->max_pages,
                          d->max_pages, (int)d->layer_pages, d->seq_lens + p.b0, d->max_len, p.n, d->H, d->H, ly.window,
@@ -1622,4 +1697,13 @@ extern "C" int dec_debug_slot_gemm_tile(int R, int K, int N, int slices) {
     const int S = slices > 0 ? slices : nc::slot_gemm_slices(R, K);
     if (S > K / 128) return -2;
     return nc::slot_gemm_tile(R, K, N, S);
+}
+
+extern "C" int dec_debug_nucleus_cut(const float *e, int rows, int vocab, const float *top_p, uint32_t *cut,
+                                     void *stream) {
+    if (rows < 0 || vocab <= 0 || vocab >= (1 << 25) || !e || !top_p || !cut) return -2;
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(nc::dec::nucleus_cut_kernel, dim3(rows), dim3(nc::dec::CHOICE_THREADS), 0,
+                       (hipStream_t)stream, e, vocab, top_p, cut);
+    return (int)hipGetLastError();
 }

@@ -31,8 +31,8 @@ struct StepArgs {
     uint16_t *q_out;            /* NULL, or [B][Hq][128]: the normed, rotated queries */
     const uint16_t *ve_h, *ve;  /* NULL ve: no value embeddings; else h [B][C], table [vocab][C] */
     const float *ve_gate;       /* [Hkv][C] */
-    const int32_t *ve_tokens;   /* [B] */
-    int C;
+    const int32_t *ve_tokens;   /* [B]; a token outside [0, ve_rows) mixes nothing */
+    int C, ve_rows;
     uint8_t *k_pages, *v_pages; /* the cache the step appends to (the launch's pools) */
     float *kv_scale;
 };

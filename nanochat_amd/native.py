@@ -89,9 +89,9 @@ SIGNATURES = {
     "nc_decode_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
                             c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_size_t, c_void_p], c_int),
     "nc_decode_step_fp8": ([c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
-                            c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int,
-                            c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p,
-                            c_size_t, c_void_p], c_int),
+                            c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p,
+                            c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_int, c_void_p,
+                            c_void_p, c_size_t, c_void_p], c_int),
     "nc_decode_attn_fp8_noalloc": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int,
                                     c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p], c_int),
     "nc_prefill_attn_fp8": ([c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int,
@@ -145,6 +145,7 @@ DECODE_SIGNATURES = {
     "dec_debug_slot_gemm_tile": ([c_int, c_int, c_int, c_int], c_int),
     "dec_debug_slot_gemm_ssq": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                  c_void_p], c_int),
+    "dec_debug_nucleus_cut": ([c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p], c_int),
 }
 
 LIBRARIES = {"nanochat_kv": (LIBRARY, SIGNATURES), "decode": (DECODE_LIBRARY, DECODE_SIGNATURES)}

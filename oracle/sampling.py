@@ -13,10 +13,18 @@ Gumbel noise: Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random number
 the Random123 constants) at counter (row, i, 0, 0) with key (seed mod 2^32, seed >> 32); the first two output
 words give r = (x0 2^32 + x1) >> 12, u = (2 r + 1) 2^-53, g = -log(-log(u)) in float64, rounded to float32.
 
+The device takes the nucleus threshold in exact fixed point (csrc/decoder.hip:nucleus_cut): a row weighs
+round(e 2^38) as an integer, and e* is the least e whose rows at or below it weigh more than (1 - top_p) of the
+total, with the drop floor((1 - top_p) total) capped at total - 1. `nucleus_cut_fixed` restates that rule by sorting;
+it differs from the float64 rule of `nucleus_keep` only for rows within about 2^-38 of the largest e of the
+threshold's mass.
+
 Pinned by tests/test_oracle_sampling.py: Philox against the Random123 known-answer vectors; the key order
 against IEEE order on random and special floats (largest score wins, ties to the lowest row); greedy choice
 against numpy argmax; Gumbel-max sampling frequencies against softmax(z / T) (chi-square); the nucleus against a
-float64 sort-and-cumsum restatement of TopPLogitsWarper.
+float64 sort-and-cumsum restatement of TopPLogitsWarper; the fixed-point cut against that float64 rule, against a
+brute-force search over every candidate threshold on small inputs, and on its special cases (top_p <= 0 keeps the
+maximum rows, equal rows are kept together, no allowed row keeps nothing).
 """
 import numpy as np
 
@@ -101,6 +109,26 @@ def nucleus_keep(z, temperature, top_p, allowed):
     idx = np.searchsorted(below, drop, side="right")
     least = order[min(idx, len(order) - 1)]
     return (e >= least) & allowed, e
+
+
+NUCLEUS_FRAC_BITS = 38
+
+
+def nucleus_cut_fixed(e, top_p):
+    """The device's nucleus threshold: e (float32, in [0, 1], 0 for rows not allowed) and top_p -> the uint32 IEEE
+    pattern of e*. Rows with e >= e* and a positive weight form the nucleus; 0xFFFFFFFF when no row has weight."""
+    e = np.asarray(e, np.float32)
+    weight = np.floor(e.astype(np.float64) * 2.0 ** NUCLEUS_FRAC_BITS + 0.5).astype(np.uint64)
+    total = int(weight.sum(dtype=np.uint64))
+    if total == 0:
+        return MASK32
+    keep_out = (1.0 - float(np.float32(top_p))) * float(total)
+    drop = total - 1 if keep_out >= float(total - 1) else int(keep_out)
+    keys, which = np.unique(e.view(np.uint32), return_inverse=True)   # ascending patterns: ascending e (e >= 0)
+    per_key = np.zeros(keys.size, np.uint64)
+    np.add.at(per_key, which, weight)
+    at_or_below = np.cumsum(per_key, dtype=np.uint64)
+    return int(keys[np.argmax(at_or_below > np.uint64(drop))])
 
 
 def choose(logits, *, temperature=0.0, top_p=1.0, seed=0, gen=0, allow=None, lazy=-1, softcap=15.0):

@@ -108,7 +108,7 @@ def step_args(**over):
     """nc_decode_step_fp8's arguments for B = 2, Hq = 16, Hkv = 4, max_seq_len 100 with dummy pointers; `over`
     replaces any of them by name."""
     args = dict(qkv=DUMMY, token_stride=24 * 128, B=2, Hq=16, Hkv=4, seq_lens=DUMMY, q_gain=DUMMY, k_gain=DUMMY,
-                cos=DUMMY, sin=DUMMY, rope_len=100, q_out=None, ve_h=None, ve=None, ve_gate=None, ve_tokens=None, C=0,
+                cos=DUMMY, sin=DUMMY, rope_len=100, q_out=None, ve_h=None, ve=None, ve_gate=None, ve_tokens=None, C=0, ve_rows=0,
                 block_table=DUMMY, max_pages=7, k_pages=DUMMY, v_pages=DUMMY, kv_scale=DUMMY, num_pages=14,
                 max_seq_len=100, window=-1, sm_scale=0.1, workers=0, out=DUMMY, workspace=DUMMY,
                 workspace_bytes=1 << 30, stream=None)
@@ -120,11 +120,12 @@ def step_args(**over):
     (dict(qkv=None), -1), (dict(cos=None), -1), (dict(workspace=None), -1), (dict(ve=DUMMY), -1),
     (dict(ve=DUMMY, ve_h=DUMMY, ve_gate=DUMMY), -1),
     (dict(rope_len=99), -2), (dict(token_stride=24 * 128 - 1), -2), (dict(Hq=6), -2), (dict(max_pages=6), -2),
-    (dict(ve=DUMMY, ve_h=DUMMY, ve_gate=DUMMY, ve_tokens=DUMMY, C=511), -2), (dict(workers=-1), -2),
+    (dict(ve=DUMMY, ve_h=DUMMY, ve_gate=DUMMY, ve_tokens=DUMMY, C=511, ve_rows=10), -2),
+    (dict(ve=DUMMY, ve_h=DUMMY, ve_gate=DUMMY, ve_tokens=DUMMY, C=512, ve_rows=0), -2), (dict(workers=-1), -2),
     (dict(workspace_bytes=0), -3)])
 def test_decode_step_rejects_bad_arguments(lib, over, code):
     """nc_decode_step_fp8 checks its pointers, shapes (rope tables covering max_seq_len, the qkv row width, the value
-    embedding width) and workspace before any device call."""
+    embedding width and table rows) and workspace before any device call."""
     assert lib.nc_decode_step_fp8(*step_args(**over)) == code
 
 
@@ -314,3 +315,15 @@ def test_slot_gemm_tiles():
     assert lib.dec_debug_slot_gemm_tile(1664, 6600, 128, 0) == -2     # K not a multiple of 128
     assert lib.dec_debug_slot_gemm_tile(1664, 1664, 129, 0) == -2     # more than 128 slots
     assert lib.dec_debug_slot_gemm_tile(1664, 256, 128, 3) == -2      # more slices than chunks
+
+
+def test_nucleus_cut_declines_shapes():
+    """The nucleus-threshold hook refuses an empty or too large vocabulary and a negative row count before any device
+    call; zero rows is a no-op."""
+    from nanochat_amd.native import hip_library
+
+    lib = hip_library("decode")
+    assert lib.dec_debug_nucleus_cut(DUMMY, 1, 0, DUMMY, DUMMY, None) == -2
+    assert lib.dec_debug_nucleus_cut(DUMMY, -1, 64, DUMMY, DUMMY, None) == -2
+    assert lib.dec_debug_nucleus_cut(DUMMY, 1, 1 << 25, DUMMY, DUMMY, None) == -2
+    assert lib.dec_debug_nucleus_cut(DUMMY, 0, 64, DUMMY, DUMMY, None) == 0

@@ -100,3 +100,66 @@ def test_nucleus_matches_sorted_cumsum():
         assert (keep == expected).all()
         tok, alt = sampling.choose(s, temperature=0.8, top_p=top_p, seed=5, gen=2)
         assert keep[tok] and alt == -1
+
+
+def brute_cut(e, top_p):
+    """Every candidate threshold tried in turn: the least e_i whose rows at or below it weigh more than the drop."""
+    w = [int(np.floor(float(x) * 2.0 ** 38 + 0.5)) for x in np.asarray(e, np.float32)]
+    total = sum(w)
+    if total == 0:
+        return None
+    keep_out = (1.0 - float(np.float32(top_p))) * float(total)
+    drop = min(total - 1, int(keep_out)) if keep_out < float(total - 1) else total - 1
+    best = None
+    for x in e:
+        mass = sum(wj for ej, wj in zip(e, w) if ej <= x)
+        if mass > drop and (best is None or x < best):
+            best = x
+    return best
+
+
+def kept_by_cut(e, cut):
+    e = np.asarray(e, np.float32)
+    return (e.view(np.uint32) >= np.uint32(cut)) & (np.floor(e.astype(np.float64) * 2.0 ** 38 + 0.5) > 0)
+
+
+def test_fixed_point_cut_matches_the_float64_rule():
+    """Away from a mass boundary (continuous random logits) the integer rule keeps exactly TopPLogitsWarper's rows."""
+    rng = np.random.default_rng(7)
+    for vocab, T, top_p, spread in ((4096, 0.8, 0.5, 3), (65536, 1.0, 0.9, 2), (50000, 0.6, 0.99, 4),
+                                    (1000, 1.3, 0.1, 1), (32768, 0.7, 0.95, 6)):
+        z = sampling.capped((rng.standard_normal(vocab) * spread).astype(np.float32), 15.0)
+        allowed = rng.random(vocab) < 0.9
+        keep, e64 = sampling.nucleus_keep(z, T, top_p, allowed)
+        zt = np.where(allowed, z / np.float32(T), -np.inf).astype(np.float32)
+        e = np.where(allowed, np.exp(zt - zt[allowed].max()), 0).astype(np.float32)
+        cut = sampling.nucleus_cut_fixed(e, top_p)
+        assert (kept_by_cut(e, cut) == keep).all(), (vocab, top_p)
+
+
+def test_fixed_point_cut_against_brute_force():
+    rng = np.random.default_rng(8)
+    for trial in range(400):
+        n = int(rng.integers(1, 9))
+        e = rng.choice([0.0, 1e-13, 0.03, 0.25, 0.5, 0.5, 0.7, 1.0], n).astype(np.float32)
+        e[int(rng.integers(n))] = 1.0                           # the largest row has e = 1
+        top_p = float(rng.choice([0.0, 0.1, 0.3, 0.5, 0.75, 0.9, 0.999, rng.random()]))
+        want = brute_cut(e, top_p)
+        got = sampling.nucleus_cut_fixed(e, top_p)
+        assert got == np.float32(want).view(np.uint32), (e, top_p)
+
+
+def test_fixed_point_cut_special_cases():
+    e = np.array([0.2, 1.0, 0.0, 1.0, 0.5], np.float32)
+    assert kept_by_cut(e, sampling.nucleus_cut_fixed(e, 0.0)).tolist() == [False, True, False, True, False]
+    # equal rows are kept or dropped together: the two 0.5 rows are 1/3 of the mass, so they go when at least 1/3 may
+    # be dropped (top_p <= 2/3) and both stay otherwise
+    e = np.array([0.5, 1.0, 0.5, 1.0], np.float32)
+    for top_p, kept in ((0.6, [False, True, False, True]), (0.66, [False, True, False, True]),
+                        (0.67, [True] * 4), (0.7, [True] * 4)):
+        assert kept_by_cut(e, sampling.nucleus_cut_fixed(e, top_p)).tolist() == kept, top_p
+    # no allowed row: nothing has weight, nothing is kept
+    assert sampling.nucleus_cut_fixed(np.zeros(64, np.float32), 0.9) == 0xFFFFFFFF
+    # a row under 2^-39 of the largest weighs nothing and is never kept, even at top_p close to 1
+    e = np.array([1.0, 2.0 ** -41], np.float32)
+    assert kept_by_cut(e, sampling.nucleus_cut_fixed(e, 0.999999)).tolist() == [True, False]
