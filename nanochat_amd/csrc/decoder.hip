@@ -13,8 +13,9 @@
  * A step's GEMMs are slot_gemm.hip's weight-streaming MFMA kernel with the epilogue fused (long-K GEMMs split into
  * K-slices whose partials a second kernel adds in order; a model wider than 2,048 computes the MLP's rstd in
  * rstd_kernel). Prefill's GEMMs (up to 8,192 rows) are hipBLASLt matmuls
- * (bf16 operands, fp32 accumulation; one plan per shape and row count, the heuristic's first algorithm; rocBLAS gemm_ex
- * where hipBLASLt offers none) followed by the epilogue kernels. Every kernel covers the slots up to the highest active
+ * on whole blocks of PREFILL_BLOCK rows (bf16 operands, fp32 accumulation; one plan per shape, the heuristic's first
+ * algorithm, so a row's sums do not depend on how many rows the call holds; rocBLAS gemm_ex where hipBLASLt offers
+ * none) followed by the epilogue kernels. Every kernel covers the slots up to the highest active
  * one (dec_set_active) and skips inactive slots.
  *
  * Numerics, op by op as decode.cu: the epilogues round once (bf16(s + residual)); the MLP reads the un-normed stream

@@ -7,8 +7,9 @@ missing library builds both once.
 
     libnanochat_kv.so      the kernel entry points of include/nanochat_amd.h
     libnanochat_decode.so  the decoder runtime of include/nanochat_decode.h (the same kernels, plus the
-                           dec_* runtime and rocBLAS GEMMs); hip_library("decode") loads it, as the
-                           reference's cuda_library("decode") loads decode.cu
+                           dec_* runtime, its hand-written step GEMMs and hipBLASLt prefill GEMMs);
+                           hip_library("decode") loads it, as the reference's cuda_library("decode")
+                           loads decode.cu
 """
 
 import ctypes
