@@ -121,6 +121,14 @@ int dec_debug_slot_gemm_tile(int R, int K, int N, int slices);
 int dec_debug_slot_gemm_ssq(int epi, const void *w, int R, int K, const void *x, int N, void *out, const void *res,
                             float *ssq, void *stream);
 
+/* The prefill GEMM alone (prefill_gemm.hip): out[m][n] = epilogue(sum_k a[m][k] w[n][k]) for M rows, bf16 w [N][K]
+ * and a [M][K]; epi 0 bf16(s) to out, 3 bf16(s + res) (res bf16 [M][N]), 4 fp32 s to out_f32, 2 bf16(relu(p) p) with
+ * p = s rstd[m] (rstd fp32 [M]). Every row's sums run over K in one fixed order whatever M is. Returns 0, a hipError_t,
+ * or -2 when the shape (K a multiple of 128, N of 4, every array under 2 GiB) or an operand the epilogue needs does
+ * not fit. Stream-ordered. */
+int dec_debug_prefill_gemm(int epi, const void *w, int N, int K, const void *a, int M, void *out, float *out_f32,
+                           const void *res, const float *rstd, void *stream);
+
 /* The nucleus threshold of choose_kernel alone: for each of `rows` rows of probabilities e (fp32 [rows][vocab],
  * device; e = exp(z / T - max z / T) in [0, 1], 0 for rows not allowed) and its top_p (fp32 [rows], device), the
  * IEEE bit pattern of e*, the least e for which the rows with e' <= e* weigh more than (1 - top_p) of the total,

@@ -12,11 +12,11 @@
  *          the allowed tokens, then the commit), the tokens to pinned host memory.
  * A step's GEMMs are slot_gemm.hip's weight-streaming MFMA kernel with the epilogue fused (long-K GEMMs split into
  * K-slices whose partials a second kernel adds in order; a model wider than 2,048 computes the MLP's rstd in
- * rstd_kernel). Prefill's GEMMs (up to 8,192 rows) are hipBLASLt matmuls
- * on whole blocks of PREFILL_BLOCK rows (bf16 operands, fp32 accumulation; one plan per shape, the heuristic's first
- * algorithm, so a row's sums do not depend on how many rows the call holds; rocBLAS gemm_ex where hipBLASLt offers
- * none) followed by the epilogue kernels. Every kernel covers the slots up to the highest active
- * one (dec_set_active) and skips inactive slots.
+ * rstd_kernel). Prefill's GEMMs (up to 8,192 rows a call) are prefill_gemm.hip's MFMA-tiled kernel over all the
+ * call's rows at once, with the epilogue fused (bf16 out, the residual, ReLU^2 with the rstd); each row's sums run in
+ * one fixed order, so they do not depend on how many rows the call holds. The o GEMM's residual sum needs its whole
+ * row for the MLP's rstd, so it writes fp32 and rstd_kernel adds the residual. Every kernel covers the slots up to
+ * the highest active one (dec_set_active) and skips inactive slots.
  *
  * Numerics, op by op as decode.cu: the epilogues round once (bf16(s + residual)); the MLP reads the un-normed stream
  * scaled by its rstd; every RMS norm is 1 / sqrt(mean x^2 + FLT_EPSILON), correctly rounded (the reference: rsqrtf).
@@ -45,9 +45,6 @@
 #include <tuple>
 #include <vector>
 
-#include <hipblaslt/hipblaslt.h>
-#include <rocblas/rocblas.h>
-
 #include "nc_device.h"
 #include "nanochat_amd.h"
 #include "nanochat_decode.h"
@@ -61,14 +58,12 @@ constexpr int MASK_BITS = 64;              /* slots per word of a slot mask */
 constexpr int MASK_WORDS = MAX_BATCH / MASK_BITS;
 constexpr int WORD_BITS = 32;              /* tokens per word of an allowed-token mask */
 constexpr int PREFILL_ROWS = 8192;         /* rows per dec_prefill call */
-constexpr int PREFILL_BLOCK = 1024;        /* prefill GEMMs run on whole blocks of this many rows */
-static_assert(PREFILL_ROWS % PREFILL_BLOCK == 0, "prefill blocks pad into the row buffers");
 constexpr int SPLIT_SLOTS = 64;            /* a step over more slots runs as two lanes (enqueue_body) */
 constexpr int GLOBAL_PTRS = 4, LAYER_PTRS = 8;
 constexpr int CHOICE_THREADS = 1024, CHOICE_WAVES = CHOICE_THREADS / WAVE;
 constexpr float SM_SCALE = 0.08838834764831845f;  /* 1 / sqrt(128) */
 
-/* A failed HIP or rocBLAS call aborts, naming it: never silently wrong tokens (decode.cu:47-53). */
+/* A failed HIP call aborts, naming it: never silently wrong tokens (decode.cu:47-53). */
 [[noreturn]] static void die(const char *what, const char *detail, int line) {
     fprintf(stderr, "decoder.hip:%d: %s: %s\n", line, what, detail);
     abort();
@@ -77,11 +72,6 @@ constexpr float SM_SCALE = 0.08838834764831845f;  /* 1 / sqrt(128) */
     do {                                                                       \
         const hipError_t e_ = (call);                                          \
         if (e_ != hipSuccess) ::nc::dec::die(#call, hipGetErrorString(e_), __LINE__);    \
-    } while (0)
-#define BLAS_CHECK(call)                                                                \
-    do {                                                                                \
-        const rocblas_status s_ = (call);                                               \
-        if (s_ != rocblas_status_success) ::nc::dec::die(#call, rocblas_status_to_string(s_), __LINE__); \
     } while (0)
 #define NC_CHECK(call)                                                         \
     do {                                                                       \
@@ -249,24 +239,6 @@ __global__ void __launch_bounds__(256) rstd_kernel(const float *s, const uint16_
     }
     ss = wave_sum_butterfly(ss);
     if (lane == 0) rstd[b] = 1.0f / __builtin_sqrtf(ss * (1.0f / (float)C) + FLT_EPS);
-}
-
-/* fc's epilogue (decode.cu:144-148): u = bf16(relu(p) p), p = s rstd[row]; four columns a thread. */
-__global__ void __launch_bounds__(256) relu2_kernel(const float *s, const float *rstd, uint16_t *u,
-                                                    const unsigned long long *active, int F) {
-    const int b = blockIdx.y;
-    if (active && !live(active, b)) return;
-    const int j = (blockIdx.x * 256 + threadIdx.x) * 4;
-    if (j >= F) return;
-    const long long at = (long long)b * F + j;
-    const float4 v = *reinterpret_cast<const float4 *>(s + at);
-    const float r = rstd[b];
-    const float p[4] = {v.x * r, v.y * r, v.z * r, v.w * r};
-    uint16_t o[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) o[i] = f32_to_bf16(fmaxf(p[i], 0.0f) * p[i]);
-    *reinterpret_cast<uint2 *>(u + at) = make_uint2((uint32_t)o[0] | (uint32_t)o[1] << 16,
-                                                   (uint32_t)o[2] | (uint32_t)o[3] << 16);
 }
 
 /* A step's layer boundary in one pass (decode.cu:149-154 and 413-443 for the same math): the proj GEMM's S K-slice
@@ -666,11 +638,9 @@ struct Acts {
     float *rstd;               /* [rows] */
 };
 
-/* Where a stretch of work runs: a stream with its own library handle and scratch, so two lanes can run at once. */
+/* Where a stretch of work runs: a stream with its own scratch, so two lanes can run at once. */
 struct Lane {
     hipStream_t stream;
-    rocblas_handle blas;
-    void *lt_ws;                         /* hipBLASLt workspace (Decoder::lt_ws_bytes) */
     void *attn_ws;                       /* decode-attention partials (Decoder::attn_ws_bytes) */
     float *part;                         /* slot_gemm's split-K partial sums (Decoder::part_bytes) */
     float *ssq;                          /* [B][ceil(C / 16)]: the o GEMM's tile sums of squares for fc's rstd */
@@ -689,8 +659,6 @@ struct Decoder {
                                             and joined back into `stream` within a step */
     hipEvent_t fork, join;
     std::vector<hipEvent_t> attn_done;   /* [2 L]: lane h's attention of layer l finished */
-    hipblasLtHandle_t lt;                /* hipBLASLt: the GEMMs' first choice (rocBLAS when it has no plan) */
-    size_t lt_ws_bytes;
     uint8_t *k_pages, *v_pages;          /* [L][layer_pages][H][2048] */
     float *kv_scale;                     /* [L][layer_pages][H][2][16] */
     int32_t *block_table;                /* [B][max_pages]: slot b's entry e is -1, a pool page of its own, or a
@@ -772,101 +740,16 @@ static Acts acts_from(const Decoder *d, const Acts &a, size_t b0) {
     return r;
 }
 
-/* A hipBLASLt plan for one GEMM shape: column-major D (rows x n) = W^T (W stored [rows][cols], so a cols x rows
- * column-major matrix, transposed) x X (cols x n), fp32 compute; the heuristic's first algorithm. */
-struct LtPlan {
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-    hipblasLtMatmulAlgo_t algo;
-    bool ok = false;
-};
-
-static std::map<std::tuple<Decoder *, int, int, int, int>, LtPlan> &lt_plans() {
-    static std::map<std::tuple<Decoder *, int, int, int, int>, LtPlan> plans;
-    return plans;
-}
-
-static const LtPlan &lt_plan(Decoder *d, int rows, int cols, int n, bool f32) {
-    LtPlan &p = lt_plans()[std::make_tuple(d, rows, cols, n, (int)f32)];
-    if (p.desc) return p;
-    const hipDataType ot = f32 ? HIP_R_32F : HIP_R_16BF;
-    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) ==
-                  HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) ==
-                  HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, cols, rows, cols) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, cols, n, cols) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&p.c, ot, rows, n, rows) == HIPBLAS_STATUS_SUCCESS;
-    hipblasLtMatmulPreference_t pref = nullptr;
-    if (ok) {
-        const uint64_t ws = d->lt_ws_bytes;
-        ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
-             hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof ws) ==
-                 HIPBLAS_STATUS_SUCCESS;
-    }
-    if (ok) {
-        hipblasLtMatmulHeuristicResult_t r[1];
-        int got = 0;
-        ok = hipblasLtMatmulAlgoGetHeuristic(d->lt, p.desc, p.a, p.b, p.c, p.c, pref, 1, r, &got) ==
-                 HIPBLAS_STATUS_SUCCESS &&
-             got > 0 && r[0].state == HIPBLAS_STATUS_SUCCESS && r[0].workspaceSize <= d->lt_ws_bytes;
-        if (ok) p.algo = r[0].algo;
-    }
-    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-    p.ok = ok;
-    return p;
-}
-
-static void lt_release(Decoder *d) {
-    auto &plans = lt_plans();
-    for (auto it = plans.begin(); it != plans.end();) {
-        if (std::get<0>(it->first) != d) {
-            ++it;
-            continue;
-        }
-        LtPlan &p = it->second;
-        if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
-        if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
-        if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
-        if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
-        it = plans.erase(it);
-    }
-}
-
-/* out[n][rows] = in[n][cols] . W[rows][cols]^T: column-major rows x n = (W as cols x rows)^T (cols x n). resid
- * non-NULL: out = bf16(s + resid) by beta = 1 (one rounding of the fp32 sum). hipBLASLt's plan for the shape,
- * else rocBLAS gemm_ex. */
-static void gemm_once(Decoder *d, const Lane &ln, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
-                 void *out, bool f32, const uint16_t *resid = nullptr) {
+/* A prefill GEMM (prefill_gemm.hip) over all n rows of the call: out[r][rows] = epilogue(in[r][cols] . W[rows][cols]^T),
+ * each row's sums in one fixed order whatever n is, so a row's result does not depend on how many rows share the call.
+ * epi: SG_STORE (bf16), SG_RESID (bf16(s + resid)), SG_F32 (fp32) or SG_RELU2 (bf16(relu(p) p), p = s rstd[r]). */
+static void gemm(const Lane &ln, const uint16_t *w, int rows, int cols, const uint16_t *in, int n, void *out, int epi,
+                 const uint16_t *resid = nullptr, const float *rstd = nullptr) {
     if (n <= 0) return;
-    const float alpha = 1.0f, beta = resid ? 1.0f : 0.0f;
-    const LtPlan &p = lt_plan(d, rows, cols, n, f32);
-    if (p.ok) {
-        const hipblasStatus_t st = hipblasLtMatmul(d->lt, p.desc, &alpha, w, p.a, in, p.b, &beta,
-                                                   resid ? (const void *)resid : out, p.c, out, p.c, &p.algo,
-                                                   ln.lt_ws, d->lt_ws_bytes, ln.stream);
-        if (st != HIPBLAS_STATUS_SUCCESS) die("hipblasLtMatmul", "failed", __LINE__);
-        return;
-    }
-    const rocblas_datatype ot = f32 ? rocblas_datatype_f32_r : rocblas_datatype_bf16_r;
-    BLAS_CHECK(rocblas_gemm_ex(ln.blas, rocblas_operation_transpose, rocblas_operation_none, rows, n, cols, &alpha, w,
-                               rocblas_datatype_bf16_r, cols, in, rocblas_datatype_bf16_r, cols, &beta,
-                               resid ? (const void *)resid : out, ot, rows, out, ot, rows, rocblas_datatype_f32_r,
-                               rocblas_gemm_algo_standard, 0, 0));
-}
-
-/* gemm over prefill rows in whole blocks of PREFILL_BLOCK (the last one padded with the rows after n, whose results
- * nothing reads; the row buffers hold PREFILL_ROWS), so every call runs one plan per shape and a row's sums do not
- * depend on how many rows share the call. */
-static void gemm(Decoder *d, const Lane &ln, const uint16_t *w, int rows, int cols, const uint16_t *in, int n,
-                 void *out, bool f32, const uint16_t *resid = nullptr) {
     if (n > PREFILL_ROWS) die("gemm", "more rows than the prefill buffers hold", __LINE__);
-    const size_t osz = f32 ? 4 : 2;
-    for (int b0 = 0; b0 < n; b0 += PREFILL_BLOCK)
-        gemm_once(d, ln, w, rows, cols, in + (size_t)b0 * cols, PREFILL_BLOCK, (char *)out + (size_t)b0 * rows * osz,
-                  f32, resid ? resid + (size_t)b0 * rows : nullptr);
+    PfGemm g = {in, w, n, rows, cols, epi == SG_F32 ? nullptr : (uint16_t *)out, epi == SG_F32 ? (float *)out : nullptr,
+                resid, rstd};
+    NC_CHECK(prefill_gemm(g, epi, ln.stream));
 }
 
 static NormArgs norm_args(Decoder *d, int kind, const Acts &a, int rows, int32_t *tokens,
@@ -911,7 +794,8 @@ static float *layer_s(Decoder *d, int l) { return d->kv_scale + (size_t)l * d->l
 
 /* A GEMM with its epilogue. A decode step (step): slot_gemm over the slots in blocks of SG_MAX_N, each slot's sums in
  * the same order whatever the block holds, so a slot's result does not depend on the others; its split-K partials (long
- * K) are reduced in slice order. Prefill rows: the library GEMM into fp32 or bf16, then the epilogue kernels. */
+ * K) are reduced in slice order. Prefill rows: prefill_gemm with the epilogue fused, except the o GEMM's residual sum,
+ * whose rstd needs the whole row (fp32 out; rstd_kernel adds the residual). */
 static void gemm_epi(Decoder *d, const Lane &ln, bool step, int epi, const uint16_t *w, int rows, int cols,
                      const uint16_t *in, int n, uint16_t *out, float *out_f32, const uint16_t *res, const float *rstd,
                      const unsigned long long *active, float *ssq = nullptr) {
@@ -931,17 +815,13 @@ static void gemm_epi(Decoder *d, const Lane &ln, bool step, int epi, const uint1
         return;
     }
     switch (epi) {
-    case SG_STORE: gemm(d, ln, w, rows, cols, in, n, out, false); break;
-    case SG_RESID: gemm(d, ln, w, rows, cols, in, n, out, false, res); break;
-    case SG_F32: gemm(d, ln, w, rows, cols, in, n, out_f32, true); break;
+    case SG_STORE: gemm(ln, w, rows, cols, in, n, out, SG_STORE); break;
+    case SG_RESID: gemm(ln, w, rows, cols, in, n, out, SG_RESID, res); break;
+    case SG_F32: gemm(ln, w, rows, cols, in, n, out_f32, SG_F32); break;
     case SG_RESID2:  /* fp32 s; the rstd kernel adds the residual and writes out */
-        gemm(d, ln, w, rows, cols, in, n, out_f32, true);
+        gemm(ln, w, rows, cols, in, n, out_f32, SG_F32);
         break;
-    case SG_RELU2:
-        gemm(d, ln, w, rows, cols, in, n, out_f32, true);
-        hipLaunchKernelGGL(relu2_kernel, dim3((rows / 4 + 255) / 256, n), dim3(256), 0, ln.stream, out_f32, rstd, out,
-                           active, rows);
-        break;
+    case SG_RELU2: gemm(ln, w, rows, cols, in, n, out, SG_RELU2, nullptr, rstd); break;
     }
 }
 
@@ -1158,17 +1038,10 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     /* lane 0 is the caller's stream; lane 1 a stream of the decoder's own (default priority) */
     d->lane[0].stream = d->stream;
     HIP_CHECK(hipStreamCreateWithFlags(&d->lane[1].stream, hipStreamNonBlocking));
-    for (Lane &ln : d->lane) {
-        BLAS_CHECK(rocblas_create_handle(&ln.blas));
-        BLAS_CHECK(rocblas_set_stream(ln.blas, ln.stream));
-        BLAS_CHECK(rocblas_set_atomics_mode(ln.blas, rocblas_atomics_not_allowed));
-    }
     HIP_CHECK(hipEventCreateWithFlags(&d->fork, hipEventDisableTiming));
     HIP_CHECK(hipEventCreateWithFlags(&d->join, hipEventDisableTiming));
     d->attn_done.resize(2 * d->L);
     for (hipEvent_t &e : d->attn_done) HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-    if (hipblasLtCreate(&d->lt) != HIPBLAS_STATUS_SUCCESS) die("hipblasLtCreate", "failed", __LINE__);
-    d->lt_ws_bytes = (size_t)32 << 20;
 
     /* fixed blocks first (prefill rows, masks, the store's pages and, with pool_pages, the pool), then the slots: B,
      * the most slots (<= max_slots) whose activations, choice buffers and (without pool_pages) max_len worth of KV
@@ -1241,7 +1114,6 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     for (Lane &ln : d->lane) {
         ln.part = (float *)device_alloc(d, (size_t)part_bytes);
         ln.ssq = (float *)device_alloc(d, (size_t)B * ((C + 15) / 16) * sizeof(float));
-        ln.lt_ws = device_alloc(d, d->lt_ws_bytes);
         ln.attn_ws = device_alloc(d, d->attn_ws_bytes);
     }
     HIP_CHECK(hipHostMalloc((void **)&d->staging, 7 * PREFILL_ROWS * sizeof(int32_t), hipHostMallocDefault));
@@ -1444,7 +1316,7 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
         r.mixed = a.xm;
         r.out = a.h;
         launch_norm(ln, r);
-        gemm(d, ln, ly.qkv, 3 * C, C, a.h, n, a.qkv, false);
+        gemm(ln, ly.qkv, 3 * C, C, a.h, n, a.qkv, SG_STORE);
         NC_CHECK(append_rows(a.qkv, 3LL * C, n, d->H, d->H, dpos, nullptr, dslot, ly.q_gain, ly.k_gain, d->cos, d->sin,
                              d->max_len, a.q, d->block_table, d->max_pages, layer_k(d, l), layer_v(d, l), layer_s(d, l),
                              (int)d->layer_pages, a.h, ly.ve, ly.ve_gate, dtok, C, d->stream));
@@ -1466,9 +1338,6 @@ static void destroy(Decoder *d) {
     hipStreamSynchronize(d->lane[1].stream);
     for (auto &kv : d->body_graphs)
         if (kv.second) hipGraphExecDestroy(kv.second);
-    lt_release(d);
-    hipblasLtDestroy(d->lt);
-    for (Lane &ln : d->lane) rocblas_destroy_handle(ln.blas);
     hipStreamDestroy(d->lane[1].stream);
     hipEventDestroy(d->fork);
     hipEventDestroy(d->join);
@@ -1707,4 +1576,11 @@ extern "C" int dec_debug_nucleus_cut(const float *e, int rows, int vocab, const 
     hipLaunchKernelGGL(nc::dec::nucleus_cut_kernel, dim3(rows), dim3(nc::dec::CHOICE_THREADS), 0,
                        (hipStream_t)stream, e, vocab, top_p, cut);
     return (int)hipGetLastError();
+}
+
+extern "C" int dec_debug_prefill_gemm(int epi, const void *w, int N, int K, const void *a, int M, void *out,
+                                      float *out_f32, const void *res, const float *rstd, void *stream) {
+    nc::PfGemm g = {(const uint16_t *)a, (const uint16_t *)w, M, N, K, (uint16_t *)out, out_f32, (const uint16_t *)res,
+                    rstd};
+    return nc::prefill_gemm(g, epi, (hipStream_t)stream);
 }

@@ -87,4 +87,18 @@ int slot_gemm_reduce(const SkinnyGemm &g, int epi, const float *part, long long 
  * finishes the sum itself. */
 int slot_gemm_partials(const SkinnyGemm &g, float *part, long long part_bytes, int S, hipStream_t stream);
 
+/* prefill_gemm.hip: out[m][n] = epilogue(sum_k a[m][k] w[n][k]) for the rows of a prefill call, every output's sum in
+ * one fixed order over K whatever M is. Epilogues SG_STORE, SG_RESID, SG_F32, SG_RELU2. Returns 0, a hipError_t, or -2
+ * when the shape (K a multiple of 128, N of 4, every array under 2 GiB) or an operand the epilogue needs does not fit. */
+struct PfGemm {
+    const uint16_t *a;     /* [M][K] bf16 */
+    const uint16_t *w;     /* [N][K] bf16 */
+    int M, N, K;
+    uint16_t *out;         /* [M][N] bf16 (SG_STORE, SG_RESID, SG_RELU2) */
+    float *out_f32;        /* [M][N] fp32 (SG_F32) */
+    const uint16_t *res;   /* [M][N] bf16 (SG_RESID) */
+    const float *rstd;     /* [M] fp32 (SG_RELU2) */
+};
+int prefill_gemm(const PfGemm &g, int epi, hipStream_t stream);
+
 }  // namespace nc

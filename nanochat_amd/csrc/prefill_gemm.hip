@@ -1,0 +1,207 @@
+/*
+ * The prefill GEMMs of the decoder runtime on gfx950: out[m][n] = epilogue(sum_k a[m][k] w[n][k]) for the rows of a
+ * dec_prefill call (M <= 8,192 prompt tokens), bf16 operands, fp32 sums. At these sizes a GEMM is bound by the matrix
+ * cores, so it is tiled for them: a workgroup of 8 waves owns a 256 x 256 output tile (2 x 4 waves of 128 x 64, 32
+ * accumulator tiles of 16 x 16 a wave; two waves a SIMD), walks K in stages of 32, and takes each
+ * stage's operands (256 rows of a and 256 rows of w, 64 bytes each: 32 KiB) from memory into LDS by LDS DMA, three
+ * stages ahead in a ring of four buffers, with hand-placed waits and a barrier without a memory fence per stage.
+ *
+ * Per stage a wave reads 4 fragments of its weight rows and 8 of its activation rows (one 16-byte LDS read each) and
+ * issues 32 MFMAs (v_mfma_f32_16x16x32_bf16: A = 16 weight rows n, B = 16 activation rows m), so lane (g, i) of a
+ * result tile holds columns n .. n + 3 (n = 16 t + 4 g) of row m = 16 u + i, and every epilogue writes 4 adjacent
+ * columns of a row. In LDS a row's 64 bytes (4 blocks of 16) keep block b at position b ^ ((row / 4) % 4), so the 16
+ * rows of a fragment read fall in distinct banks; each DMA lane fetches the global block that belongs at its LDS
+ * position.
+ *
+ * Every output's sum runs over K in one fixed order (the stages in order, each stage one MFMA's own order), whatever M
+ * is, so a row's result depends on its own a row alone: a prompt's rows give the same bits in any dec_prefill call.
+ * Every global access goes through a buffer resource over the exact extent of its array, so rows past M read zeros
+ * and store nothing; columns past N (a last partial tile of 256) are not stored.
+ *
+ * Epilogues (the SG_* kinds of nc_internal.h; decode.cu:133-168 for the math): SG_STORE bf16(s); SG_RESID
+ * bf16(s + res); SG_F32 s; SG_RELU2 bf16(relu(p) p) with p = s rstd[m].
+ *
+ * Reference: the prefill rows of dec_prefill run through the step's GEMM body, model/kernels/decode.cu:170-230,
+ * 295-359, 1041-1051.
+ */
+#include "nanochat_amd.h"
+#include "nc_device.h"
+#include "nc_internal.h"
+
+namespace nc {
+
+constexpr int PG_TM = 256, PG_TN = 256;        /* the output tile: rows m, columns n */
+constexpr int PG_KC = 32;                      /* k per stage: one MFMA's depth */
+constexpr int PG_ROWB = PG_KC * 2;             /* bytes of a row per stage */
+constexpr int PG_STAGE = (PG_TM + PG_TN) * PG_ROWB;
+constexpr int PG_RING = 4;                     /* stage buffers; three stages in flight */
+constexpr int PG_WAVES = 8;
+constexpr int PG_DMA = PG_STAGE / 1024;        /* 1 KiB DMA instructions per stage (16 rows each) */
+constexpr int PG_LOADS = PG_DMA / PG_WAVES;    /* ... per wave */
+constexpr int PG_PAST = 0x7FFF0000;            /* a byte offset past every operand's range */
+static_assert(PG_TM / 16 == PG_DMA / 2 && PG_TN / 16 == PG_DMA / 2, "DMA instructions q < 16 fill a, the rest w");
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef __attribute__((address_space(3))) void LdsPtr;
+
+__device__ __forceinline__ Rsrc pg_rsrc(const void *p, long long bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+/* Stage j's DMA into buf (j >= stages: offsets past the range, zeros and no memory access). Instruction q fills the
+ * buffer's rows 16 q .. 16 q + 15 (rows 0..255: a rows m0 + r; rows 256..511: w rows n0 + r - 256); lane l writes row
+ * 16 q + l / 4 at position l % 4 and fetches the global block (l % 4) ^ ((row / 4) % 4). Wave w issues q = w, w + 8,
+ * ... (its first two are a's, the last two w's). */
+__device__ __forceinline__ void pg_fetch(Rsrc ra, Rsrc rw, unsigned char *buf, int j, int stages, int m0, int n0,
+                                         int rowb, int wave, int lane) {
+    const bool live = j < stages;
+    const int kb = j * PG_ROWB, pos = lane & 3;
+#pragma unroll
+    for (int s = 0; s < PG_LOADS; s++) {
+        const int q = wave + PG_WAVES * s, row = 16 * q + (lane >> 2);
+        const bool is_a = s < PG_LOADS / 2;
+        const int grow = (is_a ? m0 : n0 - PG_TM) + row;
+        const int off = live ? grow * rowb + kb + ((pos ^ ((row >> 2) & 3)) << 4) : PG_PAST;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? ra : rw, (LdsPtr *)(buf + q * 1024), 16, off, 0, 0, 0);
+    }
+}
+
+/* s_waitcnt: all but this wave's DMA of the two newer stages in flight have landed, and its LDS reads are done.
+ * Encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8]. */
+__device__ __forceinline__ void pg_wait_stage() {
+    constexpr int n = 2 * PG_LOADS;
+    static_assert(n < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
+/* A workgroup barrier with no memory fence; the empty asm statements keep memory accesses from moving across it. */
+__device__ __forceinline__ void pg_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+/* One stage of a wave: fragments of its 64 weight rows (buffer rows 256 + 64 wn + 16 t + i) and 128 activation rows
+ * (128 wm + 16 u + i), then the 32 products. */
+__device__ __forceinline__ void pg_compute(const unsigned char *buf, f32x4 (&acc)[4][8], int wm, int wn, int i16,
+                                           int grp) {
+    bf16x8 fw[4], fa[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int row = PG_TM + 64 * wn + 16 * t + i16;
+        fw[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                               buf + row * PG_ROWB + ((grp ^ ((row >> 2) & 3)) << 4)));
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int row = 128 * wm + 16 * u + i16;
+        fa[u] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                               buf + row * PG_ROWB + ((grp ^ ((row >> 2) & 3)) << 4)));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc[t][u] = mfma16x16x32(fw[t], fa[u], acc[t][u]);
+}
+
+/* One ring position: wait for stage j, barrier (every wave's DMA of stage j has landed and every wave is done with
+ * stage j - 1), refill the buffer stage j - 1 used with stage j + 3, compute stage j. */
+#define PG_STEP(j, CUR, NXT)                                                                      \
+    do {                                                                                           \
+        pg_wait_stage();                                                                           \
+        pg_barrier();                                                                              \
+        pg_fetch(ra, rw, NXT, (j) + PG_RING - 1, stages, m0, n0, rowb, wave, lane);                \
+        pg_compute(CUR, acc, wm, wn, i16, grp);                                                    \
+    } while (0)
+
+template <int EPI>
+__global__ void __launch_bounds__(PG_WAVES * WAVE, 1) prefill_gemm_kernel(PfGemm g) {
+    __shared__ __align__(16) unsigned char b0[PG_STAGE], b1[PG_STAGE], b2[PG_STAGE], b3[PG_STAGE];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+    const int i16 = lane & 15, grp = lane >> 4, wm = wave >> 2, wn = wave & 3;
+    const int n0 = blockIdx.x * PG_TN, m0 = blockIdx.y * PG_TM;
+    const int rowb = g.K * 2, stages = g.K / PG_KC;
+    const Rsrc ra = pg_rsrc(g.a, (long long)g.M * rowb), rw = pg_rsrc(g.w, (long long)g.N * rowb);
+
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc[t][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    pg_fetch(ra, rw, b0, 0, stages, m0, n0, rowb, wave, lane);
+    pg_fetch(ra, rw, b1, 1, stages, m0, n0, rowb, wave, lane);
+    pg_fetch(ra, rw, b2, 2, stages, m0, n0, rowb, wave, lane);
+    for (int j = 0; j < stages; j += 4) {   /* stages is a multiple of 4 (K of 128, checked by the host) */
+        PG_STEP(j, b0, b3);
+        PG_STEP(j + 1, b1, b0);
+        PG_STEP(j + 2, b2, b1);
+        PG_STEP(j + 3, b3, b2);
+    }
+    __builtin_amdgcn_s_waitcnt(0);                 /* no DMA may land in LDS after this */
+
+    const Rsrc ro = pg_rsrc(EPI == SG_F32 ? (const void *)g.out_f32 : (const void *)g.out,
+                            (long long)g.M * g.N * (EPI == SG_F32 ? 4 : 2));
+    const Rsrc rr = pg_rsrc(g.res, EPI == SG_RESID ? (long long)g.M * g.N * 2 : 0);
+    const Rsrc rs = pg_rsrc(g.rstd, EPI == SG_RELU2 ? (long long)g.M * 4 : 0);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int m = m0 + 128 * wm + 16 * u + i16;
+        const float r = EPI == SG_RELU2 ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, m * 4, 0, 0))
+                                        : 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int n = n0 + 64 * wn + 16 * t + 4 * grp;
+            if (n >= g.N) continue;
+            const int at = m * g.N + n;   /* rows past M lie outside the views' ranges: no access */
+            float s[4] = {acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]};
+            if (EPI == SG_F32) {
+                __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(s[0]), __float_as_uint(s[1]),
+                                                             __float_as_uint(s[2]), __float_as_uint(s[3])},
+                                                       ro, at * 4, 0, 0);
+                continue;
+            }
+            if (EPI == SG_RESID) {
+                const u32x2 rv = __builtin_amdgcn_raw_buffer_load_b64(rr, at * 2, 0, 0);
+                const float res[4] = {bf16_to_f32((uint16_t)rv[0]), bf16_to_f32((uint16_t)(rv[0] >> 16)),
+                                      bf16_to_f32((uint16_t)rv[1]), bf16_to_f32((uint16_t)(rv[1] >> 16))};
+#pragma unroll
+                for (int e = 0; e < 4; e++) s[e] = s[e] + res[e];
+            } else if (EPI == SG_RELU2) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float p = s[e] * r;
+                    s[e] = fmaxf(p, 0.0f) * p;
+                }
+            }
+            uint16_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = f32_to_bf16(s[e]);
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{(uint32_t)o[0] | (uint32_t)o[1] << 16, (uint32_t)o[2] | (uint32_t)o[3] << 16}, ro, at * 2, 0, 0);
+        }
+    }
+}
+
+int prefill_gemm(const PfGemm &g, int epi, hipStream_t stream) {
+    if (g.M <= 0) return 0;
+    if (!g.a || !g.w || g.N <= 0 || g.K <= 0 || g.K % (PG_RING * PG_KC) || g.N % 4 ||
+        (long long)g.M * g.K * 2 >= (1LL << 31) || (long long)g.N * g.K * 2 >= (1LL << 31) ||
+        (long long)g.M * g.N * 4 >= (1LL << 31))
+        return NC_ERR_SHAPE;
+    const bool f32 = epi == SG_F32;
+    if ((f32 ? !g.out_f32 : !g.out) || (epi == SG_RESID && !g.res) || (epi == SG_RELU2 && !g.rstd) ||
+        (epi != SG_STORE && epi != SG_RESID && epi != SG_F32 && epi != SG_RELU2))
+        return NC_ERR_SHAPE;
+    const dim3 grid((g.N + PG_TN - 1) / PG_TN, (g.M + PG_TM - 1) / PG_TM), block(PG_WAVES * WAVE);
+    switch (epi) {
+    case SG_STORE: hipLaunchKernelGGL(prefill_gemm_kernel<SG_STORE>, grid, block, 0, stream, g); break;
+    case SG_RESID: hipLaunchKernelGGL(prefill_gemm_kernel<SG_RESID>, grid, block, 0, stream, g); break;
+    case SG_F32: hipLaunchKernelGGL(prefill_gemm_kernel<SG_F32>, grid, block, 0, stream, g); break;
+    default: hipLaunchKernelGGL(prefill_gemm_kernel<SG_RELU2>, grid, block, 0, stream, g); break;
+    }
+    return (int)hipGetLastError();
+}
+
+}  // namespace nc

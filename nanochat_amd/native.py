@@ -7,7 +7,7 @@ missing library builds both once.
 
     libnanochat_kv.so      the kernel entry points of include/nanochat_amd.h
     libnanochat_decode.so  the decoder runtime of include/nanochat_decode.h (the same kernels, plus the
-                           dec_* runtime, its hand-written step GEMMs and hipBLASLt prefill GEMMs);
+                           dec_* runtime and its hand-written step and prefill GEMMs);
                            hip_library("decode") loads it, as the reference's cuda_library("decode")
                            loads decode.cu
 """
@@ -27,7 +27,7 @@ LIB_DIR = PACKAGE / "lib"
 LIBRARY = LIB_DIR / "libnanochat_kv.so"
 DECODE_LIBRARY = LIB_DIR / "libnanochat_decode.so"
 KERNEL_SOURCES = [CSRC / "kv_append.hip", CSRC / "attention.hip", CSRC / "ve_gate.hip", CSRC / "flash_attn.hip"]
-DECODE_SOURCES = [CSRC / "decoder.hip", CSRC / "slot_gemm.hip"]
+DECODE_SOURCES = [CSRC / "decoder.hip", CSRC / "slot_gemm.hip", CSRC / "prefill_gemm.hip"]
 SOURCES = KERNEL_SOURCES + DECODE_SOURCES
 HEADERS = [CSRC / "nc_device.h", CSRC / "nc_internal.h", INCLUDE / "nanochat_amd.h", INCLUDE / "nanochat_decode.h"]
 HEAD_DIM = 128
@@ -54,15 +54,12 @@ def _run(cmd: list[str]) -> None:
 def build() -> tuple[Path, Path]:
     """Compile every source once, then link both libraries (each written to a temporary file, then renamed)."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    rocm_lib = Path(hipcc()).parent.parent / "lib"
     with tempfile.TemporaryDirectory(dir=LIB_DIR) as tmp:
         objects = {}
         for src in SOURCES:
             objects[src] = Path(tmp) / (src.stem + ".o")
             _run([hipcc(), *HIPCC_FLAGS, "-c", "-o", str(objects[src]), str(src)])
-        for output, sources, libs in ((LIBRARY, KERNEL_SOURCES, []),
-                                      (DECODE_LIBRARY, KERNEL_SOURCES + DECODE_SOURCES,
-                                       [f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lhipblaslt", "-lrocblas"])):
+        for output, sources, libs in ((LIBRARY, KERNEL_SOURCES, []), (DECODE_LIBRARY, KERNEL_SOURCES + DECODE_SOURCES, [])):
             built = Path(tmp) / output.name
             _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(built),
                   *(str(objects[s]) for s in sources), *libs])
@@ -147,6 +144,8 @@ DECODE_SIGNATURES = {
     "dec_debug_slot_gemm_ssq": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                  c_void_p], c_int),
     "dec_debug_nucleus_cut": ([c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p], c_int),
+    "dec_debug_prefill_gemm": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p], c_int),
 }
 
 LIBRARIES = {"nanochat_kv": (LIBRARY, SIGNATURES), "decode": (DECODE_LIBRARY, DECODE_SIGNATURES)}

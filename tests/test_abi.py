@@ -327,3 +327,19 @@ def test_nucleus_cut_declines_shapes():
     assert lib.dec_debug_nucleus_cut(DUMMY, -1, 64, DUMMY, DUMMY, None) == -2
     assert lib.dec_debug_nucleus_cut(DUMMY, 1, 1 << 25, DUMMY, DUMMY, None) == -2
     assert lib.dec_debug_nucleus_cut(DUMMY, 0, 64, DUMMY, DUMMY, None) == 0
+
+
+def test_prefill_gemm_declines_without_launching():
+    """Shapes and missing operands the prefill GEMM cannot take return -2 before any device call; M = 0 is a no-op."""
+    from nanochat_amd.native import hip_library
+
+    lib = hip_library("decode")
+    STORE, RELU2, RESID, F32 = 0, 2, 3, 4
+    assert lib.dec_debug_prefill_gemm(STORE, DUMMY, 4992, 1600, DUMMY, 8, DUMMY, None, None, None, None) == -2   # K
+    assert lib.dec_debug_prefill_gemm(STORE, DUMMY, 4990, 1664, DUMMY, 8, DUMMY, None, None, None, None) == -2   # N
+    assert lib.dec_debug_prefill_gemm(STORE, DUMMY, 4992, 1664, DUMMY, 8, None, None, None, None, None) == -2    # out
+    assert lib.dec_debug_prefill_gemm(F32, DUMMY, 4992, 1664, DUMMY, 8, DUMMY, None, None, None, None) == -2     # fp32
+    assert lib.dec_debug_prefill_gemm(RESID, DUMMY, 1664, 1664, DUMMY, 8, DUMMY, None, None, None, None) == -2   # res
+    assert lib.dec_debug_prefill_gemm(RELU2, DUMMY, 6656, 1664, DUMMY, 8, DUMMY, None, None, None, None) == -2   # rstd
+    assert lib.dec_debug_prefill_gemm(1, DUMMY, 1664, 1664, DUMMY, 8, DUMMY, DUMMY, DUMMY, DUMMY, None) == -2    # kind
+    assert lib.dec_debug_prefill_gemm(STORE, DUMMY, 4992, 1664, DUMMY, 0, DUMMY, None, None, None, None) == 0
