@@ -1300,7 +1300,6 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
     HIP_CHECK(hipMemcpyAsync(d->rows, s, 7 * PREFILL_ROWS * sizeof(int32_t), hipMemcpyHostToDevice, d->stream));
     HIP_CHECK(hipEventRecord(d->staged, d->stream));
     int32_t *dtok = d->rows;
-    const int32_t *dpos = d->rows + PREFILL_ROWS, *dslot = d->rows + 2 * PREFILL_ROWS;
     const int32_t *drow0 = d->rows + 3 * PREFILL_ROWS, *dcount = d->rows + 4 * PREFILL_ROWS,
                   *drslot = d->rows + 5 * PREFILL_ROWS, *dstart = d->rows + 6 * PREFILL_ROWS;
     const int C = d->C;
@@ -1317,9 +1316,10 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
         r.out = a.h;
         launch_norm(ln, r);
         gemm(ln, ly.qkv, 3 * C, C, a.h, n, a.qkv, SG_STORE);
-        NC_CHECK(append_rows(a.qkv, 3LL * C, n, d->H, d->H, dpos, nullptr, dslot, ly.q_gain, ly.k_gain, d->cos, d->sin,
-                             d->max_len, a.q, d->block_table, d->max_pages, layer_k(d, l), layer_v(d, l), layer_s(d, l),
-                             (int)d->layer_pages, a.h, ly.ve, ly.ve_gate, dtok, C, d->stream));
+        NC_CHECK(append_runs(a.qkv, 3LL * C, runs, max_count, drow0, dcount, dstart, drslot, d->H, d->H, ly.q_gain,
+                             ly.k_gain, d->cos, d->sin, d->max_len, a.q, d->block_table, d->max_pages, layer_k(d, l),
+                             layer_v(d, l), layer_s(d, l), (int)d->layer_pages, a.h, ly.ve, ly.ve_gate, dtok, C,
+                             d->stream));
         if (l == d->L - 1) break;  /* no row chooses a token: the last layer only caches its K and V */
         NC_CHECK(prefill_runs(a.q, layer_k(d, l), layer_v(d, l), layer_s(d, l), d->block_table, d->max_pages,
                               (int)d->layer_pages, dstart, drow0, dcount, drslot, runs, max_count, d->H, d->H, ly.window,

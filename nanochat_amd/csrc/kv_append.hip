@@ -14,94 +14,159 @@
 
 namespace nc {
 
-/* Quantize one row (lane pair x1 = dim l, x2 = dim l + 64, bf16 values) and store its codes into a page
- * at the byte offsets OFF(slot, dim); lane 0 stores the scale. */
-template <int (*OFF)(int, int)>
-__device__ __forceinline__ void quantize_store(float x1, float x2, uint8_t *page, float *scale_at, int slot, int lane) {
-    uint32_t c1, c2;
-    const float scale = quantize_pair(x1, x2, c1, c2);
-    page[OFF(slot, lane)] = (uint8_t)c1;
-    page[OFF(slot, lane + HALF)] = (uint8_t)c2;
-    if (lane == 0) *scale_at = scale;
-}
-
 struct AppendArgs {
     const uint16_t *k, *v;     /* plain append: [B][T][Hkv][128] at token_stride */
     const uint16_t *qkv;       /* fused append: [B][T][(Hq + 2 Hkv) 128] at token_stride */
     long long token_stride;
     int B, T, Hq, Hkv;
     const int32_t *start_pos, *num_new;
+    const int32_t *row0;       /* NULL: sequence b's tokens are rows b T + t; else rows row0[b] + t */
     const float *q_gain, *k_gain, *cos, *sin;
     int rope_len;
-    uint16_t *q_out;           /* [B][T][Hq][128] */
+    uint16_t *q_out;           /* [rows][Hq][128] */
     const int32_t *block_table;
-    const int32_t *seq_slot;   /* NULL, or sequence b's block-table row (the decoder's prefill rows) */
+    const int32_t *seq_slot;   /* NULL, or sequence b's block-table row (the decoder's prefill runs) */
     /* value embeddings (fused append, NULL ve: none): v += 2 sigmoid(ve_gate[head] . h) ve[tokens[token]] */
-    const uint16_t *ve_h, *ve;  /* h: [B T][C] the layer's normed input; ve: [vocab][C] */
+    const uint16_t *ve_h, *ve;  /* h: [rows][C] the layer's normed input; ve: [vocab][C] */
     const float *ve_gate;       /* [Hkv][C] */
-    const int32_t *ve_tokens;   /* [B T] */
+    const int32_t *ve_tokens;   /* [rows] */
     int C;
     int max_pages;
     uint8_t *k_pages, *v_pages;
     float *kv_scale;          /* [num_pages][Hkv][2][16]: K scales, then V scales */
     int num_pages;
+    int pages_per_seq;        /* grid x = B pages_per_seq: the most cache pages T positions can touch */
 };
 
-/* Grid: x = token (b T + t), y = groups of 4 head rows; block = 4 waves, one head row each.
- * FUSED: rows [0, Hq) are q heads (normed, rotated, stored to q_out), rows [Hq, Hq + Hkv) KV heads (k
- * normed and rotated, then k and v quantized into the cache). Plain: rows [0, Hkv) KV heads, no rotation. */
+/* Cache pages a run of T positions can touch: (T - 1) / 16 + 1 when aligned, one more when not. */
+static inline int append_pages_per_seq(int T) { return (T + PAGE - 2) / PAGE + 1; }
+
+/* Grid: x = (sequence b, k-th cache page its new positions touch), y = head groups; block = 4 waves.
+ * The new positions of b are [max(start, 0), start + min(T, num_new[b])), cut at rope_len when FUSED (the rest are
+ * skipped, as are all of b's positions on a page past max_pages or whose table entry lies outside the pool). The
+ * work-group takes those of them on page k: slots [s_lo, s_hi) of that page. Rows are computed four a wave, 16 lanes
+ * a row (nc_row.h's 16-lane form, the same bits as the one-row-a-wave form of the fused decode step).
+ * y < Hkv: KV head y. Wave w computes the k rows of slots 4 w .. 4 w + 3 (norm and rotation when FUSED, then the
+ * quantizer), then their v rows (the value-embedding mix when given, then the quantizer), and writes the codes into an
+ * LDS image of the page in the cache's layout. The work-group then stores the image with one 16-byte store a lane; a
+ * K block holds one slot, a V block four (slots 4 g .. 4 g + 3), and a V block holding slots outside [s_lo, s_hi) is
+ * stored byte by byte, so the page's other slots keep their bytes. The 16 scales of K and of V go out the same way.
+ * y >= Hkv (FUSED only): q head 4 (y - Hkv) + w a wave, four of the page's slots at a time, normed and rotated into
+ * q_out. */
 template <bool FUSED>
 __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (row >= (FUSED ? a.Hq + a.Hkv : a.Hkv)) return;
-    const long long tok = blockIdx.x;
-    const int b = (int)(tok / a.T), t = (int)(tok % a.T);
-    if (a.num_new && t >= a.num_new[b]) return;
-    const int p = a.start_pos[b] + t;
-    if (p < 0) return;
-    if (FUSED && p >= a.rope_len) return;
-    const uint16_t *in = (FUSED ? a.qkv : a.k) + tok * a.token_stride;
-    float c = 0.0f, s = 0.0f;
-    if (FUSED) {
-        c = a.cos[(long long)p * HALF + lane];
-        s = a.sin[(long long)p * HALF + lane];
-    }
-    if (FUSED && row < a.Hq) {
-        const uint16_t *x = in + row * HEAD_DIM;
-        float y1, y2;
-        norm_rope_pair(bf16_to_f32(x[lane]), bf16_to_f32(x[lane + HALF]), a.q_gain[lane], a.q_gain[lane + HALF], c, s,
-                       y1, y2);
-        uint16_t *q = a.q_out + (tok * a.Hq + row) * HEAD_DIM;
-        q[lane] = f32_to_bf16(y1);
-        q[lane + HALF] = f32_to_bf16(y2);
+    __shared__ __align__(16) uint8_t img[2][PAGE_BYTES];
+    __shared__ float img_scale[2][PAGE];
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+    const int r = lane >> 4, i = lane & 15;   /* the lane's row of the wave's four, its place in the row */
+    const int b = blockIdx.x / a.pages_per_seq, k = blockIdx.x % a.pages_per_seq;
+    const int sp = a.start_pos[b];
+    const int n = a.num_new ? min(a.num_new[b], a.T) : a.T;
+    const long long lo = max(sp, 0);
+    long long hi = (long long)sp + n;
+    if (FUSED && hi > a.rope_len) hi = a.rope_len;
+    if (lo >= hi) return;
+    const long long lp = lo / PAGE + k, pg0 = lp * PAGE;
+    const int s_lo = (int)(max(lo, pg0) - pg0), s_hi = (int)(min(hi, pg0 + PAGE) - pg0);
+    if (s_lo >= s_hi) return;
+    const long long tok_at = (a.row0 ? (long long)a.row0[b] : (long long)b * a.T) - sp;   /* + position = row */
+
+    if (FUSED && (int)blockIdx.y >= a.Hkv) {
+        const int h = 4 * ((int)blockIdx.y - a.Hkv) + wave;
+        if (h >= a.Hq) return;
+        float g[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) g[j] = a.q_gain[i + 16 * j];
+        for (int s0 = s_lo; s0 < s_hi; s0 += 4) {
+            const int slot = s0 + r;   /* past s_hi: computes the last slot again and stores nothing */
+            const long long p = pg0 + min(slot, s_hi - 1), tok = tok_at + p;
+            const uint16_t *row = a.qkv + tok * a.token_stride + h * HEAD_DIM;
+            float x[8], c[4], sn[4], y[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[j] = bf16_to_f32(row[i + 16 * j]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                c[j] = a.cos[p * HALF + i + 16 * j];
+                sn[j] = a.sin[p * HALF + i + 16 * j];
+            }
+            norm_rope_quad(x, g, c, sn, y);
+            if (slot < s_hi) {
+                uint16_t *q = a.q_out + (tok * a.Hq + h) * HEAD_DIM;
+#pragma unroll
+                for (int j = 0; j < 8; j++) q[i + 16 * j] = f32_to_bf16(y[j]);
+            }
+        }
         return;
     }
-    const int kvh = FUSED ? row - a.Hq : row;
-    const int lp = p / PAGE;
+
+    const int kvh = blockIdx.y;
     if (lp >= a.max_pages) return;
     const int trow = a.seq_slot ? a.seq_slot[b] : b;
     const int page = a.block_table[(long long)trow * a.max_pages + lp];
     if (page < 0 || page >= a.num_pages) return;
-    const int slot = p % PAGE;
     const long long at = (long long)page * a.Hkv + kvh;
-    const uint16_t *kx = FUSED ? in + (a.Hq + kvh) * HEAD_DIM : in + kvh * HEAD_DIM;
-    const uint16_t *vx = FUSED ? in + (a.Hq + a.Hkv + kvh) * HEAD_DIM : a.v + tok * a.token_stride + kvh * HEAD_DIM;
-    float k1 = bf16_to_f32(kx[lane]), k2 = bf16_to_f32(kx[lane + HALF]);
+
+    const int slot = 4 * wave + r;
+    const bool live = slot >= s_lo && slot < s_hi;   /* rows of other slots compute a new one and store nothing */
+    const long long p = pg0 + min(max(slot, s_lo), s_hi - 1), tok = tok_at + p;
+    const uint16_t *kx = FUSED ? a.qkv + tok * a.token_stride + (a.Hq + kvh) * HEAD_DIM
+                               : a.k + tok * a.token_stride + kvh * HEAD_DIM;
+    const uint16_t *vx = FUSED ? a.qkv + tok * a.token_stride + (a.Hq + a.Hkv + kvh) * HEAD_DIM
+                               : a.v + tok * a.token_stride + kvh * HEAD_DIM;
+    float kr[8], vr[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        kr[j] = bf16_to_f32(kx[i + 16 * j]);
+        vr[j] = bf16_to_f32(vx[i + 16 * j]);
+    }
     if (FUSED) {
-        float y1, y2;
-        norm_rope_pair(k1, k2, a.k_gain[lane], a.k_gain[lane + HALF], c, s, y1, y2);
-        k1 = bf16_to_f32(f32_to_bf16(y1));
-        k2 = bf16_to_f32(f32_to_bf16(y2));
+        float g[8], c[4], sn[4], y[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) g[j] = a.k_gain[i + 16 * j];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            c[j] = a.cos[p * HALF + i + 16 * j];
+            sn[j] = a.sin[p * HALF + i + 16 * j];
+        }
+        norm_rope_quad(kr, g, c, sn, y);
+#pragma unroll
+        for (int j = 0; j < 8; j++) kr[j] = bf16_to_f32(f32_to_bf16(y[j]));
     }
-    quantize_store<k_page_offset>(k1, k2, a.k_pages + at * PAGE_BYTES, a.kv_scale + at * 2 * PAGE + slot, slot, lane);
-    float v1 = bf16_to_f32(vx[lane]), v2 = bf16_to_f32(vx[lane + HALF]);
-    if (FUSED && a.ve) {
-        ve_mix_pair(a.ve_h + tok * a.C, a.ve_gate + (long long)kvh * a.C, a.C,
-                    a.ve + (long long)a.ve_tokens[tok] * a.C + kvh * HEAD_DIM, lane, v1, v2);
+    uint32_t code[8];
+    float scale = quantize_quad(kr, code);
+    if (live) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) img[0][k_page_offset(slot, i + 16 * j)] = (uint8_t)code[j];
+        if (i == 0) img_scale[0][slot] = scale;
     }
-    quantize_store<v_page_offset>(v1, v2, a.v_pages + at * PAGE_BYTES, a.kv_scale + (at * 2 + 1) * PAGE + slot, slot,
-                                  lane);
+    if (FUSED && a.ve)
+        ve_mix_quad(a.ve_h + tok * a.C, a.ve_gate + (long long)kvh * a.C, a.C,
+                    a.ve + (long long)a.ve_tokens[tok] * a.C + kvh * HEAD_DIM, i, vr);
+    scale = quantize_quad(vr, code);
+    if (live) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) img[1][v_page_offset(slot, i + 16 * j)] = (uint8_t)code[j];
+        if (i == 0) img_scale[1][slot] = scale;
+    }
+    __syncthreads();
+
+    const int t = threadIdx.x, blk = t & 127, kind = t >> 7;   /* kind 0: K block, 1: V block */
+    uint8_t *dst = (kind ? a.v_pages : a.k_pages) + at * PAGE_BYTES + blk * 16;
+    const uint8_t *src = img[kind] + blk * 16;
+    const int s_first = kind ? 4 * ((blk >> 4) & 3) : (blk & 15), s_count = kind ? 4 : 1;
+    if (s_first >= s_lo && s_first + s_count <= s_hi) {
+        *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
+    } else if (kind && s_first < s_hi && s_first + s_count > s_lo) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {   /* byte e holds slot s_first + e % 4 */
+            const int s = s_first + (e & 3);
+            if (s >= s_lo && s < s_hi) dst[e] = src[e];
+        }
+    }
+    if (t < 2 * PAGE) {
+        const int s = t & (PAGE - 1), kv = t >> 4;
+        if (s >= s_lo && s < s_hi) a.kv_scale[(at * 2 + kv) * PAGE + s] = img_scale[kv][s];
+    }
 }
 
 /* The training-form prologue (reference model/kernels/qk_prologue.cu:8-32): token p = blockIdx.x of rows/H,
@@ -183,9 +248,11 @@ __global__ void __launch_bounds__(HEAD_DIM) qkp_gain_sum_kernel(const float *par
 
 static thread_local int last_error = NC_OK;
 
-static int launch_append(const AppendArgs &a, bool fused, hipStream_t stream) {
-    const int rows = fused ? a.Hq + a.Hkv : a.Hkv;
-    const dim3 grid((unsigned)((long long)a.B * a.T), (unsigned)((rows + 3) / 4));
+static int launch_append(AppendArgs a, bool fused, hipStream_t stream) {
+    a.pages_per_seq = append_pages_per_seq(a.T);
+    const long long x = (long long)a.B * a.pages_per_seq;
+    if (x * 256 >= (1LL << 32)) return NC_ERR_SHAPE;
+    const dim3 grid((unsigned)x, (unsigned)(fused ? a.Hkv + (a.Hq + 3) / 4 : a.Hkv));
     if (fused)
         hipLaunchKernelGGL(append_kernel<true>, grid, dim3(256), 0, stream, a);
     else
@@ -193,21 +260,21 @@ static int launch_append(const AppendArgs &a, bool fused, hipStream_t stream) {
     return (int)hipGetLastError();
 }
 
-/* The fused append for the decoder runtime: as nc_qk_norm_rope_append_fp8 with T = 1, sequence b (a slot or a
- * prefill row) at position pos[b], using block-table row seq_slot[b] (NULL: b) and skipping b when
- * num_new[b] == 0 (NULL: none skipped); with ve non-NULL, v gets the layer's value embedding. Arguments are
- * checked by the caller. */
-int append_rows(const uint16_t *qkv, long long token_stride, int n, int Hq, int Hkv, const int32_t *pos,
-                const int32_t *num_new, const int32_t *seq_slot, const float *q_gain, const float *k_gain,
-                const float *cos, const float *sin, int rope_len, uint16_t *q_out, const int32_t *block_table,
-                int max_pages, uint8_t *k_pages, uint8_t *v_pages, float *kv_scale, int num_pages,
-                const uint16_t *ve_h, const uint16_t *ve, const float *ve_gate, const int32_t *tokens, int C,
-                hipStream_t stream) {
+/* The fused append for the decoder runtime's prefill: runs of rows, run r being rows row0[r] .. + count[r] - 1 of
+ * qkv (token_stride apart), at positions start[r] .. of block-table row seq_slot[r], max_count the longest run; with
+ * ve non-NULL, v gets the layer's value embedding. Arguments are checked by the caller. */
+int append_runs(const uint16_t *qkv, long long token_stride, int runs, int max_count, const int32_t *row0,
+                const int32_t *count, const int32_t *start, const int32_t *seq_slot, int Hq, int Hkv,
+                const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
+                uint16_t *q_out, const int32_t *block_table, int max_pages, uint8_t *k_pages, uint8_t *v_pages,
+                float *kv_scale, int num_pages, const uint16_t *ve_h, const uint16_t *ve, const float *ve_gate,
+                const int32_t *tokens, int C, hipStream_t stream) {
+    if (runs <= 0 || max_count <= 0) return NC_OK;
     AppendArgs a = {};
     a.qkv = qkv;
     a.token_stride = token_stride;
-    a.B = n; a.T = 1; a.Hq = Hq; a.Hkv = Hkv;
-    a.start_pos = pos; a.num_new = num_new; a.seq_slot = seq_slot;
+    a.B = runs; a.T = max_count; a.Hq = Hq; a.Hkv = Hkv;
+    a.start_pos = start; a.num_new = count; a.row0 = row0; a.seq_slot = seq_slot;
     a.q_gain = q_gain; a.k_gain = k_gain; a.cos = cos; a.sin = sin; a.rope_len = rope_len;
     a.q_out = q_out;
     a.block_table = block_table; a.max_pages = max_pages;

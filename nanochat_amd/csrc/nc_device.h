@@ -72,17 +72,42 @@ __device__ __forceinline__ float pair_sum16(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-/* Sum over the wave by an xor butterfly (offsets 32, 16, ..., 1): every lane ends with the same value. */
-__device__ __forceinline__ float wave_sum_butterfly(float v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v = v + __shfl_xor(v, o, WAVE);
-    return v;
+/* This lane's value of lane L ^ M (M = 8, 4, 2, 1) by DPP, a VALU operand modifier with no LDS round trip:
+ * row_ror:8 within each row of 16 lanes is xor 8; row_half_mirror (i -> 7 - i within 8 lanes) followed by
+ * quad_perm [3,2,1,0] (j -> j ^ 3) is xor 4; quad_perm [2,3,0,1] and [1,0,3,2] are xor 2 and xor 1. */
+template <int M>
+__device__ __forceinline__ float lane_xor_dpp(float v) {
+    static_assert(M == 8 || M == 4 || M == 2 || M == 1, "DPP xor partners within 16 lanes");
+    const int x = __float_as_int(v);
+    int r;
+    if constexpr (M == 8) r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);
+    else if constexpr (M == 4)
+        r = __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF, false);
+    else if constexpr (M == 2) r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);
+    else r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);
+    return __int_as_float(r);
 }
 
+/* Sum over the wave by an xor butterfly (offsets 32, 16, ..., 1): at each offset o every lane L adds its value and
+ * lane L ^ o's, so both lanes of a pair hold the same sum (a + b and b + a are the same fp32 value) and every lane
+ * ends with the same result. The partners come from permlane swaps (32, 16) and DPP (8 .. 1), all 64 lanes active. */
+__device__ __forceinline__ float wave_sum_butterfly(float v) {
+    v = pair_sum32(v);
+    v = pair_sum16(v);
+    v = v + lane_xor_dpp<8>(v);
+    v = v + lane_xor_dpp<4>(v);
+    v = v + lane_xor_dpp<2>(v);
+    return v + lane_xor_dpp<1>(v);
+}
+
+/* Max over the wave by the same butterfly. */
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
+    v = pair_max32(v);
+    v = pair_max16(v);
+    v = fmaxf(v, lane_xor_dpp<8>(v));
+    v = fmaxf(v, lane_xor_dpp<4>(v));
+    v = fmaxf(v, lane_xor_dpp<2>(v));
+    return fmaxf(v, lane_xor_dpp<1>(v));
 }
 
 /* Byte offset of (slot, dim) inside a K page: the 16x16x32 MFMA A-operand tiling (lane = group*16 + slot

@@ -12,14 +12,16 @@ namespace nc {
 /* kv_append.hip: the status nc_last_error() reports for the calling host thread (the void entry points set it). */
 void set_last_error(int status);
 
-/* kv_append.hip: the fused QK-norm/RoPE fp8 append of n sequences of one token each; ve non-NULL adds the
- * value embedding 2 sigmoid(ve_gate[head] . ve_h[b]) ve[tokens[b]] to v before it is quantized (C: ve_h's width). */
-int append_rows(const uint16_t *qkv, long long token_stride, int n, int Hq, int Hkv, const int32_t *pos,
-                const int32_t *num_new, const int32_t *seq_slot, const float *q_gain, const float *k_gain,
-                const float *cos, const float *sin, int rope_len, uint16_t *q_out, const int32_t *block_table,
-                int max_pages, uint8_t *k_pages, uint8_t *v_pages, float *kv_scale, int num_pages,
-                const uint16_t *ve_h, const uint16_t *ve, const float *ve_gate, const int32_t *tokens, int C,
-                hipStream_t stream);
+/* kv_append.hip: the fused QK-norm/RoPE fp8 append of runs of rows: run r is rows row0[r] .. + count[r] - 1 of
+ * qkv at positions start[r] .. of block-table row seq_slot[r] (max_count: the longest run); ve non-NULL adds the
+ * value embedding 2 sigmoid(ve_gate[head] . ve_h[row]) ve[tokens[row]] to v before it is quantized (C: ve_h's
+ * width). */
+int append_runs(const uint16_t *qkv, long long token_stride, int runs, int max_count, const int32_t *row0,
+                const int32_t *count, const int32_t *start, const int32_t *seq_slot, int Hq, int Hkv,
+                const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
+                uint16_t *q_out, const int32_t *block_table, int max_pages, uint8_t *k_pages, uint8_t *v_pages,
+                float *kv_scale, int num_pages, const uint16_t *ve_h, const uint16_t *ve, const float *ve_gate,
+                const int32_t *tokens, int C, hipStream_t stream);
 
 /* The fused decode step's inputs: each sequence's token row as the qkv projection left it, and what the cache
  * append needs (the fused append's arguments, for one token per sequence at position seq_lens[b] - 1). */

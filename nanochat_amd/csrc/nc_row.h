@@ -49,4 +49,72 @@ __device__ __forceinline__ void ve_mix_pair(const uint16_t *h, const float *w, i
     v2 = bf16_to_f32(f32_to_bf16(v2 + g * bf16_to_f32(e[lane + HALF])));
 }
 
+/* The same row math with 16 lanes a row, four rows a wave (the append kernel's form). Lane i of a 16-lane group
+ * holds its row's dims i + 16 j, j = 0..7, as x[j]: its rotation pairs (x[j], x[j + 4]) are dims (i + 16 j, i + 16 j
+ * + 64), and it stands for lanes l = i + 16 j (j < 4) of the one-row-a-wave form above. That form's butterfly steps 32
+ * and 16 pair l with l ^ 32 (j with j ^ 2) and l ^ 16 (j with j ^ 1), so they are lane-local here, and steps 8 .. 1
+ * are the same DPP exchanges within the group's 16 lanes: every sum is formed in the same order, and every result
+ * has the same bits as the one-row-a-wave form's. All 64 lanes of the wave must call these together. */
+__device__ __forceinline__ float quad_row_sum(const float (&p)[4]) {
+    float v = (p[0] + p[2]) + (p[1] + p[3]);
+    v = v + lane_xor_dpp<8>(v);
+    v = v + lane_xor_dpp<4>(v);
+    v = v + lane_xor_dpp<2>(v);
+    return v + lane_xor_dpp<1>(v);
+}
+
+__device__ __forceinline__ float quad_row_max(const float (&m)[4]) {
+    float v = fmaxf(fmaxf(m[0], m[2]), fmaxf(m[1], m[3]));
+    v = fmaxf(v, lane_xor_dpp<8>(v));
+    v = fmaxf(v, lane_xor_dpp<4>(v));
+    v = fmaxf(v, lane_xor_dpp<2>(v));
+    return fmaxf(v, lane_xor_dpp<1>(v));
+}
+
+/* norm_rope_pair in the 16-lane form: g, the gains of the lane's dims; c, s the rotation of its pairs. */
+__device__ __forceinline__ void norm_rope_quad(const float (&x)[8], const float (&g)[8], const float (&c)[4],
+                                               const float (&s)[4], float (&y)[8]) {
+    float part[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) part[j] = x[j] * x[j] + x[j + 4] * x[j + 4];
+    const float ss = quad_row_sum(part);
+    const float v = ss / 128.0f + FLT_EPS;
+    const float r = 1.0f / __builtin_sqrtf(v);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float n1 = (x[j] * r) * g[j];
+        const float n2 = (x[j + 4] * r) * g[j + 4];
+        y[j] = n1 * c[j] + n2 * s[j];
+        y[j + 4] = n2 * c[j] - n1 * s[j];
+    }
+}
+
+/* quantize_pair in the 16-lane form: the row's scale, and the lane's eight codes. */
+__device__ __forceinline__ float quantize_quad(const float (&x)[8], uint32_t (&code)[8]) {
+    float m[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) m[j] = fmaxf(fabsf(x[j]), fabsf(x[j + 4]));
+    const float amax = quad_row_max(m);
+    const float scale = amax > 0.0f ? amax / FP8_MAX : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) code[j] = e4m3_encode(fminf(fmaxf(x[j] / scale, -FP8_MAX), FP8_MAX));
+    return scale;
+}
+
+/* ve_mix_pair in the 16-lane form (i: the lane's index in its group): the lane runs the FMA chains of the four
+ * one-row-a-wave lanes it stands for. */
+__device__ __forceinline__ void ve_mix_quad(const uint16_t *h, const float *w, int C, const uint16_t *e, int i,
+                                            float (&v)[8]) {
+    float d[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        d[j] = 0.0f;
+        for (int k = i + 16 * j; k < C; k += WAVE) d[j] = __builtin_fmaf(bf16_to_f32(h[k]), w[k], d[j]);
+    }
+    const float t = quad_row_sum(d);
+    const float g = 2.0f * (1.0f / (1.0f + expf(-t)));
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = bf16_to_f32(f32_to_bf16(v[j] + g * bf16_to_f32(e[i + 16 * j])));
+}
+
 }  // namespace nc

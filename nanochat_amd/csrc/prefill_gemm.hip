@@ -13,6 +13,9 @@
  * rows of a fragment read fall in distinct banks; each DMA lane fetches the global block that belongs at its LDS
  * position.
  *
+ * Workgroups take their tiles in an XCD-aware order (pg_tile), so the workgroups an XCD runs together share operand
+ * tiles in its L2.
+ *
  * Every output's sum runs over K in one fixed order (the stages in order, each stage one MFMA's own order), whatever M
  * is, so a row's result depends on its own a row alone: a prompt's rows give the same bits in any dec_prefill call.
  * Every global access goes through a buffer resource over the exact extent of its array, so rows past M read zeros
@@ -116,12 +119,28 @@ __device__ __forceinline__ void pg_compute(const unsigned char *buf, f32x4 (&acc
         pg_compute(CUR, acc, wm, wn, i16, grp);                                                    \
     } while (0)
 
+/* Which output tile workgroup L of T takes. Workgroups are dispatched to the 8 XCDs in turn (L % 8), each XCD with its
+ * own L2, so tiles are numbered XCD by XCD: XCD k takes a contiguous run of the tile order, and within it consecutive
+ * workgroups walk PG_GROUP m-tiles (the fastest) by one n-tile at a time. The workgroups an XCD runs at once then share
+ * a few a and w tiles, read from its L2 rather than each from memory. Returns (n-tile, m-tile). */
+constexpr int PG_XCDS = 8, PG_GROUP = 4;
+
+__device__ __forceinline__ int2 pg_tile(int L, int T, int nx) {
+    const int k = L % PG_XCDS, r = L / PG_XCDS, per = T / PG_XCDS, extra = T % PG_XCDS;
+    const int id = k * per + min(k, extra) + r;                /* a bijection of [0, T) */
+    const int band = PG_GROUP * nx;                            /* tiles of a band of PG_GROUP m-tiles */
+    const int y0 = (id / band) * PG_GROUP, ny = (T / nx) - y0, rows = ny < PG_GROUP ? ny : PG_GROUP;
+    const int in = id - (id / band) * band;
+    return int2{in / rows, y0 + in % rows};
+}
+
 template <int EPI>
 __global__ void __launch_bounds__(PG_WAVES * WAVE, 1) prefill_gemm_kernel(PfGemm g) {
     __shared__ __align__(16) unsigned char b0[PG_STAGE], b1[PG_STAGE], b2[PG_STAGE], b3[PG_STAGE];
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const int i16 = lane & 15, grp = lane >> 4, wm = wave >> 2, wn = wave & 3;
-    const int n0 = blockIdx.x * PG_TN, m0 = blockIdx.y * PG_TM;
+    const int2 tile = pg_tile(blockIdx.x, gridDim.x, (g.N + PG_TN - 1) / PG_TN);
+    const int n0 = tile.x * PG_TN, m0 = tile.y * PG_TM;
     const int rowb = g.K * 2, stages = g.K / PG_KC;
     const Rsrc ra = pg_rsrc(g.a, (long long)g.M * rowb), rw = pg_rsrc(g.w, (long long)g.N * rowb);
 
@@ -194,7 +213,7 @@ int prefill_gemm(const PfGemm &g, int epi, hipStream_t stream) {
     if ((f32 ? !g.out_f32 : !g.out) || (epi == SG_RESID && !g.res) || (epi == SG_RELU2 && !g.rstd) ||
         (epi != SG_STORE && epi != SG_RESID && epi != SG_F32 && epi != SG_RELU2))
         return NC_ERR_SHAPE;
-    const dim3 grid((g.N + PG_TN - 1) / PG_TN, (g.M + PG_TM - 1) / PG_TM), block(PG_WAVES * WAVE);
+    const dim3 grid(((g.N + PG_TN - 1) / PG_TN) * ((g.M + PG_TM - 1) / PG_TM)), block(PG_WAVES * WAVE);
     switch (epi) {
     case SG_STORE: hipLaunchKernelGGL(prefill_gemm_kernel<SG_STORE>, grid, block, 0, stream, g); break;
     case SG_RESID: hipLaunchKernelGGL(prefill_gemm_kernel<SG_RESID>, grid, block, 0, stream, g); break;

@@ -12,6 +12,7 @@ from nanochat_amd.kv_cache import PagedKVCache, contiguous_block_table, permuted
 from nanochat_amd.qk_prologue import qk_forward
 from nanochat_amd.rotary import rotary_tables
 from nanochat_amd.workloads import DECODE, decode_inputs
+from oracle.layout import K_OFF, PAGE, V_OFF
 from oracle.numerics import bf16_bits, bf16_to_f32
 from oracle.rope import qk_norm_rope
 from tests.paged_util import device_cache, expected_codes, f32, read_sequence
@@ -203,3 +204,37 @@ def test_qk_backward_matches_oracle(device, B, T, H):
         mag = np.abs(dm * n).reshape(-1, 128).sum(axis=0)
         depth = rows // 2048 + 4 + 512
         assert np.all(np.abs(dg.double().numpy() - want_dg) <= depth * 2.0 ** -24 * mag + 1e-30)
+
+
+def test_partial_pages_keep_the_other_slots(device):
+    """Appends that start and end inside pages (misaligned starts, num_new shorter than T, new positions filling part
+    of one page, a V block's four slots split between old and new) change exactly the new positions' codes and
+    scales: the whole pool after the append, every other slot's bytes included, equals the pool before it with the
+    oracle's codes and scales put at the new positions."""
+    gen = torch.Generator().manual_seed(5)
+    B, Hkv, mp, T = 3, 2, 6, 20
+    table = permuted_block_table(B, mp, gen, device)
+    cache = PagedKVCache(B * mp, Hkv, device)
+    old = (torch.randn(B, 90, Hkv, 128, generator=gen) * 3).to(torch.bfloat16)
+    cache.append(old.to(device), old.flip(3).contiguous().to(device), torch.zeros(B, dtype=torch.int32, device=device),
+                 table)
+    torch.cuda.synchronize()
+    kp, vp, sc = (t.cpu().numpy().copy() for t in (cache.k_pages, cache.v_pages, cache.kv_scale))
+    k = torch.randn(B, T, Hkv, 128, generator=gen).to(torch.bfloat16)
+    v = (torch.randn(B, T, Hkv, 128, generator=gen) * 0.01).to(torch.bfloat16)
+    start, num_new = [37, 5, 66], [13, 20, 3]
+    cache.append(k.to(device), v.to(device), torch.tensor(start, dtype=torch.int32, device=device), table,
+                 torch.tensor(num_new, dtype=torch.int32, device=device))
+    torch.cuda.synchronize()
+    kc, ks, vc, vs = expected_codes(f32(k).reshape(B * T, Hkv, 128), f32(v).reshape(B * T, Hkv, 128))
+    tab = table.cpu().numpy()
+    for b in range(B):
+        for t in range(num_new[b]):
+            p = start[b] + t
+            page, slot, r = tab[b, p // PAGE], p % PAGE, b * T + t
+            kp[page, :, K_OFF[slot]] = kc[r].T
+            vp[page, :, V_OFF[slot]] = vc[r].T
+            sc[page, :, 0, slot], sc[page, :, 1, slot] = ks[r], vs[r]
+    assert np.array_equal(cache.k_pages.cpu().numpy(), kp)
+    assert np.array_equal(cache.v_pages.cpu().numpy(), vp)
+    assert np.array_equal(cache.kv_scale.cpu().numpy(), sc)
