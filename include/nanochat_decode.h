@@ -2,8 +2,8 @@
  * nanochat_amd decoder runtime (libnanochat_decode.so): the 14 dec_* symbols of the reference's decoder ABI,
  * model/kernels/decode.cu:904-1131, with the argument lists inference/decoder.py:132-148 binds, over an fp8
  * (e4m3fn) paged KV cache on gfx950. Every call is stream-ordered on the stream given to dec_create except
- * dec_create (synchronous allocation) and dec_tokens (synchronizes). A failed HIP or rocBLAS call, or an argument
- * out of range, aborts with a message, as in the reference (decode.cu:47-53, 926-931).
+ * dec_create (synchronous allocation) and dec_tokens (synchronizes). A failed HIP call, or an argument out of
+ * range, aborts with a message, as in the reference (decode.cu:47-53, 926-931).
  *
  * Differences from the reference, by design: the KV cache is fp8 with one scale per (token, head) (the reference
  * caches bf16); the prompt store lives in device memory, as pages of the same pools (the reference: pinned host
