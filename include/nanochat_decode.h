@@ -129,6 +129,20 @@ int dec_debug_slot_gemm_ssq(int epi, const void *w, int R, int K, const void *x,
 int dec_debug_prefill_gemm(int epi, const void *w, int N, int K, const void *a, int M, void *out, float *out_f32,
                            const void *res, const float *rstd, void *stream);
 
+/* The prefill's cache append alone (kv_append.hip, as dec_prefill runs it): run r is rows row0[r] .. + count[r] - 1
+ * of qkv (bf16 [rows][(Hq + 2 Hkv) 128] at token_stride elements) at positions start[r] .. of block-table row
+ * seq_slot[r] (int32 [*][max_pages]); max_count bounds count. q is normed and rotated into q_out ([rows][Hq][128]),
+ * k normed and rotated, v mixed with the value embedding when ve is non-NULL (v += 2 sigmoid(ve_gate[head] . ve_h[row])
+ * ve[tokens[row]], ve_h bf16 [rows][C], ve bf16 [vocab][C], ve_gate fp32 [Hkv][C]), and both quantized into the pages
+ * (k_pages, v_pages e4m3fn [num_pages][Hkv][2048], kv_scale fp32 [num_pages][Hkv][2][16]). Returns 0, a hipError_t,
+ * or -2 for a NULL operand or a shape it does not take. Stream-ordered. */
+int dec_debug_append_runs(const void *qkv, long long token_stride, int runs, int max_count, const int32_t *row0,
+                          const int32_t *count, const int32_t *start, const int32_t *seq_slot, int Hq, int Hkv,
+                          const float *q_gain, const float *k_gain, const float *cos, const float *sin, int rope_len,
+                          void *q_out, const int32_t *block_table, int max_pages, void *k_pages, void *v_pages,
+                          float *kv_scale, int num_pages, const void *ve_h, const void *ve, const float *ve_gate,
+                          const int32_t *tokens, int C, void *stream);
+
 /* The nucleus threshold of choose_kernel alone: for each of `rows` rows of probabilities e (fp32 [rows][vocab],
  * device; e = exp(z / T - max z / T) in [0, 1], 0 for rows not allowed) and its top_p (fp32 [rows], device), the
  * IEEE bit pattern of e*, the least e for which the rows with e' <= e* weigh more than (1 - top_p) of the total,

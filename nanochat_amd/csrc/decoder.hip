@@ -1578,6 +1578,25 @@ extern "C" int dec_debug_nucleus_cut(const float *e, int rows, int vocab, const 
     return (int)hipGetLastError();
 }
 
+extern "C" int dec_debug_append_runs(const void *qkv, long long token_stride, int runs, int max_count,
+                                     const int32_t *row0, const int32_t *count, const int32_t *start,
+                                     const int32_t *seq_slot, int Hq, int Hkv, const float *q_gain, const float *k_gain,
+                                     const float *cos, const float *sin, int rope_len, void *q_out,
+                                     const int32_t *block_table, int max_pages, void *k_pages, void *v_pages,
+                                     float *kv_scale, int num_pages, const void *ve_h, const void *ve,
+                                     const float *ve_gate, const int32_t *tokens, int C, void *stream) {
+    if (!qkv || !row0 || !count || !start || !seq_slot || !q_gain || !k_gain || !cos || !sin || !q_out ||
+        !block_table || !k_pages || !v_pages || !kv_scale || runs < 0 || max_count < 0 || Hq <= 0 || Hkv <= 0 ||
+        Hq % Hkv || rope_len <= 0 || max_pages <= 0 || num_pages <= 0 ||
+        token_stride < (long long)(Hq + 2 * Hkv) * HEAD_DIM)
+        return -2;
+    if (ve && (!ve_h || !ve_gate || !tokens || C < Hkv * HEAD_DIM)) return -2;
+    return nc::append_runs((const uint16_t *)qkv, token_stride, runs, max_count, row0, count, start, seq_slot, Hq, Hkv,
+                           q_gain, k_gain, cos, sin, rope_len, (uint16_t *)q_out, block_table, max_pages,
+                           (uint8_t *)k_pages, (uint8_t *)v_pages, kv_scale, num_pages, (const uint16_t *)ve_h,
+                           (const uint16_t *)ve, ve_gate, tokens, C, (hipStream_t)stream);
+}
+
 extern "C" int dec_debug_prefill_gemm(int epi, const void *w, int N, int K, const void *a, int M, void *out,
                                       float *out_f32, const void *res, const float *rstd, void *stream) {
     nc::PfGemm g = {(const uint16_t *)a, (const uint16_t *)w, M, N, K, (uint16_t *)out, out_f32, (const uint16_t *)res,

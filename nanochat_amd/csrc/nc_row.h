@@ -4,7 +4,8 @@
  * pair (dims l, l + 64). Reference row math: model/kernels/qk_row.cuh:19-51 (qk_row_sum, qk_rstd, qk_rotate) and
  * model/kernels/decode.cu:481-494 (the value-embedding gate); the summation order is fixed here (lane partial
  * x[l]^2 + x[l+64]^2, then the xor butterfly over offsets 32..1) and 1/sqrt is correctly rounded where the
- * reference has rsqrtf.
+ * reference has rsqrtf. The value-embedding gate's exponential is exp_rn (below) where the reference has expf, so
+ * the gate's bits follow from its fixed fp32 order alone.
  */
 #pragma once
 
@@ -37,6 +38,11 @@ __device__ __forceinline__ float quantize_pair(float x1, float x2, uint32_t &c1,
     return scale;
 }
 
+/* e^x of an fp32 x, rounded once to fp32: the double exponential (within an ulp of double precision) rounded to
+ * float. This is the correctly rounded e^x except where e^x lies within about 2^-52 (relative) of the midpoint of two
+ * floats, so it does not depend on a float exponential's own error. */
+__device__ __forceinline__ float exp_rn(float x) { return (float)exp((double)x); }
+
 /* Value-embedding mix of one value row: g = 2 sigmoid(w . h) from the token's normed stream h (C wide, lane-strided
  * FMAs, then the butterfly) and v = bf16(v + g e) with e the token's embedding row for this head. */
 __device__ __forceinline__ void ve_mix_pair(const uint16_t *h, const float *w, int C, const uint16_t *e, int lane,
@@ -44,7 +50,7 @@ __device__ __forceinline__ void ve_mix_pair(const uint16_t *h, const float *w, i
     float d = 0.0f;
     for (int i = lane; i < C; i += WAVE) d = __builtin_fmaf(bf16_to_f32(h[i]), w[i], d);
     d = wave_sum_butterfly(d);
-    const float g = 2.0f * (1.0f / (1.0f + expf(-d)));
+    const float g = 2.0f * (1.0f / (1.0f + exp_rn(-d)));
     v1 = bf16_to_f32(f32_to_bf16(v1 + g * bf16_to_f32(e[lane])));
     v2 = bf16_to_f32(f32_to_bf16(v2 + g * bf16_to_f32(e[lane + HALF])));
 }
@@ -112,7 +118,7 @@ __device__ __forceinline__ void ve_mix_quad(const uint16_t *h, const float *w, i
         for (int k = i + 16 * j; k < C; k += WAVE) d[j] = __builtin_fmaf(bf16_to_f32(h[k]), w[k], d[j]);
     }
     const float t = quad_row_sum(d);
-    const float g = 2.0f * (1.0f / (1.0f + expf(-t)));
+    const float g = 2.0f * (1.0f / (1.0f + exp_rn(-t)));
 #pragma unroll
     for (int j = 0; j < 8; j++) v[j] = bf16_to_f32(f32_to_bf16(v[j] + g * bf16_to_f32(e[i + 16 * j])));
 }

@@ -146,6 +146,10 @@ DECODE_SIGNATURES = {
     "dec_debug_nucleus_cut": ([c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p], c_int),
     "dec_debug_prefill_gemm": ([c_int, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_void_p], c_int),
+    "dec_debug_append_runs": ([c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                               c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p,
+                               c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p],
+                              c_int),
 }
 
 LIBRARIES = {"nanochat_kv": (LIBRARY, SIGNATURES), "decode": (DECODE_LIBRARY, DECODE_SIGNATURES)}

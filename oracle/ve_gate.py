@@ -19,6 +19,10 @@ table, the product and sum of the mix, the per-row bf16 of gate * dout) are repr
 Pinned by tests/test_oracle_ve_gate.py: the forward and all four gradients equal torch autograd of the float64
 expression v + 2 sigmoid(n w^T)[head] e (table values already bf16) within the stated roundings; a zero w gives
 gate 1 (out = v + e rounded); a token outside the table mixes in nothing.
+
+The cache append's gate (cache_gate) is the same gate in one fixed fp32 order, so its bits are fixed: fma32 is pinned
+against exact rational arithmetic (random operands and constructed midpoint ties), and cache_gate against the
+float64 gate within the fp32 chain's error bound, with a zero w giving exactly 1.
 """
 import numpy as np
 
@@ -31,6 +35,52 @@ def gate(n, w):
     """n (rows, C) bf16 values, w (H, C) fp32 -> the exact gate 2 sigmoid(n w^T) (rows, H) float64."""
     z = np.asarray(n, np.float64) @ np.asarray(w, np.float64).T
     return 2.0 / (1.0 + np.exp(-z))
+
+
+def fma32(a, b, c):
+    """a * b + c rounded once to fp32, elementwise, for fp32 arrays whose product a * b is exact in float64 (a holding
+    bf16 values: 8 + 24 significant bits). The float64 sum s and its exact error e (Knuth's TwoSum) give the exact
+    value s + e; rounding s to fp32 already rounds s + e correctly unless s is exactly the midpoint of two floats and
+    e is not zero, where the exact value lies on e's side of it."""
+    p = np.asarray(a, np.float32).astype(np.float64) * np.asarray(b, np.float32).astype(np.float64)
+    c64 = np.asarray(c, np.float32).astype(np.float64)
+    s = p + c64
+    pv = s - c64                       # the parts of s that came from p and from c
+    e = (p - pv) + (c64 - (s - pv))
+    f = s.astype(np.float32)
+    f64 = f.astype(np.float64)
+    toward = np.where(s > f64, np.float32(np.inf), np.float32(-np.inf)).astype(np.float32)
+    other = np.nextafter(f, toward)
+    tie = (f64 != s) & (s == (f64 + other.astype(np.float64)) * 0.5) & (e != 0)
+    return np.where(tie, np.where(e > 0, np.maximum(f, other), np.minimum(f, other)), f).astype(np.float32)
+
+
+def exp_rn(x):
+    """e^x of fp32 values rounded once to fp32 (the float64 exponential rounded to float)."""
+    return np.exp(np.asarray(x, np.float32).astype(np.float64)).astype(np.float32)
+
+
+def cache_gate(n, w):
+    """The cache append's gate in its fixed fp32 order (the append and the fused decode step alike; the reference's
+    attn_prologue, model/kernels/decode.cu:481-494, fixes another fp32 order): per (row, head), 64 lanes each run an
+    FMA chain d_l = fma(n[i], w[i], d_l) over i = l, l + 64, ... < C from 0; then an xor butterfly over offsets 32, 16,
+    8, 4, 2, 1 (d_l + d_(l ^ o), fp32); then g = 2 (1 / (1 + exp_rn(-d))), each operation rounded to fp32.
+    n (rows, C) bf16 values, w (H, C) fp32 -> (rows, H) fp32."""
+    n = np.asarray(n, np.float32)
+    w = np.asarray(w, np.float32)
+    rows, C = n.shape
+    H = w.shape[0]
+    d = np.zeros((rows, H, 64), np.float32)
+    for i0 in range(0, C, 64):
+        k = min(64, C - i0)
+        a = np.broadcast_to(n[:, None, i0:i0 + k], (rows, H, k))
+        b = np.broadcast_to(w[None, :, i0:i0 + k], (rows, H, k))
+        d[:, :, :k] = fma32(a, b, d[:, :, :k])
+    lanes = np.arange(64)
+    for o in (32, 16, 8, 4, 2, 1):
+        d = (d + d[:, :, lanes ^ o]).astype(np.float32)
+    one = np.float32(1.0)
+    return (np.float32(2.0) * (one / (one + exp_rn(-d[:, :, 0])))).astype(np.float32)
 
 
 def table_rows(table, idx, vocab=None):

@@ -343,3 +343,25 @@ def test_prefill_gemm_declines_without_launching():
     assert lib.dec_debug_prefill_gemm(RELU2, DUMMY, 6656, 1664, DUMMY, 8, DUMMY, None, None, None, None) == -2   # rstd
     assert lib.dec_debug_prefill_gemm(1, DUMMY, 1664, 1664, DUMMY, 8, DUMMY, DUMMY, DUMMY, DUMMY, None) == -2    # kind
     assert lib.dec_debug_prefill_gemm(STORE, DUMMY, 4992, 1664, DUMMY, 0, DUMMY, None, None, None, None) == 0
+
+
+def test_append_runs_declines_without_launching():
+    """The prefill append hook refuses NULL operands and shapes it cannot take with -2 before any device call; no runs
+    is a no-op."""
+    from nanochat_amd.native import hip_library
+
+    lib = hip_library("decode")
+    D = DUMMY
+
+    def call(qkv=D, stride=6 * 128, runs=1, max_count=4, Hq=2, Hkv=2, rope_len=64, max_pages=4, num_pages=8, ve=None,
+             ve_h=None, gate=None, tokens=None, C=256):
+        return lib.dec_debug_append_runs(qkv, stride, runs, max_count, D, D, D, D, Hq, Hkv, D, D, D, D, rope_len, D, D,
+                                         max_pages, D, D, D, num_pages, ve_h, ve, gate, tokens, C, None)
+
+    assert call(qkv=None) == -2
+    assert call(stride=5 * 128) == -2                     # shorter than a token's q, k and v
+    assert call(Hq=3, Hkv=2) == -2                        # q heads not a multiple of KV heads
+    assert call(rope_len=0) == -2
+    assert call(ve=D) == -2                               # value embeddings without their stream, gate and tokens
+    assert call(ve=D, ve_h=D, gate=D, tokens=D, C=255) == -2   # C narrower than the KV heads' rows
+    assert call(runs=0) == 0

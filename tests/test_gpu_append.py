@@ -238,3 +238,65 @@ def test_partial_pages_keep_the_other_slots(device):
     assert np.array_equal(cache.k_pages.cpu().numpy(), kp)
     assert np.array_equal(cache.v_pages.cpu().numpy(), vp)
     assert np.array_equal(cache.kv_scale.cpu().numpy(), sc)
+
+
+def test_prefill_append_runs_with_value_embeddings(device):
+    """The decoder's prefill append (dec_debug_append_runs) over runs of rows: misaligned starts, two runs of one slot
+    writing the two halves of one page (a V block split between them), a width C that is not a multiple of 64. q rows
+    and K codes equal the oracle's norm + rotation bit for bit; V codes and scales equal the value-embedding mix with
+    the gate in the append's fixed fp32 order (oracle/ve_gate.py:cache_gate), quantized; every other byte of the pool
+    keeps its value."""
+    from nanochat_amd.native import hip_library, pointer, stream
+    from oracle import ve_gate as ove
+
+    Hq, Hkv, C, vocab, mp, pool = 4, 2, 300, 23, 4, 16
+    runs = [(1, 5, 20), (0, 37, 3), (2, 0, 38), (1, 25, 7)]          # (slot, start, count)
+    rows = sum(r[2] for r in runs)
+    gen = torch.Generator().manual_seed(21)
+    qkv = (torch.randn(rows, (Hq + 2 * Hkv) * 128, generator=gen) * 2).to(torch.bfloat16)
+    qg = 1 + 0.1 * torch.randn(128, generator=gen)
+    kg = 1 + 0.1 * torch.randn(128, generator=gen)
+    h = torch.randn(rows, C, generator=gen).to(torch.bfloat16)
+    table = torch.randn(vocab, C, generator=gen).to(torch.bfloat16)
+    gate = (0.05 * torch.randn(Hkv, C, generator=gen)).float()
+    tokens = torch.randint(0, vocab, (rows,), generator=gen, dtype=torch.int32)
+    bt = torch.randperm(pool, generator=gen)[:3 * mp].view(3, mp).to(torch.int32)
+    cos, sin = rotary_tables(64, 1e4)
+    k_pages = torch.randint(0, 256, (pool, Hkv, 2048), generator=gen, dtype=torch.uint8)
+    v_pages = torch.randint(0, 256, (pool, Hkv, 2048), generator=gen, dtype=torch.uint8)
+    scales = torch.rand(pool, Hkv, 2, 16, generator=gen)
+    row0 = np.cumsum([0] + [r[2] for r in runs[:-1]]).astype(np.int32)
+    meta = [torch.tensor(x, dtype=torch.int32) for x in (row0, [r[2] for r in runs], [r[1] for r in runs],
+                                                         [r[0] for r in runs])]
+    d = {k: t.to(device) for k, t in dict(qkv=qkv, qg=qg, kg=kg, h=h, table=table, gate=gate, tokens=tokens, bt=bt,
+                                          cos=cos, sin=sin, kp=k_pages, vp=v_pages, sc=scales).items()}
+    dm = [t.to(device) for t in meta]
+    q_out = torch.zeros(rows, Hq, 128, dtype=torch.bfloat16, device=device)
+    rc = hip_library("decode").dec_debug_append_runs(
+        pointer(d["qkv"]), (Hq + 2 * Hkv) * 128, len(runs), max(r[2] for r in runs), *(pointer(t) for t in dm), Hq, Hkv,
+        pointer(d["qg"]), pointer(d["kg"]), pointer(d["cos"]), pointer(d["sin"]), 64, pointer(q_out), pointer(d["bt"]),
+        mp, pointer(d["kp"]), pointer(d["vp"]), pointer(d["sc"]), pool, pointer(d["h"]), pointer(d["table"]),
+        pointer(d["gate"]), pointer(d["tokens"]), C, stream())
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+
+    x = f32(qkv).reshape(rows, Hq + 2 * Hkv, 128)
+    pos = np.concatenate([np.arange(r[1], r[1] + r[2]) for r in runs])
+    slot = np.concatenate([np.full(r[2], r[0]) for r in runs])
+    c, s = cos.numpy()[pos][:, None], sin.numpy()[pos][:, None]
+    wq = qk_norm_rope(x[:, :Hq], qg.numpy(), c, s)
+    assert np.array_equal(bf16_bits(wq), q_out.view(torch.int16).cpu().numpy().view(np.uint16))
+    wk = qk_norm_rope(x[:, Hq:Hq + Hkv], kg.numpy(), c, s)
+    g = ove.cache_gate(f32(h), gate.numpy())                                            # (rows, Hkv)
+    v = ove.mix(x[:, Hq + Hkv:].reshape(rows, Hkv * 128), g, tokens.numpy(), f32(table)[:, :Hkv * 128])
+    kc, ks, vc, vs = expected_codes(wk, v.reshape(rows, Hkv, 128))
+    kp, vp, sc = k_pages.numpy().copy(), v_pages.numpy().copy(), scales.numpy().copy()
+    tab = bt.numpy()
+    for r in range(rows):
+        page, sl = tab[slot[r], pos[r] // PAGE], pos[r] % PAGE
+        kp[page, :, K_OFF[sl]] = kc[r].T
+        vp[page, :, V_OFF[sl]] = vc[r].T
+        sc[page, :, 0, sl], sc[page, :, 1, sl] = ks[r], vs[r]
+    assert np.array_equal(d["kp"].cpu().numpy(), kp)
+    assert np.array_equal(d["vp"].cpu().numpy(), vp)
+    assert np.array_equal(d["sc"].cpu().numpy(), sc)

@@ -100,3 +100,52 @@ def test_token_outside_table_mixes_nothing():
     ref = np.zeros_like(dtab)
     np.add.at(ref, idx[good], bf16((np.repeat(g.astype(np.float32), HEAD_DIM, axis=1) * dout).astype(np.float32))[good])
     assert np.array_equal(dtab, ref)
+
+
+def rn32(x):
+    """The fp32 value nearest the rational x (ties to an even significand)."""
+    from fractions import Fraction
+    f = np.float32(float(x))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - x), int(np.array(c).view(np.uint32)) & 1))
+    return np.float32(best)
+
+
+def test_fma32_is_one_rounding_of_the_exact_value():
+    """Random operands over many exponents, and the constructed midpoint cases: 205 x 5,237,765 = 2^30 + 1, so
+    a = 205 / 128 (bf16) times b = 5,237,765 / 2^22 (fp32) is 2^1 + 2^-29, and 2^25 + a b lies 2^-29 above the
+    midpoint of the floats 2^25 and 2^25 + 4 while its float64 sum is that midpoint (the sum's error is 2^-29)."""
+    from fractions import Fraction
+    rng = np.random.default_rng(3)
+    a = bf16(rng.standard_normal(4000) * 2.0 ** rng.integers(-20, 20, 4000))
+    b = (rng.standard_normal(4000) * 2.0 ** rng.integers(-20, 20, 4000)).astype(np.float32)
+    c = (rng.standard_normal(4000) * 2.0 ** rng.integers(-30, 30, 4000)).astype(np.float32)
+    ta, tb = np.float32(205 / 128), np.float32(5237765 / 2 ** 22)
+    assert float(ta) * float(tb) == 2.0 + 2.0 ** -29
+    a = np.concatenate([a, [ta, -ta, ta, ta]]).astype(np.float32)
+    b = np.concatenate([b, [tb, tb, -tb, tb]]).astype(np.float32)
+    c = np.concatenate([c, [2.0 ** 25, -2.0 ** 25, 2.0 ** 25, 0.0]]).astype(np.float32)
+    got = ov.fma32(a, b, c)
+    for x, y, z, g in zip(a, b, c, got):
+        want = rn32(Fraction(float(x)) * Fraction(float(y)) + Fraction(float(z)))
+        assert g == want, (x, y, z, g, want)
+    assert got[-4] == np.float32(2.0 ** 25 + 4) and got[-3] == np.float32(-(2.0 ** 25 + 4))
+    # plain float64-then-float32 rounding lands on the even neighbour, 2^25: the case the correction exists for
+    assert np.float32(float(ta) * float(tb) + 2.0 ** 25) == np.float32(2.0 ** 25)
+
+
+def test_cache_gate_is_the_gate_within_its_fp32_error():
+    """cache_gate against the float64 gate: each FMA chain, butterfly add, exponential, add, divide and scale rounds
+    once to fp32, so |g - g64| <= 0.5 (C / 64 + 6) 2^-24 sum |n w| + 10 2^-24 (sigmoid' <= 1/4, times 2; g <= 2);
+    widths that are and are not multiples of 64; zero weights give exactly 1."""
+    rng = np.random.default_rng(4)
+    for C in (768, 1664, 200, 64, 1):
+        n = bf16(rng.standard_normal((37, C)))
+        w = (rng.standard_normal((5, C)) * rng.choice([0.01, 0.05, 0.3])).astype(np.float32)
+        g = ov.cache_gate(n, w)
+        assert g.dtype == np.float32 and g.shape == (37, 5)
+        g64 = ov.gate(n, w)
+        mag = np.abs(n.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+        tol = 0.5 * (C / 64 + 6) * 2.0 ** -24 * mag + 10 * 2.0 ** -24
+        assert (np.abs(g - g64) <= tol).all(), (C, float(np.abs(g - g64).max()))
+        assert (ov.cache_gate(n, np.zeros_like(w)) == 1.0).all()
