@@ -1006,13 +1006,29 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
 /* Grid (ceil(T / (4 NT tpt)), Hkv, B), 4 waves. A wave owns NT tiles of 16 columns, each tile tpt = 16 / G
  * consecutive tokens x G heads (column c = token c / G, head c % G), and streams every page its rows can see;
  * each K/V operand it converts feeds its NT tiles. */
+/* A prefill workgroup's (row tile, KV head, sequence) from its place in the launch order, the longest key ranges
+ * first: work-groups start in linear order (x, then y, then z), and a row tile's keys grow with its index under the
+ * causal bound, so the last tiles of every (head, sequence) go first and the shortest last, where they fill the CUs
+ * the long ones leave (the grid keeps x = row tiles, y = KV heads, z = sequences). */
+struct PrefillBlock {
+    int tile, kvh, b;
+};
+
+__device__ __forceinline__ PrefillBlock prefill_block() {
+    const int yz = (int)(gridDim.y * gridDim.z);
+    const int L = (int)blockIdx.x + (int)gridDim.x * ((int)blockIdx.y + (int)gridDim.y * (int)blockIdx.z);
+    const int r = L % yz;
+    return PrefillBlock{(int)gridDim.x - 1 - L / yz, r % (int)gridDim.y, r / (int)gridDim.y};
+}
+
 template <int NT>
 __global__ void __launch_bounds__(256, 2) prefill_kernel(AttnArgs a) {
-    const int kvh = blockIdx.y, b = blockIdx.z;
+    const PrefillBlock pb = prefill_block();
+    const int kvh = pb.kvh, b = pb.b;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     const int tpt = 16 / a.G, tpw = tpt * NT;
-    const int t0 = (blockIdx.x * WAVES + wave) * tpw;
+    const int t0 = (pb.tile * WAVES + wave) * tpw;
     const int T = a.run_row0 ? a.run_count[b] : a.T;          /* this sequence's (run's) rows */
     if (t0 >= T) return;
     const long long row0 = a.run_row0 ? a.run_row0[b] : (long long)b * a.T;
@@ -1193,12 +1209,13 @@ __global__ void __launch_bounds__(256, 2) prefill_lds_kernel(AttnArgs a) {
     __shared__ __align__(16) PfScales ps0, ps1, ps2, ps3;
     __shared__ int tab[PF_TAB];
     static_assert(PF_BUFS == 4, "the loop below rotates four stage buffers");
-    const int kvh = blockIdx.y, b = blockIdx.z;
+    const PrefillBlock pb = prefill_block();
+    const int kvh = pb.kvh, b = pb.b;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     const int tpt = 16 / a.G, tpw = tpt * NT;
     const int T = a.run_row0 ? a.run_count[b] : a.T;          /* this sequence's (run's) rows */
-    const int wg_t0 = blockIdx.x * WAVES * tpw;
+    const int wg_t0 = pb.tile * WAVES * tpw;
     if (wg_t0 >= T) return;                                    /* the whole workgroup */
     const int t0 = wg_t0 + wave * tpw;
     const bool on = t0 < T;                                    /* this wave has rows */
