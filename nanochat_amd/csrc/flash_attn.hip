@@ -204,12 +204,28 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
     }
 }
 
+/* A workgroup's (rank, segment, head) from its place in the launch order: work-groups start in linear order (x,
+ * then y, then z), so rank r = L / (segments heads) takes the r-th tile of every (segment, head) before any takes
+ * the (r + 1)-th. The kernels map rank 0 to their longest tile, so the short ones of every head come last, where they
+ * fill the CUs the long ones leave (the grid keeps x = tiles, y = segments, z = heads). */
+struct FaBlock {
+    int rank, seg, h;
+};
+
+__device__ __forceinline__ FaBlock fa_block_order() {
+    const int yz = (int)(gridDim.y * gridDim.z);
+    const int L = (int)blockIdx.x + (int)gridDim.x * ((int)blockIdx.y + (int)gridDim.y * (int)blockIdx.z);
+    const int r = L % yz;
+    return FaBlock{L / yz, r % (int)gridDim.y, r / (int)gridDim.y};
+}
+
 __global__ void __launch_bounds__(FA_THREADS, 2) flash_fwd_kernel(FlashFwd a) {
     __shared__ FaStage st0, st1;   /* distinct objects: a read of one never waits for DMA into the other */
-    const int seg = blockIdx.y, h = blockIdx.z;
+    const FaBlock fb = fa_block_order();
+    const int seg = fb.seg, h = fb.h;
     const long long start = a.cu[seg];
     const int seglen = a.cu[seg + 1] - a.cu[seg];
-    const int tile = (int)gridDim.x - 1 - (int)blockIdx.x;   /* the longest key ranges first */
+    const int tile = (int)gridDim.x - 1 - fb.rank;   /* the longest key ranges first */
     const int qa = tile * FA_BM;
     if (seglen <= 0 || qa >= seglen) return;
     const int t = threadIdx.x, lane = t & (WAVE - 1), wave = t >> 6, g = lane >> 4, c = lane & 15;
@@ -335,10 +351,11 @@ constexpr int DKV_KEYS = 16 * DKV_WAVES;
 
 __global__ void __launch_bounds__(64 * DKV_WAVES, 2) flash_bwd_dkv_kernel(FlashBwd a) {
     __shared__ DkvStage s0, s1;   /* distinct objects: a read of one never waits for DMA into the other */
-    const int seg = blockIdx.y, h = blockIdx.z;
+    const FaBlock fb = fa_block_order();
+    const int seg = fb.seg, h = fb.h;
     const long long start = a.cu[seg];
     const int seglen = a.cu[seg + 1] - a.cu[seg];
-    const int k0 = blockIdx.x * DKV_KEYS;       /* the most query blocks first */
+    const int k0 = fb.rank * DKV_KEYS;          /* the most query blocks first */
     if (seglen <= 0 || k0 >= seglen) return;
     const int t = threadIdx.x, lane = t & (WAVE - 1), wave = t >> 6, g = lane >> 4, c = lane & 15;
     const int kw = k0 + wave * 16;              /* the wave's first key */
@@ -484,10 +501,11 @@ struct DqStage {
  * dQ^T += K^T dS^T as the B operand with K^T read from a transposed LDS tile. */
 __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dq_kernel(FlashBwd a) {
     __shared__ DqStage s0, s1;   /* distinct objects: a read of one never waits for DMA into the other */
-    const int seg = blockIdx.y, h = blockIdx.z;
+    const FaBlock fb = fa_block_order();
+    const int seg = fb.seg, h = fb.h;
     const long long start = a.cu[seg];
     const int seglen = a.cu[seg + 1] - a.cu[seg];
-    const int tile = (int)gridDim.x - 1 - (int)blockIdx.x;
+    const int tile = (int)gridDim.x - 1 - fb.rank;
     const int qa = tile * FA_BM;
     if (seglen <= 0 || qa >= seglen) return;
     const int t = threadIdx.x, lane = t & (WAVE - 1), wave = t >> 6, g = lane >> 4, c = lane & 15;
