@@ -28,13 +28,30 @@ __device__ __forceinline__ void norm_rope_pair(float x1, float x2, float g1, flo
     y2 = n2 * c - n1 * s;
 }
 
+/* The code e4m3_encode(clamp(x / scale, +-448)) of a bf16 value x of a row whose scale is amax / 448 (|x| <= amax).
+ * For scale >= 2^-80 (fast) the division becomes a product with r = 1 / scale (correctly rounded) and one FMA
+ * correction of |x| (Markstein), the sign copied from x: every finite bf16 x with |x| <= amax, against every bf16
+ * amax, gives the same code this way as by the division (an exhaustive check, tests/quant_division_check.c). Smaller
+ * scales divide. */
+__device__ __forceinline__ uint32_t quant_code(float x, float scale, float r, bool fast) {
+    if (!fast) return e4m3_encode(fminf(fmaxf(x / scale, -FP8_MAX), FP8_MAX));
+    const float ax = fabsf(x);
+    const float q0 = ax * r;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, scale, ax), r, q0);
+    return e4m3_encode(fminf(q, FP8_MAX)) | ((__float_as_uint(x) >> 24) & 0x80u);
+}
+
+constexpr float QUANT_FAST_SCALE = 0x1p-80f;   /* quant_code's fast path: scales from here up */
+
 /* Absmax e4m3fn quantization of one row (lane pair x1 = dim l, x2 = dim l + 64, bf16 values): the row's scale
  * amax / 448 (1 for an all-zero row), returned in every lane, and this lane's two codes. */
 __device__ __forceinline__ float quantize_pair(float x1, float x2, uint32_t &c1, uint32_t &c2) {
     const float amax = wave_max(fmaxf(fabsf(x1), fabsf(x2)));
     const float scale = amax > 0.0f ? amax / FP8_MAX : 1.0f;
-    c1 = e4m3_encode(fminf(fmaxf(x1 / scale, -FP8_MAX), FP8_MAX));
-    c2 = e4m3_encode(fminf(fmaxf(x2 / scale, -FP8_MAX), FP8_MAX));
+    const bool fast = scale >= QUANT_FAST_SCALE;
+    const float r = 1.0f / scale;
+    c1 = quant_code(x1, scale, r, fast);
+    c2 = quant_code(x2, scale, r, fast);
     return scale;
 }
 
@@ -102,8 +119,10 @@ __device__ __forceinline__ float quantize_quad(const float (&x)[8], uint32_t (&c
     for (int j = 0; j < 4; j++) m[j] = fmaxf(fabsf(x[j]), fabsf(x[j + 4]));
     const float amax = quad_row_max(m);
     const float scale = amax > 0.0f ? amax / FP8_MAX : 1.0f;
+    const bool fast = scale >= QUANT_FAST_SCALE;
+    const float r = 1.0f / scale;
 #pragma unroll
-    for (int j = 0; j < 8; j++) code[j] = e4m3_encode(fminf(fmaxf(x[j] / scale, -FP8_MAX), FP8_MAX));
+    for (int j = 0; j < 8; j++) code[j] = quant_code(x[j], scale, r, fast);
     return scale;
 }
 
