@@ -3,11 +3,14 @@
  * dec_prefill call (M <= 8,192 prompt tokens), bf16 operands, fp32 sums. At these sizes a GEMM is bound by the matrix
  * cores, so it is tiled for them: a workgroup of 8 waves owns a 256 x 256 output tile (2 x 4 waves of 128 x 64, 32
  * accumulator tiles of 16 x 16 a wave; two waves a SIMD), walks K in stages of 32, and takes each
- * stage's operands (256 rows of a and 256 rows of w, 64 bytes each: 32 KiB) from memory into LDS by LDS DMA, three
- * stages ahead in a ring of four buffers, with hand-placed waits and a barrier without a memory fence per stage.
+ * stage's operands (256 rows of a and 256 rows of w, 64 bytes each: 32 KiB) from memory into LDS by LDS DMA, in a ring
+ * of four buffers: a buffer is refilled with the stage four on as soon as every wave holds its fragments in registers,
+ * so three stages are in flight while one is computed. Hand-placed waits and one barrier without a memory fence per
+ * stage order the ring.
  *
- * Per stage a wave reads 4 fragments of its weight rows and 8 of its activation rows (one 16-byte LDS read each) and
- * issues 32 MFMAs (v_mfma_f32_16x16x32_bf16: A = 16 weight rows n, B = 16 activation rows m), so lane (g, i) of a
+ * Per stage a wave issues 32 MFMAs (v_mfma_f32_16x16x32_bf16: A = 16 weight rows n, B = 16 activation rows m) on
+ * fragments already in registers, and between them reads the next stage's 4 weight and 8 activation fragments (one
+ * 16-byte LDS read each) into a second register set. Lane (g, i) of a
  * result tile holds columns n .. n + 3 (n = 16 t + 4 g) of row m = 16 u + i, and every epilogue writes 4 adjacent
  * columns of a row. In LDS a row's 64 bytes (4 blocks of 16) keep block b at position b ^ ((row / 4) % 4), so the 16
  * rows of a fragment read fall in distinct banks; each DMA lane fetches the global block that belongs at its LDS
@@ -71,10 +74,11 @@ __device__ __forceinline__ void pg_fetch(Rsrc ra, Rsrc rw, unsigned char *buf, i
     }
 }
 
-/* s_waitcnt: all but this wave's DMA of the two newer stages in flight have landed, and its LDS reads are done.
- * Encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8]. */
+/* s_waitcnt: all but this wave's DMA of the NEWER stages most recently issued have landed, and its LDS reads are
+ * done. Encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8]. */
+template <int NEWER>
 __device__ __forceinline__ void pg_wait_stage() {
-    constexpr int n = 2 * PG_LOADS;
+    constexpr int n = NEWER * PG_LOADS;
     static_assert(n < 64, "vmcnt holds 6 bits");
     __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
 }
@@ -86,37 +90,63 @@ __device__ __forceinline__ void pg_barrier() {
     asm volatile("" ::: "memory");
 }
 
-/* One stage of a wave: fragments of its 64 weight rows (buffer rows 256 + 64 wn + 16 t + i) and 128 activation rows
- * (128 wm + 16 u + i), then the 32 products. */
-__device__ __forceinline__ void pg_compute(const unsigned char *buf, f32x4 (&acc)[4][8], int wm, int wn, int i16,
-                                           int grp) {
-    bf16x8 fw[4], fa[8];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int row = PG_TM + 64 * wn + 16 * t + i16;
-        fw[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                               buf + row * PG_ROWB + ((grp ^ ((row >> 2) & 3)) << 4)));
-    }
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int row = 128 * wm + 16 * u + i16;
-        fa[u] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                               buf + row * PG_ROWB + ((grp ^ ((row >> 2) & 3)) << 4)));
-    }
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int u = 0; u < 8; u++) acc[t][u] = mfma16x16x32(fw[t], fa[u], acc[t][u]);
+/* The LDS reads and the MFMAs are instructions of their own (inline assembly), in the order written. The compiler
+ * cannot tell a read of one stage buffer from the DMA into the others, and with builtin reads it waited for most DMA
+ * in flight before each stage's first read, which left one stage in flight instead of three. A read's result is used
+ * only after the s_waitcnt lgkmcnt(0) at the head of the next ring position (pg_wait_stage), and the MFMAs, being
+ * volatile too, stay after that wait.
+ *
+ * The compiler does not see the MFMAs as matrix instructions, so it inserts none of their wait states; the kernel
+ * keeps their hazards by construction. Operands are written only by LDS reads, waited for as above, never by VALU
+ * instructions (tests/test_prefill_gemm_isa.py checks the built code). An accumulator is used again 31 products
+ * later. The accumulators are zeroed before the first stage's DMA is issued, and read only after the last product
+ * and 32 wait states. Each accumulator tile stays in the same four AGPRs for the whole K walk ("+a"). */
+__device__ __forceinline__ void pg_mfma(f32x4 &c, const bf16x8 &a, const bf16x8 &b) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
 }
 
-/* One ring position: wait for stage j, barrier (every wave's DMA of stage j has landed and every wave is done with
- * stage j - 1), refill the buffer stage j - 1 used with stage j + 3, compute stage j. */
-#define PG_STEP(j, CUR, NXT)                                                                      \
-    do {                                                                                           \
-        pg_wait_stage();                                                                           \
-        pg_barrier();                                                                              \
-        pg_fetch(ra, rw, NXT, (j) + PG_RING - 1, stages, m0, n0, rowb, wave, lane);                \
-        pg_compute(CUR, acc, wm, wn, i16, grp);                                                    \
+/* The LDS address of a lane's row of fragment 0 of a wave's rows row0 .. row0 + 16 F - 1 in buf (row0 a multiple of
+ * 16, so rows 16 f on from it have the same swizzle and fragment f lies 16 f rows = 1 KiB further on). */
+__device__ __forceinline__ uint32_t pg_base(const unsigned char *buf, int row0, int i16, int grp) {
+    const int row = row0 + i16;
+    const LdsPtr *p = (const LdsPtr *)(buf + row * PG_ROWB + ((grp ^ ((row >> 2) & 3)) << 4));
+    return (uint32_t)reinterpret_cast<uintptr_t>(p);
+}
+
+__device__ __forceinline__ bf16x8 pg_frag(uint32_t base, int f) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(base), "i"(f * 16 * PG_ROWB));
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+/* One stage of a wave: the 32 products of its weight fragments cw (rows 256 + 64 wn + 16 t + i of the stage buffer)
+ * and activation fragments ca (rows 128 wm + 16 u + i), with the next stage's 12 fragment reads from the bases nab,
+ * nwb into (nw, na) spread between them. */
+__device__ __forceinline__ void pg_compute(uint32_t nab, uint32_t nwb, f32x4 (&acc)[4][8], const bf16x8 (&cw)[4],
+                                           const bf16x8 (&ca)[8], bf16x8 (&nw)[4], bf16x8 (&na)[8], int wm, int wn,
+                                           int i16, int grp) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            pg_mfma(acc[t][u], cw[t], ca[u]);
+            if (u == 1) na[2 * t] = pg_frag(nab, 2 * t);
+            if (u == 3) na[2 * t + 1] = pg_frag(nab, 2 * t + 1);
+            if (u == 5) nw[t] = pg_frag(nwb, t);
+        }
+    }
+}
+
+/* One ring position j: wait for this wave's DMA of stage j + 1 and its reads of stage j (now in registers), barrier
+ * (every wave's DMA of stage j + 1 has landed and every wave holds stage j), refill stage j's buffer with stage j + 4,
+ * then compute stage j while reading stage j + 1 from the next buffer into the other register set. */
+#define PG_STEP(j, CUR, NXT, C, N)                                                                  \
+    do {                                                                                             \
+        pg_wait_stage<2>();                                                                          \
+        pg_barrier();                                                                                \
+        pg_fetch(ra, rw, CUR, (j) + PG_RING, stages, m0, n0, rowb, wave, lane);                      \
+        pg_compute(pg_base(NXT, 128 * wm, i16, grp), pg_base(NXT, PG_TM + 64 * wn, i16, grp), acc, fw[C],   \
+                   fa[C], fw[N], fa[N], wm, wn, i16, grp);                                          \
     } while (0)
 
 /* Which output tile workgroup L of T takes. Workgroups are dispatched to the 8 XCDs in turn (L % 8), each XCD with its
@@ -144,21 +174,37 @@ __global__ void __launch_bounds__(PG_WAVES * WAVE, 1) prefill_gemm_kernel(PfGemm
     const int rowb = g.K * 2, stages = g.K / PG_KC;
     const Rsrc ra = pg_rsrc(g.a, (long long)g.M * rowb), rw = pg_rsrc(g.w, (long long)g.N * rowb);
 
+    /* the accumulators start at zero in their AGPRs, before the first DMA is issued */
     f32x4 acc[4][8];
 #pragma unroll
     for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int u = 0; u < 8; u++) acc[t][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int u = 0; u < 8; u++) asm volatile("" : "=a"(acc[t][u]) : "0"(f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
     pg_fetch(ra, rw, b0, 0, stages, m0, n0, rowb, wave, lane);
     pg_fetch(ra, rw, b1, 1, stages, m0, n0, rowb, wave, lane);
     pg_fetch(ra, rw, b2, 2, stages, m0, n0, rowb, wave, lane);
+    pg_fetch(ra, rw, b3, 3, stages, m0, n0, rowb, wave, lane);
+    bf16x8 fw[2][4], fa[2][8];
+    pg_wait_stage<3>();
+    pg_barrier();
+#pragma unroll
+    for (int t = 0; t < 8; t++) fa[0][t] = pg_frag(pg_base(b0, 128 * wm, i16, grp), t);
+#pragma unroll
+    for (int t = 0; t < 4; t++) fw[0][t] = pg_frag(pg_base(b0, PG_TM + 64 * wn, i16, grp), t);
     for (int j = 0; j < stages; j += 4) {   /* stages is a multiple of 4 (K of 128, checked by the host) */
-        PG_STEP(j, b0, b3);
-        PG_STEP(j + 1, b1, b0);
-        PG_STEP(j + 2, b2, b1);
-        PG_STEP(j + 3, b3, b2);
+        PG_STEP(j, b0, b1, 0, 1);
+        PG_STEP(j + 1, b1, b2, 1, 0);
+        PG_STEP(j + 2, b2, b3, 0, 1);
+        PG_STEP(j + 3, b3, b0, 1, 0);
     }
     __builtin_amdgcn_s_waitcnt(0);                 /* no DMA may land in LDS after this */
+    /* 32 wait states: every product has written its accumulator before the epilogue reads it (each accumulator is
+     * tied to this point, so no read moves above it) */
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int u = 0; u < 8; u++) asm volatile("" : "+a"(acc[t][u]));
 
     const Rsrc ro = pg_rsrc(EPI == SG_F32 ? (const void *)g.out_f32 : (const void *)g.out,
                             (long long)g.M * g.N * (EPI == SG_F32 ? 4 : 2));
