@@ -16,11 +16,14 @@
  * rows of a fragment read fall in distinct banks; each DMA lane fetches the global block that belongs at its LDS
  * position.
  *
- * Workgroups take their tiles in an XCD-aware order (pg_tile), so the workgroups an XCD runs together share operand
- * tiles in its L2.
+ * Workgroups take their tiles in an XCD-aware order (pg_order), so the workgroups an XCD runs together share operand
+ * tiles in its L2. The tiles that would leave the last round of workgroups part-filled (T mod CUs of T tiles) are cut
+ * into halves (256 x 128) or quarters (128 x 128), so that round has a workgroup on every CU and each takes in half or
+ * a quarter of the operands; the waves of a smaller tile hold fewer fragments (PgTile).
  *
  * Every output's sum runs over K in one fixed order (the stages in order, each stage one MFMA's own order), whatever M
- * is, so a row's result depends on its own a row alone: a prompt's rows give the same bits in any dec_prefill call.
+ * is and whatever size of tile holds it, so a row's result depends on its own a row alone: a prompt's rows give the
+ * same bits in any dec_prefill call.
  * Every global access goes through a buffer resource over the exact extent of its array, so rows past M read zeros
  * and store nothing; columns past N (a last partial tile of 256) are not stored.
  *
@@ -36,16 +39,26 @@
 
 namespace nc {
 
-constexpr int PG_TM = 256, PG_TN = 256;        /* the output tile: rows m, columns n */
 constexpr int PG_KC = 32;                      /* k per stage: one MFMA's depth */
 constexpr int PG_ROWB = PG_KC * 2;             /* bytes of a row per stage */
-constexpr int PG_STAGE = (PG_TM + PG_TN) * PG_ROWB;
+constexpr int PG_STAGE = 512 * PG_ROWB;        /* a stage buffer: 256 a rows and 256 w rows */
 constexpr int PG_RING = 4;                     /* stage buffers; three stages in flight */
 constexpr int PG_WAVES = 8;
-constexpr int PG_DMA = PG_STAGE / 1024;        /* 1 KiB DMA instructions per stage (16 rows each) */
-constexpr int PG_LOADS = PG_DMA / PG_WAVES;    /* ... per wave */
 constexpr int PG_PAST = 0x7FFF0000;            /* a byte offset past every operand's range */
-static_assert(PG_TM / 16 == PG_DMA / 2 && PG_TN / 16 == PG_DMA / 2, "DMA instructions q < 16 fill a, the rest w");
+
+/* A workgroup's output tile: TM rows m x TN columns n, its 8 waves as 2 (m) x 4 (n), each wave WM x WN outputs, NU
+ * activation and NT weight fragments a stage. A stage buffer holds the tile's TM a rows, then its TN w rows; its DMA
+ * is ROWS / 16 instructions of 1 KiB, LOADS a wave, the first A_LOADS of them a's. */
+template <int TM_, int TN_>
+struct PgTile {
+    static constexpr int TM = TM_, TN = TN_, WM = TM / 2, WN = TN / 4, NU = WM / 16, NT = WN / 16;
+    static constexpr int ROWS = TM + TN, LOADS = ROWS / 16 / PG_WAVES, A_LOADS = TM / 16 / PG_WAVES;
+    static_assert(ROWS * PG_ROWB <= PG_STAGE && ROWS % (16 * PG_WAVES) == 0 && TM % (16 * PG_WAVES) == 0, "DMA split");
+    static_assert(NU % NT == 0, "a-fragment reads per weight fragment");
+};
+typedef PgTile<256, 256> PgFull;
+typedef PgTile<256, 128> PgHalf;
+typedef PgTile<128, 128> PgQuarter;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -57,18 +70,19 @@ __device__ __forceinline__ Rsrc pg_rsrc(const void *p, long long bytes) {
 }
 
 /* Stage j's DMA into buf (j >= stages: offsets past the range, zeros and no memory access). Instruction q fills the
- * buffer's rows 16 q .. 16 q + 15 (rows 0..255: a rows m0 + r; rows 256..511: w rows n0 + r - 256); lane l writes row
+ * buffer's rows 16 q .. 16 q + 15 (rows below TM: a rows m0 + r; the rest: w rows n0 + r - TM); lane l writes row
  * 16 q + l / 4 at position l % 4 and fetches the global block (l % 4) ^ ((row / 4) % 4). Wave w issues q = w, w + 8,
- * ... (its first two are a's, the last two w's). */
+ * ... (its first A_LOADS are a's). */
+template <class P>
 __device__ __forceinline__ void pg_fetch(Rsrc ra, Rsrc rw, unsigned char *buf, int j, int stages, int m0, int n0,
                                          int rowb, int wave, int lane) {
     const bool live = j < stages;
     const int kb = j * PG_ROWB, pos = lane & 3;
 #pragma unroll
-    for (int s = 0; s < PG_LOADS; s++) {
+    for (int s = 0; s < P::LOADS; s++) {
         const int q = wave + PG_WAVES * s, row = 16 * q + (lane >> 2);
-        const bool is_a = s < PG_LOADS / 2;
-        const int grow = (is_a ? m0 : n0 - PG_TM) + row;
+        const bool is_a = s < P::A_LOADS;
+        const int grow = (is_a ? m0 : n0 - P::TM) + row;
         const int off = live ? grow * rowb + kb + ((pos ^ ((row >> 2) & 3)) << 4) : PG_PAST;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? ra : rw, (LdsPtr *)(buf + q * 1024), 16, off, 0, 0, 0);
     }
@@ -76,9 +90,9 @@ __device__ __forceinline__ void pg_fetch(Rsrc ra, Rsrc rw, unsigned char *buf, i
 
 /* s_waitcnt: all but this wave's DMA of the NEWER stages most recently issued have landed, and its LDS reads are
  * done. Encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8]. */
-template <int NEWER>
+template <class P, int NEWER>
 __device__ __forceinline__ void pg_wait_stage() {
-    constexpr int n = NEWER * PG_LOADS;
+    constexpr int n = NEWER * P::LOADS;
     static_assert(n < 64, "vmcnt holds 6 bits");
     __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
 }
@@ -119,20 +133,26 @@ __device__ __forceinline__ bf16x8 pg_frag(uint32_t base, int f) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
-/* One stage of a wave: the 32 products of its weight fragments cw (rows 256 + 64 wn + 16 t + i of the stage buffer)
- * and activation fragments ca (rows 128 wm + 16 u + i), with the next stage's 12 fragment reads from the bases nab,
- * nwb into (nw, na) spread between them. */
-__device__ __forceinline__ void pg_compute(uint32_t nab, uint32_t nwb, f32x4 (&acc)[4][8], const bf16x8 (&cw)[4],
-                                           const bf16x8 (&ca)[8], bf16x8 (&nw)[4], bf16x8 (&na)[8], int wm, int wn,
-                                           int i16, int grp) {
+/* One stage of a wave: the NT x NU products of its weight fragments cw (rows TM + WN wn + 16 t + i of the stage
+ * buffer) and activation fragments ca (rows WM wm + 16 u + i), with the next stage's NU + NT fragment reads from the
+ * bases nab, nwb into (nw, na) spread between them: for each t, NU / NT activation fragments and weight fragment t. */
+template <class P>
+__device__ __forceinline__ void pg_compute(uint32_t nab, uint32_t nwb, f32x4 (&acc)[P::NT][P::NU],
+                                           const bf16x8 (&cw)[P::NT], const bf16x8 (&ca)[P::NU], bf16x8 (&nw)[P::NT],
+                                           bf16x8 (&na)[P::NU]) {
+    constexpr int R = P::NU / P::NT + 1;   /* reads per t */
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+    for (int t = 0; t < P::NT; t++) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < P::NU; u++) {
             pg_mfma(acc[t][u], cw[t], ca[u]);
-            if (u == 1) na[2 * t] = pg_frag(nab, 2 * t);
-            if (u == 3) na[2 * t + 1] = pg_frag(nab, 2 * t + 1);
-            if (u == 5) nw[t] = pg_frag(nwb, t);
+#pragma unroll
+            for (int c = 0; c < R; c++) {
+                /* read c after product 2 c + 1 where that fits (the whole tile), else spread evenly */
+                if (u != (2 * R <= P::NU ? 2 * c + 1 : (2 * c + 1) * P::NU / (2 * R))) continue;
+                if (c < R - 1) na[t * (R - 1) + c] = pg_frag(nab, t * (R - 1) + c);
+                else nw[t] = pg_frag(nwb, t);
+            }
         }
     }
 }
@@ -142,55 +162,39 @@ __device__ __forceinline__ void pg_compute(uint32_t nab, uint32_t nwb, f32x4 (&a
  * then compute stage j while reading stage j + 1 from the next buffer into the other register set. */
 #define PG_STEP(j, CUR, NXT, C, N)                                                                  \
     do {                                                                                             \
-        pg_wait_stage<2>();                                                                          \
+        pg_wait_stage<P, 2>();                                                                       \
         pg_barrier();                                                                                \
-        pg_fetch(ra, rw, CUR, (j) + PG_RING, stages, m0, n0, rowb, wave, lane);                      \
-        pg_compute(pg_base(NXT, 128 * wm, i16, grp), pg_base(NXT, PG_TM + 64 * wn, i16, grp), acc, fw[C],   \
-                   fa[C], fw[N], fa[N], wm, wn, i16, grp);                                          \
+        pg_fetch<P>(ra, rw, CUR, (j) + PG_RING, stages, m0, n0, rowb, wave, lane);                   \
+        pg_compute<P>(pg_base(NXT, P::WM * wm, i16, grp), pg_base(NXT, P::TM + P::WN * wn, i16, grp), acc,  \
+                      fw[C], fa[C], fw[N], fa[N]);                                                   \
     } while (0)
 
-/* Which output tile workgroup L of T takes. Workgroups are dispatched to the 8 XCDs in turn (L % 8), each XCD with its
- * own L2, so tiles are numbered XCD by XCD: XCD k takes a contiguous run of the tile order, and within it consecutive
- * workgroups walk PG_GROUP m-tiles (the fastest) by one n-tile at a time. The workgroups an XCD runs at once then share
- * a few a and w tiles, read from its L2 rather than each from memory. Returns (n-tile, m-tile). */
-constexpr int PG_XCDS = 8, PG_GROUP = 4;
-
-__device__ __forceinline__ int2 pg_tile(int L, int T, int nx) {
-    const int k = L % PG_XCDS, r = L / PG_XCDS, per = T / PG_XCDS, extra = T % PG_XCDS;
-    const int id = k * per + min(k, extra) + r;                /* a bijection of [0, T) */
-    const int band = PG_GROUP * nx;                            /* tiles of a band of PG_GROUP m-tiles */
-    const int y0 = (id / band) * PG_GROUP, ny = (T / nx) - y0, rows = ny < PG_GROUP ? ny : PG_GROUP;
-    const int in = id - (id / band) * band;
-    return int2{in / rows, y0 + in % rows};
-}
-
-template <int EPI>
-__global__ void __launch_bounds__(PG_WAVES * WAVE, 1) prefill_gemm_kernel(PfGemm g) {
-    __shared__ __align__(16) unsigned char b0[PG_STAGE], b1[PG_STAGE], b2[PG_STAGE], b3[PG_STAGE];
+/* The output tile (rows m0.., columns n0..) of a workgroup, K walked and the epilogue applied. */
+template <class P, int EPI>
+__device__ __forceinline__ void pg_run(const PfGemm &g, int m0, int n0, unsigned char *b0, unsigned char *b1,
+                                       unsigned char *b2, unsigned char *b3) {
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
     const int i16 = lane & 15, grp = lane >> 4, wm = wave >> 2, wn = wave & 3;
-    const int2 tile = pg_tile(blockIdx.x, gridDim.x, (g.N + PG_TN - 1) / PG_TN);
-    const int n0 = tile.x * PG_TN, m0 = tile.y * PG_TM;
     const int rowb = g.K * 2, stages = g.K / PG_KC;
     const Rsrc ra = pg_rsrc(g.a, (long long)g.M * rowb), rw = pg_rsrc(g.w, (long long)g.N * rowb);
 
     /* the accumulators start at zero in their AGPRs, before the first DMA is issued */
-    f32x4 acc[4][8];
+    f32x4 acc[P::NT][P::NU];
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < P::NT; t++)
 #pragma unroll
-        for (int u = 0; u < 8; u++) asm volatile("" : "=a"(acc[t][u]) : "0"(f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
-    pg_fetch(ra, rw, b0, 0, stages, m0, n0, rowb, wave, lane);
-    pg_fetch(ra, rw, b1, 1, stages, m0, n0, rowb, wave, lane);
-    pg_fetch(ra, rw, b2, 2, stages, m0, n0, rowb, wave, lane);
-    pg_fetch(ra, rw, b3, 3, stages, m0, n0, rowb, wave, lane);
-    bf16x8 fw[2][4], fa[2][8];
-    pg_wait_stage<3>();
+        for (int u = 0; u < P::NU; u++) asm volatile("" : "=a"(acc[t][u]) : "0"(f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
+    pg_fetch<P>(ra, rw, b0, 0, stages, m0, n0, rowb, wave, lane);
+    pg_fetch<P>(ra, rw, b1, 1, stages, m0, n0, rowb, wave, lane);
+    pg_fetch<P>(ra, rw, b2, 2, stages, m0, n0, rowb, wave, lane);
+    pg_fetch<P>(ra, rw, b3, 3, stages, m0, n0, rowb, wave, lane);
+    bf16x8 fw[2][P::NT], fa[2][P::NU];
+    pg_wait_stage<P, 3>();
     pg_barrier();
 #pragma unroll
-    for (int t = 0; t < 8; t++) fa[0][t] = pg_frag(pg_base(b0, 128 * wm, i16, grp), t);
+    for (int u = 0; u < P::NU; u++) fa[0][u] = pg_frag(pg_base(b0, P::WM * wm, i16, grp), u);
 #pragma unroll
-    for (int t = 0; t < 4; t++) fw[0][t] = pg_frag(pg_base(b0, PG_TM + 64 * wn, i16, grp), t);
+    for (int t = 0; t < P::NT; t++) fw[0][t] = pg_frag(pg_base(b0, P::TM + P::WN * wn, i16, grp), t);
     for (int j = 0; j < stages; j += 4) {   /* stages is a multiple of 4 (K of 128, checked by the host) */
         PG_STEP(j, b0, b1, 0, 1);
         PG_STEP(j + 1, b1, b2, 1, 0);
@@ -202,22 +206,22 @@ __global__ void __launch_bounds__(PG_WAVES * WAVE, 1) prefill_gemm_kernel(PfGemm
      * tied to this point, so no read moves above it) */
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < P::NT; t++)
 #pragma unroll
-        for (int u = 0; u < 8; u++) asm volatile("" : "+a"(acc[t][u]));
+        for (int u = 0; u < P::NU; u++) asm volatile("" : "+a"(acc[t][u]));
 
     const Rsrc ro = pg_rsrc(EPI == SG_F32 ? (const void *)g.out_f32 : (const void *)g.out,
                             (long long)g.M * g.N * (EPI == SG_F32 ? 4 : 2));
     const Rsrc rr = pg_rsrc(g.res, EPI == SG_RESID ? (long long)g.M * g.N * 2 : 0);
     const Rsrc rs = pg_rsrc(g.rstd, EPI == SG_RELU2 ? (long long)g.M * 4 : 0);
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int m = m0 + 128 * wm + 16 * u + i16;
+    for (int u = 0; u < P::NU; u++) {
+        const int m = m0 + P::WM * wm + 16 * u + i16;
         const float r = EPI == SG_RELU2 ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, m * 4, 0, 0))
                                         : 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int n = n0 + 64 * wn + 16 * t + 4 * grp;
+        for (int t = 0; t < P::NT; t++) {
+            const int n = n0 + P::WN * wn + 16 * t + 4 * grp;
             if (n >= g.N) continue;
             const int at = m * g.N + n;   /* rows past M lie outside the views' ranges: no access */
             float s[4] = {acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]};
@@ -249,6 +253,63 @@ __global__ void __launch_bounds__(PG_WAVES * WAVE, 1) prefill_gemm_kernel(PfGemm
     }
 }
 
+/* The order workgroups take work in. Workgroups are dispatched to the 8 XCDs in turn (L % 8), each XCD with its own
+ * L2, so work items are numbered XCD by XCD: pg_order(l, count) gives XCD k a contiguous run of [0, count) (a
+ * bijection, for a first workgroup that is a multiple of 8). Tile id is then placed in bands of PG_GROUP m-tiles walked
+ * m-tile fastest, one n-tile at a time (pg_band), so the workgroups an XCD runs at once share a few a and w tiles,
+ * read from its L2 rather than each from memory. */
+constexpr int PG_XCDS = 8, PG_GROUP = 4;
+
+__device__ __forceinline__ int pg_order(int l, int count) {
+    const int k = l % PG_XCDS, r = l / PG_XCDS, per = count / PG_XCDS, extra = count % PG_XCDS;
+    return k * per + min(k, extra) + r;
+}
+
+/* (n-tile, m-tile) of tile id of the T = nx * ny tiles. */
+__device__ __forceinline__ int2 pg_band(int id, int T, int nx) {
+    const int band = PG_GROUP * nx;                            /* tiles of a band of PG_GROUP m-tiles */
+    const int y0 = (id / band) * PG_GROUP, ny = (T / nx) - y0, rows = ny < PG_GROUP ? ny : PG_GROUP;
+    const int in = id - (id / band) * band;
+    return int2{in / rows, y0 + in % rows};
+}
+
+/* Workgroups [0, full) take whole tiles 0 .. full - 1; the rest take pieces (2: halves by n, 4: quarters) of tiles
+ * full .. T - 1, the pieces of a tile on consecutive items of one XCD. A piece past M or N has nothing to compute.
+ * Launches with no pieces use the instantiation without them (SPLIT false): the same whole-tile loop ran 3-6 % slower
+ * in a kernel that also holds the pieces' code. */
+template <int EPI, bool SPLIT>
+__global__ void __launch_bounds__(PG_WAVES * WAVE, 1) prefill_gemm_kernel(PfGemm g, int full, int pieces) {
+    __shared__ __align__(16) unsigned char b0[PG_STAGE], b1[PG_STAGE], b2[PG_STAGE], b3[PG_STAGE];
+    const int nx = (g.N + 255) / 256, T = nx * ((g.M + 255) / 256), L = blockIdx.x;
+    if (!SPLIT || L < full) {
+        const int2 tile = pg_band(pg_order(L, full), T, nx);
+        pg_run<PgFull, EPI>(g, tile.y * 256, tile.x * 256, b0, b1, b2, b3);
+        return;
+    }
+    const int id = pg_order(L - full, (T - full) * pieces), p = id % pieces;
+    const int2 tile = pg_band(full + id / pieces, T, nx);
+    if (pieces == 2) {
+        const int m0 = tile.y * 256, n0 = tile.x * 256 + 128 * p;
+        if (n0 < g.N) pg_run<PgHalf, EPI>(g, m0, n0, b0, b1, b2, b3);
+    } else {
+        const int m0 = tile.y * 256 + 128 * (p >> 1), n0 = tile.x * 256 + 128 * (p & 1);
+        if (m0 < g.M && n0 < g.N) pg_run<PgQuarter, EPI>(g, m0, n0, b0, b1, b2, b3);
+    }
+}
+
+/* The number of compute units of the current device (256 if it cannot be read), once per device. */
+static int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n
+                                                                                                                : 256;
+    }
+    return cus[dev];
+}
+
 int prefill_gemm(const PfGemm &g, int epi, hipStream_t stream) {
     if (g.M <= 0) return 0;
     if (!g.a || !g.w || g.N <= 0 || g.K <= 0 || g.K % (PG_RING * PG_KC) || g.N % 4 ||
@@ -259,13 +320,25 @@ int prefill_gemm(const PfGemm &g, int epi, hipStream_t stream) {
     if ((f32 ? !g.out_f32 : !g.out) || (epi == SG_RESID && !g.res) || (epi == SG_RELU2 && !g.rstd) ||
         (epi != SG_STORE && epi != SG_RESID && epi != SG_F32 && epi != SG_RELU2))
         return NC_ERR_SHAPE;
-    const dim3 grid(((g.N + PG_TN - 1) / PG_TN) * ((g.M + PG_TM - 1) / PG_TM)), block(PG_WAVES * WAVE);
+    /* T tiles in rounds of one workgroup a CU: the R = T mod CUs tiles of a last part-filled round are cut into 4
+     * (R <= CUs / 4) or 2 (R <= CUs / 2) pieces when there are earlier full rounds; otherwise every tile is whole. */
+    const int cus = device_cus(), T = ((g.N + 255) / 256) * ((g.M + 255) / 256), R = T % cus;
+    const int pieces = T > cus && R > 0 && 4 * R <= cus ? 4 : T > cus && R > 0 && 2 * R <= cus ? 2 : 1;
+    const int full = pieces > 1 ? T - R : T;
+    const dim3 grid(full + (T - full) * pieces), block(PG_WAVES * WAVE);
+    const bool split = pieces > 1;
+#define PG_LAUNCH(E)                                                                                             \
+    do {                                                                                                         \
+        if (split) hipLaunchKernelGGL((prefill_gemm_kernel<E, true>), grid, block, 0, stream, g, full, pieces);    \
+        else hipLaunchKernelGGL((prefill_gemm_kernel<E, false>), grid, block, 0, stream, g, full, pieces);         \
+    } while (0)
     switch (epi) {
-    case SG_STORE: hipLaunchKernelGGL(prefill_gemm_kernel<SG_STORE>, grid, block, 0, stream, g); break;
-    case SG_RESID: hipLaunchKernelGGL(prefill_gemm_kernel<SG_RESID>, grid, block, 0, stream, g); break;
-    case SG_F32: hipLaunchKernelGGL(prefill_gemm_kernel<SG_F32>, grid, block, 0, stream, g); break;
-    default: hipLaunchKernelGGL(prefill_gemm_kernel<SG_RELU2>, grid, block, 0, stream, g); break;
+    case SG_STORE: PG_LAUNCH(SG_STORE); break;
+    case SG_RESID: PG_LAUNCH(SG_RESID); break;
+    case SG_F32: PG_LAUNCH(SG_F32); break;
+    default: PG_LAUNCH(SG_RELU2); break;
     }
+#undef PG_LAUNCH
     return (int)hipGetLastError();
 }
 

@@ -74,3 +74,20 @@ def test_prefill_gemm_rows_do_not_depend_on_m(device):
     # and a row in a later tile, moved to row 0 of a call of its own
     one = run(STORE, w, a[5000:5001].contiguous())
     assert torch.equal(full[5000:5001].view(torch.int16), one.view(torch.int16))
+
+
+@pytest.mark.parametrize("N,K,M,epi", [(4992, 1664, 8192, STORE), (6656, 1664, 8192, RELU2), (6656, 1664, 5000, F32)])
+def test_split_tiles_match_whole_tiles(device, N, K, M, epi):
+    """At these sizes the last round's tiles are cut into halves (qkv: 640 tiles, 128 of them in halves) or quarters
+    (fc: 832 tiles, 64 in quarters; 5,000 rows: 520 tiles, 8 in quarters, some past M); every output must equal the
+    same row computed in 256-row calls, whose few tiles are never cut."""
+    gen = torch.Generator().manual_seed(N + M + epi)
+    w = (torch.randn(N, K, generator=gen) * 0.02).bfloat16().to(device)
+    a = torch.randn(M, K, generator=gen).bfloat16().to(device)
+    rstd = (0.5 + torch.rand(M, generator=gen)).float().to(device)
+    full = run(epi, w, a, rstd=rstd)
+    bits = torch.int32 if epi == F32 else torch.int16
+    for r0 in range(0, M, 256):
+        r1 = min(M, r0 + 256)
+        part = run(epi, w, a[r0:r1].contiguous(), rstd=rstd[r0:r1].contiguous())
+        assert torch.equal(full[r0:r1].view(bits), part.view(bits)), (r0, r1)

@@ -49,9 +49,9 @@ def kernels():
                         "-o", str(out), str(SOURCE)], check=True, capture_output=True)
         text = out.read_text()
     bodies = {}
-    for m in re.finditer(r"^(_ZN2nc19prefill_gemm_kernelILi(-?\d+)EEEvNS_6PfGemmE):[^\n]*\n(.*?)\n\.Lfunc_end", text,
+    for m in re.finditer(r"^(_ZN2nc19prefill_gemm_kernelILi(-?\d+)ELb([01])EEEvNS_6PfGemmE\w*):[^\n]*\n(.*?)\n\.Lfunc_end", text,
                          re.S | re.M):
-        bodies[int(m.group(2))] = m.group(3).splitlines()
+        bodies[(int(m.group(2)), m.group(3) == "1")] = m.group(4).splitlines()
     return bodies, text
 
 
@@ -160,9 +160,12 @@ def loop_lines(lines):
     return out
 
 
+KERNELS = [(epi, split) for epi in (0, 2, 3, 4) for split in (False, True)]
+
+
 def test_every_epilogue_kernel_is_built(kernels):
     bodies, _ = kernels
-    assert sorted(bodies) == [0, 2, 3, 4]
+    assert sorted(bodies) == KERNELS
 
 
 def test_no_spills(kernels):
@@ -172,7 +175,7 @@ def test_no_spills(kernels):
     assert counts and all(int(c) == 0 for c in counts)
 
 
-@pytest.mark.parametrize("epi", [0, 2, 3, 4])
+@pytest.mark.parametrize("epi", KERNELS)
 def test_mfma_operands_come_from_lds_reads(kernels, epi):
     found = mfma_operand_writers(kernels[0][epi])
     assert len(found) >= 32, len(found)
@@ -180,7 +183,7 @@ def test_mfma_operands_come_from_lds_reads(kernels, epi):
         assert kinds == {"ds_read"}, (epi, where, kinds)
 
 
-@pytest.mark.parametrize("epi", [0, 2, 3, 4])
+@pytest.mark.parametrize("epi", KERNELS)
 def test_accumulators_stay_in_place(kernels, epi):
     body = loop_lines(kernels[0][epi])
     assert any("v_mfma" in l for l in body)
@@ -217,7 +220,7 @@ def wait_states_before_agpr_reads(lines):
     return fewest
 
 
-@pytest.mark.parametrize("epi", [0, 2, 3, 4])
+@pytest.mark.parametrize("epi", KERNELS)
 def test_accumulators_read_after_the_wait_states(kernels, epi):
     # 19 is the longest a 16-pass XDL result needs before a VALU reads it; the kernel waits 32
     assert wait_states_before_agpr_reads(kernels[0][epi]) >= 32
