@@ -605,6 +605,23 @@ __global__ void set_table_kernel(int32_t *table, long long idx0, long long count
     if (i < count) table[idx0 + i] = value0 + step * (int)i;
 }
 
+/* Runs of block-table entries written by one launch (kernel arguments, so the host's list is free once launched):
+ * run r sets table[idx0 + i] = value0 + step i for i < count. The runs of a launch are disjoint. */
+struct TableRun {
+    int32_t idx0, count, value0, step;
+};
+constexpr int TABLE_RUNS = 224;
+struct TableRuns {
+    int32_t n;
+    TableRun run[TABLE_RUNS];
+};
+
+__global__ void __launch_bounds__(256) set_table_runs_kernel(int32_t *table, TableRuns t) {
+    if ((int)blockIdx.x >= t.n) return;
+    const TableRun r = t.run[blockIdx.x];
+    for (int i = threadIdx.x; i < r.count; i += 256) table[r.idx0 + i] = r.value0 + r.step * i;
+}
+
 /* Whole pages src_page0 + z -> dst_page0 + z of layer y and head x: 2 KiB of K codes, 2 KiB of V codes, 128 bytes of
  * scales. */
 __global__ void __launch_bounds__(256) copy_pages_kernel(uint8_t *k_pages, uint8_t *v_pages, float *kv_scale,
@@ -664,6 +681,8 @@ struct Decoder {
     int32_t *block_table;                /* [B][max_pages]: slot b's entry e is -1, a pool page of its own, or a
                                             store page it shares read-only after dec_load_prompt */
     std::vector<int32_t> table;          /* host copy of block_table (what the enqueued work leaves there) */
+    std::vector<int2> dirty;             /* [B]: slot b's entries [x, y) changed since the last flush_table */
+    std::vector<int> dirty_slots;        /* the slots with changed entries, in the order first changed */
     std::vector<int32_t> hpos;           /* host copy of pos: the position a live slot's next step writes */
     std::vector<unsigned long long> live;  /* host copy of the live-slot mask of dec_set_active */
     int32_t *tokens, *alt_tokens, *pos, *first, *seq_lens, *num_new;  /* [B] */
@@ -1072,10 +1091,12 @@ static Decoder *create(const int *cfg, const uint64_t *ptrs, const float *scal, 
     d->v_pages = (uint8_t *)device_alloc(d, (size_t)d->L * d->layer_pages * d->H * PAGE_BYTES);
     d->kv_scale = (float *)device_alloc(d, (size_t)d->L * d->layer_pages * d->H * 2 * PAGE * sizeof(float));
     const long long entries = (long long)d->B * d->max_pages;
+    REQUIRE(entries < (1LL << 31), "the block table exceeds 2^31 entries");
     d->block_table = (int32_t *)device_alloc(d, (size_t)entries * sizeof(int32_t));
     hipLaunchKernelGGL(set_table_kernel, dim3((unsigned)((entries + 255) / 256)), dim3(256), 0, d->stream,
                        d->block_table, 0LL, entries, -1, 0);
     d->table.assign(entries, -1);
+    d->dirty.assign(d->B, int2{0, 0});
     d->free_pages.resize(d->pool);
     for (long long i = 0; i < d->pool; i++) d->free_pages[i] = (int32_t)(d->pool - 1 - i);   /* page 0 on top */
     d->hpos.assign(d->B, 0);
@@ -1146,17 +1167,43 @@ static bool store_page(const Decoder *d, int32_t page) { return page >= d->pool;
 
 static int32_t *table_row(Decoder *d, int b) { return d->table.data() + (size_t)b * d->max_pages; }
 
-/* Slot b's host entries [e0, e1) to the device table, one launch per run of consecutive pages or of -1. */
+/* Slot b's host entries [e0, e1) have changed: queued for the device table's next flush_table. */
 static void upload_table(Decoder *d, int b, int e0, int e1) {
-    const int32_t *row = table_row(d, b);
-    for (int e = e0; e < e1;) {
-        const int step = row[e] < 0 ? 0 : 1;
-        int f = e + 1;
-        while (f < e1 && row[f] == row[f - 1] + step && (row[f] < 0) == (row[e] < 0)) f++;
-        hipLaunchKernelGGL(set_table_kernel, dim3((unsigned)((f - e + 255) / 256)), dim3(256), 0, d->stream,
-                           d->block_table, (long long)b * d->max_pages + e, (long long)(f - e), row[e], step);
-        e = f;
+    if (e0 >= e1) return;
+    int2 &r = d->dirty[b];
+    if (r.x >= r.y) {
+        d->dirty_slots.push_back(b);
+        r = int2{e0, e1};
+    } else {
+        r = int2{e0 < r.x ? e0 : r.x, e1 > r.y ? e1 : r.y};
     }
+}
+
+/* The queued entries to the device table, each slot's changed range as runs of consecutive pages or of -1, up to
+ * TABLE_RUNS runs a launch (a prefill call changes a page of every 16 rows: 512 entries in a few launches rather than
+ * one each). Called before any launch that reads the table and at the end of each entry point that changes it. */
+static void flush_table(Decoder *d) {
+    TableRuns t;
+    t.n = 0;
+    auto launch = [&]() {
+        hipLaunchKernelGGL(set_table_runs_kernel, dim3((unsigned)t.n), dim3(256), 0, d->stream, d->block_table, t);
+        t.n = 0;
+    };
+    for (int b : d->dirty_slots) {
+        const int32_t *row = table_row(d, b);
+        const int e1 = d->dirty[b].y;
+        for (int e = d->dirty[b].x; e < e1;) {
+            const int step = row[e] < 0 ? 0 : 1;
+            int f = e + 1;
+            while (f < e1 && row[f] == row[f - 1] + step && (row[f] < 0) == (row[e] < 0)) f++;
+            t.run[t.n++] = TableRun{(int32_t)((long long)b * d->max_pages + e), f - e, row[e], step};
+            if (t.n == TABLE_RUNS) launch();
+            e = f;
+        }
+        d->dirty[b] = int2{0, 0};
+    }
+    d->dirty_slots.clear();
+    if (t.n) launch();
     HIP_CHECK(hipGetLastError());
 }
 
@@ -1208,6 +1255,7 @@ static void release_pages(Decoder *d, int b, int e0) {
  * entries of those positions hold pages (the callers' checks). */
 static void copy_positions(Decoder *d, int b, int at, int store_at, int n, bool to_store) {
     if (n <= 0) return;
+    flush_table(d);   /* the kernel finds the slot's pages through the device table */
     const int32_t *tab = d->block_table + (size_t)b * d->max_pages;
     const long long units = (long long)n * d->L * d->H;
     hipLaunchKernelGGL(copy_positions_kernel, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, d->stream, d->k_pages,
@@ -1277,6 +1325,7 @@ static void prefill(Decoder *d, int n, const int32_t *rows) {
     for (int r = 0; r < n; r++)
         if (pos[r] == 0) release_pages(d, slot[r], 0);
     for (int r = 0; r < n; r++) own_pages(d, slot[r], pos[r] / PAGE, pos[r] / PAGE + 1, true);
+    flush_table(d);
     HIP_CHECK(hipEventSynchronize(d->staged));  /* the previous upload has been read */
     int32_t *s = d->staging;
     memcpy(s, tok, n * sizeof(int32_t));
@@ -1365,6 +1414,7 @@ extern "C" void dec_release(void *handle, int b) {
     Decoder *d = (Decoder *)handle;
     if (b < 0 || b >= d->B) nc::dec::die("dec_release", "slot out of range", __LINE__);
     nc::dec::release_pages(d, b, 0);
+    nc::dec::flush_table(d);
 }
 
 extern "C" void dec_debug_pages(void *handle, long long *out) {
@@ -1389,6 +1439,7 @@ extern "C" void dec_set_prompt(void *handle, int b, int32_t token, int32_t last,
     HIP_CHECK(hipGetLastError());
     d->hpos[b] = last;
     nc::dec::release_pages(d, b, last / nc::PAGE + 1);   /* pages past the slot's position hold an older sequence */
+    nc::dec::flush_table(d);
 }
 
 extern "C" int dec_prefill_rows(void *) { return nc::dec::PREFILL_ROWS; }
@@ -1397,10 +1448,12 @@ extern "C" void dec_prefill(void *handle, int n, const int32_t *rows) { nc::dec:
 
 extern "C" void dec_save_prompt(void *handle, int b, int at, int store_at, int n) {
     nc::dec::save_prompt((Decoder *)handle, b, at, store_at, n);
+    nc::dec::flush_table((Decoder *)handle);
 }
 
 extern "C" void dec_load_prompt(void *handle, int b, int at, int store_at, int n) {
     nc::dec::load_prompt((Decoder *)handle, b, at, store_at, n);
+    nc::dec::flush_table((Decoder *)handle);
 }
 
 extern "C" uint32_t *dec_masks(void *handle) { return ((Decoder *)handle)->host_allow; }
@@ -1439,6 +1492,7 @@ extern "C" void dec_launch_body(void *handle) {
     for (int b = 0; b < d->B; b++)
         if (((d->live[b / nc::dec::MASK_BITS] >> (b % nc::dec::MASK_BITS)) & 1ull) && d->hpos[b] < d->max_len)
             nc::dec::own_pages(d, b, d->hpos[b] / nc::PAGE, d->hpos[b] / nc::PAGE + 1, true);
+    nc::dec::flush_table(d);
     nc::dec::enqueue_body(d);
     HIP_CHECK(hipGetLastError());
 }
