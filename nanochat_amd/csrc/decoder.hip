@@ -8,8 +8,8 @@
  *          attention.hip), o GEMM (+ residual: the bf16 rounding of the fp32 sum, and each 16-row tile's sum of
  *          squares), fc GEMM (+ ReLU^2 of the sum scaled by the rstd it takes from those tile sums), proj GEMM
  *          (K-slice partials), proj_norm_kernel (the partials + residual, then the next layer's residual norm) }
- *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits), choose_kernel (greedy, Gumbel-max or nucleus choice within
- *          the allowed tokens, then the commit), the tokens to pinned host memory.
+ *   head   norm_kernel(FINAL), lm_head GEMM (fp32 logits; prefill_gemm.hip's tiled kernel), choose_kernel (greedy,
+ *          Gumbel-max or nucleus choice within the allowed tokens, then the commit), the tokens to pinned host memory.
  * A step's GEMMs are slot_gemm.hip's weight-streaming MFMA kernel with the epilogue fused (long-K GEMMs split into
  * K-slices whose partials a second kernel adds in order; a model wider than 2,048 computes the MLP's rstd in
  * rstd_kernel). Prefill's GEMMs (up to 8,192 rows a call) are prefill_gemm.hip's MFMA-tiled kernel over all the
@@ -1013,8 +1013,15 @@ static void enqueue_head(Decoder *d) {
         n.in = a.x;
         n.out = a.hn;
         launch_norm(d->lane[0], n);
-        gemm_epi(d, d->lane[0], true, SG_F32, d->lm_head, d->vocab, d->C, a.hn, R, nullptr, d->logits, nullptr, nullptr,
-                 d->active);
+        /* the vocabulary's rows are many: the tiled GEMM (128-row tiles up to 128 slots) takes in a tile's slots once
+         * per 256 vocabulary rows, where the slot GEMM takes them in per 64 (config 5: 39 against 63 us). It writes
+         * every row up to R; choose_kernel reads only the active slots'. Logits past its 2 GiB of 32-bit offsets
+         * go through the slot GEMM. */
+        if ((long long)R * d->vocab * 4 < (1LL << 31))
+            gemm(d->lane[0], d->lm_head, d->vocab, d->C, a.hn, R, d->logits, SG_F32);
+        else
+            gemm_epi(d, d->lane[0], true, SG_F32, d->lm_head, d->vocab, d->C, a.hn, R, nullptr, d->logits, nullptr,
+                     nullptr, d->active);
         ChoiceArgs c = {d->logits, d->probs, d->active, d->allow, d->temperature, d->top_p, d->seed, d->first,
                         d->tokens, d->alt_tokens, d->pos, d->softcap, d->vocab, d->lazy};
         hipLaunchKernelGGL(choose_kernel, dim3(R), dim3(CHOICE_THREADS), 0, d->stream, c);

@@ -59,6 +59,7 @@ struct PgTile {
 typedef PgTile<256, 256> PgFull;
 typedef PgTile<256, 128> PgHalf;
 typedef PgTile<128, 128> PgQuarter;
+typedef PgTile<128, 256> PgThin;   /* calls of M <= 128 rows (a decode step's slots) */
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -275,13 +276,19 @@ __device__ __forceinline__ int2 pg_band(int id, int T, int nx) {
 
 /* Workgroups [0, full) take whole tiles 0 .. full - 1; the rest take pieces (2: halves by n, 4: quarters) of tiles
  * full .. T - 1, the pieces of a tile on consecutive items of one XCD. A piece past M or N has nothing to compute.
- * Launches with no pieces use the instantiation without them (SPLIT false): the same whole-tile loop ran 3-6 % slower
- * in a kernel that also holds the pieces' code. */
-template <int EPI, bool SPLIT>
+ * Launches with no pieces use the instantiation without them (MODE PG_WHOLE): the same whole-tile loop ran 3-6 %
+ * slower in a kernel that also holds the pieces' code. Calls of M <= 128 rows take tiles of 128 rows (PG_THIN). */
+enum { PG_WHOLE, PG_SPLIT, PG_THIN };
+
+template <int EPI, int MODE>
 __global__ void __launch_bounds__(PG_WAVES * WAVE, 1) prefill_gemm_kernel(PfGemm g, int full, int pieces) {
     __shared__ __align__(16) unsigned char b0[PG_STAGE], b1[PG_STAGE], b2[PG_STAGE], b3[PG_STAGE];
     const int nx = (g.N + 255) / 256, T = nx * ((g.M + 255) / 256), L = blockIdx.x;
-    if (!SPLIT || L < full) {
+    if (MODE == PG_THIN) {
+        pg_run<PgThin, EPI>(g, 0, pg_order(L, nx) * 256, b0, b1, b2, b3);
+        return;
+    }
+    if (MODE == PG_WHOLE || L < full) {
         const int2 tile = pg_band(pg_order(L, full), T, nx);
         pg_run<PgFull, EPI>(g, tile.y * 256, tile.x * 256, b0, b1, b2, b3);
         return;
@@ -323,14 +330,18 @@ int prefill_gemm(const PfGemm &g, int epi, hipStream_t stream) {
     /* T tiles in rounds of one workgroup a CU: the R = T mod CUs tiles of a last part-filled round are cut into 4
      * (R <= CUs / 4) or 2 (R <= CUs / 2) pieces when there are earlier full rounds; otherwise every tile is whole. */
     const int cus = device_cus(), T = ((g.N + 255) / 256) * ((g.M + 255) / 256), R = T % cus;
-    const int pieces = T > cus && R > 0 && 4 * R <= cus ? 4 : T > cus && R > 0 && 2 * R <= cus ? 2 : 1;
+    const bool cut = g.M > 128 && T > cus && R > 0;
+    const int pieces = cut && 4 * R <= cus ? 4 : cut && 2 * R <= cus ? 2 : 1;
     const int full = pieces > 1 ? T - R : T;
     const dim3 grid(full + (T - full) * pieces), block(PG_WAVES * WAVE);
-    const bool split = pieces > 1;
+    const int mode = g.M <= 128 ? PG_THIN : pieces > 1 ? PG_SPLIT : PG_WHOLE;
 #define PG_LAUNCH(E)                                                                                             \
     do {                                                                                                         \
-        if (split) hipLaunchKernelGGL((prefill_gemm_kernel<E, true>), grid, block, 0, stream, g, full, pieces);    \
-        else hipLaunchKernelGGL((prefill_gemm_kernel<E, false>), grid, block, 0, stream, g, full, pieces);         \
+        if (mode == PG_THIN) hipLaunchKernelGGL((prefill_gemm_kernel<E, PG_THIN>), grid, block, 0, stream, g, full,  \
+                                                pieces);                                                         \
+        else if (mode == PG_SPLIT) hipLaunchKernelGGL((prefill_gemm_kernel<E, PG_SPLIT>), grid, block, 0, stream, g, \
+                                                      full, pieces);                                             \
+        else hipLaunchKernelGGL((prefill_gemm_kernel<E, PG_WHOLE>), grid, block, 0, stream, g, full, pieces);     \
     } while (0)
     switch (epi) {
     case SG_STORE: PG_LAUNCH(SG_STORE); break;

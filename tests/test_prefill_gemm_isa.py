@@ -49,9 +49,9 @@ def kernels():
                         "-o", str(out), str(SOURCE)], check=True, capture_output=True)
         text = out.read_text()
     bodies = {}
-    for m in re.finditer(r"^(_ZN2nc19prefill_gemm_kernelILi(-?\d+)ELb([01])EEEvNS_6PfGemmE\w*):[^\n]*\n(.*?)\n\.Lfunc_end", text,
+    for m in re.finditer(r"^(_ZN2nc19prefill_gemm_kernelILi(-?\d+)ELi([012])EEEvNS_6PfGemmE\w*):[^\n]*\n(.*?)\n\.Lfunc_end", text,
                          re.S | re.M):
-        bodies[(int(m.group(2)), m.group(3) == "1")] = m.group(4).splitlines()
+        bodies[(int(m.group(2)), int(m.group(3)))] = m.group(4).splitlines()
     return bodies, text
 
 
@@ -160,7 +160,7 @@ def loop_lines(lines):
     return out
 
 
-KERNELS = [(epi, split) for epi in (0, 2, 3, 4) for split in (False, True)]
+KERNELS = [(epi, mode) for epi in (0, 2, 3, 4) for mode in (0, 1, 2)]   # modes: whole tiles, split, thin
 
 
 def test_every_epilogue_kernel_is_built(kernels):
