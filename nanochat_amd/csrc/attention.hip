@@ -679,6 +679,7 @@ __device__ __forceinline__ StepLoads step_fetch(const AttnArgs &a, const StepArg
     return f;
 }
 
+template <bool VE>
 __device__ __forceinline__ void step_rows(const AttnArgs &a, const StepArgs &s, const StepLoads &f, int b, int kvh,
                                           int p, bool own, int page, bool wait, uint16_t *q_lds, int lane) {
 #pragma unroll
@@ -706,7 +707,7 @@ __device__ __forceinline__ void step_rows(const AttnArgs &a, const StepArgs &s, 
     norm_rope_pair(bf16_to_f32(f.kx1), bf16_to_f32(f.kx2), f.kg1, f.kg2, f.cr, f.sr, y1, y2);
     const float k1 = bf16_to_f32(f32_to_bf16(y1)), k2 = bf16_to_f32(f32_to_bf16(y2));
     float v1 = bf16_to_f32(f.vx1), v2 = bf16_to_f32(f.vx2);
-    if (s.ve) {
+    if (VE && s.ve) {
         const int token = s.ve_tokens[b];
         if ((unsigned)token < (unsigned)s.ve_rows)
             ve_mix_pair(s.ve_h + (long long)b * s.C, s.ve_gate + (long long)kvh * s.C, s.C,
@@ -845,9 +846,11 @@ __device__ __forceinline__ void merge_unit(const AttnArgs &a, long long slot0, i
  *
  * STEP (the fused decode step): the sequence's token at position L - 1 is appended in the same launch (step_rows):
  * every item normalizes and rotates its query rows from the raw qkv row, and the item holding the token quantizes and
- * stores its K and V before its pass reads them back.
+ * stores its K and V before its pass reads them back. VE: the step mixes value embeddings into v; a step without them
+ * runs an instantiation without that code (243 VGPRs against 256: the gate's double exponential holds its constants
+ * in registers).
  */
-template <bool STEP>
+template <bool STEP, bool VE = false>
 __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
     extern __shared__ int sh_cum[];  /* [2][B + 1]: full, then partial chunks of the sequences < b */
     __shared__ __align__(16) uint16_t sh_q[WAVES][STEP ? MAX_G * HEAD_DIM : 8];   /* the step's query rows */
@@ -944,7 +947,7 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
         QOp qb[1];
         if (STEP) {
             const int p = L - 1;
-            step_rows(a, sa, sl, b, kvh, p, own, own ? tab_entry(tab, p / PAGE - first) : 0, late, sh_q[wave], lane);
+            step_rows<VE>(a, sa, sl, b, kvh, p, own, own ? tab_entry(tab, p / PAGE - first) : 0, late, sh_q[wave], lane);
             uint4 raw[1][4];
 #pragma unroll
             for (int cc = 0; cc < 4; cc++)
@@ -1368,7 +1371,7 @@ static int device_wave_slots() {
     if (!slots[dev]) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<true>, 256,
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<true, true>, 256,
                                                          2 * (MAX_DECODE_BATCH + 1) * sizeof(int)) != hipSuccess)
             return 2048;
         slots[dev] = max(1, cus * per_cu * WAVES);
@@ -1432,7 +1435,8 @@ static int launch_decode(const void *q, const void *k_pages, const void *v_pages
     const size_t lds = 2 * (B + 1) * sizeof(int);
     if (step) {
         a.step = *step;
-        hipLaunchKernelGGL(decode_kernel<true>, dim3(grid), dim3(256), lds, stream, a);
+        if (step->ve) hipLaunchKernelGGL((decode_kernel<true, true>), dim3(grid), dim3(256), lds, stream, a);
+        else hipLaunchKernelGGL((decode_kernel<true, false>), dim3(grid), dim3(256), lds, stream, a);
     } else {
         hipLaunchKernelGGL(decode_kernel<false>, dim3(grid), dim3(256), lds, stream, a);
     }
