@@ -7,7 +7,7 @@
  *
  * Differences from the reference, by design: the KV cache is fp8 with one scale per (token, head) (the reference
  * caches bf16); the prompt store lives in device memory, as pages of the same pools (the reference: pinned host
- * memory); dec_prefill takes up to 8192 rows (the reference: 1024); steps are launched eagerly, not as graphs.
+ * memory); dec_prefill takes up to 16384 rows (the reference: 1024); steps are launched eagerly, not as graphs.
  */
 #ifndef NANOCHAT_DECODE_H
 #define NANOCHAT_DECODE_H

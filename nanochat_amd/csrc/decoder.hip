@@ -12,7 +12,7 @@
  *          Gumbel-max or nucleus choice within the allowed tokens, then the commit), the tokens to pinned host memory.
  * A step's GEMMs are slot_gemm.hip's weight-streaming MFMA kernel with the epilogue fused (long-K GEMMs split into
  * K-slices whose partials a second kernel adds in order; a model wider than 2,048 computes the MLP's rstd in
- * rstd_kernel). Prefill's GEMMs (up to 8,192 rows a call) are prefill_gemm.hip's MFMA-tiled kernel over all the
+ * rstd_kernel). Prefill's GEMMs (up to 16,384 rows a call) are prefill_gemm.hip's MFMA-tiled kernel over all the
  * call's rows at once, with the epilogue fused (bf16 out, the residual, ReLU^2 with the rstd); each row's sums run in
  * one fixed order, so they do not depend on how many rows the call holds. The o GEMM's residual sum needs its whole
  * row for the MLP's rstd, so it writes fp32 and rstd_kernel adds the residual. Every kernel covers the slots up to
@@ -57,7 +57,7 @@ constexpr int MAX_BATCH = 1024;            /* slots (the reference's limit, deco
 constexpr int MASK_BITS = 64;              /* slots per word of a slot mask */
 constexpr int MASK_WORDS = MAX_BATCH / MASK_BITS;
 constexpr int WORD_BITS = 32;              /* tokens per word of an allowed-token mask */
-constexpr int PREFILL_ROWS = 8192;         /* rows per dec_prefill call */
+constexpr int PREFILL_ROWS = 16384;        /* rows per dec_prefill call */
 constexpr int SPLIT_SLOTS = 64;            /* a step over more slots runs as two lanes (enqueue_body) */
 constexpr int GLOBAL_PTRS = 4, LAYER_PTRS = 8;
 constexpr int CHOICE_THREADS = 1024, CHOICE_WAVES = CHOICE_THREADS / WAVE;

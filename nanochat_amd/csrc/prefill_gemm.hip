@@ -1,6 +1,6 @@
 /*
  * The prefill GEMMs of the decoder runtime on gfx950: out[m][n] = epilogue(sum_k a[m][k] w[n][k]) for the rows of a
- * dec_prefill call (M <= 8,192 prompt tokens), bf16 operands, fp32 sums. At these sizes a GEMM is bound by the matrix
+ * dec_prefill call (M <= 16,384 prompt tokens), bf16 operands, fp32 sums. At these sizes a GEMM is bound by the matrix
  * cores, so it is tiled for them: a workgroup of 8 waves owns a 256 x 256 output tile (2 x 4 waves of 128 x 64, 32
  * accumulator tiles of 16 x 16 a wave; two waves a SIMD), walks K in stages of 32, and takes each
  * stage's operands (256 rows of a and 256 rows of w, 64 bytes each: 32 KiB) from memory into LDS by LDS DMA, in a ring

@@ -239,7 +239,7 @@ def test_decode_library_exports_every_declared_symbol():
     # the kernel entry points ride along in the decoder library
     for name in declared():
         assert hasattr(dec, name), name
-    assert dec.dec_prefill_rows(None) == 8192
+    assert dec.dec_prefill_rows(None) == 16384
 
 
 def test_decode_argtypes_match_the_reference_binding():
