@@ -1,6 +1,7 @@
 """CPU replay of decode_kernel's work split (nanochat_amd/csrc/attention.hip: chunks cut at multiples of 64 pages, a last
 piece under 4 pages joined to the one before it (checked against a from-scratch cut of the page range); the
-per-work-group prefixes over sequences of full and partial chunks; full chunks numbered first, then partial ones;
+per-work-group prefixes over sequences of full and partial chunks; full chunks numbered first (a unit's rotated by its
+index), then partial ones;
 item k to work-group k % G, wave (k / G) % 4; partial slot = the chunk's unit-order index; the unit's chunks counted
 in arrived[u], the last to finish merging slots slot - j .. + nch) for many shapes: every (unit, page) is attended
 exactly once, by an item whose page range depends on nothing but the unit's own length; partial slots stay inside the
@@ -85,7 +86,7 @@ def replay(seq_lens, hkv, workers, window, max_len):
                     b = max(i for i in range(B) if cf[i] <= k)
                     nch, p0, nfull, npart = split[b]
                     kvh, jf = divmod(k - cf[b], nfull)
-                    j = jf + p0
+                    j = (jf + b * hkv + kvh) % nfull + p0   # a unit's full chunks rotated by its index
                 else:
                     k2 = k - NF
                     b = max(i for i in range(B) if cp[i] <= k2)
