@@ -839,8 +839,9 @@ __device__ __forceinline__ void merge_unit(const AttnArgs &a, long long slot0, i
  * second launch is needed.
  *
  * Schedule: the full chunks (at least SPLIT_PAGES long) are numbered first, then the partial ones, each in (sequence, KV
- * head) order, a unit's full chunks rotated by the unit's index u (its f-th full item takes full chunk (f + u) mod
- * nfull); item k goes to work-group k % G (G = gridDim.x) and, within it, to wave (k / G) % 4, round
+ * head) order, a unit's full chunks rotated (its f-th full item takes full chunk (f + u + k0 / G) mod nfull, u the
+ * unit's index, k0 its first full item); item k goes to work-group k % G (G = gridDim.x) and, within it, to wave
+ * (k / G) % 4, round
  * k / (4 G). Equal full chunks land one per work-group before any doubles up, and the short partial chunks fill in
  * last: every compute unit streams about the same number of pages (a CU's bandwidth, not a wave's, is the limit once
  * it holds more than one wave), and a wave that finishes early leaves the HBM bandwidth to the others.
@@ -901,10 +902,14 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
             us = unit_split(a, a.seq_lens[b], begin);
             const int local = k - cf[b];
             kvh = local / us.nfull;
-            /* the unit's full chunks in an order rotated by the unit's index: consecutive items run on successive
-             * XCDs (work-group L on XCD L % 8), so without it chunk j of every unit would share an XCD, and the last
-             * chunks, with the token's append and most merges, would all run on one */
-            j = (local - kvh * us.nfull + (b * a.Hkv + kvh)) % us.nfull + us.p0;
+            /* The unit's full chunks in a rotated order. Consecutive items run on successive XCDs (work-group L on XCD
+             * L % 8) and successive work-groups, so unrotated, chunk j of every unit would share an XCD, and the last
+             * chunks (the token's append, most merges) would run on one XCD and a few work-groups. Rotating by the
+             * unit's index u spreads them over the XCDs; adding the round (first item / work-groups) spreads units
+             * whose items fall on the same work-groups in successive rounds. */
+            const int first_item = cf[b] + kvh * us.nfull;
+            const int rot = (b * a.Hkv + kvh + (int)(first_item / G)) % us.nfull;
+            j = (local - kvh * us.nfull + rot) % us.nfull + us.p0;
         } else {        /* partial chunk: the first and / or the last of a unit */
             const int k2 = k - NF;
             b = find_sequence(cp, a.B, k2);

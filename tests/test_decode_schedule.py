@@ -86,7 +86,8 @@ def replay(seq_lens, hkv, workers, window, max_len):
                     b = max(i for i in range(B) if cf[i] <= k)
                     nch, p0, nfull, npart = split[b]
                     kvh, jf = divmod(k - cf[b], nfull)
-                    j = (jf + b * hkv + kvh) % nfull + p0   # a unit's full chunks rotated by its index
+                    rot = (b * hkv + kvh + (int(cf[b]) + kvh * nfull) // G) % nfull   # rotated by index and round
+                    j = (jf + rot) % nfull + p0
                 else:
                     k2 = k - NF
                     b = max(i for i in range(B) if cp[i] <= k2)
