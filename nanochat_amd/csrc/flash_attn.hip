@@ -145,12 +145,14 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int qi = q0 + 16 * j + c;
+        /* raw scores: the scale is positive, so the max of the scaled scores is the scaled max, and it is folded into
+         * one FMA per exponential below */
         float sv[16];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                float x = sc[j][kt][i] * a.scale_log2;
+                float x = sc[j][kt][i];
                 if (MASKED) {
                     const int key = kb0 + kt * 16 + 4 * g + i;
                     const bool ok = (key <= qi) & (key < seglen) & ((a.window < 0) | (qi - key <= a.window));
@@ -161,7 +163,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
         float mt = sv[0];
 #pragma unroll
         for (int i = 1; i < 16; i++) mt = fmaxf(mt, sv[i]);
-        mt = pair_max32(pair_max16(mt));
+        mt = pair_max32(pair_max16(mt)) * a.scale_log2;
         if (j == 0) {
             __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
 #pragma unroll
@@ -183,7 +185,7 @@ __device__ __forceinline__ void fa_block(const FlashFwd &a, const FaStage &s, co
         float p[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            p[i] = __builtin_amdgcn_exp2f(sv[i] - mbase);
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], a.scale_log2, -mbase));
             psum += p[i];
         }
         st.l[j] += psum;
@@ -441,7 +443,7 @@ __global__ void __launch_bounds__(64 * DKV_WAVES, 2) flash_bwd_dkv_kernel(FlashB
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = qt * 16 + 4 * g + i;
-                    const float e = __builtin_amdgcn_exp2f(sc[qt][i] * a.scale_log2 - lv[i]);
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qt][i], a.scale_log2, -lv[i]));
                     const float p = !masked || visible(key, qs + r, seglen, a.window) ? e : 0.0f;
                     const float ds = p * (dp[qt][i] - dv_[i]);
                     pb[qt >> 1][(qt & 1) * 4 + i] = (__bf16)p;
@@ -575,7 +577,7 @@ __global__ void __launch_bounds__(FA_THREADS, 2) flash_bwd_dq_kernel(FlashBwd a)
                     for (int j = 0; j < 2; j++)
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
-                            const float e = __builtin_amdgcn_exp2f(sc[j][i] * a.scale_log2 - lse2[j]);
+                            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][i], a.scale_log2, -lse2[j]));
                             const float p =
                                 !masked || visible(k0 + 16 * kt + 4 * g + i, q0 + 16 * j + c, seglen, a.window) ? e : 0.0f;
                             db[j][kk * 4 + i] = (__bf16)(p * (dp[j][i] - dd[j]));
