@@ -662,7 +662,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": ("qk_norm_rope append_kernel + decode_kernel<false>" if args.two_launch
-                                else "nc_decode_step_fp8 (decode_kernel<true>)"),
+                                else "nc_decode_step_fp8 (decode_kernel<true, false>)"),
                      "bytes_per_launch": step_b,
                      "timing": "HIP events around K back-to-back launches of the kernel on its stream"},
     }
