@@ -541,11 +541,15 @@ __device__ __forceinline__ void attend_pages_tab(const AttnArgs &a, const TabReg
 
 /* Split points of decode: a (sequence, KV head) unit's keys are cut at every multiple of SPLIT_PAGES pages (1,024
  * positions), except that a last piece of fewer than MIN_TAIL pages joins the chunk before it (a sequence one token
- * past a multiple of 1,024 would otherwise spend a work item, and a merge step, on one page). The cuts depend on
- * nothing but the sequence's own length, whatever the rest of the batch holds, so a sequence's sums (and its output
- * bits) depend only on its own query, keys and length. */
+ * past a multiple of 1,024 would otherwise spend a work item, and a merge step, on one page). A unit that would be one
+ * chunk (at most SPLIT_PAGES + MIN_TAIL - 1 pages) is cut at every multiple of SHORT_SPLIT pages instead, with the same
+ * join, so a short context is streamed by several waves rather than one. The cuts depend on nothing but the sequence's
+ * own length (and the window), whatever the rest of the batch holds, so a sequence's sums (and its output bits) depend
+ * only on its own query, keys and length. */
 constexpr int SPLIT_PAGES = 64;
+constexpr int SHORT_SPLIT = 16;
 constexpr int MIN_TAIL = 4;
+constexpr int SHORT_UNIT = SPLIT_PAGES + MIN_TAIL - 1;   /* the most pages a unit of short chunks holds */
 static_assert(SPLIT_PAGES + MIN_TAIL - 1 <= 2 * WAVE, "a chunk's block-table entries are staged in two lanes' worth");
 
 /* Key range [begin, p] of a sequence of L keys and its logical pages [pg0, pg0 + npages); npages = 0 for an
@@ -558,38 +562,48 @@ __device__ __forceinline__ int decode_pages(const AttnArgs &a, int L, int &begin
     return p / PAGE + 1 - pg0;
 }
 
-/* How a unit's logical pages [pg0, e) split (S = SPLIT_PAGES, c0 = pg0 / S): chunk j covers [pg0 or (c0 + j) S,
- * (c0 + j + 1) S or e), the first starting at pg0 and the last ending at e; the pieces are cut at the multiples of S
- * and a last piece shorter than MIN_TAIL joins the one before it. A chunk is full when it covers at least S pages; only
- * the first and the last can be partial. */
+/* How a unit's logical pages [pg0, e) split (S = SPLIT_PAGES, or SHORT_SPLIT for a unit of at most SHORT_UNIT pages;
+ * c0 = pg0 / S): chunk j covers [pg0 or (c0 + j) S, (c0 + j + 1) S or e), the first starting at pg0 and the last
+ * ending at e; the pieces are cut at the multiples of S and a last piece shorter than MIN_TAIL joins the one before
+ * it. A chunk is full when it covers at least SPLIT_PAGES pages; only the first and the last can be partial, and every
+ * chunk of a unit of short chunks is. */
 struct UnitSplit {
     int pg0, np, nch;   /* pages, chunks */
     int p0;             /* 1: chunk 0 is partial */
     int nfull, npart;   /* full and partial chunks */
+    int s;              /* the cut: SPLIT_PAGES or SHORT_SPLIT */
 };
 
 __device__ __forceinline__ UnitSplit unit_split(const AttnArgs &a, int L, int &begin) {
-    UnitSplit u = {0, 0, 0, 0, 0, 0};
+    UnitSplit u = {0, 0, 0, 0, 0, 0, SPLIT_PAGES};
     const int np = decode_pages(a, L, begin, u.pg0);
     if (np <= 0) return u;
-    const int e = u.pg0 + np, c0 = u.pg0 / SPLIT_PAGES;
+    const int S = np <= SHORT_UNIT ? SHORT_SPLIT : SPLIT_PAGES;
+    const int e = u.pg0 + np, c0 = u.pg0 / S;
     u.np = np;
-    const int pieces = (e - 1) / SPLIT_PAGES - c0 + 1;
-    const int tail = e - max(u.pg0, ((e - 1) / SPLIT_PAGES) * SPLIT_PAGES);
+    u.s = S;
+    const int pieces = (e - 1) / S - c0 + 1;
+    const int tail = e - max(u.pg0, ((e - 1) / S) * S);
     u.nch = pieces - (pieces >= 2 && tail < MIN_TAIL);
-    const int size0 = (u.nch == 1 ? e : (c0 + 1) * SPLIT_PAGES) - u.pg0;
-    const int sizel = e - (c0 + u.nch - 1) * SPLIT_PAGES;
-    u.p0 = size0 < SPLIT_PAGES;
-    u.npart = u.p0 + (u.nch > 1 && sizel < SPLIT_PAGES);
+    if (S == SHORT_SPLIT) {
+        u.p0 = 1;
+        u.npart = u.nch;
+        u.nfull = 0;
+        return u;
+    }
+    const int size0 = (u.nch == 1 ? e : (c0 + 1) * S) - u.pg0;
+    const int sizel = e - (c0 + u.nch - 1) * S;
+    u.p0 = size0 < S;
+    u.npart = u.p0 + (u.nch > 1 && sizel < S);
     u.nfull = u.nch - u.npart;
     return u;
 }
 
 /* Logical pages [first, last) of chunk j. */
 __device__ __forceinline__ void chunk_pages(const UnitSplit &u, int j, int &first, int &last) {
-    const int c = u.pg0 / SPLIT_PAGES + j;
-    first = j == 0 ? u.pg0 : c * SPLIT_PAGES;
-    last = j == u.nch - 1 ? u.pg0 + u.np : (c + 1) * SPLIT_PAGES;
+    const int c = u.pg0 / u.s + j;
+    first = j == 0 ? u.pg0 : c * u.s;
+    last = j == u.nch - 1 ? u.pg0 + u.np : (c + 1) * u.s;
 }
 
 __device__ __forceinline__ void store_bf16x4(uint16_t *dst, const float *v) {
@@ -917,7 +931,8 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(AttnArgs a) {
             const int local = k2 - cp[b];
             kvh = local / us.npart;
             const int jp = local - kvh * us.npart;
-            j = (us.p0 && jp == 0) ? 0 : us.nch - 1;
+            /* a unit of short chunks lists them all; any other unit its partial first and / or last chunk */
+            j = us.s == SHORT_SPLIT ? jp : (us.p0 && jp == 0) ? 0 : us.nch - 1;
         }
         const long long slot = (long long)cf[b] + cp[b] + (long long)kvh * us.nch + j;
         const int L = a.seq_lens[b];
@@ -1367,10 +1382,11 @@ static long long max_unit_pages(int max_seq_len, int window) {
     return n;
 }
 
-/* Items a launch can hold: a unit of n pages touches at most ceil(n / SPLIT_PAGES) + 1 chunks. */
+/* Items a launch can hold: a unit of n pages touches at most ceil(n / SPLIT_PAGES) + 1 chunks, or, cut into short
+ * chunks (n <= SHORT_UNIT), ceil(n / SHORT_SPLIT) + 1. */
 static long long item_bound(int B, int Hkv, int max_seq_len, int window) {
-    const long long n = max_unit_pages(max_seq_len, window);
-    return (long long)B * Hkv * ((n + SPLIT_PAGES - 1) / SPLIT_PAGES + 1);
+    const long long n = max_unit_pages(max_seq_len, window), ns = min(n, (long long)SHORT_UNIT);
+    return (long long)B * Hkv * max((n + SPLIT_PAGES - 1) / SPLIT_PAGES + 1, (ns + SHORT_SPLIT - 1) / SHORT_SPLIT + 1);
 }
 
 static int device_wave_slots() {

@@ -1,7 +1,8 @@
-"""CPU replay of decode_kernel's work split (nanochat_amd/csrc/attention.hip: chunks cut at multiples of 64 pages, a last
-piece under 4 pages joined to the one before it (checked against a from-scratch cut of the page range); the
+"""CPU replay of decode_kernel's work split (nanochat_amd/csrc/attention.hip: chunks cut at multiples of 64 pages, or of
+16 pages for a unit of at most 67 pages, a last piece under 4 pages joined to the one before it (checked against a
+from-scratch cut of the page range); the
 per-work-group prefixes over sequences of full and partial chunks; full chunks numbered first (a unit's rotated by its
-index), then partial ones;
+index), then partial ones (every chunk of a unit of 16-page chunks);
 item k to work-group k % G, wave (k / G) % 4; partial slot = the chunk's unit-order index; the unit's chunks counted
 in arrived[u], the last to finish merging slots slot - j .. + nch) for many shapes: every (unit, page) is attended
 exactly once, by an item whose page range depends on nothing but the unit's own length; partial slots stay inside the
@@ -14,6 +15,7 @@ import pytest
 PAGE = 16
 WAVES = 4
 SPLIT = 64
+SHORT = 16
 
 
 def unit_pages(L, window, max_len):
@@ -25,15 +27,20 @@ def unit_pages(L, window, max_len):
 
 
 MIN_TAIL = 4
+SHORT_UNIT = SPLIT + MIN_TAIL - 1   # a unit of at most this many pages is cut every 16 pages
+
+
+def cut(n):
+    return SHORT if n <= SHORT_UNIT else SPLIT
 
 
 def chunk_ranges(pg0, n):
-    """Logical page ranges of a unit's chunks, from first principles: cut [pg0, pg0 + n) at every multiple of 64 pages,
-    then join a last piece shorter than 4 pages to the one before it."""
+    """Logical page ranges of a unit's chunks, from first principles: cut [pg0, pg0 + n) at every multiple of 64 pages
+    (16 if n <= 67), then join a last piece shorter than 4 pages to the one before it."""
     if n <= 0:
         return []
-    e = pg0 + n
-    cuts = [pg0] + list(range((pg0 // SPLIT + 1) * SPLIT, e, SPLIT)) + [e]
+    e, S = pg0 + n, cut(n)
+    cuts = [pg0] + list(range((pg0 // S + 1) * S, e, S)) + [e]
     pieces = [(a, b) for a, b in zip(cuts, cuts[1:])]
     if len(pieces) >= 2 and pieces[-1][1] - pieces[-1][0] < MIN_TAIL:
         pieces[-2:] = [(pieces[-2][0], e)]
@@ -44,27 +51,31 @@ def unit_split(pg0, n):
     """(chunks, chunk 0 partial, full, partial) of logical pages [pg0, pg0 + n), as the kernel computes them."""
     if n <= 0:
         return 0, 0, 0, 0
-    e, c0 = pg0 + n, pg0 // SPLIT
-    pieces = (e - 1) // SPLIT - c0 + 1
-    tail = e - max(pg0, ((e - 1) // SPLIT) * SPLIT)
+    S = cut(n)
+    e, c0 = pg0 + n, pg0 // S
+    pieces = (e - 1) // S - c0 + 1
+    tail = e - max(pg0, ((e - 1) // S) * S)
     nch = pieces - int(pieces >= 2 and tail < MIN_TAIL)
-    size0 = (e if nch == 1 else (c0 + 1) * SPLIT) - pg0
-    sizel = e - (c0 + nch - 1) * SPLIT
-    p0 = int(size0 < SPLIT)
-    npart = p0 + int(nch > 1 and sizel < SPLIT)
+    if S == SHORT:
+        return nch, 1, 0, nch
+    size0 = (e if nch == 1 else (c0 + 1) * S) - pg0
+    sizel = e - (c0 + nch - 1) * S
+    p0 = int(size0 < S)
+    npart = p0 + int(nch > 1 and sizel < S)
     return nch, p0, nch - npart, npart
 
 
 def chunk_pages(pg0, n, nch, j):
-    c = pg0 // SPLIT + j
-    return (pg0 if j == 0 else c * SPLIT), (pg0 + n if j == nch - 1 else (c + 1) * SPLIT)
+    S = cut(n)
+    c = pg0 // S + j
+    return (pg0 if j == 0 else c * S), (pg0 + n if j == nch - 1 else (c + 1) * S)
 
 
 def item_bound(B, hkv, max_len, window):
     n = -(-max_len // PAGE)
     if window >= 0:
         n = min(n, window // PAGE + 2)
-    return B * hkv * (-(-n // SPLIT) + 1)
+    return B * hkv * max(-(-n // SPLIT) + 1, -(-min(n, SHORT_UNIT) // SHORT) + 1)
 
 
 def replay(seq_lens, hkv, workers, window, max_len):
@@ -93,7 +104,7 @@ def replay(seq_lens, hkv, workers, window, max_len):
                     b = max(i for i in range(B) if cp[i] <= k2)
                     nch, p0, nfull, npart = split[b]
                     kvh, jp = divmod(k2 - cp[b], npart)
-                    j = 0 if p0 and jp == 0 else nch - 1
+                    j = jp if cut(units[b][0]) == SHORT else (0 if p0 and jp == 0 else nch - 1)
                 n, pg0 = units[b]
                 first, last = chunk_pages(pg0, n, nch, j)
                 assert (first, last) == chunk_ranges(pg0, n)[j]
@@ -164,3 +175,20 @@ def test_a_sequences_split_does_not_depend_on_the_batch():
                 lens = others[:at] + [L] + others[at:]
                 got = replay(lens, 2, int(rng.integers(1, 50)), window, 6000)
                 assert {k[1:]: v for k, v in got.items() if k[0] == at} == mine
+
+
+@pytest.mark.parametrize("window", [-1, 0, 100, 1071, 1072, 1500])
+def test_short_and_long_cuts_at_their_boundary(window):
+    """Units of 1..70 pages either side of the 67-page boundary (16-page cuts up to it, 64-page cuts past it), alone
+    and in a batch with longer sequences, every page once, the chunk sizes as cut."""
+    for L in list(range(1, 70 * PAGE + 1, 7)) + [1056, 1057, 1072, 1073, 1088, 1089]:
+        n, pg0 = unit_pages(L, window, 8000)
+        pieces = chunk_ranges(pg0, n)
+        if n <= SHORT_UNIT:
+            assert all(b - a <= SHORT + MIN_TAIL - 1 for a, b in pieces)
+            assert len(pieces) <= -(-n // SHORT) + 1
+        else:
+            assert all(b - a <= SPLIT + MIN_TAIL - 1 for a, b in pieces)
+        alone = replay([L], 3, 8, window, 8000)
+        got = replay([5000, L, 3000], 3, 40, window, 8000)
+        assert {k[1:]: v for k, v in got.items() if k[0] == 1} == {k[1:]: v for k, v in alone.items()}
