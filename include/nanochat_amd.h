@@ -162,9 +162,10 @@ size_t nc_decode_workspace_bytes(int B, int Hq, int Hkv, int max_seq_len, int wi
  * The current token must already be appended (nc_kv_append_fp8 / nc_qk_norm_rope_append_fp8).
  * q: bf16 [B][Hq][128]; out: bf16 [B][Hq][128]; seq_lens: int32 [B] (<= 0: inactive, output zeros; more
  * than max_seq_len: output NaN); max_seq_len <= max_pages * 16; B <= 4096.
- * Work split: a (sequence, KV head)'s keys are cut at every multiple of 1,024 positions (a last piece under 256
- * positions joins the one before it) and each piece is one work item with its own softmax state; the wave that finishes a unit's last piece merges its pieces in position
- * order, in the same launch (one kernel). The split points depend on nothing but the sequence's own length, so its
+ * Work split: a (sequence, KV head)'s keys are cut at every multiple of 1,024 positions, or of 256 positions when its
+ * keys span at most 67 pages (1,072 positions); a last piece under 64 positions joins the one before it. Each piece
+ * is one work item with its own softmax state; the wave that finishes a unit's last piece merges its pieces in
+ * position order, in the same launch (one kernel). The split points depend on nothing but the sequence's own length, so its
  * output bits do not depend on the other sequences of the launch, on its place in the batch or on `workers` (waves
  * taking the items; 0: every wave slot of the device). The workspace (at least nc_decode_workspace_bytes) must be
  * zero-filled before its first use and keep one workspace_bytes value across calls.

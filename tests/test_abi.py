@@ -65,12 +65,13 @@ def test_small_workspace_rejected(lib):
 def expected_workspace(B, Hq, Hkv, max_seq, window):
     """The documented layout: fp32 partials (O [128] + max, sum) of G heads for every item a launch can hold below the
     last 1/256 of the workspace, which holds one int32 arrival count per (sequence, KV head); a unit of n pages (n
-    capped by the window) touches at most ceil(n / 64) + 1 chunks of 1,024 positions. The smallest such size that is a
-    multiple of 1,024 of the form 256 k, k a multiple of 4 with 255 k >= partials and k >= 4 B Hkv."""
+    capped by the window) touches at most ceil(n / 64) + 1 chunks of 1,024 positions, or, at most 67 pages long and cut
+    every 16 pages, ceil(n / 16) + 1 chunks. The smallest such size that is a multiple of 1,024 of the form 256 k, k a
+    multiple of 4 with 255 k >= partials and k >= 4 B Hkv."""
     unit_pages = -(-max_seq // 16)
     if window >= 0:
         unit_pages = min(unit_pages, window // 16 + 2)
-    items = B * Hkv * (-(-unit_pages // 64) + 1)
+    items = B * Hkv * max(-(-unit_pages // 64) + 1, -(-min(unit_pages, 67) // 16) + 1)
     partials = items * (Hq // Hkv) * 130 * 4
     k = max(-(-partials // 255), 4 * B * Hkv)
     k = -(-k // 4) * 4
