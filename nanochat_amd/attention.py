@@ -11,6 +11,7 @@
 
 Every function launches on the current torch stream and requires device tensors: there is no CPU path.
 """
+import functools
 from collections import OrderedDict
 
 import torch
@@ -77,8 +78,10 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+@functools.lru_cache(maxsize=256)
 def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int,
                            window: int = -1) -> int:
+    """nc_decode_workspace_bytes (0: an unsupported shape), kept per shape: a decode step asks for it every call."""
     return hip_library().nc_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_seq_len, window)
 
 
@@ -109,7 +112,7 @@ def decode_attention(q: torch.Tensor, cache: PagedKVCache, block_table: torch.Te
     if out.numel() != q.numel():
         raise ValueError(f"out must hold [{B}, {Hq}, {HEAD_DIM}]")
     lib = hip_library()
-    need = lib.nc_decode_workspace_bytes(B, Hq, cache.num_kv_heads, max_seq_len, window)
+    need = decode_workspace_bytes(B, Hq, cache.num_kv_heads, max_seq_len, window)
     if need == 0:
         raise ValueError(f"unsupported decode shape: B={B}, Hq={Hq}, Hkv={cache.num_kv_heads}")
     if workspace is None or workspace.numel() * workspace.element_size() < need:
@@ -184,7 +187,7 @@ def decode_step(qkv: torch.Tensor, num_q_heads: int, cache: PagedKVCache, block_
         if ve_tokens.numel() < B:
             raise ValueError(f"ve tokens holds {ve_tokens.numel()} entries for {B} sequences")
     lib = hip_library()
-    need = lib.nc_decode_workspace_bytes(B, num_q_heads, Hkv, max_seq_len, window)
+    need = decode_workspace_bytes(B, num_q_heads, Hkv, max_seq_len, window)
     if need == 0:
         raise ValueError(f"unsupported decode shape: B={B}, Hq={num_q_heads}, Hkv={Hkv}")
     if workspace is None or workspace.numel() * workspace.element_size() < need:
