@@ -205,3 +205,24 @@ def test_chunk_boundaries(device, window):
     out, want, _, _ = run(w, device, seed=7, window=window, inp=inp)
     mx, mean = attn_errors(out, want)
     assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("window", [-1, 300, 1000, 1060])
+def test_short_unit_cuts(device, window):
+    """Units of at most 67 pages are cut every 16 pages (a last piece under 4 pages joined): lengths around those cuts
+    (16, 17, 20, 21 pages), the 67 / 68-page boundary between the short and the 1,024-position cut, and windows that
+    leave a long sequence a short, unaligned unit. Every piece and the merge meet the oracle bound, and each sequence's
+    bits are the same decoded alone."""
+    w = DecodeWorkload("short-cuts", 12, 8, 2, 5000, ctx_min=1, paged=True, outliers=0.01)
+    inp = decode_inputs(w, seed=13)
+    inp["ctx_lens"][:] = torch.tensor([255, 256, 319, 320, 1039, 1070, 1071, 1072, 1087, 2500, 4096, 4999],
+                                      dtype=torch.int32)
+    out, want, _, (cache, table, lens, q) = run(w, device, seed=13, window=window, inp=inp)
+    mx, mean = attn_errors(out, want)
+    assert mx <= ATTN_MAX_ABS and mean <= ATTN_MEAN_ABS, (mx, mean)
+    full = out.view(torch.int16).cpu()
+    for b in range(w.batch):
+        alone = decode_attention(q[b:b + 1].contiguous(), cache, table[b:b + 1].contiguous(),
+                                 lens[b:b + 1].contiguous(), inp["max_seq_len"], window=window,
+                                 workers=2).view(torch.int16).cpu()
+        assert torch.equal(alone[0], full[b]), b

@@ -20,9 +20,10 @@ from tests.paged_util import read_sequence
 pytestmark = pytest.mark.gpu
 
 # every boundary a unit's pages can sit on: 1 token, a page (16), a page pair (32), a chunk (1,024 = 64 pages), a last
-# piece of 15 pages (joined to the chunk before it) or 16 (a chunk of its own)
-EDGE_LENGTHS = [1, 2, 15, 16, 17, 31, 32, 33, 48, 1023, 1024, 1025, 1040, 1056, 1264, 1265, 1280, 1281, 2047, 2048,
-                2049, 3000]
+# piece of 3 pages (joined to the chunk before it, 2,096 keys) or 4 (a chunk of its own, 2,097), and for a unit of at
+# most 67 pages the 16-page cuts (256, 320 keys) and the 67 / 68-page boundary (1,072 keys)
+EDGE_LENGTHS = [1, 2, 15, 16, 17, 31, 32, 33, 48, 256, 257, 320, 321, 1023, 1024, 1025, 1040, 1056, 1072, 1073, 1088,
+                1264, 1265, 1280, 1281, 2047, 2048, 2049, 2096, 2097, 3000]
 
 
 def bf16_randn(gen, *shape, outliers=0.0):
